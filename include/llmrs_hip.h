@@ -1,0 +1,240 @@
+/*
+ * llmrs_hip.h - C ABI of the MI355X (gfx950) backend for llm.rs.
+ *
+ * This is the drop-in boundary.  The first group of entry points mirrors the
+ * reference's operator plug-in interface, `trait Backend`
+ * (src/backend.rs:15-40), one export per trait method, with the same argument
+ * meaning.  The second group has no trait counterpart: it keeps the whole
+ * decode loop resident in HBM (KV cache, attention, embedding gather, greedy
+ * argmax, whole-step graph replay), because the reference's layer code reads
+ * device tensors on the host (src/core/layer.rs:41,166,191-195,219-246;
+ * src/main.rs:163), which only works on the mapped shared memory of a mobile
+ * SoC.
+ *
+ * Conventions
+ *  - Every function returns 0 on success or a negative LLMRS_E_* code.  The
+ *    message of the last failure on the calling thread is returned by
+ *    llmrs_last_error().  The reference panics instead (cpu.rs:37,46;
+ *    Cargo.toml:60 panic="abort"); a Rust shim maps non-zero to panic!.
+ *  - Tensors are opaque handles owned by the caller until llmrs_tensor_free
+ *    (the reference's Arc<Storage> drop, src/core/tensor.rs:50-57).  Ops that
+ *    return a tensor allocate it (like cpu.rs:150, opencl.rs:307).
+ *  - All work runs on one HIP stream in issue order; host visibility is at
+ *    llmrs_tensor_download / llmrs_sync / model calls that return host data,
+ *    which matches the reference's synchronous op semantics
+ *    (opencl.rs:290,389: queue.finish()).
+ *  - Exports are serialised by one internal mutex, so calls from several host
+ *    threads (rayon workers in the reference) are safe.
+ *  - No torch types and no HIP types appear here: plain pointers and sizes.
+ */
+#ifndef LLMRS_HIP_H
+#define LLMRS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes -------------------------------------------------------- */
+#define LLMRS_OK 0
+#define LLMRS_E_INVALID (-1)    /* bad argument / shape mismatch (cpu.rs:37) */
+#define LLMRS_E_DTYPE (-2)      /* wrong storage kind for the op (cpu.rs:46) */
+#define LLMRS_E_HIP (-3)        /* a HIP runtime call failed */
+#define LLMRS_E_NOINIT (-4)     /* llmrs_init not called / failed */
+#define LLMRS_E_MODULE (-5)     /* hsaco missing or kernel not found */
+#define LLMRS_E_RANGE (-6)      /* position beyond max_seq, id beyond vocab */
+#define LLMRS_E_OOM (-7)        /* device allocation failed */
+
+/* ---- devices (src/backend.rs:7-12 plus the new Hip variant) ------------- */
+#define LLMRS_DEVICE_CPU 0
+#define LLMRS_DEVICE_OPENCL 1
+#define LLMRS_DEVICE_QNN 2
+#define LLMRS_DEVICE_HIP 3
+
+/* ---- storage kinds (src/core/tensor.rs:13-44 plus extensions) ----------- */
+#define LLMRS_F32 0   /* Storage::Cpu / Storage::Shared                      */
+#define LLMRS_F16 1   /* KV cache only (extension)                           */
+#define LLMRS_Q4 2    /* Storage::CpuQ4: 4-bit codes, f32 scale per 32 block */
+#define LLMRS_Q4_0 3  /* Q4_0: 4-bit codes, fp16 scale per 32 block          */
+#define LLMRS_Q8_0 4  /* Q8_0: int8 codes, fp16 scale per 32 block (ext.)    */
+
+typedef struct llmrs_tensor llmrs_tensor;
+typedef struct llmrs_model llmrs_model;
+
+/* ---- context ------------------------------------------------------------ */
+/* Select the HIP device, create the stream, hipModuleLoad every hsaco in
+ * `hsaco_dir` (NULL = the directory of this shared library).  Replaces the
+ * OpenCL context bring-up cl_context() (src/backend/opencl.rs:11-34). */
+int llmrs_init(int device_ordinal, const char* hsaco_dir);
+int llmrs_shutdown(void);
+const char* llmrs_last_error(void);
+/* Backend::device (src/backend.rs:17): always LLMRS_DEVICE_HIP. */
+int llmrs_device(void);
+/* Backend::name (src/backend.rs:18). */
+const char* llmrs_name(void);
+/* Wait for all queued work (the reference's queue.finish()). */
+int llmrs_sync(void);
+/* Number of compute units of the current device (0 before init). */
+int llmrs_num_cus(void);
+
+/* ---- tensors (Tensor::new / to_device / data / drop) -------------------- */
+/* Cpu -> device upload of an f32 tensor (tensor.rs:232-253). */
+int llmrs_tensor_upload_f32(const float* data, const size_t* dims, int ndim,
+                            llmrs_tensor** out);
+/* CpuQ4 -> device (tensor.rs:255-281).  `qs` is the reference's planar
+ * nibble array [n][k/2] (byte i of a block = e[2i] | e[2i+1] << 4,
+ * tensor.rs:125-131) and `scales` its f32 array [n][k/32].  The device copy
+ * keeps fp16 scales when every scale is exactly representable in fp16, else
+ * f32 scales; codes and scales are bit-preserved either way. */
+int llmrs_tensor_upload_q4(const uint8_t* qs, const float* scales, size_t n,
+                           size_t k, llmrs_tensor** out);
+/* Q8_0 weights (extension): int8 codes [n][k], f32 scales [n][k/32] that are
+ * exactly representable in fp16. */
+int llmrs_tensor_upload_q8_0(const int8_t* qs, const float* scales, size_t n,
+                             size_t k, llmrs_tensor** out);
+int llmrs_tensor_zeros(const size_t* dims, int ndim, llmrs_tensor** out);
+/* Tensor::data() / to_device(Cpu) for f32 tensors: copies `count` floats. */
+int llmrs_tensor_download(const llmrs_tensor* t, float* out, size_t count);
+int llmrs_tensor_ndim(const llmrs_tensor* t);
+int llmrs_tensor_dims(const llmrs_tensor* t, size_t* dims);
+int llmrs_tensor_dtype(const llmrs_tensor* t);
+int llmrs_tensor_free(llmrs_tensor* t);
+
+/* ---- trait Backend mirror (src/backend.rs:21-39) ------------------------ */
+/* Backend::matmul (backend.rs:21): a[m,k] @ b[k,n], f32. */
+int llmrs_matmul(const llmrs_tensor* a, const llmrs_tensor* b,
+                 llmrs_tensor** out);
+/* Backend::matmul_transposed (backend.rs:24): a[m,k] @ b[n,k]^T.  b is f32,
+ * Q4, Q4_0 or Q8_0; for quantised b each row of a is first quantised to Q8_0
+ * (cpu.rs:76-110, quantize_row_q8_0 cpu.rs:663-745). */
+int llmrs_matmul_transposed(const llmrs_tensor* a, const llmrs_tensor* b,
+                            llmrs_tensor** out);
+/* Backend::matmul_slice (backend.rs:28): a[m,cols] @ other[rows,cols]^T,
+ * `other_data` is a host slice that is uploaded (opencl.rs:396-419). */
+int llmrs_matmul_slice(const llmrs_tensor* a, const float* other_data,
+                       size_t rows, size_t cols, llmrs_tensor** out);
+/* Backend::add_assign (backend.rs:31): a += b. */
+int llmrs_add_assign(llmrs_tensor* a, const llmrs_tensor* b);
+/* Backend::silu_mul (backend.rs:32): gate = gate/(1+exp(-gate)) * up. */
+int llmrs_silu_mul(llmrs_tensor* gate, const llmrs_tensor* up);
+/* Backend::rope_inplace (backend.rs:33): rotate-half RoPE, theta 500000,
+ * rows of size dims[last] at positions start_pos + row (cpu.rs:326-357). */
+int llmrs_rope_inplace(llmrs_tensor* x, size_t start_pos);
+/* Backend::rms_norm (backend.rs:36). */
+int llmrs_rms_norm(const llmrs_tensor* x, const llmrs_tensor* weight,
+                   float eps, llmrs_tensor** out);
+/* Backend::softmax (backend.rs:37), over the last dimension. */
+int llmrs_softmax(const llmrs_tensor* x, llmrs_tensor** out);
+/* Backend::scale (backend.rs:38). */
+int llmrs_scale(const llmrs_tensor* x, float value, llmrs_tensor** out);
+/* Backend::copy_from (backend.rs:39). */
+int llmrs_copy_from(const llmrs_tensor* t, llmrs_tensor** out);
+
+/* ---- resident decode model (no trait counterpart) ----------------------- */
+/* Mirrors LlamaConfig (src/core/config.rs:3-17) plus what the reference
+ * hard-codes: head_dim (loader.rs:164 derives hidden/num_heads), max_seq
+ * (loader.rs:165 fixes 2048), and the weight / KV storage kinds. */
+typedef struct {
+  int32_t n_layers;     /* num_hidden_layers   */
+  int32_t hidden;       /* hidden_size         */
+  int32_t n_heads;      /* num_attention_heads */
+  int32_t n_kv_heads;   /* num_key_value_heads */
+  int32_t head_dim;     /* hidden / n_heads in the reference */
+  int32_t ffn;          /* intermediate_size   */
+  int32_t vocab;        /* vocab_size          */
+  int32_t max_seq;      /* KV capacity in positions */
+  float rms_eps;        /* rms_norm_eps        */
+  float rope_theta;     /* 500000 (hard-coded at cpu.rs:330) */
+  int32_t weight_dtype; /* LLMRS_Q4 | LLMRS_Q4_0 | LLMRS_Q8_0 */
+  int32_t kv_dtype;     /* LLMRS_F32 | LLMRS_F16 */
+} llmrs_model_config;
+
+/* Linear weight slots of one layer (loader.rs:113-150); LM_HEAD uses
+ * layer = -1 (loader.rs:186-190). */
+#define LLMRS_W_Q 0
+#define LLMRS_W_K 1
+#define LLMRS_W_V 2
+#define LLMRS_W_O 3
+#define LLMRS_W_GATE 4
+#define LLMRS_W_UP 5
+#define LLMRS_W_DOWN 6
+#define LLMRS_W_LM_HEAD 7
+/* Norm slots (loader.rs:153-159,183); FINAL uses layer = -1. */
+#define LLMRS_N_INPUT 0
+#define LLMRS_N_POST 1
+#define LLMRS_N_FINAL 2
+
+int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out);
+int llmrs_model_free(llmrs_model* m);
+/* embed_tokens (loader.rs:105): f32 [vocab][hidden]. */
+int llmrs_model_set_embedding(llmrs_model* m, const float* table);
+int llmrs_model_set_norm(llmrs_model* m, int layer, int slot, const float* w);
+/* A linear weight in the reference CpuQ4 format (see llmrs_tensor_upload_q4)
+ * for weight_dtype LLMRS_Q4 / LLMRS_Q4_0.  K/V take true-GQA shapes
+ * [n_kv_heads*head_dim][hidden]; the reference duplicates those rows
+ * (loader.rs:62-98), which gives bit-identical outputs per query head. */
+int llmrs_model_set_linear_q4(llmrs_model* m, int layer, int slot,
+                              const uint8_t* qs, const float* scales);
+/* A linear weight in Q8_0 (weight_dtype LLMRS_Q8_0): int8 [n][k] + scales. */
+int llmrs_model_set_linear_q8_0(llmrs_model* m, int layer, int slot,
+                                const int8_t* qs, const float* scales);
+/* Write already-rotated K and V rows for positions [pos0, pos0+n) of one
+ * layer and KV head (pre-filled caches); k, v are f32 [n][head_dim], stored
+ * in the model's kv_dtype. */
+int llmrs_model_kv_write(llmrs_model* m, int layer, int kv_head, size_t pos0,
+                         size_t n, const float* k, const float* v);
+/* Read back K and V rows (as f32) - for tests. */
+int llmrs_model_kv_read(llmrs_model* m, int layer, int kv_head, size_t pos0,
+                        size_t n, float* k, float* v);
+/* One forward pass of `n` tokens at positions [start_pos, start_pos+n)
+ * (LlamaModel::forward, src/core/model.rs:17-49, driven like
+ * src/main.rs:134-190).  The rows are processed in order, which is
+ * numerically the reference's causal prefill.  Outputs (each may be NULL):
+ *   logits  f32 [vocab] of the last row;
+ *   next    greedy argmax of the last row (lowest index on ties);
+ *   trace   f32 [n][n_layers+1][hidden]: the residual stream entering each
+ *           layer and the one leaving the last layer. */
+int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n,
+                        size_t start_pos, float* logits, int32_t* next,
+                        float* trace);
+/* Greedy generation (src/main.rs:128-327 with argmax in place of sampling):
+ * processes the prompt from position 0, then emits n_steps tokens into
+ * out_tokens.  Each position runs as one replay of a captured HIP graph. */
+int llmrs_model_generate(llmrs_model* m, const int32_t* prompt,
+                         size_t n_prompt, size_t n_steps, int32_t* out_tokens);
+/* Benchmark helpers: start a greedy run (prompt processed, state resident),
+ * then replay `n` more decode steps without host synchronisation. */
+int llmrs_model_begin(llmrs_model* m, const int32_t* prompt, size_t n_prompt);
+int llmrs_model_decode_steps(llmrs_model* m, size_t n);
+/* Tokens produced since llmrs_model_begin (count = n_prompt + steps). */
+int llmrs_model_tokens(llmrs_model* m, int32_t* out, size_t count);
+/* Per-kernel timing of one eager decode step at the current position, with
+ * HIP events on the model's stream.  `names` receives up to `cap` entries of
+ * 32 chars; `ms` and `bytes` the duration and algorithmic bytes of each
+ * launch.  Returns the number of launches recorded (>= 0) or an error. */
+int llmrs_model_profile_step(llmrs_model* m, char* names, float* ms,
+                             double* bytes, int cap);
+/* Algorithmic weight bytes streamed per decode token (all linear weights). */
+double llmrs_model_weight_bytes(const llmrs_model* m);
+
+/* ---- seeded synthetic inputs (benchmark and test data) ------------------ */
+/* Counter-based SplitMix64 generator keyed by (seed, tensor_id, index).
+ * Q4 codes uniform in 0..15 packed in the reference nibble order, scales
+ * fp16-rounded uniform in [lo, hi); Q8 codes uniform in [-127, 127];
+ * normals via Box-Muller; token ids uniform in [0, vocab).  Filled with
+ * `threads` host threads (0 = all cores). */
+int llmrs_synth_q4(uint64_t seed, uint64_t tensor_id, size_t n, size_t k,
+                   float lo, float hi, uint8_t* qs, float* scales, int threads);
+int llmrs_synth_q8(uint64_t seed, uint64_t tensor_id, size_t n, size_t k,
+                   float lo, float hi, int8_t* qs, float* scales, int threads);
+int llmrs_synth_normal(uint64_t seed, uint64_t tensor_id, size_t count,
+                       float mean, float stddev, float* out, int threads);
+int llmrs_synth_tokens(uint64_t seed, uint64_t tensor_id, size_t count,
+                       int32_t vocab, int32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLMRS_HIP_H */

@@ -1,0 +1,744 @@
+// model.cpp - the HBM-resident decode model and its per-token kernel sequence.
+//
+// One decode position = 5 kernels per layer + 3 (LlamaModel::forward,
+// model.rs:17-49, over LlamaBlock::forward, layer.rs:373-406):
+//   embed_gather                      x = E[token[pos]]          (main.rs:159-167)
+//   per layer:
+//     gemv *_norm_store   (Q|K|V)     qkv = W_qkv . Q8(RMSNorm(x))  (layer.rs:177-179)
+//     attn_decode                     rope, KV append, attention, ctx (+Q8)
+//     gemv *_q8_resid     (O)         h = x + W_o . ctx             (layer.rs:329-332,386)
+//     gemv *_norm_silu    (gate|up)   m = silu(g)*u (+Q8)           (layer.rs:40-89)
+//     gemv *_q8_resid     (down)      x = h + W_down . m            (layer.rs:93-96,403)
+//   gemv *_norm_argmax    (lm_head)   logits, partial argmax        (model.rs:39-47)
+//   argmax_final                      next token, pos += 1
+// Every kernel reads the position from device memory, so one captured HIP
+// graph replays every step with no host round trip.
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <tuple>
+
+#include "../kernel_args.h"
+#include "internal.h"
+
+using namespace llmrs;
+
+namespace {
+
+struct DevLinear {
+  uint8_t* codes = nullptr;
+  void* scales = nullptr;
+  int n = 0, k = 0;
+  size_t bytes = 0;
+};
+
+struct LayerBufs {
+  DevLinear qkv, o, gu, down;
+  float* norm[2] = {nullptr, nullptr};
+  void* kc = nullptr;
+  void* vc = nullptr;
+  unsigned set_mask = 0;  // bit s = linear slot s uploaded; bits 8,9 = norms
+};
+
+int env_int(const char* name, int def) {
+  const char* v = std::getenv(name);
+  return (v && *v) ? std::atoi(v) : def;
+}
+
+}  // namespace
+
+struct llmrs_model {
+  llmrs_model_config c{};
+  int wt = WT_Q4H;
+  int qkv_rows = 0;
+  std::vector<LayerBufs> layers;
+  float* embed = nullptr;
+  float* final_norm = nullptr;
+  DevLinear lm_head;
+  bool embed_set = false, final_set = false, lm_set = false;
+  // activations and state
+  float *x = nullptr, *h = nullptr, *qkv = nullptr, *ctxv = nullptr, *mf = nullptr;
+  float *logits = nullptr, *ctx_d = nullptr, *m_d = nullptr, *part_o = nullptr, *part_ml = nullptr;
+  float *part_val = nullptr, *rope_cos = nullptr, *rope_sin = nullptr, *trace = nullptr;
+  int8_t *ctx_q = nullptr, *m_q = nullptr;
+  int *part_idx = nullptr, *counters = nullptr, *tokens = nullptr, *gen = nullptr;
+  int *pos = nullptr, *n_prompt = nullptr, *err = nullptr;
+  int nsplit = 1, lm_grid = 1, cap = 0, gemv_wgs = 0;
+  size_t host_pos = 0;
+  bool begun = false;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  bool graph_failed = false;
+  std::vector<void*> allocs;
+
+  template <class T>
+  T* dalloc(size_t count) {
+    void* p = nullptr;
+    const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+      (void)hipGetLastError();
+      fail(LLMRS_E_OOM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    }
+    allocs.push_back(p);
+    LLMRS_HIP(hipMemsetAsync(p, 0, bytes, ctx().stream));
+    return (T*)p;
+  }
+  void alloc_linear(DevLinear& L, int n, int k) {
+    L.n = n;
+    L.k = k;
+    const size_t nb = (size_t)k / 32;
+    const size_t code_bytes = (size_t)n * nb * block_code_bytes(wt);
+    const size_t off = align_up(code_bytes, 256);
+    L.bytes = off + (size_t)n * nb * block_scale_bytes(wt);
+    L.codes = dalloc<uint8_t>(L.bytes);
+    L.scales = L.codes + off;
+  }
+  ~llmrs_model() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    for (void* p : allocs) (void)hipFree(p);
+  }
+};
+
+namespace {
+
+size_t kv_elem_bytes(const llmrs_model* m) { return m->c.kv_dtype == LLMRS_F16 ? 2 : 4; }
+size_t kv_layer_elems(const llmrs_model* m) {
+  return (size_t)m->c.n_kv_heads * m->c.max_seq * m->c.head_dim;
+}
+
+// Records a (name, algorithmic bytes, start, end) tuple per launch when
+// profiling; otherwise a plain launch.
+struct Launcher {
+  hipStream_t s;
+  std::vector<std::tuple<std::string, double, hipEvent_t, hipEvent_t>>* rec = nullptr;
+  template <class A>
+  void operator()(const std::string& name, double bytes, dim3 g, dim3 b, size_t lds, const A& args) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (rec) {
+      LLMRS_HIP(hipEventCreate(&e0));
+      LLMRS_HIP(hipEventCreate(&e1));
+      LLMRS_HIP(hipEventRecord(e0, s));
+    }
+    launch(name, g, b, lds, s, args);
+    if (rec) {
+      LLMRS_HIP(hipEventRecord(e1, s));
+      rec->emplace_back(name, bytes, e0, e1);
+    }
+  }
+};
+
+double linear_weight_bytes(const llmrs_model* m, const DevLinear& L) {
+  const double nb = L.k / 32.0;
+  return (double)L.n * nb * (block_code_bytes(m->wt) + block_scale_bytes(m->wt));
+}
+
+void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
+  const llmrs_model_config& c = m->c;
+  const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
+  const std::string tag = wt_tag(m->wt);
+  const unsigned maxwg = (unsigned)m->gemv_wgs;
+  auto lds = [](int k) { return (size_t)k + 8 * (size_t)(k / 32); };
+  auto grid16 = [&](int n) { return std::min<unsigned>((unsigned)((n + 15) / 16), maxwg); };
+
+  EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, H, c.vocab};
+  L("embed_gather", 8.0 * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
+
+  const float scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
+  const std::string attn = std::string("attn_decode_hd") + std::to_string(hd) +
+                           (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32");
+  for (int li = 0; li < c.n_layers; ++li) {
+    LayerBufs& Lb = m->layers[li];
+    if (trace_dev)
+      LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)li * H, m->x, H * sizeof(float),
+                               hipMemcpyDeviceToDevice, L.s));
+    {  // Q|K|V
+      GemvArgs g{};
+      g.wq = Lb.qkv.codes;
+      g.ws = Lb.qkv.scales;
+      g.n = Lb.qkv.n;
+      g.k = H;
+      g.x = m->x;
+      g.norm_w = Lb.norm[0];
+      g.eps = c.rms_eps;
+      g.y = m->qkv;
+      L("gemv_" + tag + "_norm_store", linear_weight_bytes(m, Lb.qkv) + 8.0 * H + 4.0 * g.n,
+        dim3(grid16(g.n)), dim3(256), lds(H), g);
+    }
+    {  // attention
+      AttnArgs a{};
+      a.qkv = m->qkv;
+      a.pos_ptr = m->pos;
+      a.kc = (uint8_t*)Lb.kc;
+      a.vc = (uint8_t*)Lb.vc;
+      a.rope_cos = m->rope_cos;
+      a.rope_sin = m->rope_sin;
+      a.part_o = m->part_o;
+      a.part_ml = m->part_ml;
+      a.counters = m->counters + (size_t)li * nkv;
+      a.ctx = m->ctxv;
+      a.ctx_q = m->ctx_q;
+      a.ctx_d = m->ctx_d;
+      a.max_seq = c.max_seq;
+      a.nq = nq;
+      a.nkv = nkv;
+      a.nsplit = m->nsplit;
+      a.scale = scale;
+      const double kvb = 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
+      L(attn, kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(256), 0, a);
+    }
+    {  // O projection + residual
+      GemvArgs g{};
+      g.wq = Lb.o.codes;
+      g.ws = Lb.o.scales;
+      g.n = H;
+      g.k = nq * hd;
+      g.xq = m->ctx_q;
+      g.xd = m->ctx_d;
+      g.y = m->h;
+      g.res = m->x;
+      L("gemv_" + tag + "_q8_resid", linear_weight_bytes(m, Lb.o) + 1.125 * g.k + 8.0 * H,
+        dim3(grid16(H)), dim3(256), lds(g.k), g);
+    }
+    {  // gate|up + SiLU
+      GemvArgs g{};
+      g.wq = Lb.gu.codes;
+      g.ws = Lb.gu.scales;
+      g.n = 2 * F;
+      g.k = H;
+      g.x = m->h;
+      g.norm_w = Lb.norm[1];
+      g.eps = c.rms_eps;
+      g.y = m->mf;
+      g.yq = m->m_q;
+      g.yd = m->m_d;
+      const unsigned grid = std::min<unsigned>((unsigned)(F / 32), maxwg);
+      L("gemv_" + tag + "_norm_silu", linear_weight_bytes(m, Lb.gu) + 8.0 * H + 5.125 * F,
+        dim3(grid), dim3(256), lds(H), g);
+    }
+    {  // down projection + residual
+      GemvArgs g{};
+      g.wq = Lb.down.codes;
+      g.ws = Lb.down.scales;
+      g.n = H;
+      g.k = F;
+      g.xq = m->m_q;
+      g.xd = m->m_d;
+      g.y = m->x;
+      g.res = m->h;
+      L("gemv_" + tag + "_q8_resid", linear_weight_bytes(m, Lb.down) + 1.125 * F + 8.0 * H,
+        dim3(grid16(H)), dim3(256), lds(F), g);
+    }
+  }
+  if (trace_dev)
+    LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)c.n_layers * H, m->x, H * sizeof(float),
+                             hipMemcpyDeviceToDevice, L.s));
+  {  // lm_head + argmax
+    GemvArgs g{};
+    g.wq = m->lm_head.codes;
+    g.ws = m->lm_head.scales;
+    g.n = c.vocab;
+    g.k = H;
+    g.x = m->x;
+    g.norm_w = m->final_norm;
+    g.eps = c.rms_eps;
+    g.y = write_logits ? m->logits : nullptr;
+    g.part_val = m->part_val;
+    g.part_idx = m->part_idx;
+    L("gemv_" + tag + "_norm_argmax", linear_weight_bytes(m, m->lm_head) + 8.0 * H,
+      dim3((unsigned)m->lm_grid), dim3(256), lds(H), g);
+  }
+  ArgmaxFinalArgs f{m->part_val, m->part_idx, m->lm_grid, m->pos, m->n_prompt, m->tokens, m->gen, m->cap};
+  L("argmax_final", 8.0 * m->lm_grid, dim3(1), dim3(256), 0, f);
+}
+
+void check_ready(const llmrs_model* m) {
+  LLMRS_REQUIRE(m, LLMRS_E_INVALID, "null model");
+  LLMRS_REQUIRE(m->embed_set && m->final_set && m->lm_set, LLMRS_E_INVALID,
+                "model weights incomplete (embedding / final norm / lm_head)");
+  for (size_t i = 0; i < m->layers.size(); ++i)
+    LLMRS_REQUIRE(m->layers[i].set_mask == 0x37f, LLMRS_E_INVALID,
+                  "layer " + std::to_string(i) + " weights incomplete");
+}
+
+void check_err(llmrs_model* m) {
+  int e = 0;
+  LLMRS_HIP(hipMemcpyAsync(&e, m->err, sizeof(int), hipMemcpyDeviceToHost, ctx().stream));
+  LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+  if (e) {
+    int zero = 0;
+    LLMRS_HIP(hipMemcpyAsync(m->err, &zero, sizeof(int), hipMemcpyHostToDevice, ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    fail(LLMRS_E_RANGE, "token id out of range [0, vocab)");
+  }
+}
+
+void set_state(llmrs_model* m, size_t pos, int n_prompt) {
+  int v[2] = {(int)pos, n_prompt};
+  LLMRS_HIP(hipMemcpyAsync(m->pos, &v[0], sizeof(int), hipMemcpyHostToDevice, ctx().stream));
+  LLMRS_HIP(hipMemcpyAsync(m->n_prompt, &v[1], sizeof(int), hipMemcpyHostToDevice, ctx().stream));
+  LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+}
+
+void upload_tokens(llmrs_model* m, size_t pos0, const int32_t* ids, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    LLMRS_REQUIRE(ids[i] >= 0 && ids[i] < m->c.vocab, LLMRS_E_RANGE,
+                  "token id out of range at index " + std::to_string(i));
+  LLMRS_HIP(hipMemcpyAsync(m->tokens + pos0, ids, n * sizeof(int32_t), hipMemcpyHostToDevice,
+                           ctx().stream));
+  LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+}
+
+// One decode position through the captured graph (captured on first use).
+void replay_step(llmrs_model* m) {
+  hipStream_t s = ctx().stream;
+  if (!m->exec && !m->graph_failed && env_int("LLMRS_GRAPH", 1)) {
+    Launcher L{s};
+    hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    bool ok = e == hipSuccess;
+    if (ok) {
+      try {
+        enqueue_step(m, L, false, nullptr);
+      } catch (const Error&) {
+        ok = false;
+      }
+      hipGraph_t g = nullptr;
+      e = hipStreamEndCapture(s, &g);
+      ok = ok && e == hipSuccess && g;
+      if (ok) {
+        m->graph = g;
+        ok = hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0) == hipSuccess;
+      } else if (g) {
+        (void)hipGraphDestroy(g);
+      }
+    }
+    if (!ok) {
+      (void)hipGetLastError();
+      m->graph_failed = true;
+      m->exec = nullptr;
+      std::fprintf(stderr, "llmrs_hip: HIP graph capture failed; using per-kernel launches\n");
+    }
+  }
+  if (m->exec) {
+    LLMRS_HIP(hipGraphLaunch(m->exec, s));
+  } else {
+    Launcher L{s};
+    enqueue_step(m, L, false, nullptr);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
+  return guard([&] {
+    LLMRS_REQUIRE(cfg && out, LLMRS_E_INVALID, "null argument");
+    const llmrs_model_config& c = *cfg;
+    LLMRS_REQUIRE(c.n_layers > 0 && c.hidden > 0 && c.n_heads > 0 && c.n_kv_heads > 0 &&
+                      c.ffn > 0 && c.vocab > 0 && c.max_seq > 0,
+                  LLMRS_E_INVALID, "model dimensions must be positive");
+    LLMRS_REQUIRE(c.head_dim == 64 || c.head_dim == 128, LLMRS_E_INVALID, "head_dim must be 64 or 128");
+    LLMRS_REQUIRE(c.n_heads % c.n_kv_heads == 0 && c.n_heads / c.n_kv_heads <= 8, LLMRS_E_INVALID,
+                  "n_heads must be a multiple of n_kv_heads with at most 8 query heads per KV head");
+    LLMRS_REQUIRE(c.hidden % 32 == 0 && c.ffn % 32 == 0 && (c.n_heads * c.head_dim) % 32 == 0,
+                  LLMRS_E_INVALID, "hidden, ffn and n_heads*head_dim must be multiples of 32");
+    LLMRS_REQUIRE(c.hidden <= 32768 && c.ffn <= 32768 && c.n_heads * c.head_dim <= 32768,
+                  LLMRS_E_INVALID, "GEMV input length is limited to 32768");
+    LLMRS_REQUIRE(c.kv_dtype == LLMRS_F32 || c.kv_dtype == LLMRS_F16, LLMRS_E_INVALID, "kv_dtype");
+    std::unique_ptr<llmrs_model> m(new llmrs_model());
+    m->c = c;
+    switch (c.weight_dtype) {
+      case LLMRS_Q4: m->wt = WT_Q4F; break;
+      case LLMRS_Q4_0: m->wt = WT_Q4H; break;
+      case LLMRS_Q8_0: m->wt = WT_Q8H; break;
+      default: fail(LLMRS_E_DTYPE, "weight_dtype must be LLMRS_Q4, LLMRS_Q4_0 or LLMRS_Q8_0");
+    }
+    Context& cx = ctx();
+    const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
+    m->qkv_rows = (nq + 2 * nkv) * hd;
+    m->gemv_wgs = std::max(1, cx.num_cus * env_int("LLMRS_GEMV_WG_PER_CU", 4));
+    m->cap = c.max_seq + 1;
+    int splits = (c.max_seq + 63) / 64;
+    splits = std::min(splits, std::max(1, 2 * cx.num_cus / nkv));
+    m->nsplit = std::max(1, env_int("LLMRS_ATTN_SPLITS", splits));
+    m->lm_grid = (int)std::min<size_t>(((size_t)c.vocab + 15) / 16, (size_t)m->gemv_wgs);
+    m->layers.resize(c.n_layers);
+    for (auto& L : m->layers) {
+      m->alloc_linear(L.qkv, m->qkv_rows, H);
+      m->alloc_linear(L.o, H, nq * hd);
+      m->alloc_linear(L.gu, 2 * F, H);
+      m->alloc_linear(L.down, H, F);
+      L.norm[0] = m->dalloc<float>(H);
+      L.norm[1] = m->dalloc<float>(H);
+      L.kc = m->dalloc<uint8_t>(kv_layer_elems(m.get()) * kv_elem_bytes(m.get()));
+      L.vc = m->dalloc<uint8_t>(kv_layer_elems(m.get()) * kv_elem_bytes(m.get()));
+    }
+    m->alloc_linear(m->lm_head, c.vocab, H);
+    m->embed = m->dalloc<float>((size_t)c.vocab * H);
+    m->final_norm = m->dalloc<float>(H);
+    m->x = m->dalloc<float>(H);
+    m->h = m->dalloc<float>(H);
+    m->qkv = m->dalloc<float>(m->qkv_rows);
+    m->ctxv = m->dalloc<float>((size_t)nq * hd);
+    m->ctx_q = m->dalloc<int8_t>((size_t)nq * hd);
+    m->ctx_d = m->dalloc<float>((size_t)nq * hd / 32);
+    m->mf = m->dalloc<float>(F);
+    m->m_q = m->dalloc<int8_t>(F);
+    m->m_d = m->dalloc<float>(F / 32);
+    m->logits = m->dalloc<float>(c.vocab);
+    m->part_o = m->dalloc<float>((size_t)nq * m->nsplit * hd);
+    m->part_ml = m->dalloc<float>((size_t)nq * m->nsplit * 2);
+    m->part_val = m->dalloc<float>(m->lm_grid);
+    m->part_idx = m->dalloc<int>(m->lm_grid);
+    m->counters = m->dalloc<int>((size_t)c.n_layers * nkv);
+    m->tokens = m->dalloc<int>(m->cap);
+    m->gen = m->dalloc<int>(m->cap);
+    m->pos = m->dalloc<int>(1);
+    m->n_prompt = m->dalloc<int>(1);
+    m->err = m->dalloc<int>(1);
+    m->trace = m->dalloc<float>((size_t)(c.n_layers + 1) * H);
+    {  // RoPE tables for every position (cpu.rs:345-349)
+      const size_t mid = hd / 2;
+      std::vector<float> cs((size_t)c.max_seq * mid), sn((size_t)c.max_seq * mid);
+      rope_table(0, c.max_seq, hd, c.rope_theta, cs.data(), sn.data());
+      m->rope_cos = m->dalloc<float>(cs.size());
+      m->rope_sin = m->dalloc<float>(sn.size());
+      LLMRS_HIP(hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, cx.stream));
+      LLMRS_HIP(hipMemcpyAsync(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, cx.stream));
+    }
+    LLMRS_HIP(hipStreamSynchronize(cx.stream));
+    // Resolve every kernel of the step now, so graph capture never has to.
+    const std::string tag = wt_tag(m->wt);
+    for (const char* suffix : {"_norm_store", "_q8_resid", "_norm_silu", "_norm_argmax"})
+      (void)kernel("gemv_" + tag + suffix);
+    (void)kernel("embed_gather");
+    (void)kernel("argmax_final");
+    (void)kernel(std::string("attn_decode_hd") + std::to_string(hd) +
+                 (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32"));
+    *out = m.release();
+  });
+}
+
+int llmrs_model_free(llmrs_model* m) {
+  return guard([&] {
+    if (!m) return;
+    (void)hipStreamSynchronize(ctx().stream);
+    delete m;
+  });
+}
+
+int llmrs_model_set_embedding(llmrs_model* m, const float* table) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && table, LLMRS_E_INVALID, "null argument");
+    const size_t bytes = (size_t)m->c.vocab * m->c.hidden * sizeof(float);
+    LLMRS_HIP(hipMemcpyAsync(m->embed, table, bytes, hipMemcpyHostToDevice, ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    m->embed_set = true;
+  });
+}
+
+int llmrs_model_set_norm(llmrs_model* m, int layer, int slot, const float* w) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && w, LLMRS_E_INVALID, "null argument");
+    float* dst;
+    if (layer < 0 || slot == LLMRS_N_FINAL) {
+      dst = m->final_norm;
+      m->final_set = true;
+    } else {
+      LLMRS_REQUIRE(layer < m->c.n_layers && (slot == LLMRS_N_INPUT || slot == LLMRS_N_POST),
+                    LLMRS_E_INVALID, "bad norm slot");
+      dst = m->layers[layer].norm[slot];
+      m->layers[layer].set_mask |= 1u << (8 + slot);
+    }
+    LLMRS_HIP(hipMemcpyAsync(dst, w, m->c.hidden * sizeof(float), hipMemcpyHostToDevice, ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+  });
+}
+
+}  // extern "C"
+
+namespace {
+
+// Target matrix, source shape and device-row placement of a linear slot
+// (loader.rs:113-150,186-190; gate|up interleaved in tiles of 32 rows so one
+// GEMV tile owns matching gate and up rows).
+struct Placement {
+  DevLinear* L;
+  size_t rows, k;
+  size_t row0;        // first device row
+  bool interleave;    // gate/up: runs of 32 rows, device pitch 64 rows
+};
+
+Placement place(llmrs_model* m, int layer, int slot) {
+  const llmrs_model_config& c = m->c;
+  const size_t H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
+  if (slot == LLMRS_W_LM_HEAD || layer < 0) {
+    LLMRS_REQUIRE(slot == LLMRS_W_LM_HEAD, LLMRS_E_INVALID, "layer -1 takes only LLMRS_W_LM_HEAD");
+    return {&m->lm_head, (size_t)c.vocab, H, 0, false};
+  }
+  LLMRS_REQUIRE(layer < c.n_layers, LLMRS_E_INVALID, "layer out of range");
+  LayerBufs& Lb = m->layers[layer];
+  switch (slot) {
+    case LLMRS_W_Q: return {&Lb.qkv, nq * hd, H, 0, false};
+    case LLMRS_W_K: return {&Lb.qkv, nkv * hd, H, nq * hd, false};
+    case LLMRS_W_V: return {&Lb.qkv, nkv * hd, H, nq * hd + nkv * hd, false};
+    case LLMRS_W_O: return {&Lb.o, H, nq * hd, 0, false};
+    case LLMRS_W_GATE: return {&Lb.gu, F, H, 0, true};
+    case LLMRS_W_UP: return {&Lb.gu, F, H, 32, true};
+    case LLMRS_W_DOWN: return {&Lb.down, H, F, 0, false};
+  }
+  fail(LLMRS_E_INVALID, "bad linear slot");
+}
+
+void put_rows(llmrs_model* m, const Placement& p, const std::vector<uint8_t>& codes,
+              const std::vector<uint8_t>& scales) {
+  const size_t nb = p.k / 32;
+  const size_t cb = nb * block_code_bytes(m->wt), sb = nb * block_scale_bytes(m->wt);
+  hipStream_t s = ctx().stream;
+  uint8_t* dc = p.L->codes;
+  uint8_t* ds = (uint8_t*)p.L->scales;
+  if (!p.interleave) {
+    LLMRS_HIP(hipMemcpyAsync(dc + p.row0 * cb, codes.data(), p.rows * cb, hipMemcpyHostToDevice, s));
+    LLMRS_HIP(hipMemcpyAsync(ds + p.row0 * sb, scales.data(), p.rows * sb, hipMemcpyHostToDevice, s));
+  } else {
+    const size_t runs = p.rows / 32;
+    LLMRS_HIP(hipMemcpy2DAsync(dc + p.row0 * cb, 64 * cb, codes.data(), 32 * cb, 32 * cb, runs,
+                               hipMemcpyHostToDevice, s));
+    LLMRS_HIP(hipMemcpy2DAsync(ds + p.row0 * sb, 64 * sb, scales.data(), 32 * sb, 32 * sb, runs,
+                               hipMemcpyHostToDevice, s));
+  }
+  LLMRS_HIP(hipStreamSynchronize(s));
+}
+
+void mark_set(llmrs_model* m, int layer, int slot) {
+  if (slot == LLMRS_W_LM_HEAD || layer < 0) m->lm_set = true;
+  else m->layers[layer].set_mask |= 1u << slot;
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmrs_model_set_linear_q4(llmrs_model* m, int layer, int slot, const uint8_t* qs,
+                              const float* scales) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && qs && scales, LLMRS_E_INVALID, "null argument");
+    LLMRS_REQUIRE(m->wt == WT_Q4H || m->wt == WT_Q4F, LLMRS_E_DTYPE, "model is not a Q4 model");
+    Placement p = place(m, layer, slot);
+    const size_t nb = p.k / 32;
+    if (m->wt == WT_Q4H)
+      LLMRS_REQUIRE(scales_fit_f16(scales, p.rows * nb), LLMRS_E_INVALID,
+                    "Q4_0 scales must be exactly representable in fp16 (use LLMRS_Q4)");
+    std::vector<uint8_t> codes(p.rows * nb * 16), sc(p.rows * nb * block_scale_bytes(m->wt));
+    repack_q4_rows(qs, scales, p.rows, p.k, m->wt, {}, codes.data(), sc.data());
+    put_rows(m, p, codes, sc);
+    mark_set(m, layer, slot);
+  });
+}
+
+int llmrs_model_set_linear_q8_0(llmrs_model* m, int layer, int slot, const int8_t* qs,
+                                const float* scales) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && qs && scales, LLMRS_E_INVALID, "null argument");
+    LLMRS_REQUIRE(m->wt == WT_Q8H, LLMRS_E_DTYPE, "model is not a Q8_0 model");
+    Placement p = place(m, layer, slot);
+    const size_t nb = p.k / 32;
+    LLMRS_REQUIRE(scales_fit_f16(scales, p.rows * nb), LLMRS_E_INVALID,
+                  "Q8_0 scales must be exactly representable in fp16");
+    std::vector<uint8_t> codes(p.rows * p.k), sc(p.rows * nb * 2);
+    repack_q8_rows(qs, scales, p.rows, p.k, {}, codes.data(), sc.data());
+    put_rows(m, p, codes, sc);
+    mark_set(m, layer, slot);
+  });
+}
+
+int llmrs_model_kv_write(llmrs_model* m, int layer, int kv_head, size_t pos0, size_t n,
+                         const float* k, const float* v) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && k && v, LLMRS_E_INVALID, "null argument");
+    const llmrs_model_config& c = m->c;
+    LLMRS_REQUIRE(layer >= 0 && layer < c.n_layers && kv_head >= 0 && kv_head < c.n_kv_heads,
+                  LLMRS_E_INVALID, "layer / kv_head out of range");
+    LLMRS_REQUIRE(pos0 + n <= (size_t)c.max_seq, LLMRS_E_RANGE, "positions beyond max_seq");
+    const size_t cnt = n * c.head_dim, eb = kv_elem_bytes(m);
+    const size_t off = ((size_t)kv_head * c.max_seq + pos0) * c.head_dim * eb;
+    std::vector<uint8_t> kb(cnt * eb), vb(cnt * eb);
+    if (eb == 2) {
+      for (size_t i = 0; i < cnt; ++i) {
+        uint16_t hk = host_f2h(k[i]), hv = host_f2h(v[i]);
+        std::memcpy(&kb[2 * i], &hk, 2);
+        std::memcpy(&vb[2 * i], &hv, 2);
+      }
+    } else {
+      std::memcpy(kb.data(), k, cnt * 4);
+      std::memcpy(vb.data(), v, cnt * 4);
+    }
+    LayerBufs& Lb = m->layers[layer];
+    LLMRS_HIP(hipMemcpyAsync((uint8_t*)Lb.kc + off, kb.data(), kb.size(), hipMemcpyHostToDevice, ctx().stream));
+    LLMRS_HIP(hipMemcpyAsync((uint8_t*)Lb.vc + off, vb.data(), vb.size(), hipMemcpyHostToDevice, ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+  });
+}
+
+int llmrs_model_kv_read(llmrs_model* m, int layer, int kv_head, size_t pos0, size_t n, float* k,
+                        float* v) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && k && v, LLMRS_E_INVALID, "null argument");
+    const llmrs_model_config& c = m->c;
+    LLMRS_REQUIRE(layer >= 0 && layer < c.n_layers && kv_head >= 0 && kv_head < c.n_kv_heads,
+                  LLMRS_E_INVALID, "layer / kv_head out of range");
+    LLMRS_REQUIRE(pos0 + n <= (size_t)c.max_seq, LLMRS_E_RANGE, "positions beyond max_seq");
+    const size_t cnt = n * c.head_dim, eb = kv_elem_bytes(m);
+    const size_t off = ((size_t)kv_head * c.max_seq + pos0) * c.head_dim * eb;
+    std::vector<uint8_t> kb(cnt * eb), vb(cnt * eb);
+    LayerBufs& Lb = m->layers[layer];
+    LLMRS_HIP(hipMemcpyAsync(kb.data(), (uint8_t*)Lb.kc + off, kb.size(), hipMemcpyDeviceToHost, ctx().stream));
+    LLMRS_HIP(hipMemcpyAsync(vb.data(), (uint8_t*)Lb.vc + off, vb.size(), hipMemcpyDeviceToHost, ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    for (size_t i = 0; i < cnt; ++i) {
+      if (eb == 2) {
+        uint16_t hk, hv;
+        std::memcpy(&hk, &kb[2 * i], 2);
+        std::memcpy(&hv, &vb[2 * i], 2);
+        k[i] = host_h2f(hk);
+        v[i] = host_h2f(hv);
+      } else {
+        std::memcpy(&k[i], &kb[4 * i], 4);
+        std::memcpy(&v[i], &vb[4 * i], 4);
+      }
+    }
+  });
+}
+
+int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n, size_t start_pos,
+                        float* logits, int32_t* next, float* trace) {
+  return guard([&] {
+    check_ready(m);
+    LLMRS_REQUIRE(tokens && n > 0, LLMRS_E_INVALID, "empty token list");
+    LLMRS_REQUIRE(start_pos + n <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "positions beyond max_seq");
+    const size_t H = m->c.hidden, L = m->c.n_layers;
+    upload_tokens(m, start_pos, tokens, n);
+    set_state(m, start_pos, INT_MAX);
+    hipStream_t s = ctx().stream;
+    for (size_t i = 0; i < n; ++i) {
+      m->host_pos = start_pos + i;
+      Launcher Ln{s};
+      enqueue_step(m, Ln, logits && i + 1 == n, trace ? m->trace : nullptr);
+      if (trace) {
+        LLMRS_HIP(hipMemcpyAsync(trace + i * (L + 1) * H, m->trace, (L + 1) * H * sizeof(float),
+                                 hipMemcpyDeviceToHost, s));
+        LLMRS_HIP(hipStreamSynchronize(s));
+      }
+    }
+    if (logits)
+      LLMRS_HIP(hipMemcpyAsync(logits, m->logits, m->c.vocab * sizeof(float), hipMemcpyDeviceToHost, s));
+    if (next) LLMRS_HIP(hipMemcpyAsync(next, m->gen + start_pos + n, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    LLMRS_HIP(hipStreamSynchronize(s));
+    check_err(m);
+    m->host_pos = start_pos + n;
+    m->begun = false;
+  });
+}
+
+int llmrs_model_begin(llmrs_model* m, const int32_t* prompt, size_t n_prompt) {
+  return guard([&] {
+    check_ready(m);
+    LLMRS_REQUIRE(prompt && n_prompt > 0, LLMRS_E_INVALID, "empty prompt");
+    LLMRS_REQUIRE(n_prompt <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "prompt longer than max_seq");
+    upload_tokens(m, 0, prompt, n_prompt);
+    set_state(m, 0, (int)n_prompt);
+    for (size_t p = 0; p < n_prompt; ++p) {
+      m->host_pos = p;
+      replay_step(m);
+    }
+    m->host_pos = n_prompt;
+    m->begun = true;
+  });
+}
+
+int llmrs_model_decode_steps(llmrs_model* m, size_t n) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && m->begun, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
+    LLMRS_REQUIRE(m->host_pos + n <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
+    for (size_t i = 0; i < n; ++i) {
+      replay_step(m);
+      m->host_pos += 1;
+    }
+  });
+}
+
+int llmrs_model_tokens(llmrs_model* m, int32_t* out, size_t count) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && out, LLMRS_E_INVALID, "null argument");
+    LLMRS_REQUIRE(count <= m->host_pos + 1, LLMRS_E_RANGE, "more tokens requested than produced");
+    LLMRS_HIP(hipMemcpyAsync(out, m->tokens, count * sizeof(int32_t), hipMemcpyDeviceToHost, ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    check_err(m);
+  });
+}
+
+int llmrs_model_generate(llmrs_model* m, const int32_t* prompt, size_t n_prompt, size_t n_steps,
+                         int32_t* out_tokens) {
+  int rc = llmrs_model_begin(m, prompt, n_prompt);
+  if (rc) return rc;
+  if (n_steps == 0) return LLMRS_OK;
+  rc = llmrs_model_decode_steps(m, n_steps - 1);
+  if (rc) return rc;
+  std::vector<int32_t> all(n_prompt + n_steps);
+  rc = llmrs_model_tokens(m, all.data(), all.size());
+  if (rc) return rc;
+  std::memcpy(out_tokens, all.data() + n_prompt, n_steps * sizeof(int32_t));
+  return LLMRS_OK;
+}
+
+int llmrs_model_profile_step(llmrs_model* m, char* names, float* ms, double* bytes, int cap) {
+  int count = 0;
+  int rc = guard([&] {
+    LLMRS_REQUIRE(m && m->begun, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
+    LLMRS_REQUIRE(m->host_pos + 1 <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
+    std::vector<std::tuple<std::string, double, hipEvent_t, hipEvent_t>> rec;
+    Launcher L{ctx().stream, &rec};
+    try {
+      enqueue_step(m, L, false, nullptr);
+      LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    } catch (...) {
+      for (auto& r : rec) {
+        (void)hipEventDestroy(std::get<2>(r));
+        (void)hipEventDestroy(std::get<3>(r));
+      }
+      throw;
+    }
+    m->host_pos += 1;
+    for (auto& r : rec) {
+      float t = 0.0f;
+      (void)hipEventElapsedTime(&t, std::get<2>(r), std::get<3>(r));
+      if (count < cap) {
+        if (names) {
+          std::strncpy(names + 32 * count, std::get<0>(r).c_str(), 31);
+          names[32 * count + 31] = 0;
+        }
+        if (ms) ms[count] = t;
+        if (bytes) bytes[count] = std::get<1>(r);
+        ++count;
+      }
+      (void)hipEventDestroy(std::get<2>(r));
+      (void)hipEventDestroy(std::get<3>(r));
+    }
+  });
+  return rc ? rc : count;
+}
+
+double llmrs_model_weight_bytes(const llmrs_model* m) {
+  if (!m) return 0.0;
+  double b = linear_weight_bytes(m, m->lm_head);
+  for (const auto& L : m->layers)
+    b += linear_weight_bytes(m, L.qkv) + linear_weight_bytes(m, L.o) + linear_weight_bytes(m, L.gu) +
+         linear_weight_bytes(m, L.down);
+  return b;
+}
+
+}  // extern "C"

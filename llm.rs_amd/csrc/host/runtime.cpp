@@ -1,0 +1,261 @@
+// runtime.cpp - device context, module loading, allocator, errors, helpers.
+#include <dlfcn.h>
+#include <immintrin.h>
+
+#include <cmath>
+#include <cstring>
+#include <filesystem>
+#include <functional>
+#include <thread>
+
+#include "internal.h"
+
+namespace llmrs {
+
+namespace {
+thread_local std::string g_last_error;
+Context* g_ctx = nullptr;
+
+std::string library_dir() {
+  Dl_info info;
+  if (dladdr((void*)&library_dir, &info) && info.dli_fname) {
+    return std::filesystem::path(info.dli_fname).parent_path().string();
+  }
+  return ".";
+}
+}  // namespace
+
+void fail(int code, const std::string& msg) { throw Error(code, msg); }
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+
+std::recursive_mutex& api_mutex() {
+  static std::recursive_mutex m;
+  return m;
+}
+
+Context& ctx() {
+  if (!g_ctx) fail(LLMRS_E_NOINIT, "llmrs_init has not been called");
+  return *g_ctx;
+}
+
+hipFunction_t kernel(const std::string& name) {
+  Context& c = ctx();
+  auto it = c.kernels.find(name);
+  if (it != c.kernels.end()) return it->second;
+  for (hipModule_t m : c.modules) {
+    hipFunction_t f = nullptr;
+    if (hipModuleGetFunction(&f, m, name.c_str()) == hipSuccess && f) {
+      c.kernels[name] = f;
+      return f;
+    }
+  }
+  (void)hipGetLastError();
+  fail(LLMRS_E_MODULE, "kernel not found in any loaded hsaco: " + name);
+}
+
+const char* wt_tag(int wt) {
+  switch (wt) {
+    case WT_Q4H: return "q4h";
+    case WT_Q4F: return "q4f";
+    case WT_Q8H: return "q8h";
+  }
+  fail(LLMRS_E_DTYPE, "unknown weight type");
+}
+
+// ---- allocator -------------------------------------------------------------
+void* Allocator::alloc(size_t bytes) {
+  size_t sz = align_up(bytes ? bytes : 1, 256);
+  if (sz > (1u << 20)) {  // round large requests to 1/8 octave to improve reuse
+    size_t p = 1;
+    while (p < sz) p <<= 1;
+    size_t step = std::max<size_t>(p / 8, 256);
+    sz = align_up(sz, step);
+  }
+  auto it = free_.find(sz);
+  void* ptr = nullptr;
+  if (it != free_.end()) {
+    ptr = it->second;
+    free_.erase(it);
+  } else {
+    hipError_t e = hipMalloc(&ptr, sz);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      trim();
+      e = hipMalloc(&ptr, sz);
+    }
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      fail(LLMRS_E_OOM, "hipMalloc of " + std::to_string(sz) + " bytes failed");
+    }
+  }
+  live_[ptr] = sz;
+  return ptr;
+}
+
+void Allocator::release(void* p) {
+  if (!p) return;
+  auto it = live_.find(p);
+  if (it == live_.end()) return;
+  free_.emplace(it->second, p);
+  live_.erase(it);
+}
+
+void Allocator::trim() {
+  for (auto& kv : free_) (void)hipFree(kv.second);
+  free_.clear();
+}
+
+// ---- host helpers ----------------------------------------------------------
+uint16_t host_f2h(float f) { return _cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT); }
+float host_h2f(uint16_t h) { return _cvtsh_ss(h); }
+
+bool scales_fit_f16(const float* scales, size_t count) {
+  for (size_t i = 0; i < count; ++i) {
+    float back = host_h2f(host_f2h(scales[i]));
+    if (!(back == scales[i]) && !(std::isnan(back) && std::isnan(scales[i]))) return false;
+  }
+  return true;
+}
+
+void parallel_for(size_t n, int threads, const std::function<void(size_t, size_t)>& fn) {
+  if (threads <= 0) threads = (int)std::max(1u, std::thread::hardware_concurrency());
+  if (n < 2 || threads == 1) {
+    if (n) fn(0, n);
+    return;
+  }
+  size_t nt = std::min<size_t>((size_t)threads, n);
+  size_t chunk = (n + nt - 1) / nt;
+  std::vector<std::thread> ts;
+  for (size_t t = 0; t < nt; ++t) {
+    size_t b = t * chunk, e = std::min(n, b + chunk);
+    if (b >= e) break;
+    ts.emplace_back(fn, b, e);
+  }
+  for (auto& t : ts) t.join();
+}
+
+// Reference nibble order: byte i of a block = e[2i] | e[2i+1] << 4
+// (tensor.rs:125-131).  Device order: byte i = e[i] | e[i+16] << 4, so that
+// the low nibbles of a dword are four consecutive elements.
+void repack_q4_rows(const uint8_t* qs, const float* scales, size_t rows, size_t k, int wt,
+                    const std::vector<size_t>& row_map, uint8_t* dst_codes, uint8_t* dst_scales) {
+  const size_t nb = k / 32;
+  parallel_for(rows, 0, [&](size_t r0, size_t r1) {
+    uint8_t e[32];
+    for (size_t r = r0; r < r1; ++r) {
+      const size_t dr = row_map.empty() ? r : row_map[r];
+      for (size_t b = 0; b < nb; ++b) {
+        const uint8_t* src = qs + r * (k / 2) + b * 16;
+        for (int i = 0; i < 16; ++i) {
+          e[2 * i] = src[i] & 0x0F;
+          e[2 * i + 1] = src[i] >> 4;
+        }
+        uint8_t* dst = dst_codes + (dr * nb + b) * 16;
+        for (int i = 0; i < 16; ++i) dst[i] = (uint8_t)(e[i] | (e[i + 16] << 4));
+        const float s = scales[r * nb + b];
+        if (wt == WT_Q4F) {
+          std::memcpy(dst_scales + (dr * nb + b) * 4, &s, 4);
+        } else {
+          const uint16_t h = host_f2h(s);
+          std::memcpy(dst_scales + (dr * nb + b) * 2, &h, 2);
+        }
+      }
+    }
+  });
+}
+
+void repack_q8_rows(const int8_t* qs, const float* scales, size_t rows, size_t k,
+                    const std::vector<size_t>& row_map, uint8_t* dst_codes, uint8_t* dst_scales) {
+  const size_t nb = k / 32;
+  parallel_for(rows, 0, [&](size_t r0, size_t r1) {
+    for (size_t r = r0; r < r1; ++r) {
+      const size_t dr = row_map.empty() ? r : row_map[r];
+      std::memcpy(dst_codes + dr * k, qs + r * k, k);
+      for (size_t b = 0; b < nb; ++b) {
+        const uint16_t h = host_f2h(scales[r * nb + b]);
+        std::memcpy(dst_scales + (dr * nb + b) * 2, &h, 2);
+      }
+    }
+  });
+}
+
+void rope_table(size_t pos0, size_t npos, int hd, float theta, float* cos_out, float* sin_out) {
+  const int mid = hd / 2;
+  std::vector<float> inv(mid);
+  for (int j = 0; j < mid; ++j) {
+    float freq_idx = ((float)j * 2.0f) / (float)hd;
+    inv[j] = 1.0f / std::pow(theta, freq_idx);
+  }
+  for (size_t p = 0; p < npos; ++p)
+    for (int j = 0; j < mid; ++j) {
+      float a = (float)(pos0 + p) * inv[j];
+      cos_out[p * mid + j] = std::cos(a);
+      sin_out[p * mid + j] = std::sin(a);
+    }
+}
+
+}  // namespace llmrs
+
+using namespace llmrs;
+
+extern "C" {
+
+const char* llmrs_last_error(void) { return g_last_error.c_str(); }
+
+int llmrs_init(int device_ordinal, const char* hsaco_dir) {
+  return guard([&] {
+    if (g_ctx) return;
+    int count = 0;
+    LLMRS_HIP(hipGetDeviceCount(&count));
+    LLMRS_REQUIRE(device_ordinal >= 0 && device_ordinal < count, LLMRS_E_INVALID,
+                  "no such HIP device: " + std::to_string(device_ordinal));
+    auto* c = new Context();
+    try {
+      c->device = device_ordinal;
+      LLMRS_HIP(hipSetDevice(device_ordinal));
+      hipDeviceProp_t prop;
+      LLMRS_HIP(hipGetDeviceProperties(&prop, device_ordinal));
+      c->num_cus = prop.multiProcessorCount;
+      LLMRS_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+      std::string dir = hsaco_dir ? std::string(hsaco_dir) : library_dir();
+      for (const char* name : {"gemv", "attention", "ops"}) {
+        std::string path = dir + "/" + name + ".hsaco";
+        LLMRS_REQUIRE(std::filesystem::exists(path), LLMRS_E_MODULE, "missing code object " + path);
+        hipModule_t m = nullptr;
+        hipError_t e = hipModuleLoad(&m, path.c_str());
+        if (e != hipSuccess)
+          fail(LLMRS_E_MODULE, "hipModuleLoad(" + path + "): " + hipGetErrorString(e));
+        c->modules.push_back(m);
+      }
+    } catch (...) {
+      for (hipModule_t m : c->modules) (void)hipModuleUnload(m);
+      if (c->stream) (void)hipStreamDestroy(c->stream);
+      delete c;
+      throw;
+    }
+    g_ctx = c;
+  });
+}
+
+int llmrs_shutdown(void) {
+  return guard([&] {
+    if (!g_ctx) return;
+    (void)hipStreamSynchronize(g_ctx->stream);
+    g_ctx->alloc.trim();
+    for (hipModule_t m : g_ctx->modules) (void)hipModuleUnload(m);
+    (void)hipStreamDestroy(g_ctx->stream);
+    delete g_ctx;
+    g_ctx = nullptr;
+  });
+}
+
+int llmrs_device(void) { return LLMRS_DEVICE_HIP; }
+const char* llmrs_name(void) { return "Hip"; }
+
+int llmrs_sync(void) {
+  return guard([&] { LLMRS_HIP(hipStreamSynchronize(ctx().stream)); });
+}
+
+int llmrs_num_cus(void) { return g_ctx ? g_ctx->num_cus : 0; }
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+// common.h - device helpers shared by the gfx950 kernels.
+//
+// Wave64 reductions, fp16 conversion, and the Q8_0 activation quantiser used
+// in GEMV prologues and epilogues.  All code is written for CDNA4 (gfx950):
+// 64-lane wavefronts, v_dot4 integer dot products, 160 KB LDS per CU.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define LLMRS_WAVE 64
+
+namespace llmrs {
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (LLMRS_WAVE - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / LLMRS_WAVE; }
+
+// Butterfly sums / maxima over `width` lanes (power of two, <= 64).
+template <int W = LLMRS_WAVE>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, W);
+  return v;
+}
+template <int W = LLMRS_WAVE>
+__device__ __forceinline__ int group_sum_i(int v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, W);
+  return v;
+}
+template <int W = LLMRS_WAVE>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, W));
+  return v;
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+// IEEE binary16 round-to-nearest-even.
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+// One Q8_0 code for x with inverse scale inv (cpu.rs:736-740):
+// round-half-away-from-zero, clamp to [-127, 127], NaN -> 0.
+__device__ __forceinline__ int q8_code(float x, float inv) {
+  float p = x * inv;
+  if (p != p) return 0;  // Rust's `NaN as i8` is 0
+  float r = __builtin_roundf(p);
+  r = fminf(127.0f, fmaxf(-127.0f, r));
+  return (int)r;
+}
+
+// Quantise 32 values held one per lane of a 32-lane group (lanes with the
+// same lane_id()/32).  Returns this lane's code, writes the group's scale to
+// *d_out (the same value in every lane of the group).  Follows
+// quantize_row_q8_0 (cpu.rs:724-743): d = amax/127, inv = 1/d; the amax fold
+// starts at 0 and ignores NaN, as fmaxf does.
+__device__ __forceinline__ int q8_group32(float x, float* d_out) {
+  float amax = fmaxf(0.0f, group_max<32>(fabsf(x)));
+  if (amax == 0.0f) {
+    *d_out = 0.0f;
+    return 0;
+  }
+  float d = amax / 127.0f;
+  float inv = 1.0f / d;
+  *d_out = d;
+  return q8_code(x, inv);
+}
+
+// Packed 4 x int8 dot product with int32 accumulation (v_dot4c_i32_i8).
+__device__ __forceinline__ int dot4(int a, int b, int c) {
+  return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+}  // namespace llmrs

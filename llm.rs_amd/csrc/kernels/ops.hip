@@ -1,0 +1,141 @@
+// ops.hip - the remaining trait Backend operators (src/backend.rs:21-39) and
+// the embedding gather, for gfx950.
+//
+// The f32 matmuls keep the reference's per-output sequential order (one lane
+// per output element), so their results are bit-identical to cpu.rs:157-269
+// on non-aarch64 hosts; they are off the quantised decode hot path.
+#include "common.h"
+#include "../kernel_args.h"
+
+using namespace llmrs;
+
+
+// Backend::add_assign (cpu.rs:274-296): a += b.
+extern "C" __global__ __launch_bounds__(256) void add_assign_f32(EwArgs e) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < e.n; i += (long)gridDim.x * blockDim.x)
+    e.a[i] = e.a[i] + e.b[i];
+}
+
+// Backend::silu_mul (cpu.rs:298-324): g = g/(1+exp(-g)) * u.
+extern "C" __global__ __launch_bounds__(256) void silu_mul_f32(EwArgs e) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < e.n; i += (long)gridDim.x * blockDim.x) {
+    const float v = e.a[i];
+    e.a[i] = (v / (1.0f + expf(-v))) * e.b[i];
+  }
+}
+
+// Backend::scale (cpu.rs:425-435).
+extern "C" __global__ __launch_bounds__(256) void scale_f32(EwArgs e) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < e.n; i += (long)gridDim.x * blockDim.x)
+    e.out[i] = e.a[i] * e.value;
+}
+
+
+// Backend::rope_inplace (cpu.rs:326-357) with host-made sin/cos tables.
+extern "C" __global__ __launch_bounds__(256) void rope_f32(RopeArgs r) {
+  const int mid = r.hd / 2;
+  const long total = (long)r.rows * mid;
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    const long row = i / mid;
+    const int j = (int)(i % mid);
+    float* c = r.x + row * r.hd;
+    const float re = c[j], im = c[j + mid];
+    const float co = r.cos_t[i], s = r.sin_t[i];
+    c[j] = re * co - im * s;
+    c[j + mid] = re * s + im * co;
+  }
+}
+
+
+// Backend::rms_norm (cpu.rs:359-393); one workgroup per row.
+extern "C" __global__ __launch_bounds__(256) void rms_norm_f32(RowArgs r) {
+  __shared__ float s_red[8];
+  const int row = blockIdx.x;
+  const float* x = r.x + (size_t)row * r.dim;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < r.dim; i += blockDim.x) ss = ss + x[i] * x[i];
+  ss = group_sum(ss);
+  if (lane_id() == 0) s_red[wave_id()] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+  for (int w = 0; w < (int)(blockDim.x / LLMRS_WAVE); ++w) tot = tot + s_red[w];
+  const float rms = sqrtf(tot / (float)r.dim + r.eps);
+  const float scale = 1.0f / rms;
+  for (int i = threadIdx.x; i < r.dim; i += blockDim.x)
+    r.out[(size_t)row * r.dim + i] = x[i] * scale * r.w[i];
+}
+
+// Backend::softmax (cpu.rs:395-423): max from f32::MIN, e = exp(x - max),
+// p = e * (1/sum).  One workgroup per row.
+extern "C" __global__ __launch_bounds__(256) void softmax_f32(RowArgs r) {
+  __shared__ float s_red[8];
+  const int row = blockIdx.x;
+  const float* x = r.x + (size_t)row * r.dim;
+  float* o = r.out + (size_t)row * r.dim;
+  float mx = -3.40282347e+38f;
+  for (int i = threadIdx.x; i < r.dim; i += blockDim.x) mx = fmaxf(mx, x[i]);
+  mx = group_max(mx);
+  if (lane_id() == 0) s_red[wave_id()] = mx;
+  __syncthreads();
+  mx = s_red[0];
+  for (int w = 1; w < (int)(blockDim.x / LLMRS_WAVE); ++w) mx = fmaxf(mx, s_red[w]);
+  __syncthreads();
+  float sum = 0.0f;
+  for (int i = threadIdx.x; i < r.dim; i += blockDim.x) {
+    const float e = expf(x[i] - mx);
+    o[i] = e;
+    sum = sum + e;
+  }
+  sum = group_sum(sum);
+  if (lane_id() == 0) s_red[wave_id()] = sum;
+  __syncthreads();
+  float tot = 0.0f;
+  for (int w = 0; w < (int)(blockDim.x / LLMRS_WAVE); ++w) tot = tot + s_red[w];
+  const float inv = 1.0f / tot;
+  for (int i = threadIdx.x; i < r.dim; i += blockDim.x) o[i] = o[i] * inv;
+}
+
+
+// Backend::matmul (cpu.rs:157-224): out[i][j] = sum_p a[i][p] * b[p][j],
+// sequential over p, exact zeros of a skipped (cpu.rs:192,211).
+extern "C" __global__ __launch_bounds__(256) void matmul_f32(MatArgs g) {
+  const long total = (long)g.m * g.n;
+  for (long t = blockIdx.x * (long)blockDim.x + threadIdx.x; t < total; t += (long)gridDim.x * blockDim.x) {
+    const int i = (int)(t / g.n), j = (int)(t % g.n);
+    const float* ar = g.a + (size_t)i * g.k;
+    float s = 0.0f;
+    for (int p = 0; p < g.k; ++p) {
+      const float v = ar[p];
+      if (v == 0.0f) continue;
+      s = s + v * g.b[(size_t)p * g.n + j];
+    }
+    g.out[t] = s;
+  }
+}
+
+// matmul_transposed with f32 weights (cpu.rs:114-146) and matmul_slice
+// (cpu.rs:230-269): out[i][j] = dot(a_i, b_j), sequential over k.
+extern "C" __global__ __launch_bounds__(256) void matmul_t_f32(MatArgs g) {
+  const long total = (long)g.m * g.n;
+  for (long t = blockIdx.x * (long)blockDim.x + threadIdx.x; t < total; t += (long)gridDim.x * blockDim.x) {
+    const int i = (int)(t / g.n), j = (int)(t % g.n);
+    const float* ar = g.a + (size_t)i * g.k;
+    const float* br = g.b + (size_t)j * g.k;
+    float s = 0.0f;
+    for (int p = 0; p < g.k; ++p) s = s + ar[p] * br[p];
+    g.out[t] = s;
+  }
+}
+
+
+// Embedding gather (main.rs:159-167) for the token at the device position.
+extern "C" __global__ __launch_bounds__(256) void embed_gather(EmbedArgs e) {
+  int tok = e.tokens[*e.pos_ptr];
+  if (tok < 0 || tok >= e.vocab) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) *e.err = 1;
+    tok = 0;
+  }
+  const float* row = e.table + (size_t)tok * e.hidden;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < e.hidden; i += gridDim.x * blockDim.x)
+    e.x[i] = row[i];
+}

@@ -1,0 +1,419 @@
+"""llmrs_hip - Python host mirror of llm.rs's operator interface on MI355X.
+
+Binds the C ABI of ``include/llmrs_hip.h`` (``lib/libllmrs_hip.so`` plus the
+gfx950 code objects it loads with ``hipModuleLoad``).  ``HipBackend`` mirrors
+``trait Backend`` (reference ``src/backend.rs:15-40``) method for method;
+``HipModel`` is the HBM-resident decode loop (``src/core/model.rs:17-49``
+driven like ``src/main.rs:128-327`` with greedy argmax).
+
+There is no fallback: if the shared library is missing, importing works but
+the first call raises ``LlmrsError`` naming the missing file.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import os
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+LIB_DIR = Path(__file__).resolve().parent.parent / "lib"
+LIB_PATH = LIB_DIR / "libllmrs_hip.so"
+
+E_INVALID, E_DTYPE, E_HIP, E_NOINIT, E_MODULE, E_RANGE, E_OOM = -1, -2, -3, -4, -5, -6, -7
+
+
+class LlmrsError(RuntimeError):
+    """A non-zero return code of the C ABI (the reference panics instead)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class Device(enum.IntEnum):
+    """src/backend.rs:7-12 plus the Hip variant."""
+    Cpu = 0
+    OpenCl = 1
+    Qnn = 2
+    Hip = 3
+
+
+class DType(enum.IntEnum):
+    """Storage kinds: src/core/tensor.rs:13-44 plus extensions."""
+    F32 = 0
+    F16 = 1
+    Q4 = 2      # Storage::CpuQ4 (f32 scales)
+    Q4_0 = 3    # fp16 scales
+    Q8_0 = 4
+
+
+_lib = None
+
+_SIGS = {
+    "llmrs_init": (C.c_int, [C.c_int, C.c_char_p]),
+    "llmrs_shutdown": (C.c_int, []),
+    "llmrs_last_error": (C.c_char_p, []),
+    "llmrs_device": (C.c_int, []),
+    "llmrs_name": (C.c_char_p, []),
+    "llmrs_sync": (C.c_int, []),
+    "llmrs_num_cus": (C.c_int, []),
+    "llmrs_tensor_upload_f32": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t), C.c_int, C.POINTER(C.c_void_p)]),
+    "llmrs_tensor_upload_q4": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
+    "llmrs_tensor_upload_q8_0": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
+    "llmrs_tensor_zeros": (C.c_int, [C.POINTER(C.c_size_t), C.c_int, C.POINTER(C.c_void_p)]),
+    "llmrs_tensor_download": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "llmrs_tensor_ndim": (C.c_int, [C.c_void_p]),
+    "llmrs_tensor_dims": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t)]),
+    "llmrs_tensor_dtype": (C.c_int, [C.c_void_p]),
+    "llmrs_tensor_free": (C.c_int, [C.c_void_p]),
+    "llmrs_matmul": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]),
+    "llmrs_matmul_transposed": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]),
+    "llmrs_matmul_slice": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
+    "llmrs_add_assign": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "llmrs_silu_mul": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "llmrs_rope_inplace": (C.c_int, [C.c_void_p, C.c_size_t]),
+    "llmrs_rms_norm": (C.c_int, [C.c_void_p, C.c_void_p, C.c_float, C.POINTER(C.c_void_p)]),
+    "llmrs_softmax": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
+    "llmrs_scale": (C.c_int, [C.c_void_p, C.c_float, C.POINTER(C.c_void_p)]),
+    "llmrs_copy_from": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
+    "llmrs_model_create": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
+    "llmrs_model_free": (C.c_int, [C.c_void_p]),
+    "llmrs_model_set_embedding": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "llmrs_model_set_norm": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
+    "llmrs_model_set_linear_q4": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "llmrs_model_set_linear_q8_0": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "llmrs_model_kv_write": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
+    "llmrs_model_kv_read": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]),
+    "llmrs_model_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "llmrs_model_generate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
+    "llmrs_model_begin": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "llmrs_model_decode_steps": (C.c_int, [C.c_void_p, C.c_size_t]),
+    "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "llmrs_model_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
+    "llmrs_model_weight_bytes": (C.c_double, [C.c_void_p]),
+    "llmrs_synth_q4": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_int]),
+    "llmrs_synth_q8": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_int]),
+    "llmrs_synth_normal": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_int]),
+    "llmrs_synth_tokens": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_int32, C.c_void_p]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+def lib() -> C.CDLL:
+    """The loaded C library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise LlmrsError(E_MODULE, f"{LIB_PATH} is missing; run llm.rs_amd/build.py")
+        handle = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def _check(rc: int) -> int:
+    if rc < 0:
+        raise LlmrsError(rc, lib().llmrs_last_error().decode(errors="replace"))
+    return rc
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+_initialised = False
+
+
+def init(device: int = 0) -> None:
+    """llmrs_init: select the GPU and load the gfx950 code objects."""
+    global _initialised
+    if not _initialised:
+        _check(lib().llmrs_init(device, str(LIB_DIR).encode()))
+        _initialised = True
+
+
+def sync() -> None:
+    _check(lib().llmrs_sync())
+
+
+def num_cus() -> int:
+    return lib().llmrs_num_cus()
+
+
+class Tensor:
+    """A device tensor handle (Tensor with Storage on Device::Hip)."""
+
+    __slots__ = ("_h", "__weakref__")
+
+    def __init__(self, handle: int):
+        self._h = C.c_void_p(handle)
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def shape(self) -> tuple[int, ...]:
+        nd = _check(lib().llmrs_tensor_ndim(self._h))
+        dims = (C.c_size_t * nd)()
+        _check(lib().llmrs_tensor_dims(self._h, dims))
+        return tuple(int(d) for d in dims)
+
+    @property
+    def dtype(self) -> DType:
+        return DType(_check(lib().llmrs_tensor_dtype(self._h)))
+
+    def data(self) -> np.ndarray:
+        """Tensor::data(): download an f32 tensor."""
+        out = np.empty(self.shape, dtype=np.float32)
+        _check(lib().llmrs_tensor_download(self._h, _ptr(out), out.size))
+        return out
+
+    def free(self) -> None:
+        if self._h and self._h.value:
+            _check(lib().llmrs_tensor_free(self._h))
+            self._h = C.c_void_p(None)
+
+    def __del__(self):
+        try:
+            if _lib is not None and self._h and self._h.value:
+                _lib.llmrs_tensor_free(self._h)
+        except Exception:
+            pass
+
+    # -- construction (Tensor::new + to_device) --------------------------
+    @staticmethod
+    def from_numpy(arr) -> "Tensor":
+        a = np.ascontiguousarray(arr, dtype=np.float32)
+        dims = (C.c_size_t * max(a.ndim, 1))(*(a.shape or (1,)))
+        out = C.c_void_p()
+        _check(lib().llmrs_tensor_upload_f32(_ptr(a), dims, max(a.ndim, 1), C.byref(out)))
+        return Tensor(out.value)
+
+    @staticmethod
+    def from_q4(qs: np.ndarray, scales: np.ndarray, n: int, k: int) -> "Tensor":
+        """Storage::CpuQ4 -> device: qs [n][k/2] reference nibble order, f32 scales."""
+        qs = np.ascontiguousarray(qs, dtype=np.uint8)
+        sc = np.ascontiguousarray(scales, dtype=np.float32)
+        if qs.size != n * k // 2 or sc.size != n * k // 32:
+            raise LlmrsError(E_INVALID, "q4 buffer sizes do not match n, k")
+        out = C.c_void_p()
+        _check(lib().llmrs_tensor_upload_q4(_ptr(qs), _ptr(sc), n, k, C.byref(out)))
+        return Tensor(out.value)
+
+    @staticmethod
+    def from_q8_0(qs: np.ndarray, scales: np.ndarray, n: int, k: int) -> "Tensor":
+        qs = np.ascontiguousarray(qs, dtype=np.int8)
+        sc = np.ascontiguousarray(scales, dtype=np.float32)
+        if qs.size != n * k or sc.size != n * k // 32:
+            raise LlmrsError(E_INVALID, "q8 buffer sizes do not match n, k")
+        out = C.c_void_p()
+        _check(lib().llmrs_tensor_upload_q8_0(_ptr(qs), _ptr(sc), n, k, C.byref(out)))
+        return Tensor(out.value)
+
+    @staticmethod
+    def zeros(shape) -> "Tensor":
+        dims = (C.c_size_t * len(shape))(*shape)
+        out = C.c_void_p()
+        _check(lib().llmrs_tensor_zeros(dims, len(shape), C.byref(out)))
+        return Tensor(out.value)
+
+
+def _out_tensor(fn, *args) -> Tensor:
+    out = C.c_void_p()
+    _check(fn(*args, C.byref(out)))
+    return Tensor(out.value)
+
+
+class HipBackend:
+    """trait Backend (src/backend.rs:15-40) on the gfx950 kernels."""
+
+    def __init__(self, device: int = 0):
+        init(device)
+
+    def device(self) -> Device:                                   # backend.rs:17
+        return Device(lib().llmrs_device())
+
+    def name(self) -> str:                                        # backend.rs:18
+        return lib().llmrs_name().decode()
+
+    def matmul(self, a: Tensor, b: Tensor) -> Tensor:             # backend.rs:21
+        return _out_tensor(lib().llmrs_matmul, a.handle, b.handle)
+
+    def matmul_transposed(self, a: Tensor, b: Tensor) -> Tensor:  # backend.rs:24
+        return _out_tensor(lib().llmrs_matmul_transposed, a.handle, b.handle)
+
+    def matmul_slice(self, a: Tensor, other_data, rows: int, cols: int) -> Tensor:  # backend.rs:28
+        od = np.ascontiguousarray(other_data, dtype=np.float32)
+        if od.size < rows * cols:
+            raise LlmrsError(E_INVALID, "other_data shorter than rows*cols")
+        return _out_tensor(lib().llmrs_matmul_slice, a.handle, _ptr(od), rows, cols)
+
+    def add_assign(self, a: Tensor, b: Tensor) -> None:           # backend.rs:31
+        _check(lib().llmrs_add_assign(a.handle, b.handle))
+
+    def silu_mul(self, gate: Tensor, up: Tensor) -> None:         # backend.rs:32
+        _check(lib().llmrs_silu_mul(gate.handle, up.handle))
+
+    def rope_inplace(self, x: Tensor, start_pos: int) -> None:    # backend.rs:33
+        _check(lib().llmrs_rope_inplace(x.handle, start_pos))
+
+    def rms_norm(self, x: Tensor, weight: Tensor, eps: float) -> Tensor:  # backend.rs:36
+        return _out_tensor(lib().llmrs_rms_norm, x.handle, weight.handle, C.c_float(eps))
+
+    def softmax(self, x: Tensor) -> Tensor:                       # backend.rs:37
+        return _out_tensor(lib().llmrs_softmax, x.handle)
+
+    def scale(self, x: Tensor, value: float) -> Tensor:           # backend.rs:38
+        return _out_tensor(lib().llmrs_scale, x.handle, C.c_float(value))
+
+    def copy_from(self, t: Tensor) -> Tensor:                     # backend.rs:39
+        return _out_tensor(lib().llmrs_copy_from, t.handle)
+
+
+class ModelConfig(C.Structure):
+    """llmrs_model_config: LlamaConfig (src/core/config.rs:3-17) plus storage."""
+    _fields_ = [
+        ("n_layers", C.c_int32), ("hidden", C.c_int32), ("n_heads", C.c_int32),
+        ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32), ("ffn", C.c_int32),
+        ("vocab", C.c_int32), ("max_seq", C.c_int32), ("rms_eps", C.c_float),
+        ("rope_theta", C.c_float), ("weight_dtype", C.c_int32), ("kv_dtype", C.c_int32),
+    ]
+
+
+W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN, W_LM_HEAD = range(8)
+N_INPUT, N_POST, N_FINAL = range(3)
+
+
+@dataclass
+class KernelTiming:
+    name: str
+    ms: float
+    bytes: float
+
+
+class HipModel:
+    """The resident decode model (llmrs_model_*)."""
+
+    def __init__(self, cfg: ModelConfig, device: int = 0):
+        init(device)
+        self.cfg = cfg
+        h = C.c_void_p()
+        _check(lib().llmrs_model_create(C.byref(cfg), C.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if self._h and self._h.value:
+            _check(lib().llmrs_model_free(self._h))
+            self._h = C.c_void_p(None)
+
+    def __del__(self):
+        try:
+            if _lib is not None and self._h and self._h.value:
+                _lib.llmrs_model_free(self._h)
+        except Exception:
+            pass
+
+    def set_embedding(self, table: np.ndarray) -> None:
+        t = np.ascontiguousarray(table, dtype=np.float32)
+        _check(lib().llmrs_model_set_embedding(self._h, _ptr(t)))
+
+    def set_norm(self, layer: int, slot: int, w: np.ndarray) -> None:
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        _check(lib().llmrs_model_set_norm(self._h, layer, slot, _ptr(w)))
+
+    def set_linear_q4(self, layer: int, slot: int, qs: np.ndarray, scales: np.ndarray) -> None:
+        qs = np.ascontiguousarray(qs, dtype=np.uint8)
+        sc = np.ascontiguousarray(scales, dtype=np.float32)
+        _check(lib().llmrs_model_set_linear_q4(self._h, layer, slot, _ptr(qs), _ptr(sc)))
+
+    def set_linear_q8_0(self, layer: int, slot: int, qs: np.ndarray, scales: np.ndarray) -> None:
+        qs = np.ascontiguousarray(qs, dtype=np.int8)
+        sc = np.ascontiguousarray(scales, dtype=np.float32)
+        _check(lib().llmrs_model_set_linear_q8_0(self._h, layer, slot, _ptr(qs), _ptr(sc)))
+
+    def kv_write(self, layer: int, kv_head: int, pos0: int, k: np.ndarray, v: np.ndarray) -> None:
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        n = k.size // self.cfg.head_dim
+        _check(lib().llmrs_model_kv_write(self._h, layer, kv_head, pos0, n, _ptr(k), _ptr(v)))
+
+    def kv_read(self, layer: int, kv_head: int, pos0: int, n: int):
+        k = np.empty((n, self.cfg.head_dim), np.float32)
+        v = np.empty((n, self.cfg.head_dim), np.float32)
+        _check(lib().llmrs_model_kv_read(self._h, layer, kv_head, pos0, n, _ptr(k), _ptr(v)))
+        return k, v
+
+    def forward(self, tokens, start_pos: int, logits: bool = True, trace: bool = False):
+        """Eager forward of tokens at [start_pos, start_pos+n): (logits, next, trace)."""
+        ids = np.ascontiguousarray(tokens, dtype=np.int32)
+        n = ids.size
+        lg = np.empty(self.cfg.vocab, np.float32) if logits else None
+        nxt = np.zeros(1, np.int32)
+        tr = np.empty((n, self.cfg.n_layers + 1, self.cfg.hidden), np.float32) if trace else None
+        _check(lib().llmrs_model_forward(self._h, _ptr(ids), n, start_pos, _ptr(lg), _ptr(nxt), _ptr(tr)))
+        return lg, int(nxt[0]), tr
+
+    def generate(self, prompt, n_steps: int) -> np.ndarray:
+        ids = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(n_steps, np.int32)
+        _check(lib().llmrs_model_generate(self._h, _ptr(ids), ids.size, n_steps, _ptr(out)))
+        return out
+
+    def begin(self, prompt) -> None:
+        ids = np.ascontiguousarray(prompt, dtype=np.int32)
+        _check(lib().llmrs_model_begin(self._h, _ptr(ids), ids.size))
+
+    def decode_steps(self, n: int) -> None:
+        _check(lib().llmrs_model_decode_steps(self._h, n))
+
+    def tokens(self, count: int) -> np.ndarray:
+        out = np.empty(count, np.int32)
+        _check(lib().llmrs_model_tokens(self._h, _ptr(out), count))
+        return out
+
+    def profile_step(self, cap: int = 4096) -> list[KernelTiming]:
+        names = C.create_string_buffer(32 * cap)
+        ms = np.zeros(cap, np.float32)
+        by = np.zeros(cap, np.float64)
+        n = _check(lib().llmrs_model_profile_step(self._h, names, _ptr(ms), _ptr(by), cap))
+        raw = names.raw
+        return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(by[i]))
+                for i in range(n)]
+
+    def weight_bytes(self) -> float:
+        return float(lib().llmrs_model_weight_bytes(self._h))
+
+
+# -- seeded synthetic inputs (llmrs_synth_*) ------------------------------
+def synth_q4(seed: int, tid: int, n: int, k: int, lo: float, hi: float, threads: int = 0):
+    qs = np.empty(n * k // 2, np.uint8)
+    sc = np.empty(n * k // 32, np.float32)
+    _check(lib().llmrs_synth_q4(seed, tid, n, k, lo, hi, _ptr(qs), _ptr(sc), threads))
+    return qs, sc
+
+
+def synth_q8(seed: int, tid: int, n: int, k: int, lo: float, hi: float, threads: int = 0):
+    qs = np.empty(n * k, np.int8)
+    sc = np.empty(n * k // 32, np.float32)
+    _check(lib().llmrs_synth_q8(seed, tid, n, k, lo, hi, _ptr(qs), _ptr(sc), threads))
+    return qs, sc
+
+
+def synth_normal(seed: int, tid: int, count: int, mean: float, std: float, threads: int = 0):
+    out = np.empty(count, np.float32)
+    _check(lib().llmrs_synth_normal(seed, tid, count, mean, std, _ptr(out), threads))
+    return out
+
+
+def synth_tokens(seed: int, tid: int, count: int, vocab: int) -> np.ndarray:
+    out = np.empty(count, np.int32)
+    _check(lib().llmrs_synth_tokens(seed, tid, count, vocab, _ptr(out)))
+    return out

@@ -1,0 +1,111 @@
+/*
+ * oracle.h - CPU restatement of the llm.rs reference CPU path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing on the product path (the llmrs_hip
+ * library, its kernels, bench.py's GPU leg) may include, link or call this.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
+ * as the checker and as the timed CPU baseline.
+ *
+ * Every function follows a reference file:line (paths relative to the
+ * reference root), stated at its definition in oracle.cpp.  Floating-point
+ * order follows the reference exactly: this file is compiled with
+ * -ffp-contract=off (Rust never fuses a*b+c), glibc libm supplies
+ * expf/powf/sinf/cosf/sqrtf, roundf is ties-away like Rust's f32::round.
+ *
+ * How each part is pinned (tests/test_oracle.py):
+ *   quantize_row_q8_0   closed form per block + brute force (amax=0, ties,
+ *                       clamp) in numpy.
+ *   Q4 format / GEMV    integer block sums vs numpy int64 brute force, and vs
+ *                       a float64 dot over dequantised weights
+ *                       (test/opencl.rs:237-258 tolerance 1e-3).
+ *   rms_norm            KAT test/cpu.rs:197-212 + float64 closed form.
+ *   rope                KAT test/cpu.rs:229-245 + rotation invariants.
+ *   softmax             KAT test/cpu.rs:214-227 + float64 closed form.
+ *   attention / KV      layer.rs:430-489 (causality, KV update) + float64
+ *                       brute force; GQA row duplication == true GQA.
+ *   model / token loop  batched prefill == sequential decode (bit-exact,
+ *                       a property of the reference's arithmetic), layer
+ *                       composition vs a numpy float64 restatement.
+ * Parity unpinned at the bit level: expf/powf/sinf/cosf come from the host
+ * glibc, as in the reference; no reference test pins them beyond 1e-5.
+ */
+#ifndef LLMRS_ORACLE_H
+#define LLMRS_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
+/* ---- cpu.rs primitives -------------------------------------------------- */
+void orc_quantize_row_q8_0(const float* x, int64_t k, int8_t* q, float* d);
+void orc_quantize_q4(const float* x, int64_t count, uint8_t* qs, float* scales);
+void orc_dequantize_q4(const uint8_t* qs, const float* scales, int64_t count,
+                       float* out);
+int32_t orc_q4_block_isum(const uint8_t* q4, const int8_t* a);
+int32_t orc_q4_block_isum_scalar(const uint8_t* q4, const int8_t* a);
+void orc_matmul_transposed_q4(const float* a, int64_t m, int64_t k,
+                              const uint8_t* qs, const float* scales,
+                              int64_t n, float* out);
+void orc_matmul_transposed_q8w(const float* a, int64_t m, int64_t k,
+                               const int8_t* qs, const float* scales,
+                               int64_t n, float* out);
+void orc_matmul_transposed_f32(const float* a, int64_t m, int64_t k,
+                               const float* b, int64_t n, float* out);
+void orc_matmul(const float* a, int64_t m, int64_t k, const float* b,
+                int64_t n, float* out);
+void orc_matmul_slice(const float* a, int64_t m, int64_t k,
+                      const float* other, int64_t rows, float* out);
+void orc_add_assign(float* a, const float* b, int64_t n);
+void orc_silu_mul(float* gate, const float* up, int64_t n);
+void orc_rope_inplace(float* x, int64_t count, int64_t head_dim,
+                      int64_t start_pos);
+void orc_rms_norm(const float* x, int64_t rows, int64_t dim, const float* w,
+                  float eps, float* out);
+void orc_softmax(const float* x, int64_t rows, int64_t dim, float* out);
+void orc_scale(const float* x, int64_t n, float value, float* out);
+uint16_t orc_f32_to_f16(float x);
+float orc_f16_to_f32(uint16_t h);
+int64_t orc_argmax(const float* x, int64_t n, float* margin);
+
+/* ---- model (layer.rs / model.rs / main.rs) ------------------------------ */
+typedef struct {
+  int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_seq;
+  float rms_eps, rope_theta;
+  int32_t weight_dtype; /* 2 = Q4 (f32 scales), 3 = Q4_0, 4 = Q8_0 */
+  int32_t kv_dtype;     /* 0 = f32, 1 = f16 */
+} orc_config;
+
+typedef struct orc_model orc_model;
+orc_model* orc_model_create(const orc_config* cfg);
+void orc_model_free(orc_model* m);
+/* Weights are borrowed: the caller keeps the arrays alive. */
+int orc_model_set_embedding(orc_model* m, const float* table);
+int orc_model_set_norm(orc_model* m, int layer, int slot, const float* w);
+int orc_model_set_linear_q4(orc_model* m, int layer, int slot,
+                            const uint8_t* qs, const float* scales);
+int orc_model_set_linear_q8(orc_model* m, int layer, int slot,
+                            const int8_t* qs, const float* scales);
+int orc_model_kv_write(orc_model* m, int layer, int kv_head, int64_t pos0,
+                       int64_t n, const float* k, const float* v);
+int orc_model_kv_read(orc_model* m, int layer, int kv_head, int64_t pos0,
+                      int64_t n, float* k, float* v);
+/* LlamaModel::forward over `n` tokens at start_pos, batched like the
+ * reference prefill.  logits: [n][vocab] if all_rows else [vocab] (last
+ * row); trace: [n][n_layers+1][hidden] or NULL. */
+int orc_model_forward(orc_model* m, const int32_t* tokens, int64_t n,
+                      int64_t start_pos, float* logits, int all_rows,
+                      float* trace);
+/* Greedy token loop (main.rs:128-327 with argmax).  out: n_steps ids;
+ * margins: top1-top2 logit gap per step (may be NULL). */
+int orc_model_generate(orc_model* m, const int32_t* prompt, int64_t n_prompt,
+                       int64_t n_steps, int32_t* out, float* margins);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,181 @@
+"""GPU parity of the trait Backend operators against the CPU oracle.
+
+Inputs are identical seeded arrays on both sides.  Bar (per kernel, f32):
+|gpu - oracle| <= 1e-4 + 1e-3 * |oracle|; the GEMV's integer block sums are
+exact, only the f32 order of the block accumulation differs.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import rel_close
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+# (n, k): every decode GEMV shape of the 1B and 8B workloads (q, k|v, o,
+# gate|up, down, lm_head) plus the reference's own test shapes.
+GEMV_SHAPES = [
+    (64, 128), (128, 256), (2048, 2048), (512, 2048), (16384, 2048), (2048, 8192),
+    (128256, 2048), (4096, 4096), (1024, 4096), (28672, 4096), (4096, 14336), (128256, 4096),
+]
+
+
+def _x(rng, m, k):
+    return rng.normal(0, 1, (m, k)).astype(F32)
+
+
+@pytest.mark.parametrize("n,k", GEMV_SHAPES)
+def test_gemv_q4_0(hip, orc, rng, n, k):
+    be = hip.HipBackend()
+    qs, sc = hip.synth_q4(20260002, n * 7 + k, n, k, 0.003, 0.006)
+    x = _x(rng, 1, k)
+    w = hip.Tensor.from_q4(qs, sc, n, k)
+    assert w.dtype == hip.DType.Q4_0
+    got = be.matmul_transposed(hip.Tensor.from_numpy(x), w).data()
+    want = orc.matmul_transposed_q4(x, qs, sc, n)
+    ok, err, nbad = rel_close(got, want)
+    assert ok, f"max err {err}, {nbad} outside tolerance"
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 128), (4, 128, 256), (3, 4096, 4096)])
+def test_gemv_q4_reference_quantiser_rows(hip, orc, rng, m, n, k):
+    """Weights from the reference quantiser (f32 scales, Storage::CpuQ4) and
+    M>1 rows (test_opencl_q4_prefill_stress, test/opencl.rs:475-510)."""
+    be = hip.HipBackend()
+    b = rng.uniform(-1, 1, (n, k)).astype(F32)
+    qs, sc = orc.quantize_q4(b)
+    w = hip.Tensor.from_q4(qs, sc, n, k)
+    assert w.dtype == hip.DType.Q4
+    a = rng.uniform(-1, 1, (m, k)).astype(F32)
+    got = be.matmul_transposed(hip.Tensor.from_numpy(a), w).data()
+    want = orc.matmul_transposed_q4(a, qs, sc, n)
+    ok, err, nbad = rel_close(got, want)
+    assert ok, f"max err {err}, {nbad} outside tolerance"
+
+
+@pytest.mark.parametrize("n,k", [(64, 128), (2048, 2048), (512, 2048), (16384, 2048), (2048, 8192)])
+def test_gemv_q8_0(hip, orc, rng, n, k):
+    be = hip.HipBackend()
+    qs, sc = hip.synth_q8(20260001, n + k, n, k, 2e-4, 3.5e-4)
+    x = _x(rng, 1, k)
+    w = hip.Tensor.from_q8_0(qs, sc, n, k)
+    got = be.matmul_transposed(hip.Tensor.from_numpy(x), w).data()
+    want = orc.matmul_transposed_q8w(x, qs, sc, n)
+    ok, err, nbad = rel_close(got, want)
+    assert ok, f"max err {err}, {nbad} outside tolerance"
+
+
+def test_gemv_zero_and_special_inputs(hip, orc):
+    """amax == 0 blocks (d = 0) and a NaN input element (code 0)."""
+    be = hip.HipBackend()
+    n, k = 96, 256
+    qs, sc = hip.synth_q4(3, 4, n, k, 0.003, 0.006)
+    x = np.zeros((1, k), F32)
+    x[0, 40:70] = np.linspace(-2, 2, 30)
+    x[0, 200] = np.nan
+    w = hip.Tensor.from_q4(qs, sc, n, k)
+    got = be.matmul_transposed(hip.Tensor.from_numpy(x), w).data()
+    want = orc.matmul_transposed_q4(x, qs, sc, n)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok, err, _ = rel_close(np.nan_to_num(got), np.nan_to_num(want))
+    assert ok, err
+
+
+def test_matmul_f32_bit_exact(hip, orc, rng):
+    be = hip.HipBackend()
+    for (m, k, n) in [(1, 128, 256), (16, 64, 32)]:
+        a = rng.uniform(-1, 1, (m, k)).astype(F32)
+        a[0, 3] = 0.0
+        b = rng.uniform(-1, 1, (k, n)).astype(F32)
+        got = be.matmul(hip.Tensor.from_numpy(a), hip.Tensor.from_numpy(b)).data()
+        assert np.array_equal(got, orc.matmul(a, b))
+
+
+def test_matmul_transposed_f32_and_slice_bit_exact(hip, orc, rng):
+    be = hip.HipBackend()
+    a = rng.uniform(-1, 1, (4, 128)).astype(F32)
+    b = rng.uniform(-1, 1, (64, 128)).astype(F32)
+    got = be.matmul_transposed(hip.Tensor.from_numpy(a), hip.Tensor.from_numpy(b)).data()
+    assert np.array_equal(got, orc.matmul_transposed_f32(a, b))
+    q = rng.uniform(-1, 1, (1, 64)).astype(F32)
+    kc = rng.uniform(-1, 1, (10, 64)).astype(F32)
+    got = be.matmul_slice(hip.Tensor.from_numpy(q), kc, 10, 64).data()
+    assert np.array_equal(got, orc.matmul_slice(q, kc, 10))
+
+
+def test_rms_norm(hip, orc, rng):
+    be = hip.HipBackend()
+    d = be.rms_norm(hip.Tensor.from_numpy(np.array([[1, 2, 3, 4]], F32)),
+                    hip.Tensor.from_numpy(np.ones(4, F32)), 1e-5).data()[0]
+    assert abs(d[0] - 0.3651) < 1e-3 and abs(d[3] - 1.4605) < 1e-3
+    x = rng.normal(0, 1, (7, 4096)).astype(F32)
+    w = rng.normal(1, 0.02, 4096).astype(F32)
+    got = be.rms_norm(hip.Tensor.from_numpy(x), hip.Tensor.from_numpy(w), 1e-5).data()
+    ok, err, _ = rel_close(got, orc.rms_norm(x, w, 1e-5), rtol=1e-5, atol=1e-6)
+    assert ok, err
+
+
+def test_softmax(hip, orc, rng):
+    be = hip.HipBackend()
+    d = be.softmax(hip.Tensor.from_numpy(np.array([[1, 2, 3]], F32))).data()[0]
+    assert abs(d.sum() - 1) < 1e-5 and d[2] > d[1] > d[0]
+    x = rng.normal(0, 3, (5, 1000)).astype(F32)
+    x[1, 500:] = -np.inf  # causal-mask style row
+    got = be.softmax(hip.Tensor.from_numpy(x)).data()
+    ok, err, _ = rel_close(got, orc.softmax(x), rtol=1e-5, atol=1e-7)
+    assert ok, err
+
+
+def test_rope_bit_exact(hip, orc, rng):
+    be = hip.HipBackend()
+    t = hip.Tensor.from_numpy(np.array([[1, 0, 0, 1]], F32))
+    be.rope_inplace(t, 1)
+    d = t.data()[0]
+    assert abs(np.hypot(d[0], d[2]) - 1) < 1e-4 and d[0] != 1.0
+    for hd, pos in [(64, 0), (64, 31), (128, 511), (128, 8190)]:
+        x = rng.normal(0, 1, (3, hd)).astype(F32)
+        t = hip.Tensor.from_numpy(x)
+        be.rope_inplace(t, pos)
+        assert np.array_equal(t.data(), orc.rope_inplace(x, pos))
+
+
+def test_elementwise(hip, orc, rng):
+    be = hip.HipBackend()
+    a = rng.uniform(-1, 1, (10, 10)).astype(F32)
+    b = rng.uniform(-1, 1, (10, 10)).astype(F32)
+    ta = hip.Tensor.from_numpy(a)
+    be.add_assign(ta, hip.Tensor.from_numpy(b))
+    assert np.array_equal(ta.data(), orc.add_assign(a, b))
+    g = rng.uniform(-1, 1, 128).astype(F32)
+    u = rng.uniform(-1, 1, 128).astype(F32)
+    tg = hip.Tensor.from_numpy(g)
+    be.silu_mul(tg, hip.Tensor.from_numpy(u))
+    ok, err, _ = rel_close(tg.data(), orc.silu_mul(g, u), rtol=1e-6, atol=1e-7)
+    assert ok, err
+    s = be.scale(hip.Tensor.from_numpy(a), 0.088388).data()
+    assert np.array_equal(s, orc.scale(a, 0.088388))
+    c = be.copy_from(hip.Tensor.from_numpy(a)).data()
+    assert np.array_equal(c, a)
+
+
+def test_memory_sync_loop(hip):
+    """test_opencl_memory_sync_loop (test/opencl.rs:413-437): 100 add_assign."""
+    be = hip.HipBackend()
+    acc = hip.Tensor.zeros((1024,))
+    one = hip.Tensor.from_numpy(np.ones(1024, F32))
+    for _ in range(100):
+        be.add_assign(acc, one)
+    assert np.all(acc.data() == 100.0)
+
+
+def test_shape_errors(hip):
+    be = hip.HipBackend()
+    a = hip.Tensor.from_numpy(np.ones((2, 64), F32))
+    b = hip.Tensor.from_numpy(np.ones((3, 32), F32))
+    with pytest.raises(hip.LlmrsError) as e:
+        be.matmul_transposed(a, b)
+    assert e.value.code == hip.E_INVALID
+    with pytest.raises(hip.LlmrsError):
+        be.add_assign(a, b)
