@@ -133,6 +133,9 @@ __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
       const int t = t0 + r;
       float kf[EPC];
       kv_t vv[EPC];
+      // Rows past `end` are zero-filled: they belong to the next split
+      // (possibly the owner of pos, whose s_new this workgroup never wrote)
+      // and a 0 * NaN from stale LDS would poison P.V.
       if (t < end && t != pos) {
         const uint4 kraw = *(const uint4*)(kc + (size_t)t * HD + col);
         const uint4 vraw = *(const uint4*)(vc + (size_t)t * HD + col);
@@ -143,7 +146,7 @@ __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
           kf[e] = kv_to_f<KV16>(kp[e]);
           vv[e] = vp[e];
         }
-      } else if (t == pos) {
+      } else if (t < end) {  // t == pos: this workgroup is the owner
 #pragma unroll
         for (int e = 0; e < EPC; ++e) {
           kf[e] = s_new[0][col + e];

@@ -21,6 +21,7 @@ _P = C.c_void_p
 _SIGS = {
     "orc_set_threads": (None, [C.c_int]),
     "orc_get_threads": (C.c_int, []),
+    "orc_set_jitter": (None, [C.c_uint64, C.c_int]),
     "orc_quantize_row_q8_0": (None, [_P, _I64, _P, _P]),
     "orc_quantize_q4": (None, [_P, _I64, _P, _P]),
     "orc_dequantize_q4": (None, [_P, _P, _I64, _P]),
@@ -77,6 +78,13 @@ def _f32(a):
 
 def set_threads(n: int) -> None:
     lib().orc_set_threads(n)
+
+
+def set_jitter(seed: int, ulps: int = 1) -> None:
+    """Test-only: seed != 0 moves every linear-layer input by a pseudo-random
+    whole number of ulps in [-ulps, ulps] before the reference arithmetic
+    (seed 0 = off, the default)."""
+    lib().orc_set_jitter(seed, ulps)
 
 
 def threads() -> int:

@@ -118,6 +118,23 @@ class Pool {
   int nthreads_ = 1;
 };
 
+// Test-only noise model (orc_set_jitter): when the seed is non-zero, every
+// input of a linear layer is moved element-wise by a pseudo-random whole
+// number of ulps in [-ulps, +ulps] before the reference arithmetic runs.  It
+// measures how far the reference's own output moves under rounding-level
+// input changes - the envelope a different f32 summation order can reach.
+// Off (seed 0) by default.
+std::atomic<uint64_t> g_jitter_seed{0};
+std::atomic<uint64_t> g_jitter_calls{0};
+std::atomic<int> g_jitter_ulps{1};
+
+inline uint64_t jitter_mix(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
 Pool& pool() {
   static Pool p(0);
   return p;
@@ -199,6 +216,12 @@ inline float from_half(uint16_t h) { return _cvtsh_ss(h); }
 extern "C" {
 
 void orc_set_threads(int n) { pool().resize(n); }
+
+void orc_set_jitter(uint64_t seed, int ulps) {
+  g_jitter_ulps.store(ulps < 1 ? 1 : ulps);
+  g_jitter_seed.store(seed);
+  g_jitter_calls.store(0);
+}
 int orc_get_threads(void) { return pool().size(); }
 
 // cpu.rs:724-743 (x86 path of quantize_row_q8_0).  amax by strict '>' fold
@@ -475,6 +498,20 @@ namespace {
 
 void linear_forward(const orc_model* m, const OrcLinear& w, const float* x,
                     int64_t rows, float* out) {
+  std::vector<float> jittered;
+  const uint64_t seed = g_jitter_seed.load();
+  if (seed) {
+    const uint64_t call = g_jitter_calls.fetch_add(1);
+    jittered.assign(x, x + rows * w.k);
+    const int ulps = g_jitter_ulps.load();
+    for (int64_t i = 0; i < rows * w.k; ++i) {
+      const uint64_t h = jitter_mix(seed ^ jitter_mix(call * 0x100000001B3ull + (uint64_t)i));
+      const int steps = (int)(h % (uint64_t)(2 * ulps + 1)) - ulps;
+      for (int s = 0; s < steps; ++s) jittered[i] = std::nextafter(jittered[i], INFINITY);
+      for (int s = 0; s > steps; --s) jittered[i] = std::nextafter(jittered[i], -INFINITY);
+    }
+    x = jittered.data();
+  }
   if (m->c.weight_dtype == 4)
     orc_matmul_transposed_q8w(x, rows, w.k, w.q8, w.scales, w.n, out);
   else

@@ -40,6 +40,10 @@ extern "C" {
 
 void orc_set_threads(int n);
 int orc_get_threads(void);
+/* Test-only noise model: seed != 0 moves every linear-layer input by a
+ * pseudo-random whole number of ulps in [-ulps, ulps] (per element and call)
+ * before the reference arithmetic; seed 0 turns it off (the default). */
+void orc_set_jitter(uint64_t seed, int ulps);
 
 /* ---- cpu.rs primitives -------------------------------------------------- */
 void orc_quantize_row_q8_0(const float* x, int64_t k, int8_t* q, float* d);

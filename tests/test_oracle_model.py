@@ -137,3 +137,26 @@ def test_generate_matches_forward_loop(orc, tiny_q4):
         ids.append(t)
         lg, _ = m2.forward([t], len(ids) - 1)
     assert np.all(margins >= 0)
+
+
+def test_jitter_noise_model_is_off_by_default_and_seeded(orc, tiny_q4):
+    """The test-only jitter: seed 0 leaves results bit-identical, a seed gives
+    a reproducible, small (rounding-level input) change."""
+    spec, _, w = tiny_q4
+    toks = syn.prompt(spec)
+
+    def run(seed, ulps=16):
+        orc.set_jitter(seed, ulps)
+        try:
+            m = orc.OracleModel.from_spec(spec)
+            m.load(w)
+            return m.forward(toks, 0)[0]
+        finally:
+            orc.set_jitter(0)
+
+    base = run(0)
+    assert np.array_equal(base, run(0))
+    a, b = run(11), run(11)
+    assert np.array_equal(a, b)
+    assert not np.array_equal(a, base)
+    assert np.max(np.abs(a - base)) < 0.05 * np.max(np.abs(base))
