@@ -96,6 +96,16 @@ void set_last_error(const std::string& msg);
 enum { WT_Q4H = 0, WT_Q4F = 1, WT_Q8H = 2 };
 const char* wt_tag(int wt);
 
+// Launch plan of one GEMV: kernel name, grid and dynamic LDS bytes.
+// `kind` is the prologue/epilogue pair of gemv.hip: quant_store,
+// norm_store, q8_resid, norm_silu or norm_argmax.
+struct GemvPlan {
+  std::string name;
+  unsigned grid = 1;
+  size_t lds = 0;
+};
+GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus);
+
 // Bytes of codes per 32-element block.
 inline int block_code_bytes(int wt) { return wt == WT_Q8H ? 32 : 16; }
 inline int block_scale_bytes(int wt) { return wt == WT_Q4F ? 4 : 2; }

@@ -66,7 +66,7 @@ struct llmrs_model {
   int8_t *ctx_q = nullptr, *m_q = nullptr;
   int *part_idx = nullptr, *counters = nullptr, *tokens = nullptr, *gen = nullptr;
   int *pos = nullptr, *n_prompt = nullptr, *err = nullptr;
-  int nsplit = 1, lm_grid = 1, cap = 0, gemv_wgs = 0;
+  int nsplit = 1, lm_grid = 1, cap = 0;
   size_t host_pos = 0;
   bool begun = false;
   hipGraph_t graph = nullptr;
@@ -139,10 +139,7 @@ double linear_weight_bytes(const llmrs_model* m, const DevLinear& L) {
 void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
-  const std::string tag = wt_tag(m->wt);
-  const unsigned maxwg = (unsigned)m->gemv_wgs;
-  auto lds = [](int k) { return (size_t)k + 8 * (size_t)(k / 32); };
-  auto grid16 = [&](int n) { return std::min<unsigned>((unsigned)((n + 15) / 16), maxwg); };
+  const int cus = ctx().num_cus;
 
   EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, H, c.vocab};
   L("embed_gather", 8.0 * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
@@ -165,8 +162,8 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
       g.norm_w = Lb.norm[0];
       g.eps = c.rms_eps;
       g.y = m->qkv;
-      L("gemv_" + tag + "_norm_store", linear_weight_bytes(m, Lb.qkv) + 8.0 * H + 4.0 * g.n,
-        dim3(grid16(g.n)), dim3(256), lds(H), g);
+      const GemvPlan p = gemv_plan(m->wt, "norm_store", g.n, g.k, cus);
+      L(p.name, linear_weight_bytes(m, Lb.qkv) + 8.0 * H + 4.0 * g.n, dim3(p.grid), dim3(256), p.lds, g);
     }
     {  // attention
       AttnArgs a{};
@@ -200,8 +197,8 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
       g.xd = m->ctx_d;
       g.y = m->h;
       g.res = m->x;
-      L("gemv_" + tag + "_q8_resid", linear_weight_bytes(m, Lb.o) + 1.125 * g.k + 8.0 * H,
-        dim3(grid16(H)), dim3(256), lds(g.k), g);
+      const GemvPlan p = gemv_plan(m->wt, "q8_resid", g.n, g.k, cus);
+      L(p.name, linear_weight_bytes(m, Lb.o) + 1.125 * g.k + 8.0 * H, dim3(p.grid), dim3(256), p.lds, g);
     }
     {  // gate|up + SiLU
       GemvArgs g{};
@@ -215,9 +212,8 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
       g.y = m->mf;
       g.yq = m->m_q;
       g.yd = m->m_d;
-      const unsigned grid = std::min<unsigned>((unsigned)(F / 32), maxwg);
-      L("gemv_" + tag + "_norm_silu", linear_weight_bytes(m, Lb.gu) + 8.0 * H + 5.125 * F,
-        dim3(grid), dim3(256), lds(H), g);
+      const GemvPlan p = gemv_plan(m->wt, "norm_silu", g.n, g.k, cus);
+      L(p.name, linear_weight_bytes(m, Lb.gu) + 8.0 * H + 5.125 * F, dim3(p.grid), dim3(256), p.lds, g);
     }
     {  // down projection + residual
       GemvArgs g{};
@@ -229,8 +225,8 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
       g.xd = m->m_d;
       g.y = m->x;
       g.res = m->h;
-      L("gemv_" + tag + "_q8_resid", linear_weight_bytes(m, Lb.down) + 1.125 * F + 8.0 * H,
-        dim3(grid16(H)), dim3(256), lds(F), g);
+      const GemvPlan p = gemv_plan(m->wt, "q8_resid", g.n, g.k, cus);
+      L(p.name, linear_weight_bytes(m, Lb.down) + 1.125 * F + 8.0 * H, dim3(p.grid), dim3(256), p.lds, g);
     }
   }
   if (trace_dev)
@@ -248,8 +244,9 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
     g.y = write_logits ? m->logits : nullptr;
     g.part_val = m->part_val;
     g.part_idx = m->part_idx;
-    L("gemv_" + tag + "_norm_argmax", linear_weight_bytes(m, m->lm_head) + 8.0 * H,
-      dim3((unsigned)m->lm_grid), dim3(256), lds(H), g);
+    const GemvPlan p = gemv_plan(m->wt, "norm_argmax", g.n, g.k, cus);
+    LLMRS_REQUIRE((int)p.grid == m->lm_grid, LLMRS_E_INVALID, "lm_head grid changed since model creation");
+    L(p.name, linear_weight_bytes(m, m->lm_head) + 8.0 * H, dim3(p.grid), dim3(256), p.lds, g);
   }
   ArgmaxFinalArgs f{m->part_val, m->part_idx, m->lm_grid, m->pos, m->n_prompt, m->tokens, m->gen, m->cap};
   L("argmax_final", 8.0 * m->lm_grid, dim3(1), dim3(256), 0, f);
@@ -360,12 +357,11 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     Context& cx = ctx();
     const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
     m->qkv_rows = (nq + 2 * nkv) * hd;
-    m->gemv_wgs = std::max(1, cx.num_cus * env_int("LLMRS_GEMV_WG_PER_CU", 4));
     m->cap = c.max_seq + 1;
     int splits = (c.max_seq + 63) / 64;
     splits = std::min(splits, std::max(1, 2 * cx.num_cus / nkv));
     m->nsplit = std::max(1, env_int("LLMRS_ATTN_SPLITS", splits));
-    m->lm_grid = (int)std::min<size_t>(((size_t)c.vocab + 15) / 16, (size_t)m->gemv_wgs);
+    m->lm_grid = (int)gemv_plan(m->wt, "norm_argmax", c.vocab, H, cx.num_cus).grid;
     m->layers.resize(c.n_layers);
     for (auto& L : m->layers) {
       m->alloc_linear(L.qkv, m->qkv_rows, H);
@@ -412,9 +408,11 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     }
     LLMRS_HIP(hipStreamSynchronize(cx.stream));
     // Resolve every kernel of the step now, so graph capture never has to.
-    const std::string tag = wt_tag(m->wt);
-    for (const char* suffix : {"_norm_store", "_q8_resid", "_norm_silu", "_norm_argmax"})
-      (void)kernel("gemv_" + tag + suffix);
+    (void)kernel(gemv_plan(m->wt, "norm_store", m->qkv_rows, H, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, "q8_resid", H, nq * hd, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, "norm_silu", 2 * F, H, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, "q8_resid", H, F, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, "norm_argmax", c.vocab, H, cx.num_cus).name);
     (void)kernel("embed_gather");
     (void)kernel("argmax_final");
     (void)kernel(std::string("attn_decode_hd") + std::to_string(hd) +

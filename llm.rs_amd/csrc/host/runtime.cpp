@@ -3,6 +3,7 @@
 #include <immintrin.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <filesystem>
 #include <functional>
@@ -60,6 +61,39 @@ const char* wt_tag(int wt) {
     case WT_Q8H: return "q8h";
   }
   fail(LLMRS_E_DTYPE, "unknown weight type");
+}
+
+// Rows per wave-unit R and 64-block chunks per unit U follow the shape: U = 2
+// when the row splits into whole 128-block chunks, R = 2 for the narrow
+// (n <= 8192) projections so that more waves share them.  The SwiGLU tile is
+// 64 rows per workgroup; other kinds deal R-row groups to waves, capped at
+// LLMRS_GEMV_WG_PER_CU (default 4) workgroups per CU, beyond which waves loop.
+GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
+  const int nb = k / 32;
+  int U = (nb % 128 == 0) ? 2 : 1;
+  const char* eu = std::getenv("LLMRS_GEMV_U");
+  if (eu && (std::atoi(eu) == 1 || std::atoi(eu) == 2)) U = std::atoi(eu);
+  int R = 4;
+  if (kind == "norm_store" || kind == "q8_resid") {
+    R = n <= 8192 ? 2 : 4;
+    const char* er = std::getenv("LLMRS_GEMV_R");
+    if (er && (std::atoi(er) == 2 || std::atoi(er) == 4)) R = std::atoi(er);
+  }
+  const char* ew = std::getenv("LLMRS_GEMV_WG_PER_CU");
+  const long cap = (long)std::max(1, num_cus) * std::max(1, ew && *ew ? std::atoi(ew) : 4);
+  GemvPlan p;
+  p.name = std::string("gemv_") + wt_tag(wt) + "_" + kind + "_r" + std::to_string(R) + "u" +
+           std::to_string(U);
+  long wgs;
+  if (kind == "norm_silu") {
+    wgs = (n + 63) / 64;
+  } else {
+    const long nrg = (n + R - 1) / R;
+    wgs = (nrg + 3) / 4;
+  }
+  p.grid = (unsigned)std::max<long>(1, std::min(wgs, cap));
+  p.lds = (size_t)k + 8 * (size_t)nb;
+  return p;
 }
 
 // ---- allocator -------------------------------------------------------------

@@ -201,11 +201,9 @@ int llmrs_matmul_transposed(const llmrs_tensor* a, const llmrs_tensor* b, llmrs_
       g.k = (int)k;
       g.x = (const float*)a->data;
       g.y = (float*)o->data;
-      const unsigned tiles = (unsigned)((n + 15) / 16);
-      const unsigned grid = std::min<unsigned>(tiles, (unsigned)ctx().num_cus * 4);
-      const size_t lds = k + 8 * (k / 32);
-      launch(std::string("gemv_") + wt_tag(b->wt) + "_quant_store", dim3(grid, (unsigned)m),
-             dim3(kBlock), lds, ctx().stream, g);
+      LLMRS_REQUIRE(k <= 32768, LLMRS_E_INVALID, "matmul_transposed: k is limited to 32768");
+      const GemvPlan p = gemv_plan(b->wt, "quant_store", (int)n, (int)k, ctx().num_cus);
+      launch(p.name, dim3(p.grid, (unsigned)m), dim3(kBlock), p.lds, ctx().stream, g);
     }
     *out = o.release();
   });

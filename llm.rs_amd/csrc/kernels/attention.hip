@@ -5,16 +5,23 @@
 // pos (layer.rs:219-246), scores = q.K_t * (1/sqrt(hd)) (layer.rs:257-258),
 // softmax (cpu.rs:395-423), ctx = sum_t p_t V_t (layer.rs:276-299).
 //
-// MI355X design: one workgroup per (KV head, sequence split).  The group's
-// n_rep query heads share every K/V tile (true GQA: the reference instead
-// duplicates K/V rows per query head, loader.rs:62-98, which gives the same
-// numbers).  K/V tiles of 64 positions are staged through LDS with 16-byte
-// loads; each lane owns one position for the q.K dot (sequential over d, as
-// the reference's dot is) and two head dimensions for P.V; softmax is online
-// (running max and sum).  The workgroup owning position `pos` rotates the
-// new k and appends k and v to the cache.  Partials (m, l, acc) go to global
-// memory; the last workgroup of a KV head (atomic ticket) combines them and
-// writes ctx as f32 and as Q8_0 codes for the O projection.
+// MI355X design: one workgroup per (KV head, sequence split), 4 waves.  The
+// group's n_rep query heads share every K/V tile (true GQA: the reference
+// instead duplicates K/V rows per query head, loader.rs:62-98, which gives
+// the same numbers).  A split is a run of whole 64-position tiles.  Per tile:
+//  - the K and V rows are requested with 16-byte loads for the whole tile at
+//    once (and the next tile's loads are issued before this tile is used),
+//    then staged through LDS, K rows padded so lane-per-position reads are
+//    conflict-free;
+//  - wave w owns query heads w, w+4: lane p forms the score of position p
+//    (q broadcast from LDS, f32 accumulate of f32 q times the stored K);
+//  - softmax is online per head (running max and sum, DPP wave reductions);
+//  - for P.V lane l owns head dims 2l, 2l+1 (HD=128) or l (HD=64); the
+//    probabilities are broadcast from the lane that holds them.
+// The workgroup owning position `pos` rotates the new k and appends k and v
+// to the cache.  Partials (m, l, acc) go to global memory; the last
+// workgroup of a KV head (atomic ticket after a device-scope fence) combines
+// them and writes ctx as f32 and as Q8_0 codes for the O projection.
 //
 // RoPE uses cos/sin tables [max_seq][hd/2] computed on the host with the
 // reference's own f32 formula and glibc, so rotation is bit-exact.
@@ -23,6 +30,8 @@
 
 using namespace llmrs;
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <bool KV16>
 struct KvType;
@@ -42,19 +51,29 @@ __device__ __forceinline__ float kv_to_f(typename KvType<KV16>::T v) {
 }
 
 template <int HD, bool KV16>
-__device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
+struct AttnCfg {
   typedef typename KvType<KV16>::T kv_t;
-  constexpr int TILE = (HD == 128 && !KV16) ? 32 : 64;
-  constexpr int KP = HD + 1;  // padded K rows: lane-per-position reads are conflict-free
-  constexpr int MID = HD / 2;
-  constexpr int DPL = HD / LLMRS_WAVE;  // head dims per lane in P.V
-  constexpr int MAXREP = 8;             // query heads per KV head supported
-  constexpr int SLOTS = MAXREP / 4;     // heads per wave
+  static constexpr int TILE = KV16 ? 64 : 32;            // positions per tile
+  static constexpr int EPC = 16 / (int)sizeof(kv_t);      // elements per 16 B
+  static constexpr int CPR = HD / EPC;                    // 16 B chunks per row
+  static constexpr int CHUNKS = TILE * CPR;               // per tile, K or V
+  static constexpr int CPT = CHUNKS / 256;                // chunks per thread
+  static constexpr int KSTRIDE = HD + (KV16 ? 2 : 1);     // padded K row (elements)
+  static constexpr int MAXREP = 8;                        // query heads per KV head
+  static constexpr int HPW = MAXREP / 4;                  // heads per wave
+  static constexpr int DPL = HD / LLMRS_WAVE;             // head dims per lane in P.V
+  static_assert(CHUNKS % 256 == 0, "tile must split evenly over 256 threads");
+};
 
-  __shared__ float s_q[MAXREP][HD];
-  __shared__ float s_k[TILE][KP];
-  __shared__ kv_t s_v[TILE][HD];
-  __shared__ float s_p[4][LLMRS_WAVE];
+template <int HD, bool KV16>
+__device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
+  typedef AttnCfg<HD, KV16> C;
+  typedef typename C::kv_t kv_t;
+  constexpr int TILE = C::TILE, MID = HD / 2, HPW = C::HPW, DPL = C::DPL;
+
+  __shared__ __align__(16) float s_q[C::MAXREP][HD];
+  __shared__ __align__(16) kv_t s_k[TILE * C::KSTRIDE];
+  __shared__ __align__(16) kv_t s_v[TILE * HD];
   __shared__ float s_new[2][HD];
   __shared__ int s_ticket;
 
@@ -63,14 +82,30 @@ __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
   const int pos = *a.pos_ptr;
   const int T = pos + 1;
   const int n_rep = a.nq / a.nkv;
-  const int chunk = (T + a.nsplit - 1) / a.nsplit;
-  const int start = split * chunk;
-  const int end = min(T, start + chunk);
+  // Splits are runs of whole tiles.
+  const int ntile = (T + TILE - 1) / TILE;
+  const int tps = (ntile + a.nsplit - 1) / a.nsplit;
+  const int start = min(T, split * tps * TILE);
+  const int end = min(T, start + tps * TILE);
   const int qdim = a.nq * HD;
   const float* rc = a.rope_cos + (size_t)pos * MID;
   const float* rs = a.rope_sin + (size_t)pos * MID;
   kv_t* kc = (kv_t*)a.kc + (size_t)g * a.max_seq * HD;
   kv_t* vc = (kv_t*)a.vc + (size_t)g * a.max_seq * HD;
+
+  // Tile loader: chunk c of the tile = row c / CPR, columns (c % CPR) * EPC.
+  u32x4 pk[C::CPT], pv[C::CPT];
+  auto issue = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < C::CPT; ++i) {
+      const int c = tid + 256 * i;
+      const int t = min(t0 + c / C::CPR, T - 1);  // clamped: rows past `end` are masked
+      const int col = (c % C::CPR) * C::EPC;
+      pk[i] = *(const u32x4*)(kc + (size_t)t * HD + col);
+      pv[i] = *(const u32x4*)(vc + (size_t)t * HD + col);
+    }
+  };
+  if (start < end) issue(start);
 
   // Rotated query heads of this group (cpu.rs:351-354).
   for (int i = tid; i < n_rep * MID; i += blockDim.x) {
@@ -81,6 +116,8 @@ __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
     s_q[hr][j + MID] = re * s + im * c;
   }
   // The owner of position pos rotates k and appends k, v (layer.rs:219-246).
+  // It keeps the stored values in s_new: its own tile loads may have been
+  // issued before these stores.
   const bool owner = pos >= start && pos < end;
   if (owner) {
     const float* kr = a.qkv + qdim + (size_t)g * HD;
@@ -114,9 +151,9 @@ __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
     }
   }
 
-  float m[SLOTS], l[SLOTS], acc[SLOTS][DPL];
+  float m[HPW], l[HPW], acc[HPW][DPL];
 #pragma unroll
-  for (int j = 0; j < SLOTS; ++j) {
+  for (int j = 0; j < HPW; ++j) {
     m[j] = -INFINITY;
     l[j] = 0.0f;
 #pragma unroll
@@ -124,86 +161,100 @@ __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
   }
 
   for (int t0 = start; t0 < end; t0 += TILE) {
-    __syncthreads();  // previous tile fully consumed; s_q / s_new written
-    // Stage K (as f32) and V (as stored) rows [t0, t0+TILE) with 16-byte loads.
-    constexpr int EPC = 16 / sizeof(kv_t);  // elements per 16-byte chunk
-    constexpr int CPR = HD / EPC;           // chunks per row
-    for (int c = tid; c < TILE * CPR; c += blockDim.x) {
-      const int r = c / CPR, col = (c % CPR) * EPC;
-      const int t = t0 + r;
-      float kf[EPC];
-      kv_t vv[EPC];
-      // Rows past `end` are zero-filled: they belong to the next split
-      // (possibly the owner of pos, whose s_new this workgroup never wrote)
-      // and a 0 * NaN from stale LDS would poison P.V.
-      if (t < end && t != pos) {
-        const uint4 kraw = *(const uint4*)(kc + (size_t)t * HD + col);
-        const uint4 vraw = *(const uint4*)(vc + (size_t)t * HD + col);
-        const kv_t* kp = (const kv_t*)&kraw;
-        const kv_t* vp = (const kv_t*)&vraw;
+    __syncthreads();  // previous tile consumed; s_q / s_new written
+    // Stage the tile (already loaded into registers) into LDS: V rows with
+    // 16-byte stores, padded K rows with 4-byte stores.
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) {
-          kf[e] = kv_to_f<KV16>(kp[e]);
-          vv[e] = vp[e];
-        }
-      } else if (t < end) {  // t == pos: this workgroup is the owner
+    for (int i = 0; i < C::CPT; ++i) {
+      const int c = tid + 256 * i;
+      const int r = c / C::CPR, col = (c % C::CPR) * C::EPC;
+      u32x4 kw = pk[i], vw = pv[i];
+      if (t0 + r == pos) {  // owner only: the row it just wrote
+        kv_t* kp = (kv_t*)&kw;
+        kv_t* vp = (kv_t*)&vw;
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) {
-          kf[e] = s_new[0][col + e];
-          if constexpr (KV16) vv[e] = f2h(s_new[1][col + e]);
-          else vv[e] = s_new[1][col + e];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) {
-          kf[e] = 0.0f;
-          vv[e] = (kv_t)0;
+        for (int e = 0; e < C::EPC; ++e) {
+          if constexpr (KV16) {
+            kp[e] = f2h(s_new[0][col + e]);
+            vp[e] = f2h(s_new[1][col + e]);
+          } else {
+            kp[e] = s_new[0][col + e];
+            vp[e] = s_new[1][col + e];
+          }
         }
       }
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) {
-        s_k[r][col + e] = kf[e];
-        s_v[r][col + e] = vv[e];
-      }
+      unsigned* kd = (unsigned*)(s_k + r * C::KSTRIDE + col);
+      kd[0] = kw.x;
+      kd[1] = kw.y;
+      kd[2] = kw.z;
+      kd[3] = kw.w;
+      *(u32x4*)(s_v + r * HD + col) = vw;
     }
+    if (t0 + TILE < end) issue(t0 + TILE);  // next tile in flight during this one
     __syncthreads();
 
+    const int tvalid = min(TILE, end - t0);
 #pragma unroll
-    for (int j = 0; j < SLOTS; ++j) {
-      const int hr = 4 * j + wave;
-      const bool active = hr < n_rep;
+    for (int j = 0; j < HPW; ++j) {
+      const int hr = wave + 4 * j;
+      if (hr >= n_rep) continue;  // uniform per wave
+      // Score of position t0 + lane (sequential over d, as cpu.rs:548).
       float sc = -INFINITY;
-      const int t = t0 + lane;
-      if (active && lane < TILE && t < end) {
+      if (lane < tvalid) {
         float s = 0.0f;
-        for (int d = 0; d < HD; ++d) s = s + s_q[hr][d] * s_k[lane][d];  // cpu.rs:548
+        // 32-bit LDS reads of the padded row: bank (lane*KSTRIDE/2 + i) mod 64
+        // differs across lanes, so the reads are conflict-free.
+        const unsigned* krow = (const unsigned*)(s_k + lane * C::KSTRIDE);
+#pragma unroll 8
+        for (int d = 0; d < HD; d += 4) {
+          const f32x4 q4 = *(const f32x4*)&s_q[hr][d];
+          float k0, k1, k2, k3;
+          if constexpr (KV16) {
+            const unsigned w0 = krow[d / 2], w1 = krow[d / 2 + 1];
+            k0 = h2f((uint16_t)(w0 & 0xFFFF));
+            k1 = h2f((uint16_t)(w0 >> 16));
+            k2 = h2f((uint16_t)(w1 & 0xFFFF));
+            k3 = h2f((uint16_t)(w1 >> 16));
+          } else {
+            k0 = __uint_as_float(krow[d]);
+            k1 = __uint_as_float(krow[d + 1]);
+            k2 = __uint_as_float(krow[d + 2]);
+            k3 = __uint_as_float(krow[d + 3]);
+          }
+          s = __builtin_fmaf(q4.x, k0, s);
+          s = __builtin_fmaf(q4.y, k1, s);
+          s = __builtin_fmaf(q4.z, k2, s);
+          s = __builtin_fmaf(q4.w, k3, s);
+        }
         sc = s * a.scale;
       }
-      const float tmax = group_max(sc);
-      const float mnew = fmaxf(m[j], tmax);
+      const float mnew = fmaxf(m[j], wave_max(sc));
       const float p = (sc == -INFINITY) ? 0.0f : expf(sc - mnew);
       const float corr = (m[j] == -INFINITY) ? 0.0f : expf(m[j] - mnew);
-      l[j] = l[j] * corr + group_sum(p);
+      l[j] = l[j] * corr + wave_sum(p);
       m[j] = mnew;
-      s_p[wave][lane] = p;
-      __syncthreads();
-      if (active) {
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) {
-          const int d = lane + LLMRS_WAVE * e;
-          float o = acc[j][e] * corr;
-          for (int u = 0; u < TILE; ++u) o = o + s_p[wave][u] * kv_to_f<KV16>(s_v[u][d]);
-          acc[j][e] = o;
+      for (int e = 0; e < DPL; ++e) acc[j][e] = acc[j][e] * corr;
+      for (int u = 0; u < tvalid; ++u) {
+        const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), u));
+        const kv_t* vrow = s_v + u * HD + DPL * lane;
+        if constexpr (KV16 && DPL == 2) {
+          const unsigned w = *(const unsigned*)vrow;
+          acc[j][0] = __builtin_fmaf(pu, h2f((uint16_t)(w & 0xFFFF)), acc[j][0]);
+          acc[j][1] = __builtin_fmaf(pu, h2f((uint16_t)(w >> 16)), acc[j][1]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < DPL; ++e)
+            acc[j][e] = __builtin_fmaf(pu, kv_to_f<KV16>(vrow[e]), acc[j][e]);
         }
       }
-      __syncthreads();
     }
   }
 
   // Partials of this split.
 #pragma unroll
-  for (int j = 0; j < SLOTS; ++j) {
-    const int hr = 4 * j + wave;
+  for (int j = 0; j < HPW; ++j) {
+    const int hr = wave + 4 * j;
     if (hr < n_rep) {
       const int h = g * n_rep + hr;
       const size_t idx = (size_t)h * a.nsplit + split;
@@ -212,7 +263,7 @@ __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
         a.part_ml[2 * idx + 1] = l[j];
       }
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) a.part_o[idx * HD + lane + LLMRS_WAVE * e] = acc[j][e];
+      for (int e = 0; e < DPL; ++e) a.part_o[idx * HD + DPL * lane + e] = acc[j][e];
     }
   }
   __threadfence();
@@ -224,8 +275,8 @@ __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
 
   // Last workgroup of this KV head: combine the splits.
 #pragma unroll
-  for (int j = 0; j < SLOTS; ++j) {
-    const int hr = 4 * j + wave;
+  for (int j = 0; j < HPW; ++j) {
+    const int hr = wave + 4 * j;
     if (hr >= n_rep) continue;
     const int h = g * n_rep + hr;
     const size_t base = (size_t)h * a.nsplit;
@@ -241,18 +292,28 @@ __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
       L = L + __builtin_nontemporal_load(&a.part_ml[2 * (base + s) + 1]) * w;
 #pragma unroll
       for (int e = 0; e < DPL; ++e)
-        o[e] = o[e] + __builtin_nontemporal_load(&a.part_o[(base + s) * HD + lane + LLMRS_WAVE * e]) * w;
+        o[e] = o[e] + __builtin_nontemporal_load(&a.part_o[(base + s) * HD + DPL * lane + e]) * w;
     }
+    // ctx as f32 and as Q8_0 (32-dim blocks: 16 lanes x 2 dims, or 32 lanes x 1).
+    constexpr int LPB = 32 / DPL;  // lanes per Q8 block
+    float amax = 0.0f;
+    float v[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; ++e) {
-      const int d = lane + LLMRS_WAVE * e;
-      const float v = o[e] / L;
-      a.ctx[(size_t)h * HD + d] = v;
-      float dq;
-      const int q = q8_group32(v, &dq);  // lanes 0-31 / 32-63 hold one 32-block each
-      a.ctx_q[(size_t)h * HD + d] = (int8_t)q;
-      if ((lane & 31) == 0) a.ctx_d[((size_t)h * HD + d) / 32] = dq;
+      v[e] = o[e] / L;
+      amax = fmaxf(amax, fabsf(v[e]));
     }
+#pragma unroll
+    for (int off = LPB / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, LPB));
+    const float d = amax / 127.0f;
+    const float inv = amax == 0.0f ? 0.0f : 1.0f / d;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      const int dd = DPL * lane + e;
+      a.ctx[(size_t)h * HD + dd] = v[e];
+      a.ctx_q[(size_t)h * HD + dd] = amax == 0.0f ? (int8_t)0 : (int8_t)q8_code(v[e], inv);
+    }
+    if ((lane % LPB) == 0) a.ctx_d[((size_t)h * HD + DPL * lane) / 32] = amax == 0.0f ? 0.0f : d;
   }
   if (tid == 0) a.counters[g] = 0;
 }

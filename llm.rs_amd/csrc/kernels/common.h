@@ -35,6 +35,37 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// Wave64 sum with DPP row operations (quad_perm, half-row mirror, row
+// mirror) and the four row totals added in lane order 0, 16, 32, 48.  The
+// result is uniform across the wave; the summation order is fixed, so equal
+// inputs give bit-equal sums.
+template <int CTRL>
+__device__ __forceinline__ float dpp_c(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = v + dpp_c<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = v + dpp_c<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = v + dpp_c<0x141>(v);  // row_half_mirror
+  v = v + dpp_c<0x140>(v);  // row_mirror: every lane holds its row's sum
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return ((r0 + r1) + r2) + r3;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_c<0xB1>(v));
+  v = fmaxf(v, dpp_c<0x4E>(v));
+  v = fmaxf(v, dpp_c<0x141>(v));
+  v = fmaxf(v, dpp_c<0x140>(v));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) {
   return __half2float(__ushort_as_half(h));
 }
