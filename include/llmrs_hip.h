@@ -216,6 +216,13 @@ int llmrs_model_tokens(llmrs_model* m, int32_t* out, size_t count);
  * launch.  Returns the number of launches recorded (>= 0) or an error. */
 int llmrs_model_profile_step(llmrs_model* m, char* names, float* ms,
                              double* bytes, int cap);
+/* Phase timing of the persistent decode kernel: runs `n_steps` more decode
+ * steps in one launch and returns in `us` (up to `cap` values): the launch
+ * wall time per step, then for each layer of the first step ten intervals
+ * seen by workgroup 0 - QKV work, barrier wait, attention work, wait, O work,
+ * wait, gate|up work, wait, down work, wait (layer 0's QKV interval is 0).
+ * Returns the number of values written or an error. */
+int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int cap);
 /* Algorithmic weight bytes streamed per decode token (all linear weights). */
 double llmrs_model_weight_bytes(const llmrs_model* m);
 

@@ -105,6 +105,8 @@ struct GemvPlan {
   size_t lds = 0;
 };
 GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus);
+// LDS bytes of a GEMV's activation area (codes, scales, Q4 offsets) for input length k.
+inline size_t gemv_act_lds_host(int k) { return (size_t)k + 8 * (size_t)(k / 32); }
 
 // Bytes of codes per 32-element block.
 inline int block_code_bytes(int wt) { return wt == WT_Q8H ? 32 : 16; }

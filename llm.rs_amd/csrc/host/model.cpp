@@ -72,6 +72,14 @@ struct llmrs_model {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   bool graph_failed = false;
+  // persistent decode kernel (decode.hip)
+  LayerDesc* layer_desc = nullptr;   // device copy of the per-layer pointers
+  unsigned* bar = nullptr;           // grid barrier words
+  int* bar_err = nullptr;
+  std::string pk_name;
+  unsigned pk_grid = 0;              // 0: persistent path unavailable
+  size_t pk_lds = 0;
+  int host_n_prompt = 0;
   std::vector<void*> allocs;
 
   template <class T>
@@ -252,6 +260,102 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
   L("argmax_final", 8.0 * m->lm_grid, dim3(1), dim3(256), 0, f);
 }
 
+// The persistent decode kernel for this model, its LDS and grid: as many
+// workgroups per CU as fit (at most 2), so a cooperative launch keeps all of
+// them resident.  Opt-in with LLMRS_PERSISTENT=1: measured on MI355X it is
+// still slower than the per-kernel graph path (each of its five phases per
+// layer pays device-scope load and barrier latency of several us).
+void plan_persistent(llmrs_model* m) {
+  const llmrs_model_config& c = m->c;
+  m->pk_grid = 0;
+  if (!env_int("LLMRS_PERSISTENT", 0)) return;
+  const int H = c.hidden, F = c.ffn, qd = c.n_heads * c.head_dim;
+  const int kmax = std::max(std::max(H, qd), F);
+  // U = 2 when the hidden size splits into 128-block chunks (Q8_0 weights
+  // keep U = 1: two units of 32-byte blocks do not fit the register budget).
+  int U = (m->wt != WT_Q8H && (H / 32) % 128 == 0) ? 2 : 1;
+  const int eu = env_int("LLMRS_PERSISTENT_U", 0);
+  if (eu == 1 || eu == 2) U = eu;
+  const bool kv16 = c.kv_dtype == LLMRS_F16;
+  m->pk_name = std::string("decode_") + wt_tag(m->wt) + "_hd" + std::to_string(c.head_dim) +
+               (kv16 ? "_f16" : "_f32") + "_u" + std::to_string(U);
+  m->pk_lds = std::max(gemv_act_lds_host(kmax), attn_lds_bytes(c.head_dim, kv16));
+  hipFunction_t f = kernel(m->pk_name);
+  int per_cu = 0;
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, m->pk_lds) != hipSuccess) {
+    (void)hipGetLastError();
+    return;
+  }
+  per_cu = std::min(per_cu, std::max(1, env_int("LLMRS_PERSISTENT_WG_PER_CU", 2)));
+  if (per_cu < 1) return;
+  m->pk_grid = (unsigned)(ctx().num_cus * per_cu);
+}
+
+// One cooperative launch running positions [pos0, pos0 + n_steps).
+void run_persistent(llmrs_model* m, size_t pos0, size_t n_steps, bool want_logits,
+                    unsigned long long* ts = nullptr) {
+  const llmrs_model_config& c = m->c;
+  hipStream_t s = ctx().stream;
+  LLMRS_HIP(hipMemsetAsync(m->bar, 0, 1024 * sizeof(unsigned), s));
+  LLMRS_HIP(hipMemsetAsync(m->bar_err, 0, sizeof(int), s));
+  DecodeArgs d{};
+  d.layers = m->layer_desc;
+  d.embed = m->embed;
+  d.final_norm = m->final_norm;
+  d.lm_w = m->lm_head.codes;
+  d.lm_s = m->lm_head.scales;
+  d.rope_cos = m->rope_cos;
+  d.rope_sin = m->rope_sin;
+  d.x = m->x;
+  d.h = m->h;
+  d.qkv = m->qkv;
+  d.ctx = m->ctxv;
+  d.ctx_q = m->ctx_q;
+  d.ctx_d = m->ctx_d;
+  d.mf = m->mf;
+  d.m_q = m->m_q;
+  d.m_d = m->m_d;
+  d.logits = want_logits ? m->logits : nullptr;
+  d.part_o = m->part_o;
+  d.part_ml = m->part_ml;
+  d.counters = m->counters;
+  d.part_val = m->part_val;
+  d.part_idx = m->part_idx;
+  d.bar = m->bar;
+  d.tokens = m->tokens;
+  d.gen = m->gen;
+  d.tokens_out = m->tokens;
+  d.pos_out = m->pos;
+  d.err = m->bar_err;
+  d.ts = ts;
+  d.n_layers = c.n_layers;
+  d.hidden = c.hidden;
+  d.nq = c.n_heads;
+  d.nkv = c.n_kv_heads;
+  d.hd = c.head_dim;
+  d.ffn = c.ffn;
+  d.vocab = c.vocab;
+  d.max_seq = c.max_seq;
+  d.qkv_rows = m->qkv_rows;
+  d.pos0 = (int)pos0;
+  d.n_steps = (int)n_steps;
+  d.n_prompt = m->host_n_prompt;
+  d.cap = m->cap;
+  d.nsplit = m->nsplit;
+  d.eps = c.rms_eps;
+  d.attn_scale = 1.0f / std::sqrt((float)c.head_dim);  // layer.rs:258
+  void* params[] = {&d};
+  LLMRS_HIP(hipModuleLaunchCooperativeKernel(kernel(m->pk_name), m->pk_grid, 1, 1, 256, 1, 1,
+                                             (unsigned)m->pk_lds, s, params));
+}
+
+void check_barrier(llmrs_model* m) {
+  int e = 0;
+  LLMRS_HIP(hipMemcpyAsync(&e, m->bar_err, sizeof(int), hipMemcpyDeviceToHost, ctx().stream));
+  LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+  if (e) fail(LLMRS_E_HIP, "persistent decode: a grid barrier wait timed out");
+}
+
 void check_ready(const llmrs_model* m) {
   LLMRS_REQUIRE(m, LLMRS_E_INVALID, "null model");
   LLMRS_REQUIRE(m->embed_set && m->final_set && m->lm_set, LLMRS_E_INVALID,
@@ -388,8 +492,10 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     m->logits = m->dalloc<float>(c.vocab);
     m->part_o = m->dalloc<float>((size_t)nq * m->nsplit * hd);
     m->part_ml = m->dalloc<float>((size_t)nq * m->nsplit * 2);
-    m->part_val = m->dalloc<float>(m->lm_grid);
-    m->part_idx = m->dalloc<int>(m->lm_grid);
+    plan_persistent(m.get());
+    const size_t nparts = std::max<size_t>((size_t)m->lm_grid, m->pk_grid);
+    m->part_val = m->dalloc<float>(nparts);
+    m->part_idx = m->dalloc<int>(nparts);
     m->counters = m->dalloc<int>((size_t)c.n_layers * nkv);
     m->tokens = m->dalloc<int>(m->cap);
     m->gen = m->dalloc<int>(m->cap);
@@ -405,6 +511,19 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
       m->rope_sin = m->dalloc<float>(sn.size());
       LLMRS_HIP(hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, cx.stream));
       LLMRS_HIP(hipMemcpyAsync(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, cx.stream));
+    }
+    m->bar = m->dalloc<unsigned>(1024);
+    m->bar_err = m->dalloc<int>(1);
+    {  // per-layer pointers for the persistent kernel
+      std::vector<LayerDesc> ld(c.n_layers);
+      for (int l = 0; l < c.n_layers; ++l) {
+        const LayerBufs& B = m->layers[l];
+        ld[l] = LayerDesc{B.qkv.codes, B.qkv.scales, B.o.codes, B.o.scales, B.gu.codes, B.gu.scales,
+                          B.down.codes, B.down.scales, B.norm[0], B.norm[1], B.kc, B.vc};
+      }
+      m->layer_desc = m->dalloc<LayerDesc>(ld.size());
+      LLMRS_HIP(hipMemcpyAsync(m->layer_desc, ld.data(), ld.size() * sizeof(LayerDesc),
+                               hipMemcpyHostToDevice, cx.stream));
     }
     LLMRS_HIP(hipStreamSynchronize(cx.stream));
     // Resolve every kernel of the step now, so graph capture never has to.
@@ -649,9 +768,14 @@ int llmrs_model_begin(llmrs_model* m, const int32_t* prompt, size_t n_prompt) {
     LLMRS_REQUIRE(n_prompt <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "prompt longer than max_seq");
     upload_tokens(m, 0, prompt, n_prompt);
     set_state(m, 0, (int)n_prompt);
-    for (size_t p = 0; p < n_prompt; ++p) {
-      m->host_pos = p;
-      replay_step(m);
+    m->host_n_prompt = (int)n_prompt;
+    if (m->pk_grid) {
+      run_persistent(m, 0, n_prompt, false);
+    } else {
+      for (size_t p = 0; p < n_prompt; ++p) {
+        m->host_pos = p;
+        replay_step(m);
+      }
     }
     m->host_pos = n_prompt;
     m->begun = true;
@@ -662,6 +786,11 @@ int llmrs_model_decode_steps(llmrs_model* m, size_t n) {
   return guard([&] {
     LLMRS_REQUIRE(m && m->begun, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
     LLMRS_REQUIRE(m->host_pos + n <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
+    if (m->pk_grid) {
+      if (n) run_persistent(m, m->host_pos, n, false);
+      m->host_pos += n;
+      return;
+    }
     for (size_t i = 0; i < n; ++i) {
       replay_step(m);
       m->host_pos += 1;
@@ -676,6 +805,7 @@ int llmrs_model_tokens(llmrs_model* m, int32_t* out, size_t count) {
     LLMRS_HIP(hipMemcpyAsync(out, m->tokens, count * sizeof(int32_t), hipMemcpyDeviceToHost, ctx().stream));
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));
     check_err(m);
+    check_barrier(m);
   });
 }
 
@@ -725,6 +855,48 @@ int llmrs_model_profile_step(llmrs_model* m, char* names, float* ms, double* byt
       }
       (void)hipEventDestroy(std::get<2>(r));
       (void)hipEventDestroy(std::get<3>(r));
+    }
+  });
+  return rc ? rc : count;
+}
+
+int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int cap) {
+  int count = 0;
+  int rc = guard([&] {
+    LLMRS_REQUIRE(m && m->begun && us, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
+    LLMRS_REQUIRE(m->pk_grid, LLMRS_E_INVALID, "the persistent decode kernel is not in use");
+    LLMRS_REQUIRE(n_steps >= 1 && m->host_pos + n_steps <= (size_t)m->c.max_seq, LLMRS_E_RANGE,
+                  "decode beyond max_seq");
+    const size_t nts = (size_t)m->c.n_layers * 10;
+    unsigned long long* ts = nullptr;
+    LLMRS_HIP(hipMalloc(&ts, nts * sizeof(unsigned long long)));
+    hipEvent_t e0, e1;
+    LLMRS_HIP(hipEventCreate(&e0));
+    LLMRS_HIP(hipEventCreate(&e1));
+    LLMRS_HIP(hipEventRecord(e0, ctx().stream));
+    run_persistent(m, m->host_pos, n_steps, false, ts);
+    LLMRS_HIP(hipEventRecord(e1, ctx().stream));
+    std::vector<unsigned long long> h(nts);
+    LLMRS_HIP(hipMemcpyAsync(h.data(), ts, nts * sizeof(unsigned long long), hipMemcpyDeviceToHost,
+                             ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    float total_ms = 0.0f;
+    (void)hipEventElapsedTime(&total_ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipFree(ts);
+    m->host_pos += n_steps;
+    check_barrier(m);
+    // us[0] = launch wall time per step; then per layer 10 intervals (100 MHz ticks -> us):
+    // QKV work, wait, ATTN work, wait, O work, wait, GU work, wait, DOWN work, wait.
+    if (cap > 0) us[count++] = total_ms * 1e3 / (double)n_steps;
+    for (int l = 0; l < m->c.n_layers; ++l) {
+      const unsigned long long* t = h.data() + (size_t)l * 10;
+      const unsigned long long prev = l == 0 ? t[0] : h[(size_t)(l - 1) * 10 + 9];
+      for (int i = 0; i < 10 && count < cap; ++i) {
+        const unsigned long long a = i == 0 ? prev : t[i - 1];
+        us[count++] = (double)(t[i] - a) / 100.0;
+      }
     }
   });
   return rc ? rc : count;

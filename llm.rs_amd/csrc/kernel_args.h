@@ -5,6 +5,7 @@
 // Plain C structs: pointers, int32, float - identical layout on x86-64 and
 // amdgcn.
 #pragma once
+#include <stddef.h>
 #include <stdint.h>
 
 namespace llmrs {
@@ -96,6 +97,69 @@ struct EmbedArgs {
   float* x;             // [hidden]
   int* err;             // set to 1 on an out-of-range id
   int hidden, vocab;
+};
+
+// LDS bytes of one decode-attention work item (attn_core.h: query heads,
+// padded K tile, V tile, the new row, the ticket).  Tiles are 64 positions
+// for an f16 cache and 32 for f32; at most 8 query heads per KV head.
+constexpr size_t attn_lds_bytes(int hd, bool kv16) {
+  const size_t es = kv16 ? 2 : 4, tile = kv16 ? 64 : 32, kstride = (size_t)hd + (kv16 ? 2 : 1);
+  const size_t k = 4 * 8 * (size_t)hd;
+  const size_t v = k + (es * tile * kstride + 15) / 16 * 16;
+  const size_t nw = v + es * tile * (size_t)hd;
+  return nw + 4 * 2 * (size_t)hd + 16;
+}
+
+// Persistent decode kernel (decode.hip): the per-layer weights and caches.
+struct LayerDesc {
+  const uint8_t* qkv_w;
+  const void* qkv_s;
+  const uint8_t* o_w;
+  const void* o_s;
+  const uint8_t* gu_w;
+  const void* gu_s;
+  const uint8_t* down_w;
+  const void* down_s;
+  const float* norm_in;
+  const float* norm_post;
+  void* kc;
+  void* vc;
+};
+
+struct DecodeArgs {
+  const LayerDesc* layers;   // [n_layers], device memory
+  const float* embed;        // [vocab][hidden]
+  const float* final_norm;   // [hidden]
+  const uint8_t* lm_w;
+  const void* lm_s;
+  const float* rope_cos;     // [max_seq][hd/2]
+  const float* rope_sin;
+  // activations, exchanged between workgroups with device-scope loads/stores
+  float* x;
+  float* h;
+  float* qkv;
+  float* ctx;
+  int8_t* ctx_q;
+  float* ctx_d;
+  float* mf;
+  int8_t* m_q;
+  float* m_d;
+  float* logits;             // [vocab] of the last step, or null
+  float* part_o;             // attention partials [nq][nsplit][hd]
+  float* part_ml;            // [nq][nsplit][2]
+  int* counters;             // [n_layers][nkv] attention tickets, zero between uses
+  float* part_val;           // [grid] lm_head argmax partials
+  int* part_idx;
+  unsigned* bar;             // grid barrier words, zero at launch
+  const int* tokens;         // [cap] prompt ids (host-written)
+  int* gen;                  // [cap] argmax produced at position p, stored at p+1
+  int* tokens_out;           // [cap] generated ids stored at p+1 once past the prompt
+  int* pos_out;              // position after the launch
+  int* err;                  // non-zero: a barrier wait exceeded its spin limit
+  unsigned long long* ts;    // optional phase timestamps of workgroup 0 (100 MHz clock)
+  int n_layers, hidden, nq, nkv, hd, ffn, vocab, max_seq, qkv_rows;
+  int pos0, n_steps, n_prompt, cap, nsplit;
+  float eps, attn_scale;
 };
 
 }  // namespace llmrs

@@ -1,321 +1,16 @@
-// attention.hip - batch-1 decode attention over the KV cache for gfx950.
+// attention.hip - standalone batch-1 decode attention kernels for gfx950.
 //
-// Reference: LlamaAttention::forward, seq == 1 (layer.rs:175-299): per query
-// head, RoPE on q and k (layer.rs:216-217, cpu.rs:326-357), K/V append at
-// pos (layer.rs:219-246), scores = q.K_t * (1/sqrt(hd)) (layer.rs:257-258),
-// softmax (cpu.rs:395-423), ctx = sum_t p_t V_t (layer.rs:276-299).
-//
-// MI355X design: one workgroup per (KV head, sequence split), 4 waves.  The
-// group's n_rep query heads share every K/V tile (true GQA: the reference
-// instead duplicates K/V rows per query head, loader.rs:62-98, which gives
-// the same numbers).  A split is a run of whole 64-position tiles.  Per tile:
-//  - the K and V rows are requested with 16-byte loads for the whole tile at
-//    once (and the next tile's loads are issued before this tile is used),
-//    then staged through LDS, K rows padded so lane-per-position reads are
-//    conflict-free;
-//  - wave w owns query heads w, w+4: lane p forms the score of position p
-//    (q broadcast from LDS, f32 accumulate of f32 q times the stored K);
-//  - softmax is online per head (running max and sum, DPP wave reductions);
-//  - for P.V lane l owns head dims 2l, 2l+1 (HD=128) or l (HD=64); the
-//    probabilities are broadcast from the lane that holds them.
-// The workgroup owning position `pos` rotates the new k and appends k and v
-// to the cache.  Partials (m, l, acc) go to global memory; the last
-// workgroup of a KV head (atomic ticket after a device-scope fence) combines
-// them and writes ctx as f32 and as Q8_0 codes for the O projection.
-//
-// RoPE uses cos/sin tables [max_seq][hd/2] computed on the host with the
-// reference's own f32 formula and glibc, so rotation is bit-exact.
-#include "common.h"
-#include "../kernel_args.h"
+// One launch per layer: grid (nsplit, nkv), one work item of attn_core.h
+// (which documents the algorithm) per workgroup.  Reference:
+// LlamaAttention::forward with seq == 1 (layer.rs:175-299).
+#include "attn_core.h"
 
 using namespace llmrs;
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-template <bool KV16>
-struct KvType;
-template <>
-struct KvType<true> {
-  typedef uint16_t T;
-};
-template <>
-struct KvType<false> {
-  typedef float T;
-};
-
-template <bool KV16>
-__device__ __forceinline__ float kv_to_f(typename KvType<KV16>::T v) {
-  if constexpr (KV16) return h2f(v);
-  else return v;
-}
-
-template <int HD, bool KV16>
-struct AttnCfg {
-  typedef typename KvType<KV16>::T kv_t;
-  static constexpr int TILE = KV16 ? 64 : 32;            // positions per tile
-  static constexpr int EPC = 16 / (int)sizeof(kv_t);      // elements per 16 B
-  static constexpr int CPR = HD / EPC;                    // 16 B chunks per row
-  static constexpr int CHUNKS = TILE * CPR;               // per tile, K or V
-  static constexpr int CPT = CHUNKS / 256;                // chunks per thread
-  static constexpr int KSTRIDE = HD + (KV16 ? 2 : 1);     // padded K row (elements)
-  static constexpr int MAXREP = 8;                        // query heads per KV head
-  static constexpr int HPW = MAXREP / 4;                  // heads per wave
-  static constexpr int DPL = HD / LLMRS_WAVE;             // head dims per lane in P.V
-  static_assert(CHUNKS % 256 == 0, "tile must split evenly over 256 threads");
-};
-
 template <int HD, bool KV16>
 __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
-  typedef AttnCfg<HD, KV16> C;
-  typedef typename C::kv_t kv_t;
-  constexpr int TILE = C::TILE, MID = HD / 2, HPW = C::HPW, DPL = C::DPL;
-
-  __shared__ __align__(16) float s_q[C::MAXREP][HD];
-  __shared__ __align__(16) kv_t s_k[TILE * C::KSTRIDE];
-  __shared__ __align__(16) kv_t s_v[TILE * HD];
-  __shared__ float s_new[2][HD];
-  __shared__ int s_ticket;
-
-  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
-  const int g = blockIdx.y, split = blockIdx.x;
-  const int pos = *a.pos_ptr;
-  const int T = pos + 1;
-  const int n_rep = a.nq / a.nkv;
-  // Splits are runs of whole tiles.
-  const int ntile = (T + TILE - 1) / TILE;
-  const int tps = (ntile + a.nsplit - 1) / a.nsplit;
-  const int start = min(T, split * tps * TILE);
-  const int end = min(T, start + tps * TILE);
-  const int qdim = a.nq * HD;
-  const float* rc = a.rope_cos + (size_t)pos * MID;
-  const float* rs = a.rope_sin + (size_t)pos * MID;
-  kv_t* kc = (kv_t*)a.kc + (size_t)g * a.max_seq * HD;
-  kv_t* vc = (kv_t*)a.vc + (size_t)g * a.max_seq * HD;
-
-  // Tile loader: chunk c of the tile = row c / CPR, columns (c % CPR) * EPC.
-  u32x4 pk[C::CPT], pv[C::CPT];
-  auto issue = [&](int t0) {
-#pragma unroll
-    for (int i = 0; i < C::CPT; ++i) {
-      const int c = tid + 256 * i;
-      const int t = min(t0 + c / C::CPR, T - 1);  // clamped: rows past `end` are masked
-      const int col = (c % C::CPR) * C::EPC;
-      pk[i] = *(const u32x4*)(kc + (size_t)t * HD + col);
-      pv[i] = *(const u32x4*)(vc + (size_t)t * HD + col);
-    }
-  };
-  if (start < end) issue(start);
-
-  // Rotated query heads of this group (cpu.rs:351-354).
-  for (int i = tid; i < n_rep * MID; i += blockDim.x) {
-    const int hr = i / MID, j = i % MID;
-    const float* q = a.qkv + (size_t)(g * n_rep + hr) * HD;
-    const float re = q[j], im = q[j + MID], c = rc[j], s = rs[j];
-    s_q[hr][j] = re * c - im * s;
-    s_q[hr][j + MID] = re * s + im * c;
-  }
-  // The owner of position pos rotates k and appends k, v (layer.rs:219-246).
-  // It keeps the stored values in s_new: its own tile loads may have been
-  // issued before these stores.
-  const bool owner = pos >= start && pos < end;
-  if (owner) {
-    const float* kr = a.qkv + qdim + (size_t)g * HD;
-    const float* vr = a.qkv + qdim + (size_t)a.nkv * HD + (size_t)g * HD;
-    for (int j = tid; j < MID; j += blockDim.x) {
-      const float re = kr[j], im = kr[j + MID], c = rc[j], s = rs[j];
-      const float k0 = re * c - im * s, k1 = re * s + im * c;
-      if constexpr (KV16) {
-        const uint16_t h0 = f2h(k0), h1 = f2h(k1);
-        kc[(size_t)pos * HD + j] = h0;
-        kc[(size_t)pos * HD + j + MID] = h1;
-        s_new[0][j] = h2f(h0);
-        s_new[0][j + MID] = h2f(h1);
-      } else {
-        kc[(size_t)pos * HD + j] = k0;
-        kc[(size_t)pos * HD + j + MID] = k1;
-        s_new[0][j] = k0;
-        s_new[0][j + MID] = k1;
-      }
-    }
-    for (int d = tid; d < HD; d += blockDim.x) {
-      const float v = vr[d];
-      if constexpr (KV16) {
-        const uint16_t h = f2h(v);
-        vc[(size_t)pos * HD + d] = h;
-        s_new[1][d] = h2f(h);
-      } else {
-        vc[(size_t)pos * HD + d] = v;
-        s_new[1][d] = v;
-      }
-    }
-  }
-
-  float m[HPW], l[HPW], acc[HPW][DPL];
-#pragma unroll
-  for (int j = 0; j < HPW; ++j) {
-    m[j] = -INFINITY;
-    l[j] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[j][e] = 0.0f;
-  }
-
-  for (int t0 = start; t0 < end; t0 += TILE) {
-    __syncthreads();  // previous tile consumed; s_q / s_new written
-    // Stage the tile (already loaded into registers) into LDS: V rows with
-    // 16-byte stores, padded K rows with 4-byte stores.
-#pragma unroll
-    for (int i = 0; i < C::CPT; ++i) {
-      const int c = tid + 256 * i;
-      const int r = c / C::CPR, col = (c % C::CPR) * C::EPC;
-      u32x4 kw = pk[i], vw = pv[i];
-      if (t0 + r == pos) {  // owner only: the row it just wrote
-        kv_t* kp = (kv_t*)&kw;
-        kv_t* vp = (kv_t*)&vw;
-#pragma unroll
-        for (int e = 0; e < C::EPC; ++e) {
-          if constexpr (KV16) {
-            kp[e] = f2h(s_new[0][col + e]);
-            vp[e] = f2h(s_new[1][col + e]);
-          } else {
-            kp[e] = s_new[0][col + e];
-            vp[e] = s_new[1][col + e];
-          }
-        }
-      }
-      unsigned* kd = (unsigned*)(s_k + r * C::KSTRIDE + col);
-      kd[0] = kw.x;
-      kd[1] = kw.y;
-      kd[2] = kw.z;
-      kd[3] = kw.w;
-      *(u32x4*)(s_v + r * HD + col) = vw;
-    }
-    if (t0 + TILE < end) issue(t0 + TILE);  // next tile in flight during this one
-    __syncthreads();
-
-    const int tvalid = min(TILE, end - t0);
-#pragma unroll
-    for (int j = 0; j < HPW; ++j) {
-      const int hr = wave + 4 * j;
-      if (hr >= n_rep) continue;  // uniform per wave
-      // Score of position t0 + lane (sequential over d, as cpu.rs:548).
-      float sc = -INFINITY;
-      if (lane < tvalid) {
-        float s = 0.0f;
-        // 32-bit LDS reads of the padded row: bank (lane*KSTRIDE/2 + i) mod 64
-        // differs across lanes, so the reads are conflict-free.
-        const unsigned* krow = (const unsigned*)(s_k + lane * C::KSTRIDE);
-#pragma unroll 8
-        for (int d = 0; d < HD; d += 4) {
-          const f32x4 q4 = *(const f32x4*)&s_q[hr][d];
-          float k0, k1, k2, k3;
-          if constexpr (KV16) {
-            const unsigned w0 = krow[d / 2], w1 = krow[d / 2 + 1];
-            k0 = h2f((uint16_t)(w0 & 0xFFFF));
-            k1 = h2f((uint16_t)(w0 >> 16));
-            k2 = h2f((uint16_t)(w1 & 0xFFFF));
-            k3 = h2f((uint16_t)(w1 >> 16));
-          } else {
-            k0 = __uint_as_float(krow[d]);
-            k1 = __uint_as_float(krow[d + 1]);
-            k2 = __uint_as_float(krow[d + 2]);
-            k3 = __uint_as_float(krow[d + 3]);
-          }
-          s = __builtin_fmaf(q4.x, k0, s);
-          s = __builtin_fmaf(q4.y, k1, s);
-          s = __builtin_fmaf(q4.z, k2, s);
-          s = __builtin_fmaf(q4.w, k3, s);
-        }
-        sc = s * a.scale;
-      }
-      const float mnew = fmaxf(m[j], wave_max(sc));
-      const float p = (sc == -INFINITY) ? 0.0f : expf(sc - mnew);
-      const float corr = (m[j] == -INFINITY) ? 0.0f : expf(m[j] - mnew);
-      l[j] = l[j] * corr + wave_sum(p);
-      m[j] = mnew;
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) acc[j][e] = acc[j][e] * corr;
-      for (int u = 0; u < tvalid; ++u) {
-        const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), u));
-        const kv_t* vrow = s_v + u * HD + DPL * lane;
-        if constexpr (KV16 && DPL == 2) {
-          const unsigned w = *(const unsigned*)vrow;
-          acc[j][0] = __builtin_fmaf(pu, h2f((uint16_t)(w & 0xFFFF)), acc[j][0]);
-          acc[j][1] = __builtin_fmaf(pu, h2f((uint16_t)(w >> 16)), acc[j][1]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < DPL; ++e)
-            acc[j][e] = __builtin_fmaf(pu, kv_to_f<KV16>(vrow[e]), acc[j][e]);
-        }
-      }
-    }
-  }
-
-  // Partials of this split.
-#pragma unroll
-  for (int j = 0; j < HPW; ++j) {
-    const int hr = wave + 4 * j;
-    if (hr < n_rep) {
-      const int h = g * n_rep + hr;
-      const size_t idx = (size_t)h * a.nsplit + split;
-      if (lane == 0) {
-        a.part_ml[2 * idx] = m[j];
-        a.part_ml[2 * idx + 1] = l[j];
-      }
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) a.part_o[idx * HD + DPL * lane + e] = acc[j][e];
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_ticket = atomicAdd(&a.counters[g], 1);
-  __syncthreads();
-  if (s_ticket != a.nsplit - 1) return;
-  __threadfence();
-
-  // Last workgroup of this KV head: combine the splits.
-#pragma unroll
-  for (int j = 0; j < HPW; ++j) {
-    const int hr = wave + 4 * j;
-    if (hr >= n_rep) continue;
-    const int h = g * n_rep + hr;
-    const size_t base = (size_t)h * a.nsplit;
-    float M = -INFINITY;
-    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, __builtin_nontemporal_load(&a.part_ml[2 * (base + s)]));
-    float L = 0.0f, o[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) o[e] = 0.0f;
-    for (int s = 0; s < a.nsplit; ++s) {
-      const float ms = __builtin_nontemporal_load(&a.part_ml[2 * (base + s)]);
-      if (ms == -INFINITY) continue;
-      const float w = expf(ms - M);
-      L = L + __builtin_nontemporal_load(&a.part_ml[2 * (base + s) + 1]) * w;
-#pragma unroll
-      for (int e = 0; e < DPL; ++e)
-        o[e] = o[e] + __builtin_nontemporal_load(&a.part_o[(base + s) * HD + DPL * lane + e]) * w;
-    }
-    // ctx as f32 and as Q8_0 (32-dim blocks: 16 lanes x 2 dims, or 32 lanes x 1).
-    constexpr int LPB = 32 / DPL;  // lanes per Q8 block
-    float amax = 0.0f;
-    float v[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) {
-      v[e] = o[e] / L;
-      amax = fmaxf(amax, fabsf(v[e]));
-    }
-#pragma unroll
-    for (int off = LPB / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, LPB));
-    const float d = amax / 127.0f;
-    const float inv = amax == 0.0f ? 0.0f : 1.0f / d;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) {
-      const int dd = DPL * lane + e;
-      a.ctx[(size_t)h * HD + dd] = v[e];
-      a.ctx_q[(size_t)h * HD + dd] = amax == 0.0f ? (int8_t)0 : (int8_t)q8_code(v[e], inv);
-    }
-    if ((lane % LPB) == 0) a.ctx_d[((size_t)h * HD + DPL * lane) / 32] = amax == 0.0f ? 0.0f : d;
-  }
-  if (tid == 0) a.counters[g] = 0;
+  __shared__ __align__(16) uint8_t lds[AttnLds<HD, KV16>::BYTES];
+  attn_item<HD, KV16, false>(a, blockIdx.y, blockIdx.x, *a.pos_ptr, lds);
 }
 
 #define LLMRS_ATTN(name, HD, KV16)                                           \

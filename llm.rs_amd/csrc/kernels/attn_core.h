@@ -1,0 +1,383 @@
+// attn_core.h - batch-1 decode attention over the KV cache for gfx950,
+// shared by the standalone kernels (attention.hip) and the persistent decode
+// kernel (decode.hip).
+//
+// Reference: LlamaAttention::forward, seq == 1 (layer.rs:175-299): per query
+// head, RoPE on q and k (layer.rs:216-217, cpu.rs:326-357), K/V append at
+// pos (layer.rs:219-246), scores = q.K_t * (1/sqrt(hd)) (layer.rs:257-258),
+// softmax (cpu.rs:395-423), ctx = sum_t p_t V_t (layer.rs:276-299).
+//
+// MI355X design: one workgroup per (KV head, sequence split), 4 waves.  The
+// group's n_rep query heads share every K/V tile (true GQA: the reference
+// instead duplicates K/V rows per query head, loader.rs:62-98, which gives
+// the same numbers).  A split is a run of whole 64-position tiles.  Per tile:
+//  - the K and V rows are requested with 16-byte loads for the whole tile at
+//    once (and the next tile's loads are issued before this tile is used),
+//    then staged through LDS, K rows padded so lane-per-position reads are
+//    conflict-free;
+//  - wave w owns query heads w, w+4: lane p forms the score of position p
+//    (q broadcast from LDS, f32 accumulate of f32 q times the stored K);
+//  - softmax is online per head (running max and sum, DPP wave reductions);
+//  - for P.V lane l owns head dims 2l, 2l+1 (HD=128) or l (HD=64); the
+//    probabilities are broadcast from the lane that holds them.
+// The workgroup owning position `pos` rotates the new k and appends k and v
+// to the cache.  Partials (m, l, acc) go to global memory; the last
+// workgroup of a KV head (atomic ticket; partials move with device-scope
+// stores and loads) combines them and writes ctx as f32 and as Q8_0 codes
+// for the O projection.
+//
+// RoPE uses cos/sin tables [max_seq][hd/2] computed on the host with the
+// reference's own f32 formula and glibc, so rotation is bit-exact.
+#pragma once
+#include "common.h"
+#include "../kernel_args.h"
+
+namespace llmrs {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <bool KV16>
+struct KvType;
+template <>
+struct KvType<true> {
+  typedef uint16_t T;
+};
+template <>
+struct KvType<false> {
+  typedef float T;
+};
+
+template <bool KV16>
+__device__ __forceinline__ float kv_to_f(typename KvType<KV16>::T v) {
+  if constexpr (KV16) return h2f(v);
+  else return v;
+}
+
+
+template <bool DEV>
+__device__ __forceinline__ float ld_qkv(const float* base, size_t idx) {
+  if (DEV) return dev_ldf(base, (int)(idx * 4));
+  return base[idx];
+}
+template <bool DEV>
+__device__ __forceinline__ float ld_part(const float* base, size_t idx) {
+  if (DEV) return dev_ldf(base, (int)(idx * 4));
+  return __builtin_nontemporal_load(base + idx);
+}
+// Cache element store: `p` is the group's row base (plain path), `base` the
+// layer buffer with element index `idx` (device-scope path).
+template <bool DEV>
+__device__ __forceinline__ void st_kv(uint16_t* p, void* base, size_t idx, uint16_t v) {
+  if (DEV) dev_st_u16(base, (int)(idx * 2), v);
+  else ((uint16_t*)base)[idx] = v;
+}
+template <bool DEV>
+__device__ __forceinline__ void st_kv(float* p, void* base, size_t idx, float v) {
+  if (DEV) dev_stf(base, (int)(idx * 4), v);
+  else ((float*)base)[idx] = v;
+}
+
+template <int HD, bool KV16>
+struct AttnCfg {
+  typedef typename KvType<KV16>::T kv_t;
+  static constexpr int TILE = KV16 ? 64 : 32;            // positions per tile
+  static constexpr int EPC = 16 / (int)sizeof(kv_t);      // elements per 16 B
+  static constexpr int CPR = HD / EPC;                    // 16 B chunks per row
+  static constexpr int CHUNKS = TILE * CPR;               // per tile, K or V
+  static constexpr int CPT = CHUNKS / 256;                // chunks per thread
+  static constexpr int KSTRIDE = HD + (KV16 ? 2 : 1);     // padded K row (elements)
+  static constexpr int MAXREP = 8;                        // query heads per KV head
+  static constexpr int HPW = MAXREP / 4;                  // heads per wave
+  static constexpr int DPL = HD / LLMRS_WAVE;             // head dims per lane in P.V
+  static_assert(CHUNKS % 256 == 0, "tile must split evenly over 256 threads");
+};
+
+// LDS carve-up of one work item (bytes): s_q, padded K tile, V tile, s_new,
+// ticket.
+template <int HD, bool KV16>
+struct AttnLds {
+  typedef AttnCfg<HD, KV16> C;
+  typedef typename C::kv_t kv_t;
+  static constexpr size_t Q = 0;
+  static constexpr size_t K = Q + sizeof(float) * C::MAXREP * HD;
+  static constexpr size_t V = K + ((sizeof(kv_t) * C::TILE * C::KSTRIDE + 15) / 16) * 16;
+  static constexpr size_t NEW = V + sizeof(kv_t) * C::TILE * HD;
+  static constexpr size_t TICKET = NEW + sizeof(float) * 2 * HD;
+  static constexpr size_t BYTES = TICKET + 16;
+  static_assert(BYTES == attn_lds_bytes(HD, KV16), "host LDS size formula out of date");
+};
+
+// One (KV head g, split) work item at decode position pos.  DEV = true moves
+// the projections, the cache, the partials and ctx with device-scope loads
+// and stores (producer and consumer in one persistent launch).
+template <int HD, bool KV16, bool DEV>
+__device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, int pos, uint8_t* lds) {
+  typedef AttnCfg<HD, KV16> C;
+  typedef AttnLds<HD, KV16> LY;
+  typedef typename C::kv_t kv_t;
+  constexpr int TILE = C::TILE, MID = HD / 2, HPW = C::HPW, DPL = C::DPL;
+  constexpr int ES = (int)sizeof(kv_t);
+
+  float (*s_q)[HD] = (float (*)[HD])(lds + LY::Q);
+  kv_t* s_k = (kv_t*)(lds + LY::K);
+  kv_t* s_v = (kv_t*)(lds + LY::V);
+  float (*s_new)[HD] = (float (*)[HD])(lds + LY::NEW);
+  int& s_ticket = *(int*)(lds + LY::TICKET);
+
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int T = pos + 1;
+  const int n_rep = a.nq / a.nkv;
+  // Splits are runs of whole tiles.
+  const int ntile = (T + TILE - 1) / TILE;
+  const int tps = (ntile + a.nsplit - 1) / a.nsplit;
+  const int start = min(T, split * tps * TILE);
+  const int end = min(T, start + tps * TILE);
+  const int qdim = a.nq * HD;
+  const float* rc = a.rope_cos + (size_t)pos * MID;
+  const float* rs = a.rope_sin + (size_t)pos * MID;
+  const size_t gbase = (size_t)g * a.max_seq * HD;  // elements
+  kv_t* kc = (kv_t*)a.kc + gbase;
+  kv_t* vc = (kv_t*)a.vc + gbase;
+
+  // Tile loader: chunk c of the tile = row c / CPR, columns (c % CPR) * EPC.
+  u32x4 pk[C::CPT], pv[C::CPT];
+  auto issue = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < C::CPT; ++i) {
+      const int c = tid + 256 * i;
+      const int t = min(t0 + c / C::CPR, T - 1);  // clamped: rows past `end` are masked
+      const int col = (c % C::CPR) * C::EPC;
+      if (DEV) {
+        const int off = (int)((gbase + (size_t)t * HD + col) * ES);
+        pk[i] = dev_ld16(a.kc, off);
+        pv[i] = dev_ld16(a.vc, off);
+      } else {
+        pk[i] = *(const u32x4*)(kc + (size_t)t * HD + col);
+        pv[i] = *(const u32x4*)(vc + (size_t)t * HD + col);
+      }
+    }
+  };
+  if (start < end) issue(start);
+
+  // Rotated query heads of this group (cpu.rs:351-354).
+  for (int i = tid; i < n_rep * MID; i += blockDim.x) {
+    const int hr = i / MID, j = i % MID;
+    const size_t q = (size_t)(g * n_rep + hr) * HD;
+    const float re = ld_qkv<DEV>(a.qkv, q + j), im = ld_qkv<DEV>(a.qkv, q + j + MID);
+    const float c = rc[j], s = rs[j];
+    s_q[hr][j] = re * c - im * s;
+    s_q[hr][j + MID] = re * s + im * c;
+  }
+  // The owner of position pos rotates k and appends k, v (layer.rs:219-246).
+  // It keeps the stored values in s_new: its own tile loads may have been
+  // issued before these stores.
+  const bool owner = pos >= start && pos < end;
+  if (owner) {
+    const size_t kr = qdim + (size_t)g * HD;
+    const size_t vr = qdim + (size_t)a.nkv * HD + (size_t)g * HD;
+    for (int j = tid; j < MID; j += blockDim.x) {
+      const float re = ld_qkv<DEV>(a.qkv, kr + j), im = ld_qkv<DEV>(a.qkv, kr + j + MID);
+      const float c = rc[j], s = rs[j];
+      const float k0 = re * c - im * s, k1 = re * s + im * c;
+      if constexpr (KV16) {
+        const uint16_t h0 = f2h(k0), h1 = f2h(k1);
+        st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j, h0);
+        st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j + MID, h1);
+        s_new[0][j] = h2f(h0);
+        s_new[0][j + MID] = h2f(h1);
+      } else {
+        st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j, k0);
+        st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j + MID, k1);
+        s_new[0][j] = k0;
+        s_new[0][j + MID] = k1;
+      }
+    }
+    for (int d = tid; d < HD; d += blockDim.x) {
+      const float v = ld_qkv<DEV>(a.qkv, vr + d);
+      if constexpr (KV16) {
+        const uint16_t h = f2h(v);
+        st_kv<DEV>(vc, a.vc, gbase + (size_t)pos * HD + d, h);
+        s_new[1][d] = h2f(h);
+      } else {
+        st_kv<DEV>(vc, a.vc, gbase + (size_t)pos * HD + d, v);
+        s_new[1][d] = v;
+      }
+    }
+  }
+
+  float m[HPW], l[HPW], acc[HPW][DPL];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[j][e] = 0.0f;
+  }
+
+  for (int t0 = start; t0 < end; t0 += TILE) {
+    __syncthreads();  // previous tile consumed; s_q / s_new written
+    // Stage the tile (already loaded into registers) into LDS: V rows with
+    // 16-byte stores, padded K rows with 4-byte stores.
+#pragma unroll
+    for (int i = 0; i < C::CPT; ++i) {
+      const int c = tid + 256 * i;
+      const int r = c / C::CPR, col = (c % C::CPR) * C::EPC;
+      u32x4 kw = pk[i], vw = pv[i];
+      if (t0 + r == pos) {  // owner only: the row it just wrote
+        kv_t* kp = (kv_t*)&kw;
+        kv_t* vp = (kv_t*)&vw;
+#pragma unroll
+        for (int e = 0; e < C::EPC; ++e) {
+          if constexpr (KV16) {
+            kp[e] = f2h(s_new[0][col + e]);
+            vp[e] = f2h(s_new[1][col + e]);
+          } else {
+            kp[e] = s_new[0][col + e];
+            vp[e] = s_new[1][col + e];
+          }
+        }
+      }
+      unsigned* kd = (unsigned*)(s_k + r * C::KSTRIDE + col);
+      kd[0] = kw.x;
+      kd[1] = kw.y;
+      kd[2] = kw.z;
+      kd[3] = kw.w;
+      *(u32x4*)(s_v + r * HD + col) = vw;
+    }
+    if (t0 + TILE < end) issue(t0 + TILE);  // next tile in flight during this one
+    __syncthreads();
+
+    const int tvalid = min(TILE, end - t0);
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+      const int hr = wave + 4 * j;
+      if (hr >= n_rep) continue;  // uniform per wave
+      // Score of position t0 + lane (sequential over d, as cpu.rs:548).
+      float sc = -INFINITY;
+      if (lane < tvalid) {
+        float s = 0.0f;
+        // 32-bit LDS reads of the padded row: bank (lane*KSTRIDE/2 + i) mod 64
+        // differs across lanes, so the reads are conflict-free.
+        const unsigned* krow = (const unsigned*)(s_k + lane * C::KSTRIDE);
+#pragma unroll 8
+        for (int d = 0; d < HD; d += 4) {
+          const f32x4 q4 = *(const f32x4*)&s_q[hr][d];
+          float k0, k1, k2, k3;
+          if constexpr (KV16) {
+            const unsigned w0 = krow[d / 2], w1 = krow[d / 2 + 1];
+            k0 = h2f((uint16_t)(w0 & 0xFFFF));
+            k1 = h2f((uint16_t)(w0 >> 16));
+            k2 = h2f((uint16_t)(w1 & 0xFFFF));
+            k3 = h2f((uint16_t)(w1 >> 16));
+          } else {
+            k0 = __uint_as_float(krow[d]);
+            k1 = __uint_as_float(krow[d + 1]);
+            k2 = __uint_as_float(krow[d + 2]);
+            k3 = __uint_as_float(krow[d + 3]);
+          }
+          s = __builtin_fmaf(q4.x, k0, s);
+          s = __builtin_fmaf(q4.y, k1, s);
+          s = __builtin_fmaf(q4.z, k2, s);
+          s = __builtin_fmaf(q4.w, k3, s);
+        }
+        sc = s * a.scale;
+      }
+      const float mnew = fmaxf(m[j], wave_max(sc));
+      const float p = (sc == -INFINITY) ? 0.0f : expf(sc - mnew);
+      const float corr = (m[j] == -INFINITY) ? 0.0f : expf(m[j] - mnew);
+      l[j] = l[j] * corr + wave_sum(p);
+      m[j] = mnew;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) acc[j][e] = acc[j][e] * corr;
+      for (int u = 0; u < tvalid; ++u) {
+        const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), u));
+        const kv_t* vrow = s_v + u * HD + DPL * lane;
+        if constexpr (KV16 && DPL == 2) {
+          const unsigned w = *(const unsigned*)vrow;
+          acc[j][0] = __builtin_fmaf(pu, h2f((uint16_t)(w & 0xFFFF)), acc[j][0]);
+          acc[j][1] = __builtin_fmaf(pu, h2f((uint16_t)(w >> 16)), acc[j][1]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < DPL; ++e)
+            acc[j][e] = __builtin_fmaf(pu, kv_to_f<KV16>(vrow[e]), acc[j][e]);
+        }
+      }
+    }
+  }
+
+  // Partials of this split.
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    const int hr = wave + 4 * j;
+    if (hr < n_rep) {
+      const int h = g * n_rep + hr;
+      const size_t idx = (size_t)h * a.nsplit + split;
+      if (lane == 0) {
+        st_act<true>(a.part_ml, 2 * idx, m[j]);
+        st_act<true>(a.part_ml, 2 * idx + 1, l[j]);
+      }
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) st_act<true>(a.part_o, idx * HD + DPL * lane + e, acc[j][e]);
+    }
+  }
+  // Publish the partials, then take a ticket; the last workgroup combines.
+  // Partials always move with device-scope stores and loads, which bypass
+  // the per-XCD L2 copies: the stores only need to have completed before the
+  // ticket, and no agent-scope fence (a write-back and invalidate of the
+  // whole L2, microseconds under contention) is needed.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) s_ticket = atomicAdd(&a.counters[g], 1);
+  __syncthreads();
+  if (s_ticket != a.nsplit - 1) return;
+
+  // Last workgroup of this KV head: combine the splits.
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    const int hr = wave + 4 * j;
+    if (hr >= n_rep) continue;
+    const int h = g * n_rep + hr;
+    const size_t base = (size_t)h * a.nsplit;
+    float M = -INFINITY;
+    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, ld_part<true>(a.part_ml, 2 * (base + s)));
+    float L = 0.0f, o[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) o[e] = 0.0f;
+    for (int s = 0; s < a.nsplit; ++s) {
+      const float ms = ld_part<true>(a.part_ml, 2 * (base + s));
+      if (ms == -INFINITY) continue;
+      const float w = expf(ms - M);
+      L = L + ld_part<true>(a.part_ml, 2 * (base + s) + 1) * w;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e)
+        o[e] = o[e] + ld_part<true>(a.part_o, (base + s) * HD + DPL * lane + e) * w;
+    }
+    // ctx as f32 and as Q8_0 (32-dim blocks: 16 lanes x 2 dims, or 32 lanes x 1).
+    constexpr int LPB = 32 / DPL;  // lanes per Q8 block
+    float amax = 0.0f;
+    float v[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      v[e] = o[e] / L;
+      amax = fmaxf(amax, fabsf(v[e]));
+    }
+#pragma unroll
+    for (int off = LPB / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, LPB));
+    const float d = amax / 127.0f;
+    const float inv = amax == 0.0f ? 0.0f : 1.0f / d;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      const int dd = DPL * lane + e;
+      st_act<DEV>(a.ctx, (size_t)h * HD + dd, v[e]);
+      const int8_t q = amax == 0.0f ? (int8_t)0 : (int8_t)q8_code(v[e], inv);
+      if (DEV) dev_st8(a.ctx_q, (int)((size_t)h * HD + dd), q);
+      else a.ctx_q[(size_t)h * HD + dd] = q;
+    }
+    if ((lane % LPB) == 0) st_act<DEV>(a.ctx_d, ((size_t)h * HD + DPL * lane) / 32, amax == 0.0f ? 0.0f : d);
+  }
+  if (tid == 0) dev_stu(a.counters, 4 * g, 0u);
+}
+
+}  // namespace llmrs
+

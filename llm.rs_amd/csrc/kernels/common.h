@@ -101,6 +101,54 @@ __device__ __forceinline__ int q8_group32(float x, float* d_out) {
   return q8_code(x, inv);
 }
 
+// ---- device-coherent memory operations ---------------------------------
+// Data produced and consumed inside one launch by workgroups on different
+// XCDs (the persistent decode kernel) moves with device-scope (sc1) buffer
+// loads and stores: they bypass the per-XCD L2 copies, so no L2 write-back
+// or invalidate is needed at barriers.  The base must be wave-uniform; the
+// descriptor covers 2 GiB from it.
+typedef unsigned int dev_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kSc1 = 16;  // buffer cache-policy bit for device scope on gfx950
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7FFFFFFF, 0x00020000);
+}
+__device__ __forceinline__ float dev_ldf(const void* base, int byte_off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(dev_rsrc(base), byte_off, 0, kSc1));
+}
+__device__ __forceinline__ unsigned dev_ldu(const void* base, int byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(dev_rsrc(base), byte_off, 0, kSc1);
+}
+__device__ __forceinline__ dev_u32x4 dev_ld16(const void* base, int byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(dev_rsrc(base), byte_off, 0, kSc1);
+}
+__device__ __forceinline__ void dev_stf(void* base, int byte_off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), dev_rsrc(base), byte_off, 0, kSc1);
+}
+__device__ __forceinline__ void dev_stu(void* base, int byte_off, unsigned v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, dev_rsrc(base), byte_off, 0, kSc1);
+}
+__device__ __forceinline__ void dev_st16(void* base, int byte_off, dev_u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, dev_rsrc(base), byte_off, 0, kSc1);
+}
+__device__ __forceinline__ void dev_st8(void* base, int byte_off, int8_t v) {
+  __builtin_amdgcn_raw_buffer_store_b8((unsigned char)v, dev_rsrc(base), byte_off, 0, kSc1);
+}
+__device__ __forceinline__ void dev_st_u16(void* base, int byte_off, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, dev_rsrc(base), byte_off, 0, kSc1);
+}
+
+// f32 activation element, plain or device-scope.
+template <bool DEV>
+__device__ __forceinline__ float ld_act(const float* base, size_t idx) {
+  if (DEV) return dev_ldf(base, (int)(idx * 4));
+  return base[idx];
+}
+template <bool DEV>
+__device__ __forceinline__ void st_act(float* base, size_t idx, float v) {
+  if (DEV) dev_stf(base, (int)(idx * 4), v);
+  else base[idx] = v;
+}
+
 // Packed 4 x int8 dot product with int32 accumulation (v_dot4c_i32_i8).
 __device__ __forceinline__ int dot4(int a, int b, int c) {
   return __builtin_amdgcn_sdot4(a, b, c, false);

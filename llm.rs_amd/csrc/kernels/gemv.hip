@@ -1,429 +1,20 @@
-// gemv.hip - batch-1 dequant-GEMV for gfx950 (CDNA4).
+// gemv.hip - standalone batch-1 dequant-GEMV kernels for gfx950 (CDNA4).
 //
-// y[row] = sum_b isum_b(row) * (d_w[row,b] * d_a[b]) where isum_b is the exact
-// int32 dot product of one 32-element block of weight codes with the Q8_0
-// activation codes.  This is the reference CPU GEMV (cpu.rs:49-111,
-// kernel_avx2 cpu.rs:888-941) with the block loop spread over the 64 lanes of
-// a wavefront and the lane partials summed by a fixed DPP tree; isum_b is
-// bit-exact, only the f32 summation order differs.
-//
-// Device weight layout (written by the host at upload): for an [n, k] matrix
-// with nb = k/32 blocks per row, codes [n][nb][B] (B = 16 bytes for Q4_0:
-// byte i = e[i] | e[i+16] << 4; B = 32 bytes for Q8_0), then scales [n][nb]
-// (fp16, or f32 for the reference's Q4 storage).
-//
-// Work decomposition.  A "row group" is R consecutive rows; a "unit" is one
-// row group times 64*U consecutive blocks: lane l of the wave owns blocks
-// b = base + 64*u + l (u < U), so every weight load instruction of a wave
-// reads 64 consecutive 16-byte blocks of one row (1 KB, fully coalesced).
-// Waves walk their units in order, two units in flight: the weights of unit
-// i+2 are requested right after unit i is consumed, and the first two units
-// are requested before the activation prologue, so HBM latency overlaps the
-// prologue.  Row groups are dealt to waves round-robin (whole 64-row tiles
-// per workgroup for the SwiGLU epilogue, which needs matching gate and up
-// rows).
-//
-// The activation vector is quantised once per workgroup into LDS (prologue):
-//   PRO_QUANT  Q8_0 of an f32 row                     (matmul_transposed)
-//   PRO_NORM   RMSNorm then Q8_0                        (QKV, gate|up, lm_head)
-//   PRO_Q8     already-quantised codes from global      (O, down)
-// and each row group is finished in an epilogue:
-//   EPI_STORE  y = acc
-//   EPI_RESID  y = acc + res                            (O + residual, down + residual)
-//   EPI_SILU   gate|up rows interleaved in tiles of 32+32; m = silu(g)*u,
-//              written as f32 and as Q8_0 codes for the down projection
-//   EPI_ARGMAX logits plus a per-workgroup (max, index) partial (lm_head)
-#include "common.h"
-#include "../kernel_args.h"
+// Entry points over the shared machinery of gemv_core.h (which documents the
+// arithmetic, the weight layout and the work decomposition): one launch per
+// GEMV, row groups dealt to the waves of the whole grid.  Used by the trait
+// operator Backend::matmul_transposed (src/backend.rs:24) and by the
+// per-kernel decode step; argmax_final closes the lm_head GEMV.
+#include "gemv_core.h"
 
 using namespace llmrs;
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-enum { WT_Q4H = 0, WT_Q4F = 1, WT_Q8H = 2 };
-enum { PRO_QUANT = 0, PRO_NORM = 1, PRO_Q8 = 2 };
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
-
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / LLMRS_WAVE;
-constexpr int kSiluTile = 64;  // rows per SwiGLU tile: 32 gate + 32 up
-
-// Raw scale bits: the conversion happens at use, so a load never has to
-// complete before the next one is issued.
-template <int WT>
-__device__ __forceinline__ unsigned load_wscale_raw(const void* ws, size_t i) {
-  if (WT == WT_Q4F) return __builtin_nontemporal_load((const unsigned*)ws + i);
-  return __builtin_nontemporal_load((const uint16_t*)ws + i);
-}
-template <int WT>
-__device__ __forceinline__ float wscale(unsigned raw) {
-  if (WT == WT_Q4F) return __uint_as_float(raw);
-  return h2f((uint16_t)raw);
-}
-
-// Quantise the 32 values v[] of one block to Q8_0 (cpu.rs:724-743): amax
-// from 0, d = amax/127, inv = 1/d, round-half-away, clamp to +-127.  Writes
-// 8 packed dwords, the scale and (for Q4 weights) -8 * sum(codes).
-template <bool Q4>
-__device__ __forceinline__ void quant_block(const float* v, int blk, int8_t* s_q, float* s_d,
-                                            int* s_off) {
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  int packed[8];
-  int csum = 0;
-  float d = 0.0f;
-  if (amax == 0.0f) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) packed[j] = 0;
-  } else {
-    d = amax / 127.0f;
-    const float inv = 1.0f / d;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      unsigned w = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int q = q8_code(v[4 * j + e], inv);
-        csum += q;
-        w |= ((unsigned)q & 0xFFu) << (8 * e);
-      }
-      packed[j] = (int)w;
-    }
-  }
-  i32x4* dst = (i32x4*)(s_q + 32 * blk);
-  dst[0] = i32x4{packed[0], packed[1], packed[2], packed[3]};
-  dst[1] = i32x4{packed[4], packed[5], packed[6], packed[7]};
-  s_d[blk] = d;
-  if (Q4) s_off[blk] = -8 * csum;
-}
-
-// Prologue: the activation row as Q8_0 in LDS.  s_q holds the codes in
-// natural order, s_d the block scales, s_off = -8 * sum(codes) per block (the
-// Q4 offset: sum (q-8)*a = sum q*a - 8*sum a, with q in 0..15 read as int8).
-// One thread per block; blocks beyond the workgroup size loop.
-template <int PRO, bool Q4>
-__device__ __forceinline__ void load_activation(const GemvArgs& a, int mrow, int8_t* s_q,
-                                                float* s_d, int* s_off, float* s_red) {
-  const int k = a.k, nb = k >> 5, tid = threadIdx.x;
-  if (PRO == PRO_Q8) {
-    for (int b = tid; b < nb; b += kThreads) {
-      const i32x4* src = (const i32x4*)(a.xq + 32 * b);
-      const i32x4 c0 = src[0], c1 = src[1];
-      i32x4* dst = (i32x4*)(s_q + 32 * b);
-      dst[0] = c0;
-      dst[1] = c1;
-      s_d[b] = a.xd[b];
-      if (Q4) {
-        int s = 0;
-        s = dot4(c0.x, 0x01010101, s);
-        s = dot4(c0.y, 0x01010101, s);
-        s = dot4(c0.z, 0x01010101, s);
-        s = dot4(c0.w, 0x01010101, s);
-        s = dot4(c1.x, 0x01010101, s);
-        s = dot4(c1.y, 0x01010101, s);
-        s = dot4(c1.z, 0x01010101, s);
-        s = dot4(c1.w, 0x01010101, s);
-        s_off[b] = -8 * s;
-      }
-    }
-    return;
-  }
-  const float* x = a.x + (size_t)mrow * k;
-  float scale = 1.0f;
-  if (PRO == PRO_NORM) {
-    // cpu.rs:381-383: ss = sum v*v; rms = sqrt(ss/n + eps); scale = 1/rms.
-    float ss = 0.0f;
-    for (int b = tid; b < nb; b += kThreads) {
-      const f32x4* src = (const f32x4*)(x + 32 * b);
-      f32x4 v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = src[j];
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        ss = ss + v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
-    }
-    ss = wave_sum(ss);
-    if (lane_id() == 0) s_red[wave_id()] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) tot = tot + s_red[w];
-    const float rms = sqrtf(tot / (float)k + a.eps);
-    scale = 1.0f / rms;
-  }
-  for (int b = tid; b < nb; b += kThreads) {
-    const f32x4* src = (const f32x4*)(x + 32 * b);
-    float v[32];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const f32x4 t = src[j];
-      v[4 * j] = t.x;
-      v[4 * j + 1] = t.y;
-      v[4 * j + 2] = t.z;
-      v[4 * j + 3] = t.w;
-    }
-    if (PRO == PRO_NORM) {
-      const f32x4* wsrc = (const f32x4*)(a.norm_w + 32 * b);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const f32x4 t = wsrc[j];
-        v[4 * j] = v[4 * j] * scale * t.x;  // cpu.rs:389: x * s * w
-        v[4 * j + 1] = v[4 * j + 1] * scale * t.y;
-        v[4 * j + 2] = v[4 * j + 2] * scale * t.z;
-        v[4 * j + 3] = v[4 * j + 3] * scale * t.w;
-      }
-    }
-    quant_block<Q4>(v, b, s_q, s_d, s_off);
-  }
-}
-
-// Pair order for argmax: larger value wins, lower index breaks ties.
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-  return v > bv || (v == bv && i < bi);
-}
-
-// Weights of one unit held in registers.
-template <int WT, int R, int U>
-struct UnitRegs {
-  u32x4 c0[R][U];
-  u32x4 c1[R][WT == WT_Q8H ? U : 1];
-  unsigned sc[R][U];  // raw scale bits
-};
-
-template <int WT, int PRO, int EPI, int R, int U>
-struct Gemv {
-  static constexpr bool Q4 = (WT != WT_Q8H);
-  static constexpr int BS = Q4 ? 16 : 32;       // code bytes per block
-  static constexpr int BPU = LLMRS_WAVE * U;    // blocks per unit
-  static constexpr int SILU_RG = kSiluTile / R / kWaves;  // row groups per wave per tile
-
-  const GemvArgs& a;
-  int nb, nchunk, nrg, lane, wave;
-  int8_t* s_q;
-  float* s_d;
-  int* s_off;
-
-  __device__ Gemv(const GemvArgs& args, int8_t* q, float* d, int* off)
-      : a(args), s_q(q), s_d(d), s_off(off) {
-    nb = a.k >> 5;
-    nchunk = (nb + BPU - 1) / BPU;
-    nrg = (a.n + R - 1) / R;
-    lane = lane_id();
-    wave = wave_id();
-  }
-
-  // Row group of the j-th group this wave processes (-1 past the end).
-  __device__ __forceinline__ int row_group(int j) const {
-    if (EPI == EPI_SILU) {
-      const int per_tile = SILU_RG;
-      const int tile = blockIdx.x + (j / per_tile) * gridDim.x;
-      const int rg = tile * (kSiluTile / R) + wave * per_tile + (j % per_tile);
-      return rg < nrg ? rg : -1;
-    }
-    const int rg = blockIdx.x * kWaves + wave + j * gridDim.x * kWaves;
-    return rg < nrg ? rg : -1;
-  }
-
-  // Loads are unconditional: out-of-range rows and blocks read a clamped,
-  // valid address and are masked at use (blocks) or never written (rows),
-  // so the wave issues every load of the unit back to back.
-  __device__ __forceinline__ void load(UnitRegs<WT, R, U>& u, int unit) const {
-    const int rg = unit < 0 ? -1 : row_group(unit / nchunk);
-    const int b0 = (unit < 0 ? 0 : unit % nchunk) * BPU + lane;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = min(max(rg * R + r, 0), a.n - 1);
-#pragma unroll
-      for (int v = 0; v < U; ++v) {
-        const int b = min(b0 + LLMRS_WAVE * v, nb - 1);
-        const size_t blk = (size_t)row * nb + b;
-        u.c0[r][v] = __builtin_nontemporal_load((const u32x4*)(a.wq + blk * BS));
-        if (!Q4) u.c1[r][v] = __builtin_nontemporal_load((const u32x4*)(a.wq + blk * BS + 16));
-        u.sc[r][v] = load_wscale_raw<WT>(a.ws, blk);
-      }
-    }
-  }
-
-  // acc[r] += sum over the unit's blocks of isum * (d_w * d_a)  (cpu.rs:913,932)
-  __device__ __forceinline__ void compute(const UnitRegs<WT, R, U>& u, int unit, float* acc) const {
-    const int b0 = (unit % nchunk) * BPU + lane;
-#pragma unroll
-    for (int v = 0; v < U; ++v) {
-      const int b = b0 + LLMRS_WAVE * v;
-      if (b < nb) {
-        const i32x4* aq = (const i32x4*)(s_q + 32 * b);
-        const i32x4 a0 = aq[0], a1 = aq[1];
-        const float da = s_d[b];
-        const int off = Q4 ? s_off[b] : 0;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          int s = off;
-          const u32x4 w = u.c0[r][v];
-          if (Q4) {
-            const unsigned M = 0x0F0F0F0Fu;
-            // low nibbles of dword j = elements 4j..4j+3, high = 16+4j..
-            s = dot4((int)(w.x & M), a0.x, s);
-            s = dot4((int)(w.y & M), a0.y, s);
-            s = dot4((int)(w.z & M), a0.z, s);
-            s = dot4((int)(w.w & M), a0.w, s);
-            s = dot4((int)((w.x >> 4) & M), a1.x, s);
-            s = dot4((int)((w.y >> 4) & M), a1.y, s);
-            s = dot4((int)((w.z >> 4) & M), a1.z, s);
-            s = dot4((int)((w.w >> 4) & M), a1.w, s);
-          } else {
-            const u32x4 w1 = u.c1[r][v];
-            s = dot4((int)w.x, a0.x, s);
-            s = dot4((int)w.y, a0.y, s);
-            s = dot4((int)w.z, a0.z, s);
-            s = dot4((int)w.w, a0.w, s);
-            s = dot4((int)w1.x, a1.x, s);
-            s = dot4((int)w1.y, a1.y, s);
-            s = dot4((int)w1.z, a1.z, s);
-            s = dot4((int)w1.w, a1.w, s);
-          }
-          acc[r] = acc[r] + (float)s * (wscale<WT>(u.sc[r][v]) * da);
-        }
-      }
-    }
-  }
-};
-
 template <int WT, int PRO, int EPI, int R, int U>
 __device__ __forceinline__ void gemv_impl(const GemvArgs& a) {
-  typedef Gemv<WT, PRO, EPI, R, U> G;
-  static_assert(EPI != EPI_SILU || (kSiluTile % (R * kWaves) == 0), "SwiGLU tile must split evenly");
   extern __shared__ __align__(16) uint8_t smem[];
-  __shared__ float s_out[kSiluTile];
-  __shared__ float s_red[kWaves];
-  __shared__ float s_bv[kWaves];
-  __shared__ int s_bi[kWaves];
-
-  const int k = a.k, nb = k >> 5;
-  G g(a, (int8_t*)smem, (float*)(smem + k), (int*)(smem + k + 4 * nb));
-  const int mrow = blockIdx.y;
-  const int lane = g.lane, wave = g.wave, tid = threadIdx.x;
-
-  // Units of this wave: row groups j = 0, 1, ... each of nchunk units.  For
-  // the SwiGLU epilogue every wave of a workgroup walks the same number of
-  // tiles, so the per-tile barriers below are uniform.
-  int ngroups = 0;
-  if (EPI == EPI_SILU) {
-    const int ntiles = (a.n + kSiluTile - 1) / kSiluTile;
-    const int my_tiles = blockIdx.x < ntiles ? (ntiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
-    ngroups = my_tiles * G::SILU_RG;
-  } else {
-    const int first = blockIdx.x * kWaves + wave;
-    const int stride = gridDim.x * kWaves;
-    ngroups = first < g.nrg ? (g.nrg - 1 - first) / stride + 1 : 0;
-  }
-  const int nunits = ngroups * g.nchunk;
-
+  __shared__ GemvShared sh;
   UnitRegs<WT, R, U> ua, ub;
-  g.load(ua, nunits > 0 ? 0 : -1);
-  g.load(ub, nunits > 1 ? 1 : -1);
-
-  load_activation<PRO, G::Q4>(a, mrow, g.s_q, g.s_d, g.s_off, s_red);
-  __syncthreads();
-
-  const size_t ybase = (size_t)mrow * a.n;
-  float best_v = -INFINITY;
-  int best_i = 0x7fffffff;
-  float acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-  // Finish unit i: on the last chunk of a row group, reduce and write.
-  auto finish = [&](int i) {
-    if ((i % g.nchunk) != g.nchunk - 1) return;
-    const int j = i / g.nchunk;
-    const int rg = g.row_group(j);
-    float vals[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      vals[r] = wave_sum(acc[r]);
-      acc[r] = 0.0f;
-    }
-    if (EPI == EPI_STORE || EPI == EPI_RESID) {
-      float out = 0.0f;
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (lane == r) out = vals[r];
-      const int row = rg * R + lane;
-      if (lane < R && rg >= 0 && row < a.n) {
-        if (EPI == EPI_RESID) out = out + a.res[ybase + row];  // layer.rs:386,403
-        a.y[ybase + row] = out;
-      }
-    } else if (EPI == EPI_ARGMAX) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int row = rg * R + r;
-        if (rg >= 0 && row < a.n && better(vals[r], row, best_v, best_i)) {
-          best_v = vals[r];
-          best_i = row;
-        }
-      }
-      float out = 0.0f;
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (lane == r) out = vals[r];
-      const int row = rg * R + lane;
-      if (a.y && lane < R && rg >= 0 && row < a.n) a.y[row] = out;
-    } else if (EPI == EPI_SILU) {
-      const int local = (j % G::SILU_RG) * R + wave * (G::SILU_RG * R);
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (lane == r) s_out[local + r] = vals[r];
-      if ((j % G::SILU_RG) == G::SILU_RG - 1) {
-        // Tile complete in this wave; wait for the other waves.
-        __syncthreads();
-        const int tile = blockIdx.x + (j / G::SILU_RG) * gridDim.x;
-        if (tid < 32) {
-          // Tile = 32 gate rows then the 32 matching up rows (layer.rs:72-79).
-          const float gv = s_out[tid], uv = s_out[32 + tid];
-          const float mv = (gv / (1.0f + expf(-gv))) * uv;
-          const int idx = tile * 32 + tid;
-          if (a.y) a.y[idx] = mv;
-          float d;
-          const int q = q8_group32(mv, &d);
-          a.yq[idx] = (int8_t)q;
-          if (tid == 0) a.yd[tile] = d;
-        }
-        __syncthreads();
-      }
-    }
-  };
-
-  int i = 0;
-  while (i < nunits) {
-    g.compute(ua, i, acc);
-    g.load(ua, i + 2 < nunits ? i + 2 : -1);
-    finish(i);
-    if (++i >= nunits) break;
-    g.compute(ub, i, acc);
-    g.load(ub, i + 2 < nunits ? i + 2 : -1);
-    finish(i);
-    ++i;
-  }
-
-  if (EPI == EPI_ARGMAX) {
-    if (lane == 0) {
-      s_bv[wave] = best_v;
-      s_bi[wave] = best_i;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (int w = 1; w < kWaves; ++w)
-        if (better(s_bv[w], s_bi[w], best_v, best_i)) {
-          best_v = s_bv[w];
-          best_i = s_bi[w];
-        }
-      a.part_val[blockIdx.x] = best_v;
-      a.part_idx[blockIdx.x] = best_i;
-    }
-  }
+  gemv_body<WT, PRO, EPI, R, U, false>(a, blockIdx.y, blockIdx.x, gridDim.x, ua, ub, false, smem, sh);
 }
 
 #define LLMRS_GEMV(name, WT, PRO, EPI, R, U)                                       \

@@ -93,6 +93,7 @@ _SIGS = {
     "llmrs_model_decode_steps": (C.c_int, [C.c_void_p, C.c_size_t]),
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "llmrs_model_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
+    "llmrs_model_profile_phases": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_int]),
     "llmrs_model_weight_bytes": (C.c_double, [C.c_void_p]),
     "llmrs_synth_q4": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_synth_q8": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_int]),
@@ -387,6 +388,13 @@ class HipModel:
         raw = names.raw
         return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(by[i]))
                 for i in range(n)]
+
+    def profile_phases(self, n_steps: int = 1) -> tuple[float, np.ndarray]:
+        """Persistent-kernel phase timing: (us per step, [layers][10] intervals)."""
+        cap = 1 + 10 * self.cfg.n_layers
+        out = np.zeros(cap, np.float64)
+        n = _check(lib().llmrs_model_profile_phases(self._h, n_steps, _ptr(out), cap))
+        return float(out[0]), out[1:n].reshape(-1, 10)
 
     def weight_bytes(self) -> float:
         return float(lib().llmrs_model_weight_bytes(self._h))
