@@ -67,7 +67,8 @@ const char* wt_tag(int wt) {
 // when the row splits into whole 128-block chunks, R = 2 for the narrow
 // (n <= 8192) projections so that more waves share them.  The SwiGLU tile is
 // 64 rows per workgroup; other kinds deal R-row groups to waves, capped at
-// LLMRS_GEMV_WG_PER_CU (default 4) workgroups per CU, beyond which waves loop.
+// LLMRS_GEMV_WG_PER_CU (default 2, the best of 1/2/4/8 measured on the 8B
+// decode) workgroups per CU, beyond which waves loop.
 GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
   const int nb = k / 32;
   int U = (nb % 128 == 0) ? 2 : 1;
@@ -80,7 +81,7 @@ GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
     if (er && (std::atoi(er) == 2 || std::atoi(er) == 4)) R = std::atoi(er);
   }
   const char* ew = std::getenv("LLMRS_GEMV_WG_PER_CU");
-  const long cap = (long)std::max(1, num_cus) * std::max(1, ew && *ew ? std::atoi(ew) : 4);
+  const long cap = (long)std::max(1, num_cus) * std::max(1, ew && *ew ? std::atoi(ew) : 2);
   GemvPlan p;
   p.name = std::string("gemv_") + wt_tag(wt) + "_" + kind + "_r" + std::to_string(R) + "u" +
            std::to_string(U);
