@@ -24,7 +24,9 @@ sys.path.insert(0, str(REPO / "llm.rs_amd"))
 sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 METRIC = "decode tok/s (bs1, 8B-shape Q4_0) + Q4_0 GEMV HBM GB/s vs peak"
+PREFILL_METRIC = "prefill tok/s (8B-shape Q4_0, one 2048-token prompt) + GEMM MFMA utilisation"
 
 
 def log(msg: str) -> None:
@@ -57,11 +59,114 @@ def cpu_baseline(spec, w, seconds: float) -> dict:
                       f"(positions 8..{7 + steps}), oracle threads={oracle.threads()}"}
 
 
+def cpu_prefill_baseline(spec, w, seconds: float) -> dict:
+    """Oracle prefill tok/s on a bounded sample: one batched forward of a
+    prompt prefix sized to take about `seconds`."""
+    import oracle
+    oracle.set_threads(int(os.environ.get("ORACLE_THREADS", "0")))
+    from llmrs_hip import synthetic as syn
+    om = oracle.OracleModel.from_spec(spec, max_seq=256)
+    om.load(w)
+    toks = syn.prompt(spec)
+    n = 8
+    t0 = time.perf_counter()
+    om.forward(toks[:n], 0)
+    dt = time.perf_counter() - t0
+    # second pass sized from the first
+    n2 = int(max(8, min(256, n * seconds / max(dt, 1e-3) * 0.8)))
+    t0 = time.perf_counter()
+    om.forward(toks[:n2], 0)
+    dt = time.perf_counter() - t0
+    return {"value": round(n2 / dt, 3), "unit": "tok/s", "cores": oracle.threads(), "kind": "port",
+            "sample": f"one batched forward of the first {n2} prompt tokens of the same model, "
+                      f"oracle threads={oracle.threads()}"}
+
+
+def bench_prefill(args, lh, syn) -> int:
+    """Batched prefill of the 2048-token prompt: tok/s over `steps` whole
+    prompts (each rewrites the KV cache from position 0), per-kernel FLOP
+    rates from HIP events, GEMM MFMA utilisation against the int8 peak."""
+    spec = syn.WORKLOADS[args.workload]
+    if args.prompt:
+        spec = syn.with_sizes(spec, prompt=args.prompt, decode=0)
+    M = spec.prompt
+    lh.init(0)
+    t0 = time.perf_counter()
+    keep = not args.no_cpu_baseline
+    model = lh.HipModel(spec.config(M))
+    if keep:
+        w = syn.make_weights(spec)
+        syn.load_model(model, w)
+    else:
+        w = None
+        syn.stream_model(model, spec)
+    log(f"workload {spec.name}: weights uploaded in {time.perf_counter() - t0:.1f}s")
+    prompt = syn.prompt(spec)
+    for i in range(args.warmup):
+        model.forward(prompt, 0, logits=False)
+    lh.sync()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        model.forward(prompt, 0, logits=False)
+        log(f"prefill {i + 1}/{args.steps}")
+    lh.sync()
+    dt = time.perf_counter() - t0
+    value = args.steps * M / dt
+    log(f"prefill: {value:.1f} tok/s ({dt / args.steps * 1e3:.2f} ms per {M}-token prompt)")
+
+    per = defaultdict(lambda: [0.0, 0.0, 0])
+    for _ in range(args.profile_steps):
+        for k in model.profile_prefill(prompt):
+            e = per[k.name]
+            e[0] += k.ms
+            e[1] += k.bytes
+            e[2] += 1
+    P = max(1, args.profile_steps)
+    tot = sum(ms for ms, _, _ in per.values())
+    kernels = {}
+    for name, (ms, wk, n) in sorted(per.items(), key=lambda kv: -kv[1][0]):
+        avg_s = ms / n / 1e3
+        flop = name.startswith("gemm_") or name.startswith("attn_")
+        kernels[name] = {"launches": n // P, "avg_us": round(avg_s * 1e6, 2), "share": round(ms / tot, 4),
+                         ("tflop_s" if flop else "gb_s"): round(wk / n / avg_s / (1e12 if flop else 1e9), 1)}
+    gemm = [n for n in per if n.startswith("gemm_")]
+    g_ms = sum(per[n][0] for n in gemm)
+    g_fl = sum(per[n][1] for n in gemm)
+    dom = max(gemm, key=lambda n: per[n][0])
+    ms, fl, n = per[dom]
+    achieved = fl / n / (ms / n / 1e3) / 1e12
+
+    cpu = None
+    if keep:
+        log("timing the CPU oracle prefill on a bounded sample ...")
+        cpu = cpu_prefill_baseline(spec, w, args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads")
+    line = {
+        "metric": PREFILL_METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 MFMA (q4_0 x q8_0, exact block sums) + f32", "data": "synthetic",
+        "config": {"workload": f"{spec.name} prefill", "layers": spec.n_layers, "hidden": spec.hidden,
+                   "heads": spec.n_heads, "kv_heads": spec.n_kv_heads, "head_dim": spec.head_dim,
+                   "ffn": spec.ffn, "vocab": spec.vocab, "weights": spec.weight.name,
+                   "kv_cache": spec.kv.name.lower(), "prompt": M, "batch": 1},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
+                     "flops_per_launch": round(fl / n), "avg_us": round(ms / n * 1e3, 2), "traffic": None},
+        "gemm_mfma_utilisation": round(g_fl / (g_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
+        "gemm_share_of_prefill": round(g_ms / tot, 4),
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=240)
-    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (decode 240, prefill 5)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (decode 16, prefill 1)")
     ap.add_argument("--workload", type=int, default=2)
     ap.add_argument("--prompt", type=int, default=None, help="override the prompt length")
     ap.add_argument("--profile-steps", type=int, default=4)
@@ -78,6 +183,13 @@ def main() -> int:
     import llmrs_hip as lh
     from llmrs_hip import synthetic as syn
 
+    prefill_only = syn.WORKLOADS[args.workload].decode == 0
+    if args.steps is None:
+        args.steps = 5 if prefill_only else 240
+    if args.warmup is None:
+        args.warmup = 1 if prefill_only else 16
+    if prefill_only:
+        return bench_prefill(args, lh, syn)
     base = syn.WORKLOADS[args.workload]
     n_prompt = args.prompt or base.prompt
     spec = syn.with_sizes(base, prompt=n_prompt, decode=args.warmup + args.steps)

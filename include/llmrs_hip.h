@@ -190,8 +190,11 @@ int llmrs_model_kv_read(llmrs_model* m, int layer, int kv_head, size_t pos0,
                         size_t n, float* k, float* v);
 /* One forward pass of `n` tokens at positions [start_pos, start_pos+n)
  * (LlamaModel::forward, src/core/model.rs:17-49, driven like
- * src/main.rs:134-190).  The rows are processed in order, which is
- * numerically the reference's causal prefill.  Outputs (each may be NULL):
+ * src/main.rs:134-190).  n > 1 runs the batched prefill kernels (every
+ * linear layer as an exact int8 GEMM over Q8_0 rows, cpu.rs:90-110; causal
+ * attention, layer.rs:248-326) in chunks of up to 2048 rows; n == 1 is one
+ * decode step.  Environment LLMRS_PREFILL=0 processes the rows one decode
+ * step at a time instead.  Outputs (each may be NULL):
  *   logits  f32 [vocab] of the last row;
  *   next    greedy argmax of the last row (lowest index on ties);
  *   trace   f32 [n][n_layers+1][hidden]: the residual stream entering each
@@ -200,8 +203,9 @@ int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n,
                         size_t start_pos, float* logits, int32_t* next,
                         float* trace);
 /* Greedy generation (src/main.rs:128-327 with argmax in place of sampling):
- * processes the prompt from position 0, then emits n_steps tokens into
- * out_tokens.  Each position runs as one replay of a captured HIP graph. */
+ * processes the prompt from position 0 (batched prefill, as in
+ * llmrs_model_forward), then emits n_steps tokens into out_tokens.  Each
+ * decode position runs as one replay of a captured HIP graph. */
 int llmrs_model_generate(llmrs_model* m, const int32_t* prompt,
                          size_t n_prompt, size_t n_steps, int32_t* out_tokens);
 /* Benchmark helpers: start a greedy run (prompt processed, state resident),
@@ -216,6 +220,14 @@ int llmrs_model_tokens(llmrs_model* m, int32_t* out, size_t count);
  * launch.  Returns the number of launches recorded (>= 0) or an error. */
 int llmrs_model_profile_step(llmrs_model* m, char* names, float* ms,
                              double* bytes, int cap);
+/* Per-kernel timing of one batched prefill of `n` tokens (n at most one
+ * chunk, 2048 rows by default) at positions [start_pos, start_pos+n), as in
+ * llmrs_model_forward.  Same outputs as llmrs_model_profile_step, with
+ * `work` = FLOPs for the GEMM and attention launches (2 per multiply-add) and
+ * bytes for the others. */
+int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
+                                size_t start_pos, char* names, float* ms,
+                                double* work, int cap);
 /* Phase timing of the persistent decode kernel: runs `n_steps` more decode
  * steps in one launch and returns in `us` (up to `cap` values): the launch
  * wall time per step, then for each layer of the first step ten intervals

@@ -80,6 +80,13 @@ struct llmrs_model {
   unsigned pk_grid = 0;              // 0: persistent path unavailable
   size_t pk_lds = 0;
   int host_n_prompt = 0;
+  // batched prompt (prefill) buffers for chunks of up to pf_cap rows,
+  // allocated on first use
+  int pf_cap = 0;
+  float *pf_x = nullptr, *pf_h = nullptr, *pf_qkv = nullptr, *pf_q = nullptr;
+  float *pf_ad = nullptr, *pf_ctx_d = nullptr, *pf_m_d = nullptr;
+  int8_t *pf_aq = nullptr, *pf_ctx_q = nullptr, *pf_m_q = nullptr;
+  int* pf_start = nullptr;   // first position of the chunk (device copy)
   std::vector<void*> allocs;
 
   template <class T>
@@ -143,6 +150,8 @@ double linear_weight_bytes(const llmrs_model* m, const DevLinear& L) {
   const double nb = L.k / 32.0;
   return (double)L.n * nb * (block_code_bytes(m->wt) + block_scale_bytes(m->wt));
 }
+
+void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits);
 
 void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
   const llmrs_model_config& c = m->c;
@@ -240,6 +249,15 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
   if (trace_dev)
     LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)c.n_layers * H, m->x, H * sizeof(float),
                              hipMemcpyDeviceToDevice, L.s));
+  enqueue_head(m, L, write_logits);
+}
+
+// Final RMSNorm + lm_head GEMV of the row in m->x, then the greedy step
+// bookkeeping at the device position (model.rs:39-47, main.rs:185-190).
+void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits) {
+  const llmrs_model_config& c = m->c;
+  const int H = c.hidden;
+  const int cus = ctx().num_cus;
   {  // lm_head + argmax
     GemvArgs g{};
     g.wq = m->lm_head.codes;
@@ -258,6 +276,160 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
   }
   ArgmaxFinalArgs f{m->part_val, m->part_idx, m->lm_grid, m->pos, m->n_prompt, m->tokens, m->gen, m->cap};
   L("argmax_final", 8.0 * m->lm_grid, dim3(1), dim3(256), 0, f);
+}
+
+// Batched prompt processing (prefill).  The reference runs the whole prompt
+// as one forward of M rows (main.rs:134-138,179; model.rs:17-49): every
+// linear layer quantises each activation row to Q8_0 and runs the block loop
+// per output (cpu.rs:90-110), which the exact int8 MFMA GEMM reproduces bit
+// for bit; attention is causal over the cache (layer.rs:248-326).  Prompts
+// longer than pf_cap rows run as consecutive chunks at increasing start
+// positions, which gives the same values: each row's projections depend only
+// on that row, and its attention reads the K/V already in the cache.
+void ensure_prefill(llmrs_model* m) {
+  if (m->pf_cap) return;
+  const llmrs_model_config& c = m->c;
+  const int cap = std::max(1, std::min(c.max_seq, env_int("LLMRS_PREFILL_CHUNK", 2048)));
+  const size_t M = (size_t)cap, H = c.hidden, F = c.ffn, qd = (size_t)c.n_heads * c.head_dim;
+  const size_t kmax = std::max(H, std::max(F, qd));
+  m->pf_x = m->dalloc<float>(M * H);
+  m->pf_h = m->dalloc<float>(M * H);
+  m->pf_qkv = m->dalloc<float>(M * m->qkv_rows);
+  m->pf_q = m->dalloc<float>(M * qd);
+  m->pf_aq = m->dalloc<int8_t>(M * kmax);
+  m->pf_ad = m->dalloc<float>(M * kmax / 32);
+  m->pf_ctx_q = m->dalloc<int8_t>(M * qd);
+  m->pf_ctx_d = m->dalloc<float>(M * qd / 32);
+  m->pf_m_q = m->dalloc<int8_t>(M * F);
+  m->pf_m_d = m->dalloc<float>(M * F / 32);
+  m->pf_start = m->dalloc<int>(1);
+  LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+  m->pf_cap = cap;
+}
+
+std::string gemm_kernel(const llmrs_model* m, const char* epi) {
+  return std::string("gemm_") + wt_tag(m->wt) + "_" + epi;
+}
+
+dim3 gemm_grid(int M, int N) { return dim3((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128)); }
+
+// One chunk of M <= pf_cap rows at positions [start, start+M): embeddings,
+// every layer, and (head) the lm_head of the last row with the greedy step
+// at the device position.  The recorded figure per launch is its FLOPs for
+// the GEMMs and attention, bytes for the rest.  trace_dev, when set, is
+// [M][n_layers+1][hidden].
+void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head, bool write_logits,
+                     float* trace_dev) {
+  const llmrs_model_config& c = m->c;
+  const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
+  const int qd = nq * hd, QR = m->qkv_rows;
+  const bool kv16 = c.kv_dtype == LLMRS_F16;
+  const dim3 blk(256);
+  auto trace = [&](int li) {
+    if (trace_dev)
+      LLMRS_HIP(hipMemcpy2DAsync(trace_dev + (size_t)li * H, (size_t)(c.n_layers + 1) * H * sizeof(float),
+                                 m->pf_x, H * sizeof(float), H * sizeof(float), M,
+                                 hipMemcpyDeviceToDevice, L.s));
+  };
+  auto flops = [](double a, double b, double k) { return 2.0 * a * b * k; };
+
+  EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab};
+  L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), blk, 0, e);
+  const float scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
+  const std::string attn = "attn_prefill_hd" + std::to_string(hd) + (kv16 ? "_f16" : "_f32");
+  // causal score and P.V products over the chunk
+  const double attn_flops = 4.0 * nq * hd * ((double)M * start + (double)M * (M + 1) / 2.0);
+  for (int li = 0; li < c.n_layers; ++li) {
+    LayerBufs& Lb = m->layers[li];
+    trace(li);
+    {  // RMSNorm + Q8_0 of each row (layer.rs:378; cpu.rs:90-93)
+      PrefillRowArgs r{m->pf_x, Lb.norm[0], m->pf_aq, m->pf_ad, M, H, c.rms_eps};
+      L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
+    }
+    {  // Q|K|V
+      PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.qkv.codes, Lb.qkv.scales, m->pf_qkv, nullptr,
+                        nullptr, nullptr, M, QR, H, QR};
+      L(gemm_kernel(m, "store"), flops(M, QR, H), gemm_grid(M, QR), blk, 0, g);
+    }
+    {  // RoPE + K/V append
+      PrefillRopeArgs r{m->pf_qkv, m->pf_q, Lb.kc, Lb.vc, m->rope_cos, m->rope_sin, M, nq, nkv, hd,
+                        c.max_seq, (int)start, QR, kv16 ? 1 : 0};
+      const long total = (long)M * (nq + 2 * nkv) * (hd / 2);
+      const unsigned grid = (unsigned)std::min<long>((total + 255) / 256, 8192);
+      L("prefill_rope_kv", 4.0 * QR * M * 2, dim3(grid), blk, 0, r);
+    }
+    {  // causal attention
+      PrefillAttnArgs a{m->pf_q, Lb.kc, Lb.vc, nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq, nkv,
+                        c.max_seq, (int)start, scale};
+      L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nq), blk, 0, a);
+    }
+    {  // O projection + residual (layer.rs:386)
+      PrefillGemmArgs g{m->pf_ctx_q, m->pf_ctx_d, Lb.o.codes, Lb.o.scales, m->pf_h, m->pf_x,
+                        nullptr, nullptr, M, H, qd, H};
+      L(gemm_kernel(m, "resid"), flops(M, H, qd), gemm_grid(M, H), blk, 0, g);
+    }
+    {  // post-attention RMSNorm + Q8_0
+      PrefillRowArgs r{m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, M, H, c.rms_eps};
+      L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
+    }
+    {  // gate|up + SiLU + Q8_0 of m (layer.rs:40-89)
+      PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.gu.codes, Lb.gu.scales, nullptr, nullptr,
+                        m->pf_m_q, m->pf_m_d, M, 2 * F, H, F};
+      L(gemm_kernel(m, "silu"), flops(M, 2 * F, H), gemm_grid(M, 2 * F), blk, 0, g);
+    }
+    {  // down projection + residual (layer.rs:403)
+      PrefillGemmArgs g{m->pf_m_q, m->pf_m_d, Lb.down.codes, Lb.down.scales, m->pf_x, m->pf_h,
+                        nullptr, nullptr, M, H, F, H};
+      L(gemm_kernel(m, "resid"), flops(M, H, F), gemm_grid(M, H), blk, 0, g);
+    }
+  }
+  trace(c.n_layers);
+  if (head) {
+    LLMRS_HIP(hipMemcpyAsync(m->x, m->pf_x + (size_t)(M - 1) * H, H * sizeof(float),
+                             hipMemcpyDeviceToDevice, L.s));
+    enqueue_head(m, L, write_logits);
+  }
+}
+
+bool prefill_enabled() { return env_int("LLMRS_PREFILL", 1) != 0; }
+
+void set_state(llmrs_model* m, size_t pos, int n_prompt);
+
+// Runs rows [start, start+n) through the prefill kernels in chunks; the last
+// chunk ends with the lm_head and greedy step, leaving the device position
+// at start+n.  trace (host, may be null) is [n][n_layers+1][hidden].
+void run_prefill(llmrs_model* m, size_t start, size_t n, int n_prompt, bool write_logits, float* trace) {
+  ensure_prefill(m);
+  const llmrs_model_config& c = m->c;
+  const size_t rowf = (size_t)(c.n_layers + 1) * c.hidden;
+  float* tdev = nullptr;
+  if (trace) {
+    LLMRS_HIP(hipMalloc(&tdev, std::min<size_t>(n, m->pf_cap) * rowf * sizeof(float)));
+  }
+  try {
+    for (size_t done = 0; done < n;) {
+      const int M = (int)std::min<size_t>(m->pf_cap, n - done);
+      const bool last = done + M == n;
+      const int s0 = (int)(start + done);
+      LLMRS_HIP(hipMemcpyAsync(m->pf_start, &s0, sizeof(int), hipMemcpyHostToDevice, ctx().stream));
+      set_state(m, start + done + M - 1, n_prompt);  // synchronises the stream
+      Launcher L{ctx().stream};
+      enqueue_prefill(m, L, start + done, M, last, write_logits && last, tdev);
+      if (trace) {
+        LLMRS_HIP(hipMemcpyAsync(trace + done * rowf, tdev, (size_t)M * rowf * sizeof(float),
+                                 hipMemcpyDeviceToHost, ctx().stream));
+        LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+      }
+      done += M;
+    }
+  } catch (...) {
+    if (tdev) (void)hipFree(tdev);
+    throw;
+  }
+  if (tdev) {
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    (void)hipFree(tdev);
+  }
 }
 
 // The persistent decode kernel for this model, its LDS and grid: as many
@@ -739,9 +911,13 @@ int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n, size_t 
     LLMRS_REQUIRE(start_pos + n <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "positions beyond max_seq");
     const size_t H = m->c.hidden, L = m->c.n_layers;
     upload_tokens(m, start_pos, tokens, n);
-    set_state(m, start_pos, INT_MAX);
     hipStream_t s = ctx().stream;
-    for (size_t i = 0; i < n; ++i) {
+    const bool batched = n > 1 && prefill_enabled();
+    if (batched)
+      run_prefill(m, start_pos, n, INT_MAX, logits != nullptr, trace);
+    else
+      set_state(m, start_pos, INT_MAX);
+    for (size_t i = 0; i < n && !batched; ++i) {
       m->host_pos = start_pos + i;
       Launcher Ln{s};
       enqueue_step(m, Ln, logits && i + 1 == n, trace ? m->trace : nullptr);
@@ -769,7 +945,9 @@ int llmrs_model_begin(llmrs_model* m, const int32_t* prompt, size_t n_prompt) {
     upload_tokens(m, 0, prompt, n_prompt);
     set_state(m, 0, (int)n_prompt);
     m->host_n_prompt = (int)n_prompt;
-    if (m->pk_grid) {
+    if (n_prompt > 1 && prefill_enabled()) {
+      run_prefill(m, 0, n_prompt, (int)n_prompt, false, nullptr);
+    } else if (m->pk_grid) {
       run_persistent(m, 0, n_prompt, false);
     } else {
       for (size_t p = 0; p < n_prompt; ++p) {
@@ -823,39 +1001,80 @@ int llmrs_model_generate(llmrs_model* m, const int32_t* prompt, size_t n_prompt,
   return LLMRS_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Runs `body` with an event-recording launcher, then reports each launch's
+// name, duration and recorded work figure.  Returns the number reported.
+template <class F>
+int profile_launches(F&& body, char* names, float* ms, double* work, int cap) {
+  std::vector<std::tuple<std::string, double, hipEvent_t, hipEvent_t>> rec;
+  Launcher L{ctx().stream, &rec};
+  try {
+    body(L);
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+  } catch (...) {
+    for (auto& r : rec) {
+      (void)hipEventDestroy(std::get<2>(r));
+      (void)hipEventDestroy(std::get<3>(r));
+    }
+    throw;
+  }
+  int count = 0;
+  for (auto& r : rec) {
+    float t = 0.0f;
+    (void)hipEventElapsedTime(&t, std::get<2>(r), std::get<3>(r));
+    if (count < cap) {
+      if (names) {
+        std::strncpy(names + 32 * count, std::get<0>(r).c_str(), 31);
+        names[32 * count + 31] = 0;
+      }
+      if (ms) ms[count] = t;
+      if (work) work[count] = std::get<1>(r);
+      ++count;
+    }
+    (void)hipEventDestroy(std::get<2>(r));
+    (void)hipEventDestroy(std::get<3>(r));
+  }
+  return count;
+}
+
+}  // namespace
+
+extern "C" {
+
 int llmrs_model_profile_step(llmrs_model* m, char* names, float* ms, double* bytes, int cap) {
   int count = 0;
   int rc = guard([&] {
     LLMRS_REQUIRE(m && m->begun, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
     LLMRS_REQUIRE(m->host_pos + 1 <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
-    std::vector<std::tuple<std::string, double, hipEvent_t, hipEvent_t>> rec;
-    Launcher L{ctx().stream, &rec};
-    try {
-      enqueue_step(m, L, false, nullptr);
-      LLMRS_HIP(hipStreamSynchronize(ctx().stream));
-    } catch (...) {
-      for (auto& r : rec) {
-        (void)hipEventDestroy(std::get<2>(r));
-        (void)hipEventDestroy(std::get<3>(r));
-      }
-      throw;
-    }
+    count = profile_launches([&](Launcher& L) { enqueue_step(m, L, false, nullptr); }, names, ms, bytes,
+                             cap);
     m->host_pos += 1;
-    for (auto& r : rec) {
-      float t = 0.0f;
-      (void)hipEventElapsedTime(&t, std::get<2>(r), std::get<3>(r));
-      if (count < cap) {
-        if (names) {
-          std::strncpy(names + 32 * count, std::get<0>(r).c_str(), 31);
-          names[32 * count + 31] = 0;
-        }
-        if (ms) ms[count] = t;
-        if (bytes) bytes[count] = std::get<1>(r);
-        ++count;
-      }
-      (void)hipEventDestroy(std::get<2>(r));
-      (void)hipEventDestroy(std::get<3>(r));
-    }
+  });
+  return rc ? rc : count;
+}
+
+int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n, size_t start_pos,
+                                char* names, float* ms, double* work, int cap) {
+  int count = 0;
+  int rc = guard([&] {
+    check_ready(m);
+    LLMRS_REQUIRE(tokens && n > 0, LLMRS_E_INVALID, "empty token list");
+    LLMRS_REQUIRE(start_pos + n <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "positions beyond max_seq");
+    ensure_prefill(m);
+    LLMRS_REQUIRE(n <= (size_t)m->pf_cap, LLMRS_E_RANGE, "more rows than one prefill chunk");
+    upload_tokens(m, start_pos, tokens, n);
+    const int s0 = (int)start_pos;
+    LLMRS_HIP(hipMemcpyAsync(m->pf_start, &s0, sizeof(int), hipMemcpyHostToDevice, ctx().stream));
+    set_state(m, start_pos + n - 1, INT_MAX);
+    count = profile_launches(
+        [&](Launcher& L) { enqueue_prefill(m, L, start_pos, (int)n, true, false, nullptr); }, names, ms,
+        work, cap);
+    check_err(m);
+    m->host_pos = start_pos + n;
+    m->begun = false;
   });
   return rc ? rc : count;
 }

@@ -192,6 +192,23 @@ int llmrs_matmul_transposed(const llmrs_tensor* a, const llmrs_tensor* b, llmrs_
     if (b->dtype == LLMRS_F32) {
       MatArgs g{(const float*)a->data, (const float*)b->data, (float*)o->data, (int)m, (int)k, (int)n};
       launch("matmul_t_f32", dim3(grid_for(m * n)), dim3(kBlock), 0, ctx().stream, g);
+    } else if (m > 1) {
+      // Several rows (cpu.rs:90-110): Q8_0 codes of each row, then the exact
+      // int8 GEMM, whose outputs equal the reference's bit for bit.
+      LLMRS_REQUIRE(b->wt >= 0, LLMRS_E_DTYPE, "Unsupported storage type for B in matmul_transposed");
+      LLMRS_REQUIRE(k <= 32768, LLMRS_E_INVALID, "matmul_transposed: k is limited to 32768");
+      LLMRS_REQUIRE(m <= 65535 * 128, LLMRS_E_INVALID, "matmul_transposed: too many rows");
+      hipStream_t s = ctx().stream;
+      int8_t* xq = (int8_t*)ctx().alloc.alloc(m * k);
+      float* xd = (float*)ctx().alloc.alloc(m * (k / 32) * sizeof(float));
+      PrefillRowArgs r{(const float*)a->data, nullptr, xq, xd, (int)m, (int)k, 0.0f};
+      launch("prefill_rows_q8", dim3((unsigned)m), dim3(kBlock), gemv_act_lds_host((int)k), s, r);
+      PrefillGemmArgs g{xq, xd, (const uint8_t*)b->data, b->scales, (float*)o->data, nullptr,
+                        nullptr, nullptr, (int)m, (int)n, (int)k, (int)n};
+      launch(std::string("gemm_") + wt_tag(b->wt) + "_store",
+             dim3((unsigned)((n + 127) / 128), (unsigned)((m + 127) / 128)), dim3(kBlock), 0, s, g);
+      ctx().alloc.release(xd);  // stream-ordered reuse only
+      ctx().alloc.release(xq);
     } else {
       LLMRS_REQUIRE(b->wt >= 0, LLMRS_E_DTYPE, "Unsupported storage type for B in matmul_transposed");
       GemvArgs g{};

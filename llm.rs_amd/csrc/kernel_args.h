@@ -99,6 +99,54 @@ struct EmbedArgs {
   int hidden, vocab;
 };
 
+// Prefill GEMM (prefill.hip): Y[t][r] = sum_b isum_b(t, r) * (d_w[r,b] * d_a[t,b])
+// over M token rows of Q8_0 activation codes and an [N, K] quantised weight.
+struct PrefillGemmArgs {
+  const int8_t* xq;      // [M][K] activation codes
+  const float* xd;       // [M][K/32] activation scales
+  const uint8_t* wq;     // weight codes [N][nb][B]
+  const void* ws;        // weight scales [N][nb]
+  float* y;              // [M][ldy]: GEMM out (STORE, RESID) or m (SILU, may be null)
+  const float* res;      // [M][N] residual (RESID; may alias y)
+  int8_t* yq;            // SILU: [M][N/2] codes of m
+  float* yd;             // SILU: [M][N/64] scales of m
+  int M, N, K, ldy;
+};
+
+// Prefill row kernels (prefill.hip).
+struct PrefillRowArgs {
+  const float* x;        // [M][dim] input rows
+  const float* w;        // [dim] RMSNorm weight (null: plain Q8_0)
+  int8_t* xq;            // [M][dim] codes
+  float* xd;             // [M][dim/32] scales
+  int M, dim;
+  float eps;
+};
+
+// RoPE of the projections and K/V append for positions start_pos + t.
+struct PrefillRopeArgs {
+  const float* qkv;      // [M][qkv_rows] projections
+  float* q;              // [M][nq*hd] rotated queries
+  void* kc;              // layer K cache [nkv][max_seq][hd]
+  void* vc;              // layer V cache
+  const float* rope_cos; // [max_seq][hd/2]
+  const float* rope_sin;
+  int M, nq, nkv, hd, max_seq, start_pos, qkv_rows, kv16;
+};
+
+// Causal prefill attention: query rows t at positions start_pos + t attend to
+// cache positions [0, start_pos + t].
+struct PrefillAttnArgs {
+  const float* q;        // [M][nq*hd] rotated queries
+  const void* kc;        // layer K cache [nkv][max_seq][hd]
+  const void* vc;
+  float* ctx;            // [M][nq*hd] (may be null)
+  int8_t* ctx_q;         // [M][nq*hd] Q8_0 codes of ctx
+  float* ctx_d;          // [M][nq*hd/32]
+  int M, nq, nkv, max_seq, start_pos;
+  float scale;           // fl(1 / fl(sqrt(hd)))
+};
+
 // LDS bytes of one decode-attention work item (attn_core.h: query heads,
 // padded K tile, V tile, the new row, the ticket).  Tiles are 64 positions
 // for an f16 cache and 32 for f32; at most 8 query heads per KV head.

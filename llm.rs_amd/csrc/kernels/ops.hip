@@ -130,12 +130,14 @@ extern "C" __global__ __launch_bounds__(256) void matmul_t_f32(MatArgs g) {
 
 // Embedding gather (main.rs:159-167) for the token at the device position.
 extern "C" __global__ __launch_bounds__(256) void embed_gather(EmbedArgs e) {
-  int tok = e.tokens[*e.pos_ptr];
+  // Row blockIdx.y of a chunk starting at *pos_ptr (one row when decoding).
+  int tok = e.tokens[*e.pos_ptr + blockIdx.y];
   if (tok < 0 || tok >= e.vocab) {
     if (threadIdx.x == 0 && blockIdx.x == 0) *e.err = 1;
     tok = 0;
   }
   const float* row = e.table + (size_t)tok * e.hidden;
+  float* x = e.x + (size_t)blockIdx.y * e.hidden;
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < e.hidden; i += gridDim.x * blockDim.x)
-    e.x[i] = row[i];
+    x[i] = row[i];
 }

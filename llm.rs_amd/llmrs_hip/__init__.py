@@ -94,6 +94,8 @@ _SIGS = {
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "llmrs_model_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_profile_phases": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_int]),
+    "llmrs_model_profile_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_char_p,
+                                               C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_weight_bytes": (C.c_double, [C.c_void_p]),
     "llmrs_synth_q4": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_synth_q8": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_int]),
@@ -387,6 +389,19 @@ class HipModel:
         n = _check(lib().llmrs_model_profile_step(self._h, names, _ptr(ms), _ptr(by), cap))
         raw = names.raw
         return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(by[i]))
+                for i in range(n)]
+
+    def profile_prefill(self, tokens, start_pos: int = 0, cap: int = 4096) -> list[KernelTiming]:
+        """Per-launch timing of one batched prefill chunk; `bytes` holds FLOPs
+        for the GEMM and attention launches."""
+        ids = np.ascontiguousarray(tokens, dtype=np.int32)
+        names = C.create_string_buffer(32 * cap)
+        ms = np.zeros(cap, np.float32)
+        wk = np.zeros(cap, np.float64)
+        n = _check(lib().llmrs_model_profile_prefill(self._h, _ptr(ids), ids.size, start_pos, names,
+                                                     _ptr(ms), _ptr(wk), cap))
+        raw = names.raw
+        return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(wk[i]))
                 for i in range(n)]
 
     def profile_phases(self, n_steps: int = 1) -> tuple[float, np.ndarray]:

@@ -219,6 +219,64 @@ def test_workload_greedy_stream(hip, orc, index, prompt_len, steps):
           flush=True)
 
 
+@pytest.mark.parametrize("spec", TINY[:3], ids=lambda s: s.name)
+def test_prefill_chunks_and_start_pos_exact(hip, orc, spec, monkeypatch):
+    """Batched prefill is row-independent except for causal attention over
+    the cache: chunks of 7 rows, or a prompt split at position 10 with the
+    second part at start_pos 10, give bit-identical residual streams, K/V and
+    logits to one whole-prompt batch."""
+    w = syn.make_weights(spec)
+    toks = list(syn.prompt(spec)) * 3   # a longer prompt: several chunks
+    gm = hip.HipModel(spec.config(128))
+    syn.load_model(gm, w)
+    lg, nxt, tr = gm.forward(toks, 0, trace=True)
+    kv = [gm.kv_read(l, 0, 0, len(toks)) for l in range(spec.n_layers)]
+    gm.close()
+    monkeypatch.setenv("LLMRS_PREFILL_CHUNK", "7")
+    gc = hip.HipModel(spec.config(128))
+    syn.load_model(gc, w)
+    lg7, nxt7, tr7 = gc.forward(toks, 0, trace=True)
+    assert np.array_equal(tr7, tr) and np.array_equal(lg7, lg) and nxt7 == nxt
+    for l in range(spec.n_layers):
+        for a, b in zip(gc.kv_read(l, 0, 0, len(toks)), kv[l]):
+            assert np.array_equal(a, b)
+    gc.close()
+    monkeypatch.delenv("LLMRS_PREFILL_CHUNK")
+    gs = hip.HipModel(spec.config(128))
+    syn.load_model(gs, w)
+    gs.forward(toks[:10], 0, logits=False)
+    lgs, nxts, trs = gs.forward(toks[10:], 10, trace=True)
+    assert np.array_equal(trs, tr[10:]) and np.array_equal(lgs, lg) and nxts == nxt
+    gs.close()
+
+
+@pytest.mark.parametrize("spec", TINY, ids=lambda s: s.name)
+def test_prefill_vs_row_by_row_decode(hip, orc, spec, monkeypatch):
+    """The batched prefill and the one-row-per-step decode path (the GEMV
+    kernels) agree on the residual stream within Q8 code steps and on the
+    logits within 1e-2; both agree with the oracle's batched forward."""
+    w = syn.make_weights(spec)
+    toks = syn.prompt(spec)
+    om = orc.OracleModel.from_spec(spec, max_seq=96)
+    om.load(w)
+    olg, otr = om.forward(toks, 0, all_rows=False, trace=True)
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("LLMRS_PREFILL", mode)
+        gm = hip.HipModel(spec.config(96))
+        syn.load_model(gm, w)
+        outs[mode] = gm.forward(toks, 0, trace=True)
+        gm.close()
+    for mode, (lg, _, tr) in outs.items():
+        assert np.array_equal(tr[:, 0], otr[:, 0]), f"prefill={mode}: embedding rows"
+        for li in range(1, spec.n_layers + 1):
+            e = rel_norm_err(tr[:, li], otr[:, li])
+            assert e < 1e-2, f"prefill={mode}: layer {li} residual relative error {e:.3g}"
+        assert np.max(np.abs(lg - olg)) < 1e-2, f"prefill={mode}"
+    e = rel_norm_err(outs["1"][2], outs["0"][2])
+    assert e < 1e-2, f"batched vs row-by-row residual relative error {e:.3g}"
+
+
 def test_error_paths(hip, orc):
     spec = syn.tiny(DType.Q4_0, DType.F32)
     gm, _, _ = build(hip, orc, spec, max_seq=16)

@@ -67,6 +67,41 @@ def test_gemv_q8_0(hip, orc, rng, n, k):
     assert ok, f"max err {err}, {nbad} outside tolerance"
 
 
+# (m, n, k): prompt-batch GEMMs.  m and n cover full and ragged 128-row
+# tiles; k covers one block, a partial and several 16-block scale chunks.
+GEMM_SHAPES = [(2, 64, 32), (37, 256, 4096), (200, 1000, 1024), (130, 4096, 256),
+               (129, 6144, 4096), (512, 128, 14336)]
+
+
+@pytest.mark.parametrize("wtype", ["q4_0", "q4_ref", "q8_0"])
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+def test_gemm_bit_exact(hip, orc, rng, wtype, m, n, k):
+    """M > 1 rows (cpu.rs:90-110): per-row Q8_0 codes, then per output the
+    block loop total += isum_b * (d_w * d_a) from 0.0 in block order.  The
+    int8 MFMA gives every isum_b exactly and the epilogue keeps the order, so
+    the GPU result equals the oracle bit for bit."""
+    be = hip.HipBackend()
+    a = _x(rng, m, k)
+    a[0, :32] = 0.0                  # an all-zero block (d_a = 0)
+    a[m - 1, 5] = 1e-30              # a tiny value next to the block maximum
+    if wtype == "q8_0":
+        qs, sc = hip.synth_q8(20260003, m + n + k, n, k, 2e-4, 3.5e-4)
+        w = hip.Tensor.from_q8_0(qs, sc, n, k)
+        want = orc.matmul_transposed_q8w(a, qs, sc, n)
+    else:
+        if wtype == "q4_0":
+            qs, sc = hip.synth_q4(20260004, m + n + k, n, k, 0.003, 0.006)
+        else:
+            qs, sc = orc.quantize_q4(rng.uniform(-1, 1, (n, k)).astype(F32))
+        w = hip.Tensor.from_q4(qs, sc, n, k)
+        want = orc.matmul_transposed_q4(a, qs, sc, n)
+    got = be.matmul_transposed(hip.Tensor.from_numpy(a), w).data()
+    bad = np.nonzero(got != want)
+    assert bad[0].size == 0, (
+        f"{bad[0].size} of {got.size} outputs differ; first at {bad[0][0]},{bad[1][0]}: "
+        f"{got[bad[0][0], bad[1][0]]!r} vs {want[bad[0][0], bad[1][0]]!r}")
+
+
 def test_gemv_zero_and_special_inputs(hip, orc):
     """amax == 0 blocks (d = 0) and a NaN input element (code 0)."""
     be = hip.HipBackend()
