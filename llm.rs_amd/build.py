@@ -23,9 +23,13 @@ ARCH = "gfx950"
 
 # -ffp-contract=off keeps a*b+c as two roundings, as in the reference (Rust
 # never contracts).  Packed FP32 instructions are disabled for all device code.
+# MFMA results go to ordinary VGPRs (-amdgpu-mfma-vgpr-form): the prefill
+# GEMM's epilogue reads every MFMA result once, and accumulation registers
+# would cost a copy instruction per element.
 HIP_FLAGS = [
     "--genco", f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 HOST_FLAGS = [
     "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-mf16c",

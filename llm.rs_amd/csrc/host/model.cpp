@@ -332,6 +332,7 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
                                  hipMemcpyDeviceToDevice, L.s));
   };
   auto flops = [](double a, double b, double k) { return 2.0 * a * b * k; };
+  const size_t glds = gemm_lds_bytes();
 
   EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab};
   L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), blk, 0, e);
@@ -349,7 +350,7 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
     {  // Q|K|V
       PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.qkv.codes, Lb.qkv.scales, m->pf_qkv, nullptr,
                         nullptr, nullptr, M, QR, H, QR};
-      L(gemm_kernel(m, "store"), flops(M, QR, H), gemm_grid(M, QR), blk, 0, g);
+      L(gemm_kernel(m, "store"), flops(M, QR, H), gemm_grid(M, QR), blk, glds, g);
     }
     {  // RoPE + K/V append
       PrefillRopeArgs r{m->pf_qkv, m->pf_q, Lb.kc, Lb.vc, m->rope_cos, m->rope_sin, M, nq, nkv, hd,
@@ -366,7 +367,7 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
     {  // O projection + residual (layer.rs:386)
       PrefillGemmArgs g{m->pf_ctx_q, m->pf_ctx_d, Lb.o.codes, Lb.o.scales, m->pf_h, m->pf_x,
                         nullptr, nullptr, M, H, qd, H};
-      L(gemm_kernel(m, "resid"), flops(M, H, qd), gemm_grid(M, H), blk, 0, g);
+      L(gemm_kernel(m, "resid"), flops(M, H, qd), gemm_grid(M, H), blk, glds, g);
     }
     {  // post-attention RMSNorm + Q8_0
       PrefillRowArgs r{m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, M, H, c.rms_eps};
@@ -375,12 +376,12 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
     {  // gate|up + SiLU + Q8_0 of m (layer.rs:40-89)
       PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.gu.codes, Lb.gu.scales, nullptr, nullptr,
                         m->pf_m_q, m->pf_m_d, M, 2 * F, H, F};
-      L(gemm_kernel(m, "silu"), flops(M, 2 * F, H), gemm_grid(M, 2 * F), blk, 0, g);
+      L(gemm_kernel(m, "silu"), flops(M, 2 * F, H), gemm_grid(M, 2 * F), blk, glds, g);
     }
     {  // down projection + residual (layer.rs:403)
       PrefillGemmArgs g{m->pf_m_q, m->pf_m_d, Lb.down.codes, Lb.down.scales, m->pf_x, m->pf_h,
                         nullptr, nullptr, M, H, F, H};
-      L(gemm_kernel(m, "resid"), flops(M, H, F), gemm_grid(M, H), blk, 0, g);
+      L(gemm_kernel(m, "resid"), flops(M, H, F), gemm_grid(M, H), blk, glds, g);
     }
   }
   trace(c.n_layers);

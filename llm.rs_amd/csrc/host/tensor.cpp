@@ -206,7 +206,8 @@ int llmrs_matmul_transposed(const llmrs_tensor* a, const llmrs_tensor* b, llmrs_
       PrefillGemmArgs g{xq, xd, (const uint8_t*)b->data, b->scales, (float*)o->data, nullptr,
                         nullptr, nullptr, (int)m, (int)n, (int)k, (int)n};
       launch(std::string("gemm_") + wt_tag(b->wt) + "_store",
-             dim3((unsigned)((n + 127) / 128), (unsigned)((m + 127) / 128)), dim3(kBlock), 0, s, g);
+             dim3((unsigned)((n + 127) / 128), (unsigned)((m + 127) / 128)), dim3(kBlock),
+             gemm_lds_bytes(), s, g);
       ctx().alloc.release(xd);  // stream-ordered reuse only
       ctx().alloc.release(xq);
     } else {

@@ -7,19 +7,24 @@
 //   y[t][r] = (...((0 + isum_0 * s_0) + isum_1 * s_1) + ...),  s_b = d_w[r,b] * d_a[t,b]
 // with isum_b the exact int32 dot product of one 32-element block.
 //
-// gemm_*: one v_mfma_i32_32x32x32_i8 per 32-block gives isum_b for a 32 x 32
-// (token x row) tile exactly; the epilogue applies the reference's scale and
-// f32 accumulation in the same block order, so every GEMM output is
-// bit-identical to the reference for identical activation codes.  The f32
-// epilogue (convert, two multiplies, add per element and block) is the
-// kernel's bottleneck, not the MFMA: four VALU operations per 32 MACs.
+// gemm_*: per 32-element block and 32 x 32 (token x row) tile, one
+// v_mfma_i32_32x32x32_i8 gives every isum_b exactly, and one
+// v_mfma_f32_32x32x2_f32 with the k = 1 operands zero gives every scale
+// s_b = d_w * d_a as a single IEEE product (round to nearest even, the same
+// value as the reference's f32 multiply).  The epilogue per element and
+// block is then the reference's own two roundings, total = total + isum * s,
+// in block order, so every output is bit-identical to the reference for
+// identical activation codes.  Three VALU operations per element and block
+// (convert, multiply, add) bound the kernel, not the MFMA.
 //
 // Workgroup tile 128 tokens x 128 rows, four waves of 64 x 64 (2 x 2 MFMA
-// tiles).  Operands come straight from global memory (the token rows and
-// weight rows are L2-resident across the grid): lane l reads the 16 codes
-// k = 16*(l/32) .. +15 of token / weight row l % 32 for each block; Q4 codes
-// become (q - 8) bytes with ((q | 0x80) - 8) ^ 0x80.  Activation scales are
-// staged in LDS 16 blocks at a time.
+// tiles).  Operands are staged in LDS four blocks at a time, double-buffered:
+// the global loads of stage s+1 are issued before stage s is computed and
+// written to LDS after it, so their latency hides behind a whole stage.
+// LDS layouts make each MFMA operand read conflict-free: 16-byte chunk
+// (c, token) lives at c * 128 + (token ^ c), so the 32 lanes of a half-wave
+// read 32 distinct consecutive chunks.  Q4 codes become (q - 8) bytes with
+// ((q | 0x80) - 8) ^ 0x80.
 #include "attn_core.h"
 #include "gemv_core.h"
 
@@ -27,58 +32,170 @@ using namespace llmrs;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 namespace {
 
+#ifndef LLMRS_GEMM_SCALE_MFMA
+#define LLMRS_GEMM_SCALE_MFMA 1  // d_w * d_a on the f32 MFMA (else on the VALU)
+#endif
+#ifndef LLMRS_GEMM_WAVES
+#define LLMRS_GEMM_WAVES 2    // workgroups per CU the register budget allows
+#endif
 constexpr int kBM = 128, kBN = 128;  // workgroup tile (tokens x rows)
-constexpr int kKCH = 16;             // blocks of activation scales per LDS chunk
+constexpr int kKB = 4;               // 32-element blocks per pipeline stage
 
 // 16 Q4 codes (low or high nibbles of a 16-byte block) as int8 (q - 8).
+// Branch-free: the half-wave selects its nibble with a per-lane shift.
 __device__ __forceinline__ v4i q4_bytes(u32x4 w, int high) {
-  const unsigned M = 0x0F0F0F0Fu;
-  u32x4 q;
-  if (high) q = u32x4{(w.x >> 4) & M, (w.y >> 4) & M, (w.z >> 4) & M, (w.w >> 4) & M};
-  else q = u32x4{w.x & M, w.y & M, w.z & M, w.w & M};
+  const unsigned M = 0x0F0F0F0Fu, sh = 4u * (unsigned)high;
+  const u32x4 q = u32x4{(w.x >> sh) & M, (w.y >> sh) & M, (w.z >> sh) & M, (w.w >> sh) & M};
   // per byte: ((q + 128) - 8) - 128 without borrows between bytes
   const u32x4 r = ((q | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
   return v4i{(int)r.x, (int)r.y, (int)r.z, (int)r.w};
 }
 
+// LDS of one pipeline stage (bytes): activation codes and weight codes as
+// int8 in 16-byte chunks, chunk (c, i) at c * 128 + i for c = 2 b + h (codes
+// 16 h .. 16 h + 15 of block b) and token / row i, then f32 scales
+// d_w [kKB][kBN] and d_a [kKB][kBM].  A half-wave's MFMA operand read is 32
+// consecutive chunks (conflict-free); staging writes are the strided side.
+struct GemmStage {
+  static constexpr int A = 0;
+  static constexpr int B = A + 2 * kKB * kBM * 16;
+  static constexpr int DW = B + 2 * kKB * kBN * 16;
+  static constexpr int DA = DW + kKB * kBN * 4;
+  static constexpr int BYTES = DA + kKB * kBM * 4;
+};
+
 template <int WT>
-__device__ __forceinline__ void load_b(const PrefillGemmArgs& a, const uint8_t* row, size_t srow,
-                                       int b, int high, v4i& bv, float& dw) {
-  if (WT == WT_Q8H) {
-    const i32x4 v = *(const i32x4*)(row + (size_t)b * 32 + 16 * high);
-    bv = v4i{v.x, v.y, v.z, v.w};
-  } else {
-    bv = q4_bytes(*(const u32x4*)(row + (size_t)b * 16), high);
-  }
-  dw = wscale<WT>(load_wscale_raw<WT>(a.ws, srow + b));
-}
+struct GemmLoads {
+  static constexpr int BCH = WT == WT_Q8H ? 2 : 1;             // 16-byte chunks per weight block
+  static constexpr int A_PER_T = 2 * kKB * kBM / 256;          // activation chunks per thread
+  static constexpr int B_PER_T = kKB * BCH * kBN / 256;        // weight chunks per thread
+  static constexpr int S_PER_T = kKB * kBN / 256;              // scales per thread (d_w and d_a)
+};
+
+// MFMA operands of one block for a wave's 2 x 2 tiles.
+struct GemmOps {
+  v4i A[2], B[2];
+  float da[2], dw[2];
+#if !LLMRS_GEMM_SCALE_MFMA
+  f32x4 dav[2][4];  // d_a of the lane's 16 tokens per token tile
+#endif
+};
 
 }  // namespace
 
 template <int WT, int EPI>
-__device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a) {
-  constexpr int BS = WT == WT_Q8H ? 32 : 16;
-  __shared__ float s_da[kKCH][kBM];
+__device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds) {
+  typedef GemmStage S;
+  typedef GemmLoads<WT> G;
+  constexpr int BCH = G::BCH;
   const int lane = lane_id(), wave = wave_id(), tid = threadIdx.x;
   const int half = lane >> 5, col = lane & 31;
   const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const int nb = a.K >> 5;
+  const int nstage = (nb + kKB - 1) / kKB;
+  const unsigned kmask = half ? 0u : ~0u;  // lanes 32..63 hold the k = 1 scale operands
 
-  const int8_t* arow[2];
-  const uint8_t* brow[2];
-  size_t srow[2];
+  // ---- staging: global -> registers -> LDS -------------------------------
+  // activation chunk q: token q / (2 kKB), c = q % (2 kKB); weight chunk q:
+  // row q / (kKB BCH), chunk q % (kKB BCH) of that row's stage bytes;
+  // scales: (token | row) q / kKB, block q % kKB.  Scales stay raw until the
+  // LDS write, so nothing waits on the loads before the stage's compute.
+  i32x4 ra[G::A_PER_T], rb[G::B_PER_T];
+  unsigned rdw[G::S_PER_T];
+  float rda[G::S_PER_T];
+  auto load_stage = [&](int st) {
+    const int b0 = st * kKB;
+#pragma unroll
+    for (int j = 0; j < G::A_PER_T; ++j) {
+      const int q = tid + 256 * j;
+      const int tok = min(m0 + q / (2 * kKB), a.M - 1);
+      const int c = q % (2 * kKB);
+      const int blk = min(b0 + c / 2, nb - 1);
+      ra[j] = *(const i32x4*)(a.xq + (size_t)tok * a.K + (size_t)blk * 32 + 16 * (c & 1));
+    }
+#pragma unroll
+    for (int j = 0; j < G::B_PER_T; ++j) {
+      const int q = tid + 256 * j;
+      const int row = min(n0 + q / (kKB * BCH), a.N - 1);
+      const int c = q % (kKB * BCH);
+      const int blk = min(b0 + c / BCH, nb - 1);
+      rb[j] = *(const i32x4*)(a.wq + ((size_t)row * nb + blk) * (16 * BCH) + 16 * (c % BCH));
+    }
+#pragma unroll
+    for (int j = 0; j < G::S_PER_T; ++j) {
+      const int q = tid + 256 * j;
+      const int blk = min(b0 + q % kKB, nb - 1);
+      const int row = min(n0 + q / kKB, a.N - 1);
+      const size_t si = (size_t)row * nb + blk;
+      rdw[j] = WT == WT_Q4F ? ((const unsigned*)a.ws)[si] : ((const uint16_t*)a.ws)[si];
+      const int tok = min(m0 + q / kKB, a.M - 1);
+      rda[j] = a.xd[(size_t)tok * nb + blk];
+    }
+  };
+  auto store_stage = [&](int buf) {
+    uint8_t* base = lds + buf * S::BYTES;
+#pragma unroll
+    for (int j = 0; j < G::A_PER_T; ++j) {
+      const int q = tid + 256 * j;
+      const int tok = q / (2 * kKB), c = q % (2 * kKB);
+      *(i32x4*)(base + S::A + (c * kBM + tok) * 16) = ra[j];
+    }
+#pragma unroll
+    for (int j = 0; j < G::B_PER_T; ++j) {
+      const int q = tid + 256 * j;
+      const int row = q / (kKB * BCH), c = q % (kKB * BCH);
+      if (WT == WT_Q8H) {
+        *(i32x4*)(base + S::B + (c * kBN + row) * 16) = rb[j];
+      } else {  // one Q4 block: low nibbles are codes 0..15, high 16..31
+        const u32x4 w = u32x4{(unsigned)rb[j].x, (unsigned)rb[j].y, (unsigned)rb[j].z, (unsigned)rb[j].w};
+        const v4i lo = q4_bytes(w, 0), hi = q4_bytes(w, 1);
+        *(v4i*)(base + S::B + ((2 * c) * kBN + row) * 16) = lo;
+        *(v4i*)(base + S::B + ((2 * c + 1) * kBN + row) * 16) = hi;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < G::S_PER_T; ++j) {
+      const int q = tid + 256 * j;
+      const int b = q % kKB, r = q / kKB;
+      ((float*)(base + S::DW))[b * kBN + r] = wscale<WT>(rdw[j]);
+      ((float*)(base + S::DA))[b * kBM + r] = rda[j];
+    }
+  };
+
+  // ---- compute -------------------------------------------------------------
+  // Per-lane LDS offsets of the operands (the block adds a constant).
+  int offA[2], offB[2], offDA[2], offDW[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int tok = min(m0 + wm + 32 * t + col, a.M - 1);
-    arow[t] = a.xq + (size_t)tok * a.K + 16 * half;
-    const int r = min(n0 + wn + 32 * t + col, a.N - 1);
-    brow[t] = a.wq + (size_t)r * nb * BS;
-    srow[t] = (size_t)r * nb;
+    offA[t] = S::A + (half * kBM + wm + 32 * t + col) * 16;
+    offB[t] = S::B + (half * kBN + wn + 32 * t + col) * 16;
+    offDA[t] = S::DA + (wm + 32 * t + col) * 4;
+    offDW[t] = S::DW + (wn + 32 * t + col) * 4;
   }
+  auto load_ops = [&](const uint8_t* base, int b, GemmOps& o) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const i32x4 va = *(const i32x4*)(base + offA[t] + b * (2 * kBM * 16));
+      o.A[t] = v4i{va.x, va.y, va.z, va.w};
+      const i32x4 vb = *(const i32x4*)(base + offB[t] + b * (2 * kBN * 16));
+      o.B[t] = v4i{vb.x, vb.y, vb.z, vb.w};
+      // k = 1 operands of the scale product are zero
+#if LLMRS_GEMM_SCALE_MFMA
+      o.da[t] = __uint_as_float(*(const unsigned*)(base + offDA[t] + b * (kBM * 4)) & kmask);
+      o.dw[t] = __uint_as_float(*(const unsigned*)(base + offDW[t] + b * (kBN * 4)) & kmask);
+#else
+      o.dw[t] = *(const float*)(base + offDW[t] + b * (kBN * 4));
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        o.dav[t][g] = *(const f32x4*)(base + S::DA + b * (kBM * 4) + (wm + 32 * t + 8 * g + 4 * half) * 4);
+#endif
+    }
+  };
 
   float acc[2][2][16];
 #pragma unroll
@@ -87,63 +204,83 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a) {
     for (int r = 0; r < 2; ++r)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[t][r][i] = 0.0f;
-
-  // operands of the next block, loaded one block ahead
-  v4i An[2], Bn[2];
-  float dwn[2];
+  auto epi = [&](int t, int r, const v16i& p, const v16f& sc) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    An[t] = *(const v4i*)(arow[t]);
-    load_b<WT>(a, brow[t], srow[t], 0, half, Bn[t], dwn[t]);
-  }
-
-  for (int b0 = 0; b0 < nb; b0 += kKCH) {
-    __syncthreads();  // the previous chunk of scales is consumed
-    for (int i = tid; i < kKCH * kBM; i += kThreads) {
-      const int kb = i / kBM, t = i % kBM;
-      const int tok = min(m0 + t, a.M - 1);
-      s_da[kb][t] = (b0 + kb < nb) ? a.xd[(size_t)tok * nb + b0 + kb] : 0.0f;
+    for (int i = 0; i < 16; ++i)  // cpu.rs:913,932: total += isum * (d_w * d_a)
+      acc[t][r][i] = acc[t][r][i] + (float)p[i] * sc[i];
+  };
+#if !LLMRS_GEMM_SCALE_MFMA
+  auto epi_v = [&](int t, int r, const v16i& p, const GemmOps& o) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const f32x4 d4 = o.dav[t][i / 4];
+      const float da = (i % 4 == 0) ? d4.x : (i % 4 == 1) ? d4.y : (i % 4 == 2) ? d4.z : d4.w;
+      acc[t][r][i] = acc[t][r][i] + (float)p[i] * (o.dw[r] * da);
     }
+  };
+#endif
+
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  for (int st = 0; st < nstage; ++st) {
+    if (st + 1 < nstage) load_stage(st + 1);
+    const uint8_t* base = lds + (st & 1) * S::BYTES;
+    const int kvalid = min(kKB, nb - st * kKB);
+    if (kvalid == kKB) {
+      // Software pipeline over the stage's 4 kKB tiles k = 4 b + 2 t + r:
+      // the MFMAs of tile k+1 are issued before the VALU work of tile k, and
+      // the operands of block b+1 are read while block b is in flight.
+      GemmOps o[2];
+      v16i P[2];
+      v16f SC[2];
+      load_ops(base, 0, o[0]);
+      P[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o[0].A[0], o[0].B[0], v16i{}, 0, 0, 0);
+#if LLMRS_GEMM_SCALE_MFMA
+      SC[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o[0].da[0], o[0].dw[0], v16f{}, 0, 0, 0);
+#endif
+#pragma unroll
+      for (int k = 0; k < 4 * kKB; ++k) {
+        const int b = k / 4, t = (k / 2) % 2, r = k % 2;
+        if (k % 4 == 0 && b + 1 < kKB) load_ops(base, b + 1, o[(b + 1) % 2]);
+        if (k + 1 < 4 * kKB) {
+          const int kn = k + 1;
+          const GemmOps& on = o[(kn / 4) % 2];
+          P[kn % 2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(on.A[(kn / 2) % 2], on.B[kn % 2], v16i{}, 0, 0, 0);
+#if LLMRS_GEMM_SCALE_MFMA
+          SC[kn % 2] = __builtin_amdgcn_mfma_f32_32x32x2f32(on.da[(kn / 2) % 2], on.dw[kn % 2], v16f{}, 0, 0, 0);
+#endif
+        }
+#if LLMRS_GEMM_SCALE_MFMA
+        epi(t, r, P[k % 2], SC[k % 2]);
+#else
+        epi_v(t, r, P[k % 2], o[b % 2]);
+#endif
+      }
+    } else {
+      for (int b = 0; b < kvalid; ++b) {
+        GemmOps o;
+        load_ops(base, b, o);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.A[t], o.B[r], v16i{}, 0, 0, 0);
+#if LLMRS_GEMM_SCALE_MFMA
+            const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(o.da[t], o.dw[r], v16f{}, 0, 0, 0);
+            epi(t, r, p, sc);
+#else
+            epi_v(t, r, p, o);
+#endif
+          }
+      }
+    }
+    if (st + 1 < nstage) store_stage((st + 1) & 1);
     __syncthreads();
-    const int kend = min(kKCH, nb - b0);
-    for (int kb = 0; kb < kend; ++kb) {
-      const int b = b0 + kb;
-      v4i A[2] = {An[0], An[1]}, B[2] = {Bn[0], Bn[1]};
-      const float dw[2] = {dwn[0], dwn[1]};
-      if (b + 1 < nb) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          An[t] = *(const v4i*)(arow[t] + (size_t)(b + 1) * 32);
-          load_b<WT>(a, brow[t], srow[t], b + 1, half, Bn[t], dwn[t]);
-        }
-      }
-      v16i p[2][2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 2; ++r) p[t][r] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[t], B[r], v16i{}, 0, 0, 0);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        // token of register i: 8*(i/4) + 4*half + i%4 within the 32-token tile
-        float da[16];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 v = *(const f32x4*)&s_da[kb][wm + 32 * t + 8 * g + 4 * half];
-          da[4 * g] = v.x;
-          da[4 * g + 1] = v.y;
-          da[4 * g + 2] = v.z;
-          da[4 * g + 3] = v.w;
-        }
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)  // cpu.rs:913,932: total += isum * (d_w * d_a)
-            acc[t][r][i] = acc[t][r][i] + (float)p[t][r][i] * (dw[r] * da[i]);
-      }
-    }
   }
 
-  // Epilogues.
+  // Epilogues.  Register i of a tile holds token 8 (i / 4) + 4 half + i % 4
+  // and row col.
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -181,9 +318,12 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a) {
   }
 }
 
+// Dynamic LDS: two pipeline stages, gemm_lds_bytes(weights) at launch.
+static_assert(2 * GemmStage::BYTES == gemm_lds_bytes(), "GEMM LDS size");
 #define LLMRS_GEMM(name, WT, EPI)                                                 \
-  extern "C" __global__ __launch_bounds__(kThreads) void name(PrefillGemmArgs a) { \
-    gemm_impl<WT, EPI>(a);                                                        \
+  extern "C" __global__ __launch_bounds__(kThreads, LLMRS_GEMM_WAVES) void name(PrefillGemmArgs a) { \
+    extern __shared__ __align__(16) uint8_t gemm_lds[];                            \
+    gemm_impl<WT, EPI>(a, gemm_lds);                                              \
   }
 LLMRS_GEMM(gemm_q4h_store, WT_Q4H, EPI_STORE)
 LLMRS_GEMM(gemm_q4h_resid, WT_Q4H, EPI_RESID)

@@ -138,7 +138,8 @@ def init(device: int = 0) -> None:
     """llmrs_init: select the GPU and load the gfx950 code objects."""
     global _initialised
     if not _initialised:
-        _check(lib().llmrs_init(device, str(LIB_DIR).encode()))
+        hsaco = os.environ.get("LLMRS_HSACO_DIR", str(LIB_DIR))  # alternate code objects
+        _check(lib().llmrs_init(device, hsaco.encode()))
         _initialised = True
 
 
