@@ -337,7 +337,12 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
   EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab};
   L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), blk, 0, e);
   const float scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
-  const std::string attn = "attn_prefill_hd" + std::to_string(hd) + (kv16 ? "_f16" : "_f32");
+  // f16 caches use the matrix-core kernel (LLMRS_PREFILL_ATTN=valu selects the
+  // vector kernel, which also serves f32 caches)
+  const char* pa = std::getenv("LLMRS_PREFILL_ATTN");
+  const bool mfma_attn = kv16 && !(pa && std::string(pa) == "valu");
+  const std::string attn = mfma_attn ? "attn_prefill_mfma_hd" + std::to_string(hd)
+                                     : "attn_prefill_hd" + std::to_string(hd) + (kv16 ? "_f16" : "_f32");
   // causal score and P.V products over the chunk
   const double attn_flops = 4.0 * nq * hd * ((double)M * start + (double)M * (M + 1) / 2.0);
   for (int li = 0; li < c.n_layers; ++li) {
@@ -362,7 +367,10 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
     {  // causal attention
       PrefillAttnArgs a{m->pf_q, Lb.kc, Lb.vc, nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq, nkv,
                         c.max_seq, (int)start, scale};
-      L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nq), blk, 0, a);
+      if (mfma_attn)
+        L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nkv), blk, 0, a);
+      else
+        L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nq), blk, 0, a);
     }
     {  // O projection + residual (layer.rs:386)
       PrefillGemmArgs g{m->pf_ctx_q, m->pf_ctx_d, Lb.o.codes, Lb.o.scales, m->pf_h, m->pf_x,

@@ -553,6 +553,187 @@ __device__ __forceinline__ void attn_prefill_impl(const PrefillAttnArgs& a) {
   }
 }
 
+// Causal prefill attention on the matrix cores, f16 K/V cache.  One
+// workgroup per (32-query tile, KV group); wave w takes query head
+// g * n_rep + w (+4, +8, ... for larger groups), so the four waves share each
+// staged K/V tile.  Per key tile of 32:
+//   S^T = K Q^T        (v_mfma_f32_32x32x16_f16; q split into f16 hi + lo,
+//                       so the products carry ~22 bits of q, as in f32)
+//   online softmax      one query per lane column: row max / sum over the
+//                       lane's 16 keys and its partner lane's 16
+//   O^T += V^T P^T      (P split into f16 hi + lo; keys taken in the order
+//                       the S^T registers hold them, V^T staged to match)
+// The causal mask keeps key j <= start_pos + t (layer.rs:264-266).  Query
+// tiles run longest-first.  ctx is written as Q8_0 (and f32 when asked).
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+template <int HD>
+struct AttnMfmaLds {
+  static constexpr int KT = 32;                 // keys per tile
+  static constexpr int KROW = HD * 2 + 16;      // padded K row (bytes)
+  static constexpr int VROW = KT * 2 + 8;       // padded V^T row (bytes)
+  static constexpr int K = 0;
+  static constexpr int V = K + KT * KROW;
+  static constexpr int BYTES = V + HD * VROW;
+};
+
+template <int HD>
+__device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a) {
+  typedef AttnMfmaLds<HD> LY;
+  constexpr int NS = HD / 16, ND = HD / 32, KT = LY::KT;
+  __shared__ __align__(16) uint8_t lds[LY::BYTES];
+  const int lane = lane_id(), wave = wave_id(), tid = threadIdx.x;
+  const int h2 = lane >> 5, col = lane & 31;
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * 32, g = blockIdx.y;  // longest tiles first
+  const int n_rep = a.nq / a.nkv;
+  const int qdim = a.nq * HD;
+  const uint16_t* kc = (const uint16_t*)a.kc + (size_t)g * a.max_seq * HD;
+  const uint16_t* vc = (const uint16_t*)a.vc + (size_t)g * a.max_seq * HD;
+  const int kend = a.start_pos + min(q0 + 32, a.M);  // keys [0, kend)
+  const int ntile = (kend + KT - 1) / KT;
+  const int myq = q0 + col;
+  const int qpos = a.start_pos + myq;
+
+  for (int rp = 0; rp < n_rep; rp += 4) {
+    const int r = rp + wave;
+    const bool active = r < n_rep;  // wave-uniform
+    const int h = g * n_rep + min(r, n_rep - 1);
+    v8h qh[NS], ql[NS];
+    {
+      const float* qrow = a.q + (size_t)min(myq, a.M - 1) * qdim + (size_t)h * HD;
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) {
+        const f32x4 x0 = *(const f32x4*)(qrow + 16 * sl + 8 * h2);
+        const f32x4 x1 = *(const f32x4*)(qrow + 16 * sl + 8 * h2 + 4);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const _Float16 hi = (_Float16)xv[j];
+          qh[sl][j] = hi;
+          ql[sl][j] = (_Float16)(xv[j] - (float)hi);
+        }
+      }
+    }
+    v16f o[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) o[d] = v16f{};
+    float m = -INFINITY, l = 0.0f;
+
+    for (int kt = 0; kt < ntile; ++kt) {
+      __syncthreads();  // the previous tile is consumed
+      // K rows [key][HD] and V^T [HD][key] of keys kt*32 .. +31 (clamped;
+      // keys past kend are masked below)
+      for (int c = tid; c < KT * HD / 8; c += 256) {
+        const int key = c / (HD / 8), part = c % (HD / 8);
+        const size_t src = (size_t)min(kt * KT + key, kend - 1) * HD + part * 8;
+        *(u32x4*)(lds + LY::K + key * LY::KROW + part * 16) = *(const u32x4*)(kc + src);
+        const u32x4 v = *(const u32x4*)(vc + src);
+        const unsigned vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          *(uint16_t*)(lds + LY::V + (part * 8 + j) * LY::VROW + key * 2) =
+              (uint16_t)(vw[j / 2] >> (16 * (j % 2)));
+      }
+      __syncthreads();
+      if (!active) continue;
+      // S^T: lane holds keys kt*32 + 8(i/4) + 4 h2 + i%4 for query col
+      v16f st = v16f{};
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) {
+        const v8h kop = *(const v8h*)(lds + LY::K + col * LY::KROW + (16 * sl + 8 * h2) * 2);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qh[sl], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, ql[sl], st, 0, 0, 0);
+      }
+      float p[16];
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kt * KT + 8 * (i / 4) + 4 * h2 + (i % 4);
+        p[i] = key <= qpos ? st[i] * a.scale : -INFINITY;
+        mloc = fmaxf(mloc, p[i]);
+      }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+      const float mn = fmaxf(m, mloc);  // finite: key 0 is in every query's range
+      const float corr = m == -INFINITY ? 0.0f : expf(m - mn);
+      float lsum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        p[i] = p[i] == -INFINITY ? 0.0f : expf(p[i] - mn);
+        lsum += p[i];
+      }
+      lsum += __shfl_xor(lsum, 32);
+      l = l * corr + lsum;
+      m = mn;
+#pragma unroll
+      for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[d][i] *= corr;
+      // O^T += V^T P^T over the two 16-key slices
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        v8h ph, pl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float x = p[8 * s2 + j];
+          const _Float16 hi = (_Float16)x;
+          ph[j] = hi;
+          pl[j] = (_Float16)(x - (float)hi);
+        }
+#pragma unroll
+        for (int d = 0; d < ND; ++d) {
+          const uint8_t* vrow = lds + LY::V + (32 * d + col) * LY::VROW;
+          const v4h v0 = *(const v4h*)(vrow + (16 * s2 + 4 * h2) * 2);
+          const v4h v1 = *(const v4h*)(vrow + (16 * s2 + 8 + 4 * h2) * 2);
+          const v8h vop = v8h{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, ph, o[d], 0, 0, 0);
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pl, o[d], 0, 0, 0);
+        }
+      }
+    }
+    if (!active) continue;
+    // o[d][i] = O[query col][dim 32 d + 8 (i/4) + 4 h2 + i%4] * l
+    const float inv_l = 1.0f / l;
+    const bool write = myq < a.M;
+    const size_t base = (size_t)min(myq, a.M - 1) * qdim + (size_t)h * HD;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      float v[16];
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        v[i] = o[d][i] * inv_l;
+        amax = fmaxf(amax, fabsf(v[i]));
+      }
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      const float dq = amax / 127.0f;
+      const float inv = amax == 0.0f ? 0.0f : 1.0f / dq;
+      if (write) {
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const size_t e = base + 32 * d + 8 * gq + 4 * h2;
+          unsigned w = 0;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int q8 = amax == 0.0f ? 0 : q8_code(v[4 * gq + c], inv);
+            w |= ((unsigned)q8 & 0xFFu) << (8 * c);
+          }
+          *(unsigned*)(a.ctx_q + e) = w;
+          if (a.ctx) *(f32x4*)(a.ctx + e) = f32x4{v[4 * gq], v[4 * gq + 1], v[4 * gq + 2], v[4 * gq + 3]};
+        }
+        if (h2 == 0) a.ctx_d[base / 32 + d] = amax == 0.0f ? 0.0f : dq;
+      }
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void attn_prefill_mfma_hd64(PrefillAttnArgs a) {
+  attn_prefill_mfma_impl<64>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void attn_prefill_mfma_hd128(PrefillAttnArgs a) {
+  attn_prefill_mfma_impl<128>(a);
+}
+
 #define LLMRS_ATTN_PREFILL(name, HD, KV16)                                        \
   extern "C" __global__ __launch_bounds__(256) void name(PrefillAttnArgs a) {   \
     attn_prefill_impl<HD, KV16>(a);                                             \

@@ -277,6 +277,34 @@ def test_prefill_vs_row_by_row_decode(hip, orc, spec, monkeypatch):
     assert e < 1e-2, f"batched vs row-by-row residual relative error {e:.3g}"
 
 
+@pytest.mark.parametrize("spec", [TINY[1], TINY[2], TINY[4]], ids=lambda s: s.name)
+def test_prefill_attention_mfma_vs_vector(hip, orc, spec, monkeypatch):
+    """f16 caches: the matrix-core prefill attention (f16 hi+lo operand
+    splits, f32 accumulation) and the f32 vector kernel give the same
+    residual streams within Q8 code steps, and both follow the oracle."""
+    w = syn.make_weights(spec)
+    toks = list(syn.prompt(spec)) * 5   # 40 rows: two query tiles, a ragged one
+    om = orc.OracleModel.from_spec(spec, max_seq=64)
+    om.load(w)
+    olg, otr = om.forward(toks, 0, all_rows=False, trace=True)
+    outs = {}
+    for mode in ("mfma", "valu"):
+        monkeypatch.setenv("LLMRS_PREFILL_ATTN", mode)
+        gm = hip.HipModel(spec.config(64))
+        syn.load_model(gm, w)
+        outs[mode] = gm.forward(toks, 0, trace=True)
+        gm.close()
+    env, _ = oracle_envelope(orc, spec, w, toks, 0, max_seq=64)
+    for mode, (lg, _, tr) in outs.items():
+        for li in range(1, spec.n_layers + 1):
+            e = rel_norm_err(tr[:, li], otr[:, li])
+            assert e < 1e-2, f"{mode}: layer {li} residual relative error {e:.3g}"
+        err = float(np.max(np.abs(lg - olg)))
+        assert err < max(1e-2, ENVELOPE * env), f"{mode}: logits error {err:.3g}, envelope {env:.3g}"
+    e = rel_norm_err(outs["mfma"][2], outs["valu"][2])
+    assert e < 1e-2, f"mfma vs vector attention: residual relative error {e:.3g}"
+
+
 def test_error_paths(hip, orc):
     spec = syn.tiny(DType.Q4_0, DType.F32)
     gm, _, _ = build(hip, orc, spec, max_seq=16)
