@@ -5,9 +5,17 @@ a 512-token random prompt, then 256 greedy decode steps (warmup + timed).
 value = decode tok/s over the timed steps, weights resident in HBM.
 
 roofline: the dominant kernel (gate|up dequant-GEMV) - algorithmic bytes per
-launch over its mean duration from HIP events on the model's stream.
+launch over its mean launch duration, timed with HIP events on the model's
+stream around the gate|up GEMV of every layer launched back to back
+(llmrs_model_time_linear).  traffic: HBM bytes per launch from the committed
+rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.json), each
+counter scaled by its reading for a known 256 MiB scale_f32 pass.
 cpu_baseline: the CPU oracle (C++ restatement of the reference CPU backend)
 on a bounded sample of the same workload, timed on this host.
+
+--workload 3: the 2048-token batched prefill of the same 8B model instead
+(prefill tok/s; roofline against the int8 MFMA peak).
+--traffic-probe: the dispatches the rocprofv3 --pmc runs measure.
 """
 from __future__ import annotations
 
@@ -31,6 +39,17 @@ PREFILL_METRIC = "prefill tok/s (8B-shape Q4_0, one 2048-token prompt) + GEMM MF
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def hbm_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    rocprofv3 counter summary, or None when it holds no entry."""
+    path = REPO / "profiles" / "hbm_traffic.json"
+    try:
+        e = json.loads(path.read_text())[workload][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return e["fetch_kib"] * 1024 * e["fetch_scale"] + e["write_kib"] * 1024 * e["write_scale"]
 
 
 def cpu_baseline(spec, w, seconds: float) -> dict:
@@ -162,6 +181,31 @@ def bench_prefill(args, lh, syn) -> int:
     return 0
 
 
+def traffic_probe(args, lh, syn) -> int:
+    """Dispatches for HBM-traffic counters: two eager decode steps (every
+    decode kernel once each) and a scale_f32 pass over 64 Mi floats, whose
+    FETCH_SIZE / WRITE_SIZE readings calibrate the counters (each ideally
+    256 MiB)."""
+    import numpy as np
+    spec = syn.with_sizes(syn.WORKLOADS[args.workload], prompt=16, decode=8)
+    lh.init(0)
+    model = lh.HipModel(spec.config(64))
+    syn.stream_model(model, spec)
+    model.begin(syn.prompt(spec))
+    model.decode_steps(2)
+    lh.sync()
+    for _ in range(2):
+        model.profile_step()
+    lh.sync()
+    n = 64 << 20
+    x = lh.Tensor.from_numpy(np.ones((n // 4096, 4096), np.float32))
+    lh.HipBackend().scale(x, 1.0)
+    lh.sync()
+    print(json.dumps({"probe": "traffic", "workload": spec.name, "calibration_kernel": "scale_f32",
+                      "calibration_read_bytes": 4 * n, "calibration_write_bytes": 4 * n}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +216,9 @@ def main() -> int:
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: eager decode steps of the workload, then one "
+                         "256 MiB scale_f32 pass (reads and writes 256 MiB) that calibrates the counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs on one GPU; multi-GPU figures are not produced "
@@ -183,6 +230,8 @@ def main() -> int:
     import llmrs_hip as lh
     from llmrs_hip import synthetic as syn
 
+    if args.traffic_probe:
+        return traffic_probe(args, lh, syn)
     prefill_only = syn.WORKLOADS[args.workload].decode == 0
     if args.steps is None:
         args.steps = 5 if prefill_only else 240
@@ -253,9 +302,13 @@ def main() -> int:
     tot = sum(ms for ms, _, _ in per.values())
     for name, (ms, _, _) in per.items():
         kernels[name]["share"] = round(ms / tot, 4)
-    dom = max((n for n in kernels if n.startswith("gemv_")), key=lambda n: per[n][0])
-    ms, by, n = per[dom]
-    achieved = by / n / (ms / n / 1e3) / 1e9
+    # The dominant kernel: the gate|up GEMV, timed back to back over all layers.
+    dom = next(n for n in kernels if n.startswith("gemv_") and "_norm_silu_" in n)
+    gu_us, gu_bytes = model.time_linear(lh.W_GATE, reps=4)
+    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    traffic = hbm_traffic(f"{spec.name} decode", dom)
+    log(f"{dom}: {gu_us:.2f} us per launch, {achieved:.0f} GB/s; HBM traffic per launch "
+        f"{traffic if traffic is None else round(traffic / 1e6, 2)} MB")
     wbytes = model.weight_bytes()
     roof_tok_s = HBM_PEAK_GBS * 1e9 / wbytes
 
@@ -277,8 +330,8 @@ def main() -> int:
                    "decode_steps": args.warmup + args.steps, "batch": 1},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "bytes_per_launch": round(by / n), "avg_us": round(ms / n * 1e3, 2),
-                     "traffic": None},
+                     "bytes_per_launch": round(gu_bytes), "avg_us": round(gu_us, 2),
+                     "traffic": None if traffic is None else round(traffic)},
         "cpu_baseline": cpu,
         "decode_roofline_tok_s": round(roof_tok_s, 1),
         "frac_of_decode_roofline": round(value / roof_tok_s, 4),

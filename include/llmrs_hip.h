@@ -220,6 +220,15 @@ int llmrs_model_tokens(llmrs_model* m, int32_t* out, size_t count);
  * launch.  Returns the number of launches recorded (>= 0) or an error. */
 int llmrs_model_profile_step(llmrs_model* m, char* names, float* ms,
                              double* bytes, int cap);
+/* Mean duration of one decode GEMV launch: the `slot` GEMV (LLMRS_W_Q = the
+ * stacked Q|K|V rows, LLMRS_W_O, LLMRS_W_GATE = gate|up, LLMRS_W_DOWN) of
+ * every layer in turn, `reps` times back to back between two HIP events on
+ * the model's stream (each launch streams a different layer's weights, as
+ * in decoding).  Uses the decode activation buffers as they are (scratch
+ * that the next step recomputes).  Also returns the launch's algorithmic
+ * bytes.  Requires llmrs_model_begin. */
+int llmrs_model_time_linear(llmrs_model* m, int slot, int reps, double* us_per_launch,
+                            double* bytes_per_launch);
 /* Per-kernel timing of one batched prefill of `n` tokens (n at most one
  * chunk, 2048 rows by default) at positions [start_pos, start_pos+n), as in
  * llmrs_model_forward.  Same outputs as llmrs_model_profile_step, with

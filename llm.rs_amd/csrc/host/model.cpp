@@ -153,10 +153,78 @@ double linear_weight_bytes(const llmrs_model* m, const DevLinear& L) {
 
 void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits);
 
+// The decode GEMV of one linear slot of layer li (LLMRS_W_Q = the stacked
+// Q|K|V rows, LLMRS_W_O, LLMRS_W_GATE = gate|up, LLMRS_W_DOWN) with its fused
+// prologue and epilogue, on the decode activation buffers.
+void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot) {
+  const llmrs_model_config& c = m->c;
+  const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, F = c.ffn;
+  const int cus = ctx().num_cus;
+  LayerBufs& Lb = m->layers[li];
+  GemvArgs g{};
+  const char* kind = nullptr;
+  double bytes = 0.0;
+  switch (slot) {
+    case LLMRS_W_Q:  // Q|K|V, RMSNorm prologue (layer.rs:378)
+      g.wq = Lb.qkv.codes;
+      g.ws = Lb.qkv.scales;
+      g.n = Lb.qkv.n;
+      g.k = H;
+      g.x = m->x;
+      g.norm_w = Lb.norm[0];
+      g.eps = c.rms_eps;
+      g.y = m->qkv;
+      kind = "norm_store";
+      bytes = linear_weight_bytes(m, Lb.qkv) + 8.0 * H + 4.0 * g.n;
+      break;
+    case LLMRS_W_O:  // O projection + residual (layer.rs:386)
+      g.wq = Lb.o.codes;
+      g.ws = Lb.o.scales;
+      g.n = H;
+      g.k = nq * hd;
+      g.xq = m->ctx_q;
+      g.xd = m->ctx_d;
+      g.y = m->h;
+      g.res = m->x;
+      kind = "q8_resid";
+      bytes = linear_weight_bytes(m, Lb.o) + 1.125 * g.k + 8.0 * H;
+      break;
+    case LLMRS_W_GATE:  // gate|up + SiLU (layer.rs:40-89, 400)
+      g.wq = Lb.gu.codes;
+      g.ws = Lb.gu.scales;
+      g.n = 2 * F;
+      g.k = H;
+      g.x = m->h;
+      g.norm_w = Lb.norm[1];
+      g.eps = c.rms_eps;
+      g.y = m->mf;
+      g.yq = m->m_q;
+      g.yd = m->m_d;
+      kind = "norm_silu";
+      bytes = linear_weight_bytes(m, Lb.gu) + 8.0 * H + 5.125 * F;
+      break;
+    case LLMRS_W_DOWN:  // down projection + residual (layer.rs:403)
+      g.wq = Lb.down.codes;
+      g.ws = Lb.down.scales;
+      g.n = H;
+      g.k = F;
+      g.xq = m->m_q;
+      g.xd = m->m_d;
+      g.y = m->x;
+      g.res = m->h;
+      kind = "q8_resid";
+      bytes = linear_weight_bytes(m, Lb.down) + 1.125 * F + 8.0 * H;
+      break;
+    default:
+      fail(LLMRS_E_INVALID, "enqueue_linear: slot must be Q, O, GATE or DOWN");
+  }
+  const GemvPlan p = gemv_plan(m->wt, kind, g.n, g.k, cus);
+  L(p.name, bytes, dim3(p.grid), dim3(256), p.lds, g);
+}
+
 void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
   const llmrs_model_config& c = m->c;
-  const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
-  const int cus = ctx().num_cus;
+  const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
 
   EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, H, c.vocab};
   L("embed_gather", 8.0 * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
@@ -169,19 +237,7 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
     if (trace_dev)
       LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)li * H, m->x, H * sizeof(float),
                                hipMemcpyDeviceToDevice, L.s));
-    {  // Q|K|V
-      GemvArgs g{};
-      g.wq = Lb.qkv.codes;
-      g.ws = Lb.qkv.scales;
-      g.n = Lb.qkv.n;
-      g.k = H;
-      g.x = m->x;
-      g.norm_w = Lb.norm[0];
-      g.eps = c.rms_eps;
-      g.y = m->qkv;
-      const GemvPlan p = gemv_plan(m->wt, "norm_store", g.n, g.k, cus);
-      L(p.name, linear_weight_bytes(m, Lb.qkv) + 8.0 * H + 4.0 * g.n, dim3(p.grid), dim3(256), p.lds, g);
-    }
+    enqueue_linear(m, L, li, LLMRS_W_Q);
     {  // attention
       AttnArgs a{};
       a.qkv = m->qkv;
@@ -204,47 +260,9 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
       const double kvb = 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
       L(attn, kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(256), 0, a);
     }
-    {  // O projection + residual
-      GemvArgs g{};
-      g.wq = Lb.o.codes;
-      g.ws = Lb.o.scales;
-      g.n = H;
-      g.k = nq * hd;
-      g.xq = m->ctx_q;
-      g.xd = m->ctx_d;
-      g.y = m->h;
-      g.res = m->x;
-      const GemvPlan p = gemv_plan(m->wt, "q8_resid", g.n, g.k, cus);
-      L(p.name, linear_weight_bytes(m, Lb.o) + 1.125 * g.k + 8.0 * H, dim3(p.grid), dim3(256), p.lds, g);
-    }
-    {  // gate|up + SiLU
-      GemvArgs g{};
-      g.wq = Lb.gu.codes;
-      g.ws = Lb.gu.scales;
-      g.n = 2 * F;
-      g.k = H;
-      g.x = m->h;
-      g.norm_w = Lb.norm[1];
-      g.eps = c.rms_eps;
-      g.y = m->mf;
-      g.yq = m->m_q;
-      g.yd = m->m_d;
-      const GemvPlan p = gemv_plan(m->wt, "norm_silu", g.n, g.k, cus);
-      L(p.name, linear_weight_bytes(m, Lb.gu) + 8.0 * H + 5.125 * F, dim3(p.grid), dim3(256), p.lds, g);
-    }
-    {  // down projection + residual
-      GemvArgs g{};
-      g.wq = Lb.down.codes;
-      g.ws = Lb.down.scales;
-      g.n = H;
-      g.k = F;
-      g.xq = m->m_q;
-      g.xd = m->m_d;
-      g.y = m->x;
-      g.res = m->h;
-      const GemvPlan p = gemv_plan(m->wt, "q8_resid", g.n, g.k, cus);
-      L(p.name, linear_weight_bytes(m, Lb.down) + 1.125 * F + 8.0 * H, dim3(p.grid), dim3(256), p.lds, g);
-    }
+    enqueue_linear(m, L, li, LLMRS_W_O);
+    enqueue_linear(m, L, li, LLMRS_W_GATE);
+    enqueue_linear(m, L, li, LLMRS_W_DOWN);
   }
   if (trace_dev)
     LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)c.n_layers * H, m->x, H * sizeof(float),
@@ -368,7 +386,7 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
       PrefillAttnArgs a{m->pf_q, Lb.kc, Lb.vc, nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq, nkv,
                         c.max_seq, (int)start, scale};
       if (mfma_attn)
-        L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nkv), blk, 0, a);
+        L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nkv), dim3(512), 0, a);
       else
         L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nq), blk, 0, a);
     }
@@ -1063,6 +1081,39 @@ int llmrs_model_profile_step(llmrs_model* m, char* names, float* ms, double* byt
     m->host_pos += 1;
   });
   return rc ? rc : count;
+}
+
+int llmrs_model_time_linear(llmrs_model* m, int slot, int reps, double* us_per_launch,
+                            double* bytes_per_launch) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && m->begun, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
+    LLMRS_REQUIRE(us_per_launch && reps > 0, LLMRS_E_INVALID, "null argument or reps < 1");
+    hipStream_t s = ctx().stream;
+    std::vector<std::tuple<std::string, double, hipEvent_t, hipEvent_t>> rec;
+    Launcher probe{s, &rec};
+    enqueue_linear(m, probe, 0, slot);  // validates the slot; records the bytes
+    LLMRS_HIP(hipStreamSynchronize(s));
+    const double bytes = std::get<1>(rec[0]);
+    for (auto& r : rec) {
+      (void)hipEventDestroy(std::get<2>(r));
+      (void)hipEventDestroy(std::get<3>(r));
+    }
+    hipEvent_t e0, e1;
+    LLMRS_HIP(hipEventCreate(&e0));
+    LLMRS_HIP(hipEventCreate(&e1));
+    Launcher L{s};
+    LLMRS_HIP(hipEventRecord(e0, s));
+    for (int r = 0; r < reps; ++r)
+      for (int li = 0; li < m->c.n_layers; ++li) enqueue_linear(m, L, li, slot);
+    LLMRS_HIP(hipEventRecord(e1, s));
+    LLMRS_HIP(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *us_per_launch = ms * 1e3 / ((double)reps * m->c.n_layers);
+    if (bytes_per_launch) *bytes_per_launch = bytes;
+  });
 }
 
 int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n, size_t start_pos,

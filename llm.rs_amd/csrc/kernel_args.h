@@ -114,9 +114,9 @@ struct PrefillGemmArgs {
 };
 
 // Dynamic LDS of the prefill GEMM: two pipeline stages of 4 blocks, each
-// activation and weight codes (int8) 2 x 128 x 128 B, f32 scales 2 x 2 KB.
+// activation and weight codes (int8) 2 x 128 x 128 B, f32 scales 2 x 4 x 132.
 constexpr size_t gemm_lds_bytes() {
-  return 2 * ((size_t)2 * 4 * 128 * 16 * 2 + (size_t)4 * 128 * 4 * 2);
+  return 2 * ((size_t)2 * 4 * 128 * 16 * 2 + (size_t)4 * 132 * 4 * 2);
 }
 
 // Prefill row kernels (prefill.hip).

@@ -56,16 +56,19 @@ __device__ __forceinline__ v4i q4_bytes(u32x4 w, int high) {
 }
 
 // LDS of one pipeline stage (bytes): activation codes and weight codes as
-// int8 in 16-byte chunks, chunk (c, i) at c * 128 + i for c = 2 b + h (codes
-// 16 h .. 16 h + 15 of block b) and token / row i, then f32 scales
-// d_w [kKB][kBN] and d_a [kKB][kBM].  A half-wave's MFMA operand read is 32
-// consecutive chunks (conflict-free); staging writes are the strided side.
+// int8 in 16-byte chunks, chunk (c, i) at c * 128 + (i ^ c) for c = 2 b + h
+// (codes 16 h .. 16 h + 15 of block b) and token / row i, then f32 scales
+// d_w [kKB][SW] and d_a [kKB][SW] (rows padded by 4).  A half-wave's MFMA
+// operand read is a permutation of 32 consecutive chunks, and the XOR and
+// the padding spread the staging writes (8 chunks of one token, 4 scales of
+// one row) over distinct banks.
 struct GemmStage {
   static constexpr int A = 0;
   static constexpr int B = A + 2 * kKB * kBM * 16;
   static constexpr int DW = B + 2 * kKB * kBN * 16;
-  static constexpr int DA = DW + kKB * kBN * 4;
-  static constexpr int BYTES = DA + kKB * kBM * 4;
+  static constexpr int SW = kBN + 4;            // padded scale row (floats)
+  static constexpr int DA = DW + kKB * SW * 4;
+  static constexpr int BYTES = DA + kKB * SW * 4;
 };
 
 template <int WT>
@@ -143,27 +146,27 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds
     for (int j = 0; j < G::A_PER_T; ++j) {
       const int q = tid + 256 * j;
       const int tok = q / (2 * kKB), c = q % (2 * kKB);
-      *(i32x4*)(base + S::A + (c * kBM + tok) * 16) = ra[j];
+      *(i32x4*)(base + S::A + (c * kBM + (tok ^ c)) * 16) = ra[j];
     }
 #pragma unroll
     for (int j = 0; j < G::B_PER_T; ++j) {
       const int q = tid + 256 * j;
       const int row = q / (kKB * BCH), c = q % (kKB * BCH);
       if (WT == WT_Q8H) {
-        *(i32x4*)(base + S::B + (c * kBN + row) * 16) = rb[j];
+        *(i32x4*)(base + S::B + (c * kBN + (row ^ c)) * 16) = rb[j];
       } else {  // one Q4 block: low nibbles are codes 0..15, high 16..31
         const u32x4 w = u32x4{(unsigned)rb[j].x, (unsigned)rb[j].y, (unsigned)rb[j].z, (unsigned)rb[j].w};
         const v4i lo = q4_bytes(w, 0), hi = q4_bytes(w, 1);
-        *(v4i*)(base + S::B + ((2 * c) * kBN + row) * 16) = lo;
-        *(v4i*)(base + S::B + ((2 * c + 1) * kBN + row) * 16) = hi;
+        *(v4i*)(base + S::B + ((2 * c) * kBN + (row ^ (2 * c))) * 16) = lo;
+        *(v4i*)(base + S::B + ((2 * c + 1) * kBN + (row ^ (2 * c + 1))) * 16) = hi;
       }
     }
 #pragma unroll
     for (int j = 0; j < G::S_PER_T; ++j) {
       const int q = tid + 256 * j;
       const int b = q % kKB, r = q / kKB;
-      ((float*)(base + S::DW))[b * kBN + r] = wscale<WT>(rdw[j]);
-      ((float*)(base + S::DA))[b * kBM + r] = rda[j];
+      ((float*)(base + S::DW))[b * S::SW + r] = wscale<WT>(rdw[j]);
+      ((float*)(base + S::DA))[b * S::SW + r] = rda[j];
     }
   };
 
@@ -172,27 +175,28 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds
   int offA[2], offB[2], offDA[2], offDW[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    offA[t] = S::A + (half * kBM + wm + 32 * t + col) * 16;
-    offB[t] = S::B + (half * kBN + wn + 32 * t + col) * 16;
+    offA[t] = S::A + (half * kBM + wm + 32 * t) * 16;  // + (col ^ c) per block
+    offB[t] = S::B + (half * kBN + wn + 32 * t) * 16;
     offDA[t] = S::DA + (wm + 32 * t + col) * 4;
     offDW[t] = S::DW + (wn + 32 * t + col) * 4;
   }
   auto load_ops = [&](const uint8_t* base, int b, GemmOps& o) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const i32x4 va = *(const i32x4*)(base + offA[t] + b * (2 * kBM * 16));
+      const int cx = (col ^ half) ^ (2 * b);  // token / row swizzle of chunk c = 2 b + half
+      const i32x4 va = *(const i32x4*)(base + offA[t] + (b * (2 * kBM) + cx) * 16);
       o.A[t] = v4i{va.x, va.y, va.z, va.w};
-      const i32x4 vb = *(const i32x4*)(base + offB[t] + b * (2 * kBN * 16));
+      const i32x4 vb = *(const i32x4*)(base + offB[t] + (b * (2 * kBN) + cx) * 16);
       o.B[t] = v4i{vb.x, vb.y, vb.z, vb.w};
       // k = 1 operands of the scale product are zero
 #if LLMRS_GEMM_SCALE_MFMA
-      o.da[t] = __uint_as_float(*(const unsigned*)(base + offDA[t] + b * (kBM * 4)) & kmask);
-      o.dw[t] = __uint_as_float(*(const unsigned*)(base + offDW[t] + b * (kBN * 4)) & kmask);
+      o.da[t] = __uint_as_float(*(const unsigned*)(base + offDA[t] + b * (S::SW * 4)) & kmask);
+      o.dw[t] = __uint_as_float(*(const unsigned*)(base + offDW[t] + b * (S::SW * 4)) & kmask);
 #else
-      o.dw[t] = *(const float*)(base + offDW[t] + b * (kBN * 4));
+      o.dw[t] = *(const float*)(base + offDW[t] + b * (S::SW * 4));
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        o.dav[t][g] = *(const f32x4*)(base + S::DA + b * (kBM * 4) + (wm + 32 * t + 8 * g + 4 * half) * 4);
+        o.dav[t][g] = *(const f32x4*)(base + S::DA + b * (S::SW * 4) + (wm + 32 * t + 8 * g + 4 * half) * 4);
 #endif
     }
   };
@@ -554,17 +558,21 @@ __device__ __forceinline__ void attn_prefill_impl(const PrefillAttnArgs& a) {
 }
 
 // Causal prefill attention on the matrix cores, f16 K/V cache.  One
-// workgroup per (32-query tile, KV group); wave w takes query head
-// g * n_rep + w (+4, +8, ... for larger groups), so the four waves share each
-// staged K/V tile.  Per key tile of 32:
+// workgroup of 8 waves per (32-query tile, KV group): wave w takes query head
+// g * n_rep + w % 4 (+4, +8, ... for larger groups) and key stream w / 4,
+// which covers the even or odd key tiles, so the four heads share each
+// staged K/V tile and the two streams halve the serial path of long tiles.
+// Per key tile of 32:
 //   S^T = K Q^T        (v_mfma_f32_32x32x16_f16; q split into f16 hi + lo,
 //                       so the products carry ~22 bits of q, as in f32)
 //   online softmax      one query per lane column: row max / sum over the
-//                       lane's 16 keys and its partner lane's 16
+//                       lane's 16 keys and its partner lane's 16; exp as
+//                       exp2 of log2(e)-scaled scores
 //   O^T += V^T P^T      (P split into f16 hi + lo; keys taken in the order
 //                       the S^T registers hold them, V^T staged to match)
-// The causal mask keeps key j <= start_pos + t (layer.rs:264-266).  Query
-// tiles run longest-first.  ctx is written as Q8_0 (and f32 when asked).
+// The two streams' (max, sum, O) are merged through LDS at the end.  The
+// causal mask keeps key j <= start_pos + t (layer.rs:264-266).  Query tiles
+// run longest-first.  ctx is written as Q8_0 (and f32 when asked).
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
@@ -575,16 +583,22 @@ struct AttnMfmaLds {
   static constexpr int VROW = KT * 2 + 8;       // padded V^T row (bytes)
   static constexpr int K = 0;
   static constexpr int V = K + KT * KROW;
-  static constexpr int BYTES = V + HD * VROW;
+  static constexpr int TILE = V + HD * VROW;    // one staged tile
+  static constexpr int BYTES = 2 * TILE;        // the even and odd tiles
+  // merge area (reuses the tiles): per head, lane: 16 O values of one pass + m, l
+  static constexpr int MERGE = 4 * 64 * 18 * 4;
+  static_assert(MERGE <= BYTES, "merge area fits in the tile buffers");
 };
 
 template <int HD>
 __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a) {
   typedef AttnMfmaLds<HD> LY;
   constexpr int NS = HD / 16, ND = HD / 32, KT = LY::KT;
+  constexpr float kLog2e = 1.4426950408889634f;
   __shared__ __align__(16) uint8_t lds[LY::BYTES];
   const int lane = lane_id(), wave = wave_id(), tid = threadIdx.x;
   const int h2 = lane >> 5, col = lane & 31;
+  const int hw = wave & 3, stream = wave >> 2;
   const int q0 = (gridDim.x - 1 - blockIdx.x) * 32, g = blockIdx.y;  // longest tiles first
   const int n_rep = a.nq / a.nkv;
   const int qdim = a.nq * HD;
@@ -592,11 +606,13 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
   const uint16_t* vc = (const uint16_t*)a.vc + (size_t)g * a.max_seq * HD;
   const int kend = a.start_pos + min(q0 + 32, a.M);  // keys [0, kend)
   const int ntile = (kend + KT - 1) / KT;
+  const int npair = (ntile + 1) / 2;
   const int myq = q0 + col;
   const int qpos = a.start_pos + myq;
+  const float sl2 = a.scale * kLog2e;
 
   for (int rp = 0; rp < n_rep; rp += 4) {
-    const int r = rp + wave;
+    const int r = rp + hw;
     const bool active = r < n_rep;  // wave-uniform
     const int h = g * n_rep + min(r, n_rep - 1);
     v8h qh[NS], ql[NS];
@@ -618,30 +634,50 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
     v16f o[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d) o[d] = v16f{};
-    float m = -INFINITY, l = 0.0f;
+    float m = -INFINITY, l = 0.0f;  // m in the log2 domain
 
-    for (int kt = 0; kt < ntile; ++kt) {
-      __syncthreads();  // the previous tile is consumed
-      // K rows [key][HD] and V^T [HD][key] of keys kt*32 .. +31 (clamped;
-      // keys past kend are masked below)
-      for (int c = tid; c < KT * HD / 8; c += 256) {
-        const int key = c / (HD / 8), part = c % (HD / 8);
-        const size_t src = (size_t)min(kt * KT + key, kend - 1) * HD + part * 8;
-        *(u32x4*)(lds + LY::K + key * LY::KROW + part * 16) = *(const u32x4*)(kc + src);
-        const u32x4 v = *(const u32x4*)(vc + src);
-        const unsigned vw[4] = {v.x, v.y, v.z, v.w};
+    // K rows [key][HD] and V^T [HD][key] of tile pair (2i, 2i+1): thread
+    // chunk c < 2 * 32 * HD / 8 = (tile c / (32 HD / 8), key, part); keys
+    // clamped (those past kend are masked below).  Loaded a pair ahead.
+    constexpr int CPT = 2 * KT * HD / 8 / 512;
+    u32x4 rk[CPT], rv[CPT];
+    auto fetch = [&](int pr) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          *(uint16_t*)(lds + LY::V + (part * 8 + j) * LY::VROW + key * 2) =
-              (uint16_t)(vw[j / 2] >> (16 * (j % 2)));
+      for (int j = 0; j < CPT; ++j) {
+        const int c = tid + 512 * j;
+        const int t = c / (KT * HD / 8), cc = c % (KT * HD / 8);
+        const int key = cc / (HD / 8), part = cc % (HD / 8);
+        const size_t src = (size_t)min((2 * pr + t) * KT + key, kend - 1) * HD + part * 8;
+        rk[j] = *(const u32x4*)(kc + src);
+        rv[j] = *(const u32x4*)(vc + src);
+      }
+    };
+    fetch(0);
+    for (int pr = 0; pr < npair; ++pr) {
+      __syncthreads();  // the previous pair is consumed
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        const int c = tid + 512 * j;
+        const int t = c / (KT * HD / 8), cc = c % (KT * HD / 8);
+        const int key = cc / (HD / 8), part = cc % (HD / 8);
+        uint8_t* tb = lds + t * LY::TILE;
+        *(u32x4*)(tb + LY::K + key * LY::KROW + part * 16) = rk[j];
+        const unsigned vw[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *(uint16_t*)(tb + LY::V + (part * 8 + e) * LY::VROW + key * 2) =
+              (uint16_t)(vw[e / 2] >> (16 * (e % 2)));
       }
       __syncthreads();
-      if (!active) continue;
+      if (pr + 1 < npair) fetch(pr + 1);
+      const int kt = 2 * pr + stream;
+      if (!active || kt >= ntile) continue;
+      const uint8_t* tb = lds + stream * LY::TILE;
       // S^T: lane holds keys kt*32 + 8(i/4) + 4 h2 + i%4 for query col
       v16f st = v16f{};
 #pragma unroll
       for (int sl = 0; sl < NS; ++sl) {
-        const v8h kop = *(const v8h*)(lds + LY::K + col * LY::KROW + (16 * sl + 8 * h2) * 2);
+        const v8h kop = *(const v8h*)(tb + LY::K + col * LY::KROW + (16 * sl + 8 * h2) * 2);
         st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, qh[sl], st, 0, 0, 0);
         st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop, ql[sl], st, 0, 0, 0);
       }
@@ -650,16 +686,19 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int key = kt * KT + 8 * (i / 4) + 4 * h2 + (i % 4);
-        p[i] = key <= qpos ? st[i] * a.scale : -INFINITY;
+        p[i] = key <= qpos ? st[i] * sl2 : -INFINITY;
         mloc = fmaxf(mloc, p[i]);
       }
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-      const float mn = fmaxf(m, mloc);  // finite: key 0 is in every query's range
-      const float corr = m == -INFINITY ? 0.0f : expf(m - mn);
+      // The stream's first tile holds a key <= qpos for every query (key 0
+      // or, for stream 1, key 32 <= qpos whenever that tile is reached with
+      // an unmasked key); a fully masked tile keeps mn = m.
+      const float mn = fmaxf(m, mloc);
+      const float corr = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
       float lsum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        p[i] = p[i] == -INFINITY ? 0.0f : expf(p[i] - mn);
+        p[i] = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(p[i] - mn);
         lsum += p[i];
       }
       lsum += __shfl_xor(lsum, 32);
@@ -682,7 +721,7 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
         }
 #pragma unroll
         for (int d = 0; d < ND; ++d) {
-          const uint8_t* vrow = lds + LY::V + (32 * d + col) * LY::VROW;
+          const uint8_t* vrow = tb + LY::V + (32 * d + col) * LY::VROW;
           const v4h v0 = *(const v4h*)(vrow + (16 * s2 + 4 * h2) * 2);
           const v4h v1 = *(const v4h*)(vrow + (16 * s2 + 8 + 4 * h2) * 2);
           const v8h vop = v8h{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
@@ -691,7 +730,34 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
         }
       }
     }
-    if (!active) continue;
+    // Merge stream 1 into stream 0 through LDS, one 32-dim block at a time.
+    float* mg = (float*)lds + (hw * 64 + lane) * 18;
+    float m1 = -INFINITY, l1 = 0.0f, c0 = 1.0f, c1 = 0.0f;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      __syncthreads();  // tiles (or the previous block) consumed
+      if (stream == 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mg[i] = o[d][i];
+        mg[16] = m;
+        mg[17] = l;
+      }
+      __syncthreads();
+      if (stream == 0) {
+        if (d == 0) {
+          m1 = mg[16];
+          l1 = mg[17];
+          const float mm = fmaxf(m, m1);  // finite: stream 0 saw key 0
+          c0 = __builtin_amdgcn_exp2f(m - mm);
+          c1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+          l = l * c0 + l1 * c1;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[d][i] = o[d][i] * c0 + mg[i] * c1;
+      }
+    }
+    __syncthreads();  // merge reads done before the next pass stages tiles
+    if (!active || stream != 0) continue;
     // o[d][i] = O[query col][dim 32 d + 8 (i/4) + 4 h2 + i%4] * l
     const float inv_l = 1.0f / l;
     const bool write = myq < a.M;
@@ -727,10 +793,10 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void attn_prefill_mfma_hd64(PrefillAttnArgs a) {
+extern "C" __global__ __launch_bounds__(512) void attn_prefill_mfma_hd64(PrefillAttnArgs a) {
   attn_prefill_mfma_impl<64>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void attn_prefill_mfma_hd128(PrefillAttnArgs a) {
+extern "C" __global__ __launch_bounds__(512) void attn_prefill_mfma_hd128(PrefillAttnArgs a) {
   attn_prefill_mfma_impl<128>(a);
 }
 

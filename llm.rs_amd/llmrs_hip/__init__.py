@@ -94,6 +94,7 @@ _SIGS = {
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "llmrs_model_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_profile_phases": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_int]),
+    "llmrs_model_time_linear": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "llmrs_model_profile_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_char_p,
                                                C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_weight_bytes": (C.c_double, [C.c_void_p]),
@@ -391,6 +392,14 @@ class HipModel:
         raw = names.raw
         return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(by[i]))
                 for i in range(n)]
+
+    def time_linear(self, slot: int, reps: int = 4) -> tuple[float, float]:
+        """(us per launch, algorithmic bytes per launch) of one decode GEMV
+        slot over every layer, back to back."""
+        us = np.zeros(1, np.float64)
+        by = np.zeros(1, np.float64)
+        _check(lib().llmrs_model_time_linear(self._h, slot, reps, _ptr(us), _ptr(by)))
+        return float(us[0]), float(by[0])
 
     def profile_prefill(self, tokens, start_pos: int = 0, cap: int = 4096) -> list[KernelTiming]:
         """Per-launch timing of one batched prefill chunk; `bytes` holds FLOPs
