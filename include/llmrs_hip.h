@@ -241,7 +241,9 @@ int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
  * steps in one launch and returns in `us` (up to `cap` values): the launch
  * wall time per step, then for each layer of the first step ten intervals
  * seen by workgroup 0 - QKV work, barrier wait, attention work, wait, O work,
- * wait, gate|up work, wait, down work, wait (layer 0's QKV interval is 0).
+ * wait, gate|up work, wait, down work, wait (layer 0's QKV interval is 0);
+ * then, for layer 1, each workgroup's ten phase timestamps (us after the end
+ * of workgroup 0's layer 0), as far as `cap` allows.
  * Returns the number of values written or an error. */
 int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int cap);
 /* Algorithmic weight bytes streamed per decode token (all linear weights). */

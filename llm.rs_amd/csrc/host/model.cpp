@@ -1146,7 +1146,7 @@ int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int c
     LLMRS_REQUIRE(m->pk_grid, LLMRS_E_INVALID, "the persistent decode kernel is not in use");
     LLMRS_REQUIRE(n_steps >= 1 && m->host_pos + n_steps <= (size_t)m->c.max_seq, LLMRS_E_RANGE,
                   "decode beyond max_seq");
-    const size_t nts = (size_t)m->c.n_layers * 10;
+    const size_t nts = (size_t)m->c.n_layers * 10 + (size_t)m->pk_grid * 10;
     unsigned long long* ts = nullptr;
     LLMRS_HIP(hipMalloc(&ts, nts * sizeof(unsigned long long)));
     hipEvent_t e0, e1;
@@ -1176,6 +1176,14 @@ int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int c
         const unsigned long long a = i == 0 ? prev : t[i - 1];
         us[count++] = (double)(t[i] - a) / 100.0;
       }
+    }
+    // then, for layer 1, every workgroup's ten timestamps relative to the
+    // end of workgroup 0's layer-0 block
+    if (m->c.n_layers > 1) {
+      const unsigned long long t0 = h[9];
+      for (size_t w = 0; w < m->pk_grid; ++w)
+        for (int i = 0; i < 10 && count < cap; ++i)
+          us[count++] = ((double)h[(size_t)m->c.n_layers * 10 + w * 10 + i] - (double)t0) / 100.0;
     }
   });
   return rc ? rc : count;

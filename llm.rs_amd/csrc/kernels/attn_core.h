@@ -290,7 +290,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
       m[j] = mnew;
 #pragma unroll
       for (int e = 0; e < DPL; ++e) acc[j][e] = acc[j][e] * corr;
-      for (int u = 0; u < tvalid; ++u) {
+      // P.V over the tile's positions in order; a full tile is unrolled so
+      // the LDS reads of successive rows overlap instead of each waiting.
+      auto pv_row = [&](int u) {
         const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), u));
         const kv_t* vrow = s_v + u * HD + DPL * lane;
         if constexpr (KV16 && DPL == 2) {
@@ -302,6 +304,12 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
           for (int e = 0; e < DPL; ++e)
             acc[j][e] = __builtin_fmaf(pu, kv_to_f<KV16>(vrow[e]), acc[j][e]);
         }
+      };
+      if (tvalid == TILE) {
+#pragma unroll 16
+        for (int u = 0; u < TILE; ++u) pv_row(u);
+      } else {
+        for (int u = 0; u < tvalid; ++u) pv_row(u);
       }
     }
   }
@@ -339,19 +347,35 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
     if (hr >= n_rep) continue;
     const int h = g * n_rep + hr;
     const size_t base = (size_t)h * a.nsplit;
+    // (m, l) of split s0 + lane, 64 splits per round, so the loads of all
+    // splits are in flight together (every split writes its partials; an
+    // empty one has m = -inf, l = 0, o = 0).
     float M = -INFINITY;
-    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, ld_part<true>(a.part_ml, 2 * (base + s)));
+    for (int s0 = 0; s0 < a.nsplit; s0 += LLMRS_WAVE) {
+      const int sp = s0 + lane;
+      const float ms = sp < a.nsplit ? ld_part<true>(a.part_ml, 2 * (base + sp)) : -INFINITY;
+      M = fmaxf(M, wave_max(ms));
+    }
     float L = 0.0f, o[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; ++e) o[e] = 0.0f;
-    for (int s = 0; s < a.nsplit; ++s) {
-      const float ms = ld_part<true>(a.part_ml, 2 * (base + s));
-      if (ms == -INFINITY) continue;
-      const float w = expf(ms - M);
-      L = L + ld_part<true>(a.part_ml, 2 * (base + s) + 1) * w;
+    for (int s0 = 0; s0 < a.nsplit; s0 += LLMRS_WAVE) {
+      const int sp = s0 + lane;
+      float ms = -INFINITY, ls = 0.0f;
+      if (sp < a.nsplit) {
+        ms = ld_part<true>(a.part_ml, 2 * (base + sp));
+        ls = ld_part<true>(a.part_ml, 2 * (base + sp) + 1);
+      }
+      const float w = ms == -INFINITY ? 0.0f : expf(ms - M);
+      L = L + wave_sum(ls * w);
+      const int cnt = min(LLMRS_WAVE, a.nsplit - s0);
+#pragma unroll 8
+      for (int u = 0; u < cnt; ++u) {
+        const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
 #pragma unroll
-      for (int e = 0; e < DPL; ++e)
-        o[e] = o[e] + ld_part<true>(a.part_o, (base + s) * HD + DPL * lane + e) * w;
+        for (int e = 0; e < DPL; ++e)
+          o[e] = o[e] + ld_part<true>(a.part_o, (base + s0 + u) * HD + DPL * lane + e) * wu;
+      }
     }
     // ctx as f32 and as Q8_0 (32-dim blocks: 16 lanes x 2 dims, or 32 lanes x 1).
     constexpr int LPB = 32 / DPL;  // lanes per Q8 block

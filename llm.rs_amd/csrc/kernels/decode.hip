@@ -66,20 +66,24 @@ struct GridBarrier {
   }
 
   // Arrival, in two halves so the next phase's weight loads can be issued
-  // in between: publish() waits until this workgroup's stores have completed
-  // (on gfx9 loads and stores share one counter, so this must precede the
-  // prefetch, or the prefetch would be waited for too); wait() arrives and
-  // spins.  wait() returns false when this workgroup must leave (a wait
-  // timed out).
+  // in between.  publish() waits until this workgroup's stores have
+  // completed, then arrives: the counter atomics are issued while nothing
+  // else is outstanding (on gfx9 loads, stores and atomics share one
+  // in-order counter, so an arrival issued after the prefetch would wait for
+  // the prefetch's HBM latency before the last arriver could advance the top
+  // counter).  wait() spins on the top counter; it returns false when this
+  // workgroup must leave (a wait timed out).
   __device__ __forceinline__ void publish() {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-  }
-  __device__ __forceinline__ bool wait() {
     ++round;
     if (threadIdx.x == 0) {
       const unsigned t = add_dev_u(grp, 1u);
       if (t == gsize * round - 1) add_dev_u(top, 1u);
+    }
+  }
+  __device__ __forceinline__ bool wait() {
+    if (threadIdx.x == 0) {
       const unsigned target = (unsigned)ng * round;
       long spins = 0;
       int bad = 0;
@@ -140,9 +144,14 @@ __device__ __forceinline__ int reduce_argmax(const float* pv, const int* pi, int
 // Phase timestamps: workgroup 0 records the 100 MHz real-time counter when a
 // phase's own work ends and when the following barrier releases it, layer by
 // layer, for the first step of the launch (profiling only; null = off).
+// Layer 1 of the first step is also recorded for every workgroup, after the
+// per-layer block: ts[10 L + 10 wg + slot].
 #define LLMRS_TS(slot)                                                              \
   do {                                                                              \
-    if (d.ts && s == 0 && wg == 0 && tid == 0) d.ts[(size_t)l * 10 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+    if (d.ts && s == 0 && tid == 0) {                                               \
+      if (wg == 0) d.ts[(size_t)l * 10 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+      if (l == 1) d.ts[(size_t)L * 10 + (size_t)wg * 10 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+    }                                                                               \
   } while (0)
 
 template <int WT, int HD, bool KV16, int U>

@@ -414,12 +414,17 @@ class HipModel:
         return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(wk[i]))
                 for i in range(n)]
 
-    def profile_phases(self, n_steps: int = 1) -> tuple[float, np.ndarray]:
-        """Persistent-kernel phase timing: (us per step, [layers][10] intervals)."""
-        cap = 1 + 10 * self.cfg.n_layers
+    def profile_phases(self, n_steps: int = 1, per_wg: int = 0):
+        """Persistent-kernel phase timing: (us per step, [layers][10] intervals)
+        and, with per_wg = the grid size, ([per_wg][10] layer-1 timestamps)."""
+        cap = 1 + 10 * self.cfg.n_layers + 10 * per_wg
         out = np.zeros(cap, np.float64)
         n = _check(lib().llmrs_model_profile_phases(self._h, n_steps, _ptr(out), cap))
-        return float(out[0]), out[1:n].reshape(-1, 10)
+        nl = 10 * self.cfg.n_layers
+        layers = out[1:1 + nl].reshape(-1, 10)
+        if per_wg:
+            return float(out[0]), layers, out[1 + nl:n].reshape(-1, 10)
+        return float(out[0]), layers
 
     def weight_bytes(self) -> float:
         return float(lib().llmrs_model_weight_bytes(self._h))
