@@ -243,7 +243,8 @@ int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
  * seen by workgroup 0 - QKV work, barrier wait, attention work, wait, O work,
  * wait, gate|up work, wait, down work, wait (layer 0's QKV interval is 0);
  * then, for layer 1, each workgroup's ten phase timestamps (us after the end
- * of workgroup 0's layer 0), as far as `cap` allows.
+ * of workgroup 0's layer 0), then 8 stage timestamps of each attention work
+ * item (0 where not reached), as far as `cap` allows.
  * Returns the number of values written or an error. */
 int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int cap);
 /* Algorithmic weight bytes streamed per decode token (all linear weights). */

@@ -1146,9 +1146,11 @@ int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int c
     LLMRS_REQUIRE(m->pk_grid, LLMRS_E_INVALID, "the persistent decode kernel is not in use");
     LLMRS_REQUIRE(n_steps >= 1 && m->host_pos + n_steps <= (size_t)m->c.max_seq, LLMRS_E_RANGE,
                   "decode beyond max_seq");
-    const size_t nts = (size_t)m->c.n_layers * 10 + (size_t)m->pk_grid * 10;
+    const size_t items = (size_t)m->c.n_kv_heads * m->nsplit;
+    const size_t nts = (size_t)m->c.n_layers * 10 + (size_t)m->pk_grid * 10 + items * 8;
     unsigned long long* ts = nullptr;
     LLMRS_HIP(hipMalloc(&ts, nts * sizeof(unsigned long long)));
+    LLMRS_HIP(hipMemsetAsync(ts, 0, nts * sizeof(unsigned long long), ctx().stream));
     hipEvent_t e0, e1;
     LLMRS_HIP(hipEventCreate(&e0));
     LLMRS_HIP(hipEventCreate(&e1));
@@ -1184,6 +1186,10 @@ int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int c
       for (size_t w = 0; w < m->pk_grid; ++w)
         for (int i = 0; i < 10 && count < cap; ++i)
           us[count++] = ((double)h[(size_t)m->c.n_layers * 10 + w * 10 + i] - (double)t0) / 100.0;
+      // and the attention items' stage timestamps (8 each; 0 = not reached)
+      const size_t ab = (size_t)m->c.n_layers * 10 + (size_t)m->pk_grid * 10;
+      for (size_t i = 0; i < items * 8 && count < cap; ++i)
+        us[count++] = h[ab + i] ? ((double)h[ab + i] - (double)t0) / 100.0 : 0.0;
     }
   });
   return rc ? rc : count;

@@ -57,6 +57,7 @@ struct AttnArgs {
   float* ctx_d;            // [nq*hd/32]
   int max_seq, nq, nkv, nsplit;
   float scale;             // fl(1 / fl(sqrt(hd))), layer.rs:258
+  unsigned long long* ts;  // profiling: 8 stage timestamps per item (null = off)
 };
 
 // Elementwise trait operators (ops.hip).

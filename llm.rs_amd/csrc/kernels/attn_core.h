@@ -126,6 +126,11 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
   int& s_ticket = *(int*)(lds + LY::TICKET);
 
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  unsigned long long* ts = (a.ts && tid == 0) ? a.ts + ((size_t)g * a.nsplit + split) * 8 : nullptr;
+  auto stamp = [&](int k) {
+    if (ts) ts[k] = __builtin_amdgcn_s_memrealtime();
+  };
+  stamp(0);
   const int T = pos + 1;
   const int n_rep = a.nq / a.nkv;
   // Splits are runs of whole tiles.
@@ -160,49 +165,70 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
   };
   if (start < end) issue(start);
 
-  // Rotated query heads of this group (cpu.rs:351-354).
-  for (int i = tid; i < n_rep * MID; i += blockDim.x) {
+  // Rotated query heads of this group (cpu.rs:351-354) and, for the owner
+  // of position pos, the rotated k and the v it appends (layer.rs:219-246).
+  // Every projection and table value is loaded first, in one batch, so the
+  // section costs one memory round trip.
+  const bool owner = pos >= start && pos < end;
+  constexpr int QPT = (C::MAXREP * MID + 255) / 256;  // query pairs per thread
+  const size_t kr = qdim + (size_t)g * HD;
+  const size_t vr = qdim + (size_t)a.nkv * HD + (size_t)g * HD;
+  float qre[QPT], qim[QPT], qc[QPT], qs[QPT];
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int i = min(tid + 256 * u, n_rep * MID - 1);  // clamped: extra ones unused
     const int hr = i / MID, j = i % MID;
     const size_t q = (size_t)(g * n_rep + hr) * HD;
-    const float re = ld_qkv<DEV>(a.qkv, q + j), im = ld_qkv<DEV>(a.qkv, q + j + MID);
-    const float c = rc[j], s = rs[j];
-    s_q[hr][j] = re * c - im * s;
-    s_q[hr][j + MID] = re * s + im * c;
+    qre[u] = ld_qkv<DEV>(a.qkv, q + j);
+    qim[u] = ld_qkv<DEV>(a.qkv, q + j + MID);
+    qc[u] = rc[j];
+    qs[u] = rs[j];
   }
-  // The owner of position pos rotates k and appends k, v (layer.rs:219-246).
-  // It keeps the stored values in s_new: its own tile loads may have been
-  // issued before these stores.
-  const bool owner = pos >= start && pos < end;
-  if (owner) {
-    const size_t kr = qdim + (size_t)g * HD;
-    const size_t vr = qdim + (size_t)a.nkv * HD + (size_t)g * HD;
-    for (int j = tid; j < MID; j += blockDim.x) {
-      const float re = ld_qkv<DEV>(a.qkv, kr + j), im = ld_qkv<DEV>(a.qkv, kr + j + MID);
-      const float c = rc[j], s = rs[j];
-      const float k0 = re * c - im * s, k1 = re * s + im * c;
-      if constexpr (KV16) {
-        const uint16_t h0 = f2h(k0), h1 = f2h(k1);
-        st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j, h0);
-        st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j + MID, h1);
-        s_new[0][j] = h2f(h0);
-        s_new[0][j + MID] = h2f(h1);
-      } else {
-        st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j, k0);
-        st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j + MID, k1);
-        s_new[0][j] = k0;
-        s_new[0][j + MID] = k1;
-      }
+  const bool kown = owner && tid < MID, vown = owner && tid < HD;
+  float kre = 0.0f, kim = 0.0f, kcs = 0.0f, ksn = 0.0f, vv = 0.0f;
+  if (kown) {
+    kre = ld_qkv<DEV>(a.qkv, kr + tid);
+    kim = ld_qkv<DEV>(a.qkv, kr + tid + MID);
+    kcs = rc[tid];
+    ksn = rs[tid];
+  }
+  if (vown) vv = ld_qkv<DEV>(a.qkv, vr + tid);
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int i = tid + 256 * u;
+    if (i < n_rep * MID) {
+      const int hr = i / MID, j = i % MID;
+      s_q[hr][j] = qre[u] * qc[u] - qim[u] * qs[u];
+      s_q[hr][j + MID] = qre[u] * qs[u] + qim[u] * qc[u];
     }
-    for (int d = tid; d < HD; d += blockDim.x) {
-      const float v = ld_qkv<DEV>(a.qkv, vr + d);
-      if constexpr (KV16) {
-        const uint16_t h = f2h(v);
-        st_kv<DEV>(vc, a.vc, gbase + (size_t)pos * HD + d, h);
-        s_new[1][d] = h2f(h);
-      } else {
-        st_kv<DEV>(vc, a.vc, gbase + (size_t)pos * HD + d, v);
-        s_new[1][d] = v;
-      }
+  }
+  // The owner keeps the stored values in s_new: its own tile loads may have
+  // been issued before these stores.
+  if (kown) {
+    const int j = tid;
+    const float k0 = kre * kcs - kim * ksn, k1 = kre * ksn + kim * kcs;
+    if constexpr (KV16) {
+      const uint16_t h0 = f2h(k0), h1 = f2h(k1);
+      st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j, h0);
+      st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j + MID, h1);
+      s_new[0][j] = h2f(h0);
+      s_new[0][j + MID] = h2f(h1);
+    } else {
+      st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j, k0);
+      st_kv<DEV>(kc, a.kc, gbase + (size_t)pos * HD + j + MID, k1);
+      s_new[0][j] = k0;
+      s_new[0][j + MID] = k1;
+    }
+  }
+  if (vown) {
+    const int d = tid;
+    if constexpr (KV16) {
+      const uint16_t h = f2h(vv);
+      st_kv<DEV>(vc, a.vc, gbase + (size_t)pos * HD + d, h);
+      s_new[1][d] = h2f(h);
+    } else {
+      st_kv<DEV>(vc, a.vc, gbase + (size_t)pos * HD + d, vv);
+      s_new[1][d] = vv;
     }
   }
 
@@ -215,6 +241,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
     for (int e = 0; e < DPL; ++e) acc[j][e] = 0.0f;
   }
 
+  stamp(1);
   for (int t0 = start; t0 < end; t0 += TILE) {
     __syncthreads();  // previous tile consumed; s_q / s_new written
     // Stage the tile (already loaded into registers) into LDS: V rows with
@@ -247,6 +274,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
     }
     if (t0 + TILE < end) issue(t0 + TILE);  // next tile in flight during this one
     __syncthreads();
+    if (t0 == start) stamp(2);
 
     const int tvalid = min(TILE, end - t0);
 #pragma unroll
@@ -314,6 +342,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
     }
   }
 
+  stamp(3);
   // Partials of this split.
 #pragma unroll
   for (int j = 0; j < HPW; ++j) {
@@ -336,8 +365,10 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
   // whole L2, microseconds under contention) is needed.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  stamp(4);
   if (tid == 0) s_ticket = atomicAdd(&a.counters[g], 1);
   __syncthreads();
+  stamp(5);
   if (s_ticket != a.nsplit - 1) return;
 
   // Last workgroup of this KV head: combine the splits.
@@ -350,6 +381,15 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
     // (m, l) of split s0 + lane, 64 splits per round, so the loads of all
     // splits are in flight together (every split writes its partials; an
     // empty one has m = -inf, l = 0, o = 0).
+    // The first PF splits' partial-O values are loaded together with the
+    // (m, l) values, so a short combine costs one memory round trip.
+    constexpr int PF = 16;
+    float opf[PF][DPL];
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e)
+        opf[u][e] = u < a.nsplit ? ld_part<true>(a.part_o, (base + u) * HD + DPL * lane + e) : 0.0f;
     float M = -INFINITY;
     for (int s0 = 0; s0 < a.nsplit; s0 += LLMRS_WAVE) {
       const int sp = s0 + lane;
@@ -369,8 +409,18 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
       const float w = ms == -INFINITY ? 0.0f : expf(ms - M);
       L = L + wave_sum(ls * w);
       const int cnt = min(LLMRS_WAVE, a.nsplit - s0);
+      int u0 = 0;
+      if (s0 == 0) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+          const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) o[e] = o[e] + opf[u][e] * wu;  // 0 * 0 past nsplit
+        }
+        u0 = PF;
+      }
 #pragma unroll 8
-      for (int u = 0; u < cnt; ++u) {
+      for (int u = u0; u < cnt; ++u) {
         const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
 #pragma unroll
         for (int e = 0; e < DPL; ++e)
@@ -401,6 +451,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
     if ((lane % LPB) == 0) st_act<DEV>(a.ctx_d, ((size_t)h * HD + DPL * lane) / 32, amax == 0.0f ? 0.0f : d);
   }
   if (tid == 0) dev_stu(a.counters, 4 * g, 0u);
+  stamp(6);
 }
 
 }  // namespace llmrs

@@ -278,6 +278,7 @@ __device__ __forceinline__ void decode_impl(const DecodeArgs& d) {
         a.nkv = d.nkv;
         a.nsplit = d.nsplit;
         a.scale = d.attn_scale;
+        a.ts = (d.ts && s == 0 && l == 1) ? d.ts + (size_t)L * 10 + (size_t)nwg * 10 : nullptr;
         for (int it = wg; it < items; it += nwg)
           attn_item<HD, KV16, true>(a, it / d.nsplit, it % d.nsplit, pos, smem);
       }

@@ -414,16 +414,18 @@ class HipModel:
         return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(wk[i]))
                 for i in range(n)]
 
-    def profile_phases(self, n_steps: int = 1, per_wg: int = 0):
+    def profile_phases(self, n_steps: int = 1, grid: int = 0):
         """Persistent-kernel phase timing: (us per step, [layers][10] intervals)
-        and, with per_wg = the grid size, ([per_wg][10] layer-1 timestamps)."""
-        cap = 1 + 10 * self.cfg.n_layers + 10 * per_wg
+        and, with grid = the launch's workgroup count, ([grid][10] layer-1
+        timestamps, [items][8] attention stage timestamps)."""
+        cap = 1 + 10 * self.cfg.n_layers + (10 * grid + 8 * 4096 if grid else 0)
         out = np.zeros(cap, np.float64)
         n = _check(lib().llmrs_model_profile_phases(self._h, n_steps, _ptr(out), cap))
         nl = 10 * self.cfg.n_layers
         layers = out[1:1 + nl].reshape(-1, 10)
-        if per_wg:
-            return float(out[0]), layers, out[1 + nl:n].reshape(-1, 10)
+        if grid:
+            wgs = out[1 + nl:1 + nl + 10 * grid].reshape(-1, 10)
+            return float(out[0]), layers, wgs, out[1 + nl + 10 * grid:n].reshape(-1, 8)
         return float(out[0]), layers
 
     def weight_bytes(self) -> float:
