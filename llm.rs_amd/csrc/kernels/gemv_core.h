@@ -242,6 +242,135 @@ __device__ __forceinline__ void load_activation(const GemvArgs& a, int mrow, int
   }
 }
 
+// The prologue in two halves: issue_activation() requests this thread's
+// activation values (and RMSNorm weights) into registers, finish_activation()
+// turns them into the LDS operand.  gemv_body issues them BEFORE the weight
+// prefetch: a wave's loads complete in issue order, so activation loads
+// issued after the prefetch could only be used once every prefetched weight
+// had arrived, and no further weight loads would be issued until the
+// prologue's second round trip and reductions were done.  Issued first, the
+// prologue overlaps the prefetch and the weight stream never pauses.
+// Register-resident when k <= 32 * kThreads (RMSNorm / plain quantisation)
+// or k <= 32 * kQ8Blocks * kThreads (Q8 codes); larger inputs fall back to
+// load_activation after the prefetch.
+constexpr int kQ8Blocks = 4;
+
+template <int PRO>
+struct ActRegs {
+  f32x4 x[PRO == PRO_Q8 ? 1 : 8];
+  f32x4 w[PRO == PRO_NORM ? 8 : 1];
+  i32x4 c0[PRO == PRO_Q8 ? kQ8Blocks : 1];
+  i32x4 c1[PRO == PRO_Q8 ? kQ8Blocks : 1];
+  float d[PRO == PRO_Q8 ? kQ8Blocks : 1];
+};
+
+template <int PRO>
+__device__ __forceinline__ bool act_in_regs(int k) {
+  const int nb = k >> 5;
+  return PRO == PRO_Q8 ? nb <= kQ8Blocks * kThreads : nb <= kThreads;
+}
+
+template <int PRO, bool DEV>
+__device__ __forceinline__ void issue_activation(const GemvArgs& a, int mrow, ActRegs<PRO>& r) {
+  const int k = a.k, nb = k >> 5, tid = threadIdx.x;
+  if (!act_in_regs<PRO>(k)) return;
+  if (PRO == PRO_Q8) {
+#pragma unroll
+    for (int i = 0; i < kQ8Blocks; ++i) {
+      const int b = min(tid + kThreads * i, nb - 1);  // clamped; extra ones unused
+      if (kThreads * i < nb) {
+        if (DEV) {
+          const dev_u32x4 u0 = dev_ld16(a.xq, 32 * b), u1 = dev_ld16(a.xq, 32 * b + 16);
+          r.c0[i] = i32x4{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w};
+          r.c1[i] = i32x4{(int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
+        } else {
+          const i32x4* src = (const i32x4*)(a.xq + 32 * b);
+          r.c0[i] = src[0];
+          r.c1[i] = src[1];
+        }
+        r.d[i] = ld_act<DEV>(a.xd, b);
+      }
+    }
+    return;
+  }
+  const int b = tid < nb ? tid : nb - 1;
+  const size_t xrow = (size_t)mrow * k;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r.x[j] = ld_act4<DEV>(a.x, xrow + 32 * b + 4 * j);
+  if (PRO == PRO_NORM) {
+    const f32x4* wsrc = (const f32x4*)(a.norm_w + 32 * b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r.w[j] = wsrc[j];
+  }
+}
+
+template <int PRO, bool Q4, bool DEV>
+__device__ __forceinline__ void finish_activation(const GemvArgs& a, int mrow, ActRegs<PRO>& r,
+                                                  int8_t* s_q, float* s_d, int* s_off, float* s_red) {
+  const int k = a.k, nb = k >> 5, tid = threadIdx.x;
+  if (!act_in_regs<PRO>(k)) {
+    load_activation<PRO, Q4, DEV>(a, mrow, s_q, s_d, s_off, s_red);
+    return;
+  }
+  if (PRO == PRO_Q8) {
+#pragma unroll
+    for (int i = 0; i < kQ8Blocks; ++i) {
+      const int b = tid + kThreads * i;
+      if (kThreads * i < nb && b < nb) {
+        i32x4* dst = (i32x4*)(s_q + 32 * b);
+        dst[0] = r.c0[i];
+        dst[1] = r.c1[i];
+        s_d[b] = r.d[i];
+        if (Q4) {
+          int s = 0;
+          s = dot4(r.c0[i].x, 0x01010101, s);
+          s = dot4(r.c0[i].y, 0x01010101, s);
+          s = dot4(r.c0[i].z, 0x01010101, s);
+          s = dot4(r.c0[i].w, 0x01010101, s);
+          s = dot4(r.c1[i].x, 0x01010101, s);
+          s = dot4(r.c1[i].y, 0x01010101, s);
+          s = dot4(r.c1[i].z, 0x01010101, s);
+          s = dot4(r.c1[i].w, 0x01010101, s);
+          s_off[b] = -8 * s;
+        }
+      }
+    }
+    return;
+  }
+  float v[32];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v[4 * j] = r.x[j].x;
+    v[4 * j + 1] = r.x[j].y;
+    v[4 * j + 2] = r.x[j].z;
+    v[4 * j + 3] = r.x[j].w;
+  }
+  if (PRO == PRO_NORM) {
+    // cpu.rs:381-383: ss = sum v*v; rms = sqrt(ss/n + eps); scale = 1/rms.
+    float ss = 0.0f;
+    if (tid < nb) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) ss = ss + v[i] * v[i];
+    }
+    ss = wave_sum(ss);
+    if (lane_id() == 0) s_red[wave_id()] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot = tot + s_red[w];
+    const float rms = sqrtf(tot / (float)k + a.eps);
+    const float scale = 1.0f / rms;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[4 * j] = v[4 * j] * scale * r.w[j].x;  // cpu.rs:389: x * s * w
+      v[4 * j + 1] = v[4 * j + 1] * scale * r.w[j].y;
+      v[4 * j + 2] = v[4 * j + 2] * scale * r.w[j].z;
+      v[4 * j + 3] = v[4 * j + 3] * scale * r.w[j].w;
+    }
+  }
+  if (tid < nb) quant_block<Q4>(v, tid, s_q, s_d, s_off);
+}
+
 // Pair order for argmax: larger value wins, lower index breaks ties.
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
@@ -398,8 +527,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
   const int lane = g.lane, wave = g.wave, tid = threadIdx.x;
   const int nunits = g.nunits;
 
-  if (!preloaded) g.prefetch(ua, ub);
-  load_activation<PRO, G::Q4, DEV>(a, mrow, s_q, s_d, s_off, sh.red);
+  {
+    ActRegs<PRO> ar;
+    issue_activation<PRO, DEV>(a, mrow, ar);
+    if (!preloaded) g.prefetch(ua, ub);
+    finish_activation<PRO, G::Q4, DEV>(a, mrow, ar, s_q, s_d, s_off, sh.red);
+  }
   __syncthreads();
 
   const size_t ybase = (size_t)mrow * a.n;
