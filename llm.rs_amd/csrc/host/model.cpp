@@ -478,7 +478,16 @@ void plan_persistent(llmrs_model* m) {
   const bool kv16 = c.kv_dtype == LLMRS_F16;
   m->pk_name = std::string("decode_") + wt_tag(m->wt) + "_hd" + std::to_string(c.head_dim) +
                (kv16 ? "_f16" : "_f32") + "_u" + std::to_string(U);
-  m->pk_lds = std::max(gemv_act_lds_host(kmax), attn_lds_bytes(c.head_dim, kv16));
+  // LDS for the largest phase; results areas sized for one workgroup per CU
+  // (the fewest workgroups a launch can have), so any resident grid fits.
+  const int nw = std::max(1, ctx().num_cus);
+  size_t gl = gemv_lds_bytes(false, m->qkv_rows, H, 2, nw);
+  gl = std::max(gl, gemv_lds_bytes(false, H, qd, 2, nw));
+  gl = std::max(gl, gemv_lds_bytes(true, 2 * F, H, 2, nw));
+  gl = std::max(gl, gemv_lds_bytes(false, H, F, 2, nw));
+  gl = std::max(gl, gemv_lds_bytes(false, c.vocab, H, 2, nw));
+  (void)kmax;
+  m->pk_lds = std::max(gl, attn_lds_bytes(c.head_dim, kv16));
   hipFunction_t f = kernel(m->pk_name);
   int per_cu = 0;
   if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, m->pk_lds) != hipSuccess) {

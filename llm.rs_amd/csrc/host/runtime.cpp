@@ -9,6 +9,7 @@
 #include <functional>
 #include <thread>
 
+#include "../kernel_args.h"
 #include "internal.h"
 
 namespace llmrs {
@@ -93,7 +94,7 @@ GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
     wgs = (nrg + 3) / 4;
   }
   p.grid = (unsigned)std::max<long>(1, std::min(wgs, cap));
-  p.lds = (size_t)k + 8 * (size_t)nb;
+  p.lds = llmrs::gemv_lds_bytes(kind == "norm_silu", n, k, R, (int)p.grid);
   return p;
 }
 

@@ -27,7 +27,22 @@ struct GemvArgs {
   float* yd;             // [n/64] scales of silu(g)*u (EPI_SILU)
   float* part_val;       // [gridDim.x] (EPI_ARGMAX)
   int* part_idx;         // [gridDim.x] (EPI_ARGMAX)
+  unsigned long long* ts;  // profiling: 4 stamps per workgroup (null = off)
 };
+
+// Dynamic LDS of a decode GEMV (gemv_core.h): the quantised activation row
+// (k codes, k/32 scales, k/32 Q4 offsets; 16-byte aligned), then the row
+// results parked until the unit loop ends: per wave (4 per workgroup) R
+// values of each of its row groups, or for the SwiGLU epilogue 64 values per
+// tile of the workgroup.  nwg = workgroups of the launch.
+constexpr size_t gemv_act_bytes(int k) { return (size_t)k + 8 * (size_t)(k / 32); }
+constexpr size_t gemv_out_floats(bool silu, int n, int r, int nwg) {
+  return silu ? (size_t)(((n + 63) / 64 + nwg - 1) / nwg) * 64
+              : (size_t)((((size_t)n + r - 1) / r + (size_t)nwg * 4 - 1) / ((size_t)nwg * 4)) * r * 4;
+}
+constexpr size_t gemv_lds_bytes(bool silu, int n, int k, int r, int nwg) {
+  return (gemv_act_bytes(k) + 15) / 16 * 16 + 4 * gemv_out_floats(silu, n, r, nwg);
+}
 
 // lm_head partial reduction + greedy bookkeeping (gemv.hip: argmax_final).
 struct ArgmaxFinalArgs {

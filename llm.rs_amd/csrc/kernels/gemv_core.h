@@ -105,6 +105,52 @@ __device__ __forceinline__ void quant_block(const float* v, int blk, int8_t* s_q
   if (Q4) s_off[blk] = -8 * csum;
 }
 
+// Q8_0 of one 32-element block held by 32/EPT adjacent lanes, EPT values
+// each (lane t holds elements [t*EPT, (t+1)*EPT) of the row; block t*EPT/32).
+// Same arithmetic as quant_block; the amax is combined across the lanes.
+template <bool Q4, int EPT>
+__device__ __forceinline__ void quant_part(const float* v, int t, int8_t* s_q, float* s_d, int* s_off) {
+  constexpr int LPB = 32 / EPT;
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int o = LPB / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, LPB));
+  int packed[EPT / 4];
+  int csum = 0;
+  float d = 0.0f;
+  if (amax == 0.0f) {
+#pragma unroll
+    for (int j = 0; j < EPT / 4; ++j) packed[j] = 0;
+  } else {
+    d = amax / 127.0f;
+    const float inv = 1.0f / d;
+#pragma unroll
+    for (int j = 0; j < EPT / 4; ++j) {
+      unsigned w = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int q = q8_code(v[4 * j + e], inv);
+        csum += q;
+        w |= ((unsigned)q & 0xFFu) << (8 * e);
+      }
+      packed[j] = (int)w;
+    }
+  }
+  int* dst = (int*)(s_q + EPT * t);
+#pragma unroll
+  for (int j = 0; j < EPT / 4; ++j) dst[j] = packed[j];
+  if (Q4) {
+#pragma unroll
+    for (int o = LPB / 2; o > 0; o >>= 1) csum += __shfl_xor(csum, o, LPB);
+  }
+  if ((t % LPB) == 0) {
+    const int blk = t / LPB;
+    s_d[blk] = d;
+    if (Q4) s_off[blk] = -8 * csum;
+  }
+}
+
 template <bool DEV>
 __device__ __forceinline__ f32x4 ld_act4(const float* base, size_t idx) {
   if (DEV) {
@@ -264,6 +310,12 @@ struct ActRegs {
   float d[PRO == PRO_Q8 ? kQ8Blocks : 1];
 };
 
+// Elements per thread when the whole input spreads evenly over the
+// workgroup in runs of 8, 16 or 32 (k = 2048, 4096, 8192); 0 otherwise.
+__device__ __forceinline__ int act_ept(int k) {
+  return (k == 8 * kThreads || k == 16 * kThreads || k == 32 * kThreads) ? k / kThreads : 0;
+}
+
 template <int PRO>
 __device__ __forceinline__ bool act_in_regs(int k) {
   const int nb = k >> 5;
@@ -293,20 +345,89 @@ __device__ __forceinline__ void issue_activation(const GemvArgs& a, int mrow, Ac
     }
     return;
   }
-  const int b = tid < nb ? tid : nb - 1;
+  // k = kThreads * ept: thread t owns elements [t*ept, (t+1)*ept); else one
+  // 32-element block per thread.
+  const int ept = act_ept(k);
   const size_t xrow = (size_t)mrow * k;
+  const int e0 = ept ? tid * ept : 32 * (tid < nb ? tid : nb - 1);
+  const int nv = ept ? ept / 4 : 8;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) r.x[j] = ld_act4<DEV>(a.x, xrow + 32 * b + 4 * j);
+  for (int j = 0; j < 8; ++j)
+    if (j < nv) r.x[j] = ld_act4<DEV>(a.x, xrow + e0 + 4 * j);
   if (PRO == PRO_NORM) {
-    const f32x4* wsrc = (const f32x4*)(a.norm_w + 32 * b);
+    const f32x4* wsrc = (const f32x4*)(a.norm_w + e0);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r.w[j] = wsrc[j];
+    for (int j = 0; j < 8; ++j)
+      if (j < nv) r.w[j] = wsrc[j];
   }
+}
+
+// Profiling stamps of one workgroup (100 MHz clock), kept in registers and
+// stored once at the end of the kernel: a store issued mid-kernel would make
+// the next reuse of its data registers wait for every outstanding load.
+// 0 start, 1 operand ready, 2 loop done, 3 end, 4 input arrived, 5 norm
+// scale known, 6 operand quantised.
+struct Stamps {
+  bool on;
+  unsigned long long t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  __device__ __forceinline__ void rec(int i) {
+    if (on) t[i] = __builtin_amdgcn_s_memrealtime();
+  }
+  __device__ __forceinline__ void write(unsigned long long* dst) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = t[i];
+  }
+};
+
+// RMSNorm (PRO_NORM) and Q8_0 of the register-resident row: EPT values per
+// thread (EPT = 32 also covers one block per thread with nb <= kThreads).
+template <int PRO, bool Q4, int EPT>
+__device__ __forceinline__ void finish_norm(const GemvArgs& a, ActRegs<PRO>& r, int8_t* s_q, float* s_d,
+                                            int* s_off, float* s_red, Stamps& ts) {
+  const int k = a.k, nb = k >> 5, tid = threadIdx.x;
+  const bool active = EPT < 32 || tid < nb;
+  float v[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT / 4; ++j) {
+    v[4 * j] = r.x[j].x;
+    v[4 * j + 1] = r.x[j].y;
+    v[4 * j + 2] = r.x[j].z;
+    v[4 * j + 3] = r.x[j].w;
+  }
+  if (PRO == PRO_NORM) {
+    // cpu.rs:381-383: ss = sum v*v; rms = sqrt(ss/n + eps); scale = 1/rms.
+    float ss = 0.0f;
+    if (active) {
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) ss = ss + v[i] * v[i];
+    }
+    ts.rec(4);
+    ss = wave_sum(ss);
+    if (lane_id() == 0) s_red[wave_id()] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot = tot + s_red[w];
+    const float rms = sqrtf(tot / (float)k + a.eps);
+    const float scale = 1.0f / rms;
+    ts.rec(5);
+#pragma unroll
+    for (int j = 0; j < EPT / 4; ++j) {
+      v[4 * j] = v[4 * j] * scale * r.w[j].x;  // cpu.rs:389: x * s * w
+      v[4 * j + 1] = v[4 * j + 1] * scale * r.w[j].y;
+      v[4 * j + 2] = v[4 * j + 2] * scale * r.w[j].z;
+      v[4 * j + 3] = v[4 * j + 3] * scale * r.w[j].w;
+    }
+  }
+  if (EPT < 32) quant_part<Q4, EPT>(v, tid, s_q, s_d, s_off);
+  else if (active) quant_block<Q4>(v, tid, s_q, s_d, s_off);
+  ts.rec(6);
 }
 
 template <int PRO, bool Q4, bool DEV>
 __device__ __forceinline__ void finish_activation(const GemvArgs& a, int mrow, ActRegs<PRO>& r,
-                                                  int8_t* s_q, float* s_d, int* s_off, float* s_red) {
+                                                  int8_t* s_q, float* s_d, int* s_off, float* s_red,
+                                                  Stamps& ts) {
   const int k = a.k, nb = k >> 5, tid = threadIdx.x;
   if (!act_in_regs<PRO>(k)) {
     load_activation<PRO, Q4, DEV>(a, mrow, s_q, s_d, s_off, s_red);
@@ -337,38 +458,11 @@ __device__ __forceinline__ void finish_activation(const GemvArgs& a, int mrow, A
     }
     return;
   }
-  float v[32];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    v[4 * j] = r.x[j].x;
-    v[4 * j + 1] = r.x[j].y;
-    v[4 * j + 2] = r.x[j].z;
-    v[4 * j + 3] = r.x[j].w;
+  switch (act_ept(k)) {
+    case 8: finish_norm<PRO, Q4, 8>(a, r, s_q, s_d, s_off, s_red, ts); break;
+    case 16: finish_norm<PRO, Q4, 16>(a, r, s_q, s_d, s_off, s_red, ts); break;
+    default: finish_norm<PRO, Q4, 32>(a, r, s_q, s_d, s_off, s_red, ts); break;
   }
-  if (PRO == PRO_NORM) {
-    // cpu.rs:381-383: ss = sum v*v; rms = sqrt(ss/n + eps); scale = 1/rms.
-    float ss = 0.0f;
-    if (tid < nb) {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) ss = ss + v[i] * v[i];
-    }
-    ss = wave_sum(ss);
-    if (lane_id() == 0) s_red[wave_id()] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) tot = tot + s_red[w];
-    const float rms = sqrtf(tot / (float)k + a.eps);
-    const float scale = 1.0f / rms;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      v[4 * j] = v[4 * j] * scale * r.w[j].x;  // cpu.rs:389: x * s * w
-      v[4 * j + 1] = v[4 * j + 1] * scale * r.w[j].y;
-      v[4 * j + 2] = v[4 * j + 2] * scale * r.w[j].z;
-      v[4 * j + 3] = v[4 * j + 3] * scale * r.w[j].w;
-    }
-  }
-  if (tid < nb) quant_block<Q4>(v, tid, s_q, s_d, s_off);
 }
 
 // Pair order for argmax: larger value wins, lower index breaks ties.
@@ -461,8 +555,13 @@ struct Gemv {
     const int b0 = (unit % nchunk) * BPU + lane;
 #pragma unroll
     for (int v = 0; v < U; ++v) {
-      const int b = b0 + LLMRS_WAVE * v;
-      if (b < nb) {
+      // Branch-free: a block past the row end (partial last chunk) reads a
+      // clamped block and contributes 0.  Divergent branches here would make
+      // the compiler drain every outstanding load at the join.
+      const int bb = b0 + LLMRS_WAVE * v;
+      const bool ok = bb < nb;
+      const int b = ok ? bb : nb - 1;
+      {
         const i32x4* aq = (const i32x4*)(s_q + 32 * b);
         const i32x4 a0 = aq[0], a1 = aq[1];
         const float da = s_d[b];
@@ -493,7 +592,8 @@ struct Gemv {
             s = dot4((int)w1.z, a1.z, s);
             s = dot4((int)w1.w, a1.w, s);
           }
-          acc[r] = acc[r] + (float)s * (wscale<WT>(u.sc[r][v]) * da);
+          const float t = (float)s * (wscale<WT>(u.sc[r][v]) * da);
+          acc[r] = acc[r] + (ok ? t : 0.0f);
         }
       }
     }
@@ -502,18 +602,25 @@ struct Gemv {
 
 // LDS used by gemv_body beyond the activation area.
 struct GemvShared {
-  float out[kSiluTile];
   float red[kWaves];
   float bv[kWaves];
   int bi[kWaves];
 };
 
 // Bytes of the activation area in LDS for an input of length k.
-__host__ __device__ constexpr size_t gemv_act_lds(int k) { return (size_t)k + 8 * (size_t)(k / 32); }
+__host__ __device__ constexpr size_t gemv_act_lds(int k) { return gemv_act_bytes(k); }
+static_assert(kThreads == 4 * LLMRS_WAVE && kSiluTile == 64, "gemv_lds_bytes assumes 4 waves, 64-row tiles");
 
 // One GEMV over the waves of workgroup `wg` of `nwg`: prologue, pipelined
 // unit loop, epilogues.  `ua`/`ub` hold the first two units already when
 // `preloaded`.  Argmax partials go to slot `wg`.
+//
+// The unit loop issues no global stores and has no divergent branches, and
+// the last two units are peeled off so it never requests weights it will not
+// use: the memory counter of a wave is in order, so a store, or a branch
+// join the compiler cannot count through, inside the loop would make the
+// next compute wait for every outstanding load and collapse the two-unit
+// pipeline.  Row results go to LDS and are written after the loop.
 template <int WT, int PRO, int EPI, int R, int U, bool DEV>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, int nwg,
                                           UnitRegs<WT, R, U>& ua, UnitRegs<WT, R, U>& ub,
@@ -523,47 +630,44 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
   int8_t* s_q = (int8_t*)act;
   float* s_d = (float*)(act + k);
   int* s_off = (int*)(act + k + 4 * nb);
+  float* s_out = (float*)(act + (gemv_act_lds(k) + 15) / 16 * 16);
   G g(a, wg, nwg);
   const int lane = g.lane, wave = g.wave, tid = threadIdx.x;
   const int nunits = g.nunits;
+  // Row groups per wave (non-SwiGLU): the wave's slice of s_out.
+  const int gmax = (g.nrg + nwg * kWaves - 1) / (nwg * kWaves);
+  Stamps ts;
+  ts.on = a.ts != nullptr;
+  ts.rec(0);
 
   {
     ActRegs<PRO> ar;
     issue_activation<PRO, DEV>(a, mrow, ar);
     if (!preloaded) g.prefetch(ua, ub);
-    finish_activation<PRO, G::Q4, DEV>(a, mrow, ar, s_q, s_d, s_off, sh.red);
+    finish_activation<PRO, G::Q4, DEV>(a, mrow, ar, s_q, s_d, s_off, sh.red, ts);
   }
   __syncthreads();
+  ts.rec(1);
 
-  const size_t ybase = (size_t)mrow * a.n;
   float best_v = -INFINITY;
   int best_i = 0x7fffffff;
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 
-  // Finish unit i: on the last chunk of a row group, reduce and write.
+  // Finish unit i: on the last chunk of a row group, reduce the lane
+  // partials and park the R results in LDS (lane r writes row r).
   auto finish = [&](int i) {
     if ((i % g.nchunk) != g.nchunk - 1) return;
     const int j = i / g.nchunk;
-    const int rg = g.row_group(j);
     float vals[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       vals[r] = wave_sum(acc[r]);
       acc[r] = 0.0f;
     }
-    if (EPI == EPI_STORE || EPI == EPI_RESID) {
-      float out = 0.0f;
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (lane == r) out = vals[r];
-      const int row = rg * R + lane;
-      if (lane < R && rg >= 0 && row < a.n) {
-        if (EPI == EPI_RESID) out = out + ld_act<DEV>(a.res, ybase + row);  // layer.rs:386,403
-        st_act<DEV>(a.y, ybase + row, out);
-      }
-    } else if (EPI == EPI_ARGMAX) {
+    if (EPI == EPI_ARGMAX) {
+      const int rg = g.row_group(j);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int row = rg * R + r;
@@ -572,48 +676,84 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
           best_i = row;
         }
       }
-      float out = 0.0f;
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (lane == r) out = vals[r];
-      const int row = rg * R + lane;
-      if (a.y && lane < R && rg >= 0 && row < a.n) st_act<DEV>(a.y, row, out);
-    } else if (EPI == EPI_SILU) {
-      const int local = (j % G::SILU_RG) * R + wave * (G::SILU_RG * R);
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (lane == r) sh.out[local + r] = vals[r];
-      if ((j % G::SILU_RG) == G::SILU_RG - 1) {
-        // Tile complete in this wave; wait for the other waves.
-        __syncthreads();
-        const int tile = wg + (j / G::SILU_RG) * nwg;
-        if (tid < 32) {
-          // Tile = 32 gate rows then the 32 matching up rows (layer.rs:72-79).
-          const float gv = sh.out[tid], uv = sh.out[32 + tid];
-          const float mv = (gv / (1.0f + expf(-gv))) * uv;
-          const int idx = tile * 32 + tid;
-          if (a.y) st_act<DEV>(a.y, idx, mv);
-          float d;
-          const int q = q8_group32(mv, &d);
-          if (DEV) dev_st8(a.yq, idx, (int8_t)q);
-          else a.yq[idx] = (int8_t)q;
-          if (tid == 0) st_act<DEV>(a.yd, tile, d);
-        }
-        __syncthreads();
-      }
     }
+    float out = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (lane == r) out = vals[r];
+    int slot;
+    if (EPI == EPI_SILU)
+      slot = (j / G::SILU_RG) * kSiluTile + wave * (G::SILU_RG * R) + (j % G::SILU_RG) * R;
+    else
+      slot = (wave * gmax + j) * R;
+    if (lane < R) s_out[slot + lane] = out;
   };
 
   int i = 0;
-  while (i < nunits) {
+  for (; i + 3 < nunits; i += 2) {
     g.compute(ua, i, acc, s_q, s_d, s_off);
-    g.load(ua, i + 2 < nunits ? i + 2 : -1);
+    g.load(ua, i + 2);
     finish(i);
-    if (++i >= nunits) break;
-    g.compute(ub, i, acc, s_q, s_d, s_off);
-    g.load(ub, i + 2 < nunits ? i + 2 : -1);
+    g.compute(ub, i + 1, acc, s_q, s_d, s_off);
+    g.load(ub, i + 3);
+    finish(i + 1);
+  }
+  // Tail: 0-3 units left, at most one more load.
+  if (i + 2 < nunits) {
+    g.compute(ua, i, acc, s_q, s_d, s_off);
+    g.load(ua, i + 2);
     finish(i);
-    ++i;
+    g.compute(ub, i + 1, acc, s_q, s_d, s_off);
+    finish(i + 1);
+    g.compute(ua, i + 2, acc, s_q, s_d, s_off);
+    finish(i + 2);
+  } else if (i + 1 < nunits) {
+    g.compute(ua, i, acc, s_q, s_d, s_off);
+    finish(i);
+    g.compute(ub, i + 1, acc, s_q, s_d, s_off);
+    finish(i + 1);
+  } else if (i < nunits) {
+    g.compute(ua, i, acc, s_q, s_d, s_off);
+    finish(i);
+  }
+  ts.rec(2);
+
+  // Epilogues from the parked results.
+  const size_t ybase = (size_t)mrow * a.n;
+  if (EPI == EPI_SILU) {
+    __syncthreads();
+    const int ntiles = (a.n + kSiluTile - 1) / kSiluTile;
+    const int my_tiles = wg < ntiles ? (ntiles - 1 - wg) / nwg + 1 : 0;
+    // 32 threads per tile: tile = 32 gate rows then the 32 matching up rows
+    // (layer.rs:72-79); m = silu(g) * u and its Q8_0 block.
+    for (int q0 = 0; q0 < my_tiles; q0 += kThreads / 32) {
+      const int q = q0 + tid / 32, e = tid % 32;
+      if (q < my_tiles) {  // uniform per 32-lane half-wave
+        const int tile = wg + q * nwg;
+        const float gv = s_out[q * kSiluTile + e], uv = s_out[q * kSiluTile + 32 + e];
+        const float mv = (gv / (1.0f + expf(-gv))) * uv;
+        const int idx = tile * 32 + e;
+        if (a.y) st_act<DEV>(a.y, idx, mv);
+        float d;
+        const int qc = q8_group32(mv, &d);
+        if (DEV) dev_st8(a.yq, idx, (int8_t)qc);
+        else a.yq[idx] = (int8_t)qc;
+        if (e == 0) st_act<DEV>(a.yd, tile, d);
+      }
+    }
+  } else if (EPI == EPI_STORE || EPI == EPI_RESID || (EPI == EPI_ARGMAX && a.y)) {
+    // This wave's rows: value v = j * R + r of its slice, one per lane.
+    const int nv = (nunits / g.nchunk) * R;
+    for (int v0 = 0; v0 < nv; v0 += LLMRS_WAVE) {
+      const int v = v0 + lane;
+      const int rg = v < nv ? g.row_group(v / R) : -1;
+      const int row = rg * R + v % R;
+      if (rg >= 0 && row < a.n) {
+        float out = s_out[wave * gmax * R + v];
+        if (EPI == EPI_RESID) out = out + ld_act<DEV>(a.res, ybase + row);  // layer.rs:386,403
+        st_act<DEV>(a.y, ybase + row, out);
+      }
+    }
   }
 
   if (EPI == EPI_ARGMAX) {
@@ -633,6 +773,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
       else a.part_idx[wg] = best_i;
     }
   }
+  ts.rec(3);
+  if (ts.on && tid == 0) ts.write(a.ts + 8 * ((size_t)mrow * nwg + wg));
 }
 
 }  // namespace llmrs
