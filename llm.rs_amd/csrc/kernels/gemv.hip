@@ -14,7 +14,8 @@ __device__ __forceinline__ void gemv_impl(const GemvArgs& a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ GemvShared sh;
   UnitRegs<WT, R, U> ua, ub;
-  gemv_body<WT, PRO, EPI, R, U, false>(a, blockIdx.y, blockIdx.x, gridDim.x, ua, ub, false, smem, sh);
+  gemv_body<WT, PRO, EPI, R, U, false, EPI == EPI_SILU ? 1 : 2>(a, blockIdx.y, blockIdx.x, gridDim.x, ua, ub,
+                                                                false, smem, sh);
 }
 
 #define LLMRS_GEMV(name, WT, PRO, EPI, R, U)                                       \

@@ -613,7 +613,12 @@ static_assert(kThreads == 4 * LLMRS_WAVE && kSiluTile == 64, "gemv_lds_bytes ass
 
 // One GEMV over the waves of workgroup `wg` of `nwg`: prologue, pipelined
 // unit loop, epilogues.  `ua`/`ub` hold the first two units already when
-// `preloaded`.  Argmax partials go to slot `wg`.
+// `preloaded`; otherwise PRE of them (0-2) are requested before the
+// activation prologue and the rest right after it.  Requests issued before
+// the prologue overlap its latency, but they also queue ahead of the
+// activation loads of later workgroups; the best depth depends on the
+// launch (measured: 1 for the 64-row-tile SwiGLU GEMV, 2 otherwise).
+// Argmax partials go to slot `wg`.
 //
 // The unit loop issues no global stores and has no divergent branches, and
 // the last two units are peeled off so it never requests weights it will not
@@ -621,7 +626,7 @@ static_assert(kThreads == 4 * LLMRS_WAVE && kSiluTile == 64, "gemv_lds_bytes ass
 // join the compiler cannot count through, inside the loop would make the
 // next compute wait for every outstanding load and collapse the two-unit
 // pipeline.  Row results go to LDS and are written after the loop.
-template <int WT, int PRO, int EPI, int R, int U, bool DEV>
+template <int WT, int PRO, int EPI, int R, int U, bool DEV, int PRE = 2>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, int nwg,
                                           UnitRegs<WT, R, U>& ua, UnitRegs<WT, R, U>& ub,
                                           bool preloaded, uint8_t* act, GemvShared& sh) {
@@ -643,9 +648,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
   {
     ActRegs<PRO> ar;
     issue_activation<PRO, DEV>(a, mrow, ar);
-    if (!preloaded) g.prefetch(ua, ub);
+    if (!preloaded && PRE > 0) g.load(ua, nunits > 0 ? 0 : -1);
+    if (!preloaded && PRE > 1) g.load(ub, nunits > 1 ? 1 : -1);
     finish_activation<PRO, G::Q4, DEV>(a, mrow, ar, s_q, s_d, s_off, sh.red, ts);
   }
+  if (!preloaded && PRE < 1) g.load(ua, nunits > 0 ? 0 : -1);
+  if (!preloaded && PRE < 2) g.load(ub, nunits > 1 ? 1 : -1);
   __syncthreads();
   ts.rec(1);
 
