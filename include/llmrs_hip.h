@@ -247,6 +247,12 @@ int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
  * item (0 where not reached), as far as `cap` allows.
  * Returns the number of values written or an error. */
 int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int cap);
+/* Profiling (no reference counterpart): one decode step in which `layer`'s
+ * fused launch records per-workgroup stamps.  us[0..4] = workgroups of the
+ * Q|K|V, attention, O, gate|up and down roles, then 4 values per workgroup
+ * (start, producer wait released, own work done, end) in us from the
+ * earliest start (0 = not recorded).  Returns the count written. */
+int llmrs_model_profile_layer(llmrs_model* m, int layer, double* us, int cap);
 /* Algorithmic weight bytes streamed per decode token (all linear weights). */
 double llmrs_model_weight_bytes(const llmrs_model* m);
 

@@ -80,6 +80,14 @@ struct llmrs_model {
   unsigned pk_grid = 0;              // 0: persistent path unavailable
   size_t pk_lds = 0;
   int host_n_prompt = 0;
+  // fused per-layer decode kernel (layer.hip)
+  std::string lk_name;
+  unsigned lk_grid = 0;              // 0: one launch per GEMV / attention instead
+  size_t lk_lds = 0;
+  int lk_roles[5] = {0, 0, 0, 0, 0}; // workgroups: Q|K|V, attention, O, gate|up, down
+  size_t lk_flag_words = 0;          // completion flags per layer
+  unsigned* lflags = nullptr;        // [n_layers][lk_flag_words]
+  unsigned* epoch = nullptr;         // decode-step counter (embed_gather bumps it)
   // batched prompt (prefill) buffers for chunks of up to pf_cap rows,
   // allocated on first use
   int pf_cap = 0;
@@ -222,12 +230,73 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot) {
   L(p.name, bytes, dim3(p.grid), dim3(256), p.lds, g);
 }
 
+// One whole decoder layer in one launch (layer.hip); `ts` = per-workgroup
+// profiling stamps or null.
+void enqueue_layer(llmrs_model* m, Launcher& L, int li, unsigned long long* ts = nullptr) {
+  const llmrs_model_config& c = m->c;
+  const LayerBufs& B = m->layers[li];
+  LayerArgs a{};
+  a.w = LayerDesc{B.qkv.codes, B.qkv.scales, B.o.codes, B.o.scales, B.gu.codes, B.gu.scales,
+                  B.down.codes, B.down.scales, B.norm[0], B.norm[1], B.kc, B.vc};
+  a.x = m->x;
+  a.qkv = m->qkv;
+  a.h = m->h;
+  a.ctx = m->ctxv;
+  a.ctx_q = m->ctx_q;
+  a.ctx_d = m->ctx_d;
+  a.mf = m->mf;
+  a.m_q = m->m_q;
+  a.m_d = m->m_d;
+  a.rope_cos = m->rope_cos;
+  a.rope_sin = m->rope_sin;
+  a.pos_ptr = m->pos;
+  a.part_o = m->part_o;
+  a.part_ml = m->part_ml;
+  a.counters = m->counters + (size_t)li * c.n_kv_heads;
+  a.flags = m->lflags + (size_t)li * m->lk_flag_words;
+  a.epoch = m->epoch;
+  a.err = m->bar_err;
+  a.hidden = c.hidden;
+  a.nq = c.n_heads;
+  a.nkv = c.n_kv_heads;
+  a.ffn = c.ffn;
+  a.max_seq = c.max_seq;
+  a.qkv_rows = m->qkv_rows;
+  a.nsplit = m->nsplit;
+  a.eps = c.rms_eps;
+  a.attn_scale = 1.0f / std::sqrt((float)c.head_dim);  // layer.rs:258
+  a.n_qkv = m->lk_roles[0];
+  a.n_attn = m->lk_roles[1];
+  a.n_o = m->lk_roles[2];
+  a.n_gu = m->lk_roles[3];
+  a.n_down = m->lk_roles[4];
+  a.ts = ts;
+  const double bytes = linear_weight_bytes(m, B.qkv) + linear_weight_bytes(m, B.o) +
+                       linear_weight_bytes(m, B.gu) + linear_weight_bytes(m, B.down) +
+                       2.0 * c.n_kv_heads * (double)(m->host_pos + 1) * c.head_dim * kv_elem_bytes(m);
+  L(m->lk_name, bytes, dim3(m->lk_grid), dim3(256), m->lk_lds, a);
+}
+
 void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
 
-  EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, H, c.vocab};
+  EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, H, c.vocab, m->epoch};
   L("embed_gather", 8.0 * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
+
+  if (m->lk_grid) {
+    for (int li = 0; li < c.n_layers; ++li) {
+      if (trace_dev)
+        LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)li * H, m->x, H * sizeof(float),
+                                 hipMemcpyDeviceToDevice, L.s));
+      enqueue_layer(m, L, li);
+    }
+    if (trace_dev)
+      LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)c.n_layers * H, m->x, H * sizeof(float),
+                               hipMemcpyDeviceToDevice, L.s));
+    enqueue_head(m, L, write_logits);
+    return;
+  }
 
   const float scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
   const std::string attn = std::string("attn_decode_hd") + std::to_string(hd) +
@@ -352,7 +421,7 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
   auto flops = [](double a, double b, double k) { return 2.0 * a * b * k; };
   const size_t glds = gemm_lds_bytes();
 
-  EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab};
+  EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab, nullptr};
   L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), blk, 0, e);
   const float scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
   // f16 caches use the matrix-core kernel (LLMRS_PREFILL_ATTN=valu selects the
@@ -499,6 +568,54 @@ void plan_persistent(llmrs_model* m) {
   m->pk_grid = (unsigned)(ctx().num_cus * per_cu);
 }
 
+// The fused per-layer kernel for this model: role sizes follow the
+// standalone GEMV plans (with the fused kernel's row-group sizes), LDS is the
+// largest role's.  Opt-in with LLMRS_FUSED=1 (and only for shapes with a
+// compiled variant): measured on the 8B decode it is still slower than one
+// launch per GEMV (53 vs 44 us per layer): each producer-to-consumer hand-off
+// through device-scope flags costs 1-4 us, and with two workgroups per CU
+// resident the later roles are dispatched late and cannot prefetch early.
+void plan_layer(llmrs_model* m) {
+  const llmrs_model_config& c = m->c;
+  m->lk_grid = 0;
+  if (!env_int("LLMRS_FUSED", 0)) return;
+  const int H = c.hidden, F = c.ffn, qd = c.n_heads * c.head_dim, cus = ctx().num_cus;
+  if (qd != H) return;
+  const int uh = (H / 32) % 128 == 0 ? 2 : 1, uf = (F / 32) % 128 == 0 ? 2 : 1;
+  if (uh == uf) return;
+  const bool kv16 = c.kv_dtype == LLMRS_F16;
+  m->lk_name = std::string("layer_") + wt_tag(m->wt) + "_hd" + std::to_string(c.head_dim) +
+               (kv16 ? "_f16" : "_f32") + "_h" + std::to_string(uh) + "f" + std::to_string(uf);
+  const double bpw = m->wt == WT_Q8H ? 34.0 / 32 : m->wt == WT_Q4F ? 20.0 / 32 : 18.0 / 32;
+  // workgroups of a GEMV role: 4 row groups of R rows each, at most 1 per CU
+  // below 24 MB of weights and 2 above (the standalone plan's rule)
+  auto role = [&](int n, int k, int R) {
+    const long per_cu = (double)n * k * bpw < 24e6 ? 1 : 2;
+    const long wgs = (((long)n + R - 1) / R + 3) / 4;
+    return (int)std::max<long>(1, std::min(wgs, per_cu * cus));
+  };
+  m->lk_roles[0] = role(m->qkv_rows, H, 2);
+  m->lk_roles[1] = c.n_kv_heads * m->nsplit;
+  m->lk_roles[2] = role(H, qd, 2);
+  m->lk_roles[3] = (int)std::max<long>(1, std::min<long>((2L * F + 63) / 64, 2L * cus));
+  m->lk_roles[4] = role(H, F, 2);
+  size_t lds = attn_lds_bytes(c.head_dim, kv16);
+  lds = std::max(lds, gemv_lds_bytes(false, m->qkv_rows, H, 2, m->lk_roles[0]));
+  lds = std::max(lds, gemv_lds_bytes(false, H, qd, 2, m->lk_roles[2]));
+  lds = std::max(lds, gemv_lds_bytes(true, 2 * F, H, 2, m->lk_roles[3]));
+  lds = std::max(lds, gemv_lds_bytes(false, H, F, 2, m->lk_roles[4]));
+  m->lk_lds = lds;
+  int per_cu = 0;
+  hipFunction_t f = kernel(m->lk_name);
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, lds) != hipSuccess || per_cu < 1) {
+    (void)hipGetLastError();
+    return;
+  }
+  unsigned total = 0;
+  for (int r : m->lk_roles) total += (unsigned)r;
+  m->lk_grid = total;
+}
+
 // One cooperative launch running positions [pos0, pos0 + n_steps).
 void run_persistent(llmrs_model* m, size_t pos0, size_t n_steps, bool want_logits,
                     unsigned long long* ts = nullptr) {
@@ -561,7 +678,7 @@ void check_barrier(llmrs_model* m) {
   int e = 0;
   LLMRS_HIP(hipMemcpyAsync(&e, m->bar_err, sizeof(int), hipMemcpyDeviceToHost, ctx().stream));
   LLMRS_HIP(hipStreamSynchronize(ctx().stream));
-  if (e) fail(LLMRS_E_HIP, "persistent decode: a grid barrier wait timed out");
+  if (e) fail(LLMRS_E_HIP, "decode: a cross-workgroup wait exceeded its spin limit");
 }
 
 void check_ready(const llmrs_model* m) {
@@ -701,6 +818,10 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     m->part_o = m->dalloc<float>((size_t)nq * m->nsplit * hd);
     m->part_ml = m->dalloc<float>((size_t)nq * m->nsplit * 2);
     plan_persistent(m.get());
+    plan_layer(m.get());
+    m->lk_flag_words = layer_flag_words(m->lk_roles[0], nkv, m->lk_roles[2], m->lk_roles[3]);
+    m->lflags = m->dalloc<unsigned>((size_t)c.n_layers * m->lk_flag_words);
+    m->epoch = m->dalloc<unsigned>(1);
     const size_t nparts = std::max<size_t>((size_t)m->lm_grid, m->pk_grid);
     m->part_val = m->dalloc<float>(nparts);
     m->part_idx = m->dalloc<int>(nparts);
@@ -968,6 +1089,7 @@ int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n, size_t 
     if (next) LLMRS_HIP(hipMemcpyAsync(next, m->gen + start_pos + n, sizeof(int32_t), hipMemcpyDeviceToHost, s));
     LLMRS_HIP(hipStreamSynchronize(s));
     check_err(m);
+    check_barrier(m);
     m->host_pos = start_pos + n;
     m->begun = false;
   });
@@ -1200,6 +1322,41 @@ int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int c
       for (size_t i = 0; i < items * 8 && count < cap; ++i)
         us[count++] = h[ab + i] ? ((double)h[ab + i] - (double)t0) / 100.0 : 0.0;
     }
+  });
+  return rc ? rc : count;
+}
+
+int llmrs_model_profile_layer(llmrs_model* m, int layer, double* us, int cap) {
+  int count = 0;
+  int rc = guard([&] {
+    LLMRS_REQUIRE(m && m->begun && us, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
+    LLMRS_REQUIRE(m->lk_grid, LLMRS_E_INVALID, "the fused layer kernel is not in use");
+    LLMRS_REQUIRE(layer >= 0 && layer < m->c.n_layers, LLMRS_E_RANGE, "layer out of range");
+    LLMRS_REQUIRE(m->host_pos + 1 <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
+    const size_t nts = (size_t)m->lk_grid * 4;
+    unsigned long long* ts = nullptr;
+    LLMRS_HIP(hipMalloc(&ts, nts * sizeof(unsigned long long)));
+    hipStream_t s = ctx().stream;
+    LLMRS_HIP(hipMemsetAsync(ts, 0, nts * sizeof(unsigned long long), s));
+    const llmrs_model_config& c = m->c;
+    Launcher L{s};
+    EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, c.hidden, c.vocab, m->epoch};
+    L("embed_gather", 0.0, dim3((unsigned)((c.hidden + 255) / 256)), dim3(256), 0, e);
+    for (int li = 0; li < c.n_layers; ++li) enqueue_layer(m, L, li, li == layer ? ts : nullptr);
+    enqueue_head(m, L, false);
+    std::vector<unsigned long long> h(nts);
+    LLMRS_HIP(hipMemcpyAsync(h.data(), ts, nts * sizeof(unsigned long long), hipMemcpyDeviceToHost, s));
+    LLMRS_HIP(hipStreamSynchronize(s));
+    (void)hipFree(ts);
+    m->host_pos += 1;
+    check_barrier(m);
+    // us[0..4] = role sizes; then per workgroup 4 stamps in us relative to the
+    // earliest start (0 = not recorded)
+    unsigned long long t0 = ~0ull;
+    for (size_t i = 0; i < nts; i += 4)
+      if (h[i]) t0 = std::min(t0, h[i]);
+    for (int r = 0; r < 5 && count < cap; ++r) us[count++] = m->lk_roles[r];
+    for (size_t i = 0; i < nts && count < cap; ++i) us[count++] = h[i] ? (double)(h[i] - t0) / 100.0 : 0.0;
   });
   return rc ? rc : count;
 }

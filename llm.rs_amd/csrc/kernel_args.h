@@ -113,6 +113,7 @@ struct EmbedArgs {
   float* x;             // [hidden]
   int* err;             // set to 1 on an out-of-range id
   int hidden, vocab;
+  unsigned* epoch;      // decode-step counter, incremented once per launch (may be null)
 };
 
 // Prefill GEMM (prefill.hip): Y[t][r] = sum_b isum_b(t, r) * (d_w[r,b] * d_a[t,b])
@@ -195,6 +196,42 @@ struct LayerDesc {
   void* kc;
   void* vc;
 };
+
+// One decoder layer of the batch-1 decode step in a single launch
+// (layer.hip).  The grid holds five roles in launch order - Q|K|V GEMV,
+// attention, O GEMV, gate|up GEMV, down GEMV - each a contiguous run of
+// workgroups; a role waits for its producer through a counter in `sync`.
+struct LayerArgs {
+  LayerDesc w;               // this layer's weights, norms and caches
+  float* x;                  // [hidden] layer input; the down role writes the output here
+  float* qkv;                // [qkv_rows]
+  float* h;                  // [hidden] x + O . ctx
+  float* ctx;                // [nq*hd]
+  int8_t* ctx_q;
+  float* ctx_d;
+  float* mf;                 // [ffn] silu(g)*u (may be null)
+  int8_t* m_q;
+  float* m_d;
+  const float* rope_cos;
+  const float* rope_sin;
+  const int* pos_ptr;        // device position of the token
+  float* part_o;             // attention partials [nq][nsplit][hd]
+  float* part_ml;
+  int* counters;             // [nkv] attention tickets of this layer, zero between uses
+  unsigned* flags;           // this layer's completion flags: Q|K|V, attention, O, gate|up
+                             // workgroups in that order (layer_flag_words entries)
+  const unsigned* epoch;     // decode-step counter: a flag equal to it is set for this step
+  int* err;                  // set when a wait exceeds its spin limit
+  int hidden, nq, nkv, ffn, max_seq, qkv_rows, nsplit;
+  float eps, attn_scale;
+  int n_qkv, n_attn, n_o, n_gu, n_down;  // workgroups per role
+  unsigned long long* ts;    // profiling: 4 stamps per workgroup (start, released, done, end); null = off
+};
+
+// Completion-flag words per layer of the fused layer kernel.
+constexpr size_t layer_flag_words(int n_qkv, int n_attn_heads, int n_o, int n_gu) {
+  return (size_t)n_qkv + n_attn_heads + n_o + n_gu;
+}
 
 struct DecodeArgs {
   const LayerDesc* layers;   // [n_layers], device memory

@@ -111,8 +111,17 @@ struct AttnLds {
 // One (KV head g, split) work item at decode position pos.  DEV = true moves
 // the projections, the cache, the partials and ctx with device-scope loads
 // and stores (producer and consumer in one persistent launch).
-template <int HD, bool KV16, bool DEV>
-__device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, int pos, uint8_t* lds) {
+struct NoWait {
+  __device__ __forceinline__ bool operator()() const { return true; }
+};
+
+// `wait` runs after the first K/V tile has been requested and before the
+// projections are read: a launch that also computes the projections waits
+// there for them (returning false abandons the item).  Returns true for the
+// workgroup that combined the splits of KV head g (ctx written).
+template <int HD, bool KV16, bool DEV, class Wait = NoWait>
+__device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, int pos, uint8_t* lds,
+                                          const Wait& wait = Wait()) {
   typedef AttnCfg<HD, KV16> C;
   typedef AttnLds<HD, KV16> LY;
   typedef typename C::kv_t kv_t;
@@ -126,9 +135,20 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
   int& s_ticket = *(int*)(lds + LY::TICKET);
 
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
-  unsigned long long* ts = (a.ts && tid == 0) ? a.ts + ((size_t)g * a.nsplit + split) * 8 : nullptr;
+  // Profiling stamps, kept in registers and stored when the item ends (a
+  // store issued mid-kernel would make the next reuse of its data registers
+  // wait for every outstanding load).
+  const bool prof = a.ts != nullptr;
+  unsigned long long st[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   auto stamp = [&](int k) {
-    if (ts) ts[k] = __builtin_amdgcn_s_memrealtime();
+    if (prof) st[k] = __builtin_amdgcn_s_memrealtime();
+  };
+  auto flush_stamps = [&]() {
+    if (prof && tid == 0) {
+      unsigned long long* dst = a.ts + ((size_t)g * a.nsplit + split) * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dst[i] = st[i];
+    }
   };
   stamp(0);
   const int T = pos + 1;
@@ -164,6 +184,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
     }
   };
   if (start < end) issue(start);
+  if (!wait()) return false;
 
   // Rotated query heads of this group (cpu.rs:351-354) and, for the owner
   // of position pos, the rotated k and the v it appends (layer.rs:219-246).
@@ -369,7 +390,10 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
   if (tid == 0) s_ticket = atomicAdd(&a.counters[g], 1);
   __syncthreads();
   stamp(5);
-  if (s_ticket != a.nsplit - 1) return;
+  if (s_ticket != a.nsplit - 1) {
+    flush_stamps();
+    return false;
+  }
 
   // Last workgroup of this KV head: combine the splits.
 #pragma unroll
@@ -452,6 +476,8 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int g, int split, i
   }
   if (tid == 0) dev_stu(a.counters, 4 * g, 0u);
   stamp(6);
+  flush_stamps();
+  return true;
 }
 
 }  // namespace llmrs

@@ -94,6 +94,7 @@ _SIGS = {
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "llmrs_model_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_profile_phases": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_int]),
+    "llmrs_model_profile_layer": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
     "llmrs_model_time_linear": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "llmrs_model_profile_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_char_p,
                                                C.c_void_p, C.c_void_p, C.c_int]),
@@ -427,6 +428,13 @@ class HipModel:
             wgs = out[1 + nl:1 + nl + 10 * grid].reshape(-1, 10)
             return float(out[0]), layers, wgs, out[1 + nl + 10 * grid:n].reshape(-1, 8)
         return float(out[0]), layers
+
+    def profile_layer(self, layer: int = 1, cap: int = 1 << 16):
+        """Per-workgroup stamps of one fused layer launch: (role sizes,
+        [workgroups][4] = start, wait released, work done, end in us)."""
+        out = np.zeros(cap, np.float64)
+        n = _check(lib().llmrs_model_profile_layer(self._h, layer, _ptr(out), cap))
+        return [int(v) for v in out[:5]], out[5:n].reshape(-1, 4)
 
     def weight_bytes(self) -> float:
         return float(lib().llmrs_model_weight_bytes(self._h))

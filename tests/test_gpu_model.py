@@ -346,3 +346,40 @@ def test_attention_split_counts_agree(hip, orc, kv, monkeypatch):
         # only summation order differs: equal up to Q8 code steps
         assert rel_norm_err(tr, ref[1]) < 1e-2, f"splits={splits}"
         assert np.max(np.abs(lg - ref[0])) < 2e-2, f"splits={splits}"
+
+
+FUSED = [
+    syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_heads=8, n_kv_heads=2, ffn=4096, decode=24),
+    syn.tiny(DType.Q8_0, DType.F32, head_dim=64, n_heads=16, n_kv_heads=4, ffn=4096, decode=24),
+    syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_heads=32, n_kv_heads=8, ffn=2048, decode=24),
+]
+
+
+@pytest.mark.parametrize("spec", FUSED, ids=lambda s: f"{s.name}-h{s.hidden}-f{s.ffn}")
+def test_fused_layer_kernel(hip, orc, spec, monkeypatch):
+    """The opt-in one-launch-per-layer decode (LLMRS_FUSED=1; role workgroups
+    hand results over through device-scope completion flags): greedy stream
+    vs the oracle, logits vs the per-kernel path within rounding (only the
+    f32 summation order differs), and the step counter keeps the flags valid
+    across a second generation that revisits the same positions."""
+    w = syn.make_weights(spec)
+    toks = syn.prompt(spec)
+    om = orc.OracleModel.from_spec(spec)
+    om.load(w)
+    otoks, margins = om.generate(toks, spec.decode)
+    monkeypatch.setenv("LLMRS_FUSED", "0")
+    ref = hip.HipModel(spec.config())
+    syn.load_model(ref, w)
+    rlg, _, _ = ref.forward(toks[:1], 0)
+    ref.close()
+    monkeypatch.setenv("LLMRS_FUSED", "1")
+    gm = hip.HipModel(spec.config())
+    syn.load_model(gm, w)
+    for rep in range(2):
+        gtoks = gm.generate(toks, spec.decode)
+        check_stream(gtoks, otoks, np.array(margins), min_steps=spec.decode)
+    roles, stamps = gm.profile_layer(0)  # raises unless the fused kernel is in use
+    assert roles[1] == spec.n_kv_heads * (roles[1] // spec.n_kv_heads) and np.all(stamps[:, 3] >= 0)
+    lg, _, _ = gm.forward(toks[:1], 0)  # one decode step at position 0
+    gm.close()
+    assert np.max(np.abs(lg - rlg)) < 2e-2
