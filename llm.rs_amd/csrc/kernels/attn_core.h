@@ -302,10 +302,12 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     for (int j = 0; j < HPW; ++j) {
       const int hr = wave + 4 * j;
       if (hr >= n_rep) continue;  // uniform per wave
-      // Score of position t0 + lane (sequential over d, as cpu.rs:548).
+      // Score of position t0 + lane.  Four partial sums (d mod 4) instead of
+      // the reference's one sequential sum (cpu.rs:548): with one wave per
+      // SIMD nothing hides the latency of a single dependent FMA chain.
       float sc = -INFINITY;
       if (lane < tvalid) {
-        float s = 0.0f;
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
         // 32-bit LDS reads of the padded row: bank (lane*KSTRIDE/2 + i) mod 64
         // differs across lanes, so the reads are conflict-free.
         const unsigned* krow = (const unsigned*)(s_k + lane * C::KSTRIDE);
@@ -325,41 +327,52 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
             k2 = __uint_as_float(krow[d + 2]);
             k3 = __uint_as_float(krow[d + 3]);
           }
-          s = __builtin_fmaf(q4.x, k0, s);
-          s = __builtin_fmaf(q4.y, k1, s);
-          s = __builtin_fmaf(q4.z, k2, s);
-          s = __builtin_fmaf(q4.w, k3, s);
+          s0 = __builtin_fmaf(q4.x, k0, s0);
+          s1 = __builtin_fmaf(q4.y, k1, s1);
+          s2 = __builtin_fmaf(q4.z, k2, s2);
+          s3 = __builtin_fmaf(q4.w, k3, s3);
         }
-        sc = s * a.scale;
+        sc = ((s0 + s1) + (s2 + s3)) * a.scale;
       }
       const float mnew = fmaxf(m[j], wave_max(sc));
       const float p = (sc == -INFINITY) ? 0.0f : expf(sc - mnew);
       const float corr = (m[j] == -INFINITY) ? 0.0f : expf(m[j] - mnew);
       l[j] = l[j] * corr + wave_sum(p);
       m[j] = mnew;
+      // P.V over the tile's positions in four independent partial sums
+      // (position mod 4); a full tile is unrolled so the LDS reads of
+      // successive rows overlap.
+      float pt[4][DPL];
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) acc[j][e] = acc[j][e] * corr;
-      // P.V over the tile's positions in order; a full tile is unrolled so
-      // the LDS reads of successive rows overlap instead of each waiting.
-      auto pv_row = [&](int u) {
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) pt[c][e] = 0.0f;
+      auto pv_row = [&](int u, int c) {
         const float pu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), u));
         const kv_t* vrow = s_v + u * HD + DPL * lane;
         if constexpr (KV16 && DPL == 2) {
           const unsigned w = *(const unsigned*)vrow;
-          acc[j][0] = __builtin_fmaf(pu, h2f((uint16_t)(w & 0xFFFF)), acc[j][0]);
-          acc[j][1] = __builtin_fmaf(pu, h2f((uint16_t)(w >> 16)), acc[j][1]);
+          pt[c][0] = __builtin_fmaf(pu, h2f((uint16_t)(w & 0xFFFF)), pt[c][0]);
+          pt[c][1] = __builtin_fmaf(pu, h2f((uint16_t)(w >> 16)), pt[c][1]);
         } else {
 #pragma unroll
-          for (int e = 0; e < DPL; ++e)
-            acc[j][e] = __builtin_fmaf(pu, kv_to_f<KV16>(vrow[e]), acc[j][e]);
+          for (int e = 0; e < DPL; ++e) pt[c][e] = __builtin_fmaf(pu, kv_to_f<KV16>(vrow[e]), pt[c][e]);
         }
       };
       if (tvalid == TILE) {
 #pragma unroll 16
-        for (int u = 0; u < TILE; ++u) pv_row(u);
+        for (int u = 0; u < TILE; u += 4) {
+          pv_row(u, 0);
+          pv_row(u + 1, 1);
+          pv_row(u + 2, 2);
+          pv_row(u + 3, 3);
+        }
       } else {
-        for (int u = 0; u < tvalid; ++u) pv_row(u);
+        for (int u = 0; u < tvalid; ++u) pv_row(u, 0);
       }
+#pragma unroll
+      for (int e = 0; e < DPL; ++e)
+        acc[j][e] = acc[j][e] * corr + ((pt[0][e] + pt[1][e]) + (pt[2][e] + pt[3][e]));
     }
   }
 
@@ -402,33 +415,50 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     if (hr >= n_rep) continue;
     const int h = g * n_rep + hr;
     const size_t base = (size_t)h * a.nsplit;
-    // (m, l) of split s0 + lane, 64 splits per round, so the loads of all
-    // splits are in flight together (every split writes its partials; an
-    // empty one has m = -inf, l = 0, o = 0).
-    // The first PF splits' partial-O values are loaded together with the
-    // (m, l) values, so a short combine costs one memory round trip.
-    constexpr int PF = 16;
+    // One batch of device-scope loads: (m, l) of split `lane` (8 bytes) and
+    // this lane's dims of the first PF splits' partial O, so a combine of up
+    // to PF splits costs one memory round trip (every split writes its
+    // partials; an empty one has m = -inf, l = 0, o = 0).  Splits beyond PF
+    // (and beyond 64, in further rounds) are loaded as they are used.
+    constexpr int PF = 32;
     float opf[PF][DPL];
 #pragma unroll
-    for (int u = 0; u < PF; ++u)
-#pragma unroll
-      for (int e = 0; e < DPL; ++e)
-        opf[u][e] = u < a.nsplit ? ld_part<true>(a.part_o, (base + u) * HD + DPL * lane + e) : 0.0f;
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < a.nsplit; s0 += LLMRS_WAVE) {
+    for (int u = 0; u < PF; ++u) {
+      const int uu = min(u, a.nsplit - 1);  // clamped; weighted by 0 past nsplit
+      const int off = (int)(((base + uu) * HD + DPL * lane) * 4);
+      if constexpr (DPL == 2) {
+        const dev_u32x2 t = dev_ld8(a.part_o, off);
+        opf[u][0] = __uint_as_float(t.x);
+        opf[u][1] = __uint_as_float(t.y);
+      } else {
+        opf[u][0] = dev_ldf(a.part_o, off);
+      }
+    }
+    float ms, ls;
+    {
+      const int sp = min(lane, a.nsplit - 1);
+      const dev_u32x2 t = dev_ld8(a.part_ml, (int)(2 * (base + sp) * 4));
+      ms = lane < a.nsplit ? __uint_as_float(t.x) : -INFINITY;
+      ls = lane < a.nsplit ? __uint_as_float(t.y) : 0.0f;
+    }
+    float M = wave_max(ms);
+    for (int s0 = LLMRS_WAVE; s0 < a.nsplit; s0 += LLMRS_WAVE) {
       const int sp = s0 + lane;
-      const float ms = sp < a.nsplit ? ld_part<true>(a.part_ml, 2 * (base + sp)) : -INFINITY;
-      M = fmaxf(M, wave_max(ms));
+      const float mx = sp < a.nsplit ? ld_part<true>(a.part_ml, 2 * (base + sp)) : -INFINITY;
+      M = fmaxf(M, wave_max(mx));
     }
     float L = 0.0f, o[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; ++e) o[e] = 0.0f;
     for (int s0 = 0; s0 < a.nsplit; s0 += LLMRS_WAVE) {
       const int sp = s0 + lane;
-      float ms = -INFINITY, ls = 0.0f;
-      if (sp < a.nsplit) {
-        ms = ld_part<true>(a.part_ml, 2 * (base + sp));
-        ls = ld_part<true>(a.part_ml, 2 * (base + sp) + 1);
+      if (s0 > 0) {
+        ms = -INFINITY;
+        ls = 0.0f;
+        if (sp < a.nsplit) {
+          ms = ld_part<true>(a.part_ml, 2 * (base + sp));
+          ls = ld_part<true>(a.part_ml, 2 * (base + sp) + 1);
+        }
       }
       const float w = ms == -INFINITY ? 0.0f : expf(ms - M);
       L = L + wave_sum(ls * w);
@@ -437,9 +467,10 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
       if (s0 == 0) {
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
+          // w is 0 in lanes past nsplit, so the clamped extra loads add 0
           const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) o[e] = o[e] + opf[u][e] * wu;  // 0 * 0 past nsplit
+          for (int e = 0; e < DPL; ++e) o[e] = o[e] + opf[u][e] * wu;
         }
         u0 = PF;
       }

@@ -118,6 +118,10 @@ __device__ __forceinline__ float dev_ldf(const void* base, int byte_off) {
 __device__ __forceinline__ unsigned dev_ldu(const void* base, int byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b32(dev_rsrc(base), byte_off, 0, kSc1);
 }
+typedef unsigned int dev_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ dev_u32x2 dev_ld8(const void* base, int byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(dev_rsrc(base), byte_off, 0, kSc1);
+}
 __device__ __forceinline__ dev_u32x4 dev_ld16(const void* base, int byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(dev_rsrc(base), byte_off, 0, kSc1);
 }
