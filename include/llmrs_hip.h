@@ -237,21 +237,12 @@ int llmrs_model_time_linear(llmrs_model* m, int slot, int reps, double* us_per_l
 int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
                                 size_t start_pos, char* names, float* ms,
                                 double* work, int cap);
-/* Phase timing of the persistent decode kernel: runs `n_steps` more decode
- * steps in one launch and returns in `us` (up to `cap` values): the launch
- * wall time per step, then for each layer of the first step ten intervals
- * seen by workgroup 0 - QKV work, barrier wait, attention work, wait, O work,
- * wait, gate|up work, wait, down work, wait (layer 0's QKV interval is 0);
- * then, for layer 1, each workgroup's ten phase timestamps (us after the end
- * of workgroup 0's layer 0), then 8 stage timestamps of each attention work
- * item (0 where not reached), as far as `cap` allows.
- * Returns the number of values written or an error. */
-int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int cap);
 /* Profiling (no reference counterpart): one decode step in which `layer`'s
- * fused launch records per-workgroup stamps.  us[0..4] = workgroups of the
- * Q|K|V, attention, O, gate|up and down roles, then 4 values per workgroup
- * (start, producer wait released, own work done, end) in us from the
- * earliest start (0 = not recorded).  Returns the count written. */
+ * attention + O and gate|up + down launches record per-workgroup stamps.
+ * us[0..3] = workgroups of the attention, O, gate|up and down roles, then 4
+ * values per workgroup of the two launches in turn (start, producer wait
+ * released, own work done, end) in us from that launch's earliest start
+ * (0 = not recorded).  Returns the count written. */
 int llmrs_model_profile_layer(llmrs_model* m, int layer, double* us, int cap);
 /* Algorithmic weight bytes streamed per decode token (all linear weights). */
 double llmrs_model_weight_bytes(const llmrs_model* m);

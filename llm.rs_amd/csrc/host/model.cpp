@@ -72,19 +72,13 @@ struct llmrs_model {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   bool graph_failed = false;
-  // persistent decode kernel (decode.hip)
-  LayerDesc* layer_desc = nullptr;   // device copy of the per-layer pointers
-  unsigned* bar = nullptr;           // grid barrier words
-  int* bar_err = nullptr;
-  std::string pk_name;
-  unsigned pk_grid = 0;              // 0: persistent path unavailable
-  size_t pk_lds = 0;
+  int* bar_err = nullptr;            // set by a cross-workgroup wait that exceeded its spin limit
   int host_n_prompt = 0;
-  // fused per-layer decode kernel (layer.hip)
-  std::string lk_name;
-  unsigned lk_grid = 0;              // 0: one launch per GEMV / attention instead
-  size_t lk_lds = 0;
-  int lk_roles[5] = {0, 0, 0, 0, 0}; // workgroups: Q|K|V, attention, O, gate|up, down
+  // attention + O and gate|up + down launches (layer.hip)
+  std::string ao_name, mlp_name;
+  unsigned ao_grid = 0, mlp_grid = 0;  // 0: one launch per GEMV / attention instead
+  size_t ao_lds = 0, mlp_lds = 0;
+  int lk_roles[4] = {0, 0, 0, 0};      // workgroups: attention, O, gate|up, down
   size_t lk_flag_words = 0;          // completion flags per layer
   unsigned* lflags = nullptr;        // [n_layers][lk_flag_words]
   unsigned* epoch = nullptr;         // decode-step counter (embed_gather bumps it)
@@ -230,9 +224,10 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot) {
   L(p.name, bytes, dim3(p.grid), dim3(256), p.lds, g);
 }
 
-// One whole decoder layer in one launch (layer.hip); `ts` = per-workgroup
-// profiling stamps or null.
-void enqueue_layer(llmrs_model* m, Launcher& L, int li, unsigned long long* ts = nullptr) {
+// Attention + O, then gate|up + down, of layer li (layer.hip); `ts` =
+// per-workgroup profiling stamps of both launches ([ao_grid + mlp_grid][4])
+// or null.
+void enqueue_layer_tail(llmrs_model* m, Launcher& L, int li, unsigned long long* ts = nullptr) {
   const llmrs_model_config& c = m->c;
   const LayerBufs& B = m->layers[li];
   LayerArgs a{};
@@ -265,16 +260,16 @@ void enqueue_layer(llmrs_model* m, Launcher& L, int li, unsigned long long* ts =
   a.nsplit = m->nsplit;
   a.eps = c.rms_eps;
   a.attn_scale = 1.0f / std::sqrt((float)c.head_dim);  // layer.rs:258
-  a.n_qkv = m->lk_roles[0];
-  a.n_attn = m->lk_roles[1];
-  a.n_o = m->lk_roles[2];
-  a.n_gu = m->lk_roles[3];
-  a.n_down = m->lk_roles[4];
+  a.n_attn = m->lk_roles[0];
+  a.n_o = m->lk_roles[1];
+  a.n_gu = m->lk_roles[2];
+  a.n_down = m->lk_roles[3];
   a.ts = ts;
-  const double bytes = linear_weight_bytes(m, B.qkv) + linear_weight_bytes(m, B.o) +
-                       linear_weight_bytes(m, B.gu) + linear_weight_bytes(m, B.down) +
-                       2.0 * c.n_kv_heads * (double)(m->host_pos + 1) * c.head_dim * kv_elem_bytes(m);
-  L(m->lk_name, bytes, dim3(m->lk_grid), dim3(256), m->lk_lds, a);
+  const double kvb = 2.0 * c.n_kv_heads * (double)(m->host_pos + 1) * c.head_dim * kv_elem_bytes(m);
+  L(m->ao_name, linear_weight_bytes(m, B.o) + kvb, dim3(m->ao_grid), dim3(256), m->ao_lds, a);
+  a.ts = ts ? ts + 4 * (size_t)m->ao_grid : nullptr;
+  L(m->mlp_name, linear_weight_bytes(m, B.gu) + linear_weight_bytes(m, B.down), dim3(m->mlp_grid),
+    dim3(256), m->mlp_lds, a);
 }
 
 void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
@@ -284,12 +279,13 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
   EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, H, c.vocab, m->epoch};
   L("embed_gather", 8.0 * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
 
-  if (m->lk_grid) {
+  if (m->ao_grid) {
     for (int li = 0; li < c.n_layers; ++li) {
       if (trace_dev)
         LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)li * H, m->x, H * sizeof(float),
                                  hipMemcpyDeviceToDevice, L.s));
-      enqueue_layer(m, L, li);
+      enqueue_linear(m, L, li, LLMRS_W_Q);
+      enqueue_layer_tail(m, L, li);
     }
     if (trace_dev)
       LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)c.n_layers * H, m->x, H * sizeof(float),
@@ -528,150 +524,45 @@ void run_prefill(llmrs_model* m, size_t start, size_t n, int n_prompt, bool writ
   }
 }
 
-// The persistent decode kernel for this model, its LDS and grid: as many
-// workgroups per CU as fit (at most 2), so a cooperative launch keeps all of
-// them resident.  Opt-in with LLMRS_PERSISTENT=1: measured on MI355X it is
-// still slower than the per-kernel graph path (each of its five phases per
-// layer pays device-scope load and barrier latency of several us).
-void plan_persistent(llmrs_model* m) {
-  const llmrs_model_config& c = m->c;
-  m->pk_grid = 0;
-  if (!env_int("LLMRS_PERSISTENT", 0)) return;
-  const int H = c.hidden, F = c.ffn, qd = c.n_heads * c.head_dim;
-  const int kmax = std::max(std::max(H, qd), F);
-  // U = 2 when the hidden size splits into 128-block chunks (Q8_0 weights
-  // keep U = 1: two units of 32-byte blocks do not fit the register budget).
-  int U = (m->wt != WT_Q8H && (H / 32) % 128 == 0) ? 2 : 1;
-  const int eu = env_int("LLMRS_PERSISTENT_U", 0);
-  if (eu == 1 || eu == 2) U = eu;
-  const bool kv16 = c.kv_dtype == LLMRS_F16;
-  m->pk_name = std::string("decode_") + wt_tag(m->wt) + "_hd" + std::to_string(c.head_dim) +
-               (kv16 ? "_f16" : "_f32") + "_u" + std::to_string(U);
-  // LDS for the largest phase; results areas sized for one workgroup per CU
-  // (the fewest workgroups a launch can have), so any resident grid fits.
-  const int nw = std::max(1, ctx().num_cus);
-  size_t gl = gemv_lds_bytes(false, m->qkv_rows, H, 2, nw);
-  gl = std::max(gl, gemv_lds_bytes(false, H, qd, 2, nw));
-  gl = std::max(gl, gemv_lds_bytes(true, 2 * F, H, 2, nw));
-  gl = std::max(gl, gemv_lds_bytes(false, H, F, 2, nw));
-  gl = std::max(gl, gemv_lds_bytes(false, c.vocab, H, 2, nw));
-  (void)kmax;
-  m->pk_lds = std::max(gl, attn_lds_bytes(c.head_dim, kv16));
-  hipFunction_t f = kernel(m->pk_name);
-  int per_cu = 0;
-  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, m->pk_lds) != hipSuccess) {
-    (void)hipGetLastError();
-    return;
-  }
-  per_cu = std::min(per_cu, std::max(1, env_int("LLMRS_PERSISTENT_WG_PER_CU", 2)));
-  if (per_cu < 1) return;
-  m->pk_grid = (unsigned)(ctx().num_cus * per_cu);
-}
-
-// The fused per-layer kernel for this model: role sizes follow the
-// standalone GEMV plans (with the fused kernel's row-group sizes), LDS is the
-// largest role's.  Opt-in with LLMRS_FUSED=1 (and only for shapes with a
-// compiled variant): measured on the 8B decode it is still slower than one
-// launch per GEMV (53 vs 44 us per layer): each producer-to-consumer hand-off
-// through device-scope flags costs 1-4 us, and with two workgroups per CU
-// resident the later roles are dispatched late and cannot prefetch early.
+// The attention + O and gate|up + down launches for this model (opt-in with
+// LLMRS_FUSED=1; the O input length must equal the hidden size): role sizes
+// follow the standalone GEMV plans, LDS is the larger role's.  Measured on
+// the 8B decode they are slower than one launch per GEMV and attention (645
+// vs 706 tok/s): a consumer sees its producers' completion flags 1.5-3.5 us
+// after the last one is set, more than a kernel boundary costs in a graph,
+// and the consumers' early weight requests slow the producers' own loads.
 void plan_layer(llmrs_model* m) {
   const llmrs_model_config& c = m->c;
-  m->lk_grid = 0;
+  m->ao_grid = m->mlp_grid = 0;
   if (!env_int("LLMRS_FUSED", 0)) return;
   const int H = c.hidden, F = c.ffn, qd = c.n_heads * c.head_dim, cus = ctx().num_cus;
   if (qd != H) return;
   const int uh = (H / 32) % 128 == 0 ? 2 : 1, uf = (F / 32) % 128 == 0 ? 2 : 1;
-  if (uh == uf) return;
   const bool kv16 = c.kv_dtype == LLMRS_F16;
-  m->lk_name = std::string("layer_") + wt_tag(m->wt) + "_hd" + std::to_string(c.head_dim) +
-               (kv16 ? "_f16" : "_f32") + "_h" + std::to_string(uh) + "f" + std::to_string(uf);
-  const double bpw = m->wt == WT_Q8H ? 34.0 / 32 : m->wt == WT_Q4F ? 20.0 / 32 : 18.0 / 32;
-  // workgroups of a GEMV role: 4 row groups of R rows each, at most 1 per CU
-  // below 24 MB of weights and 2 above (the standalone plan's rule)
-  auto role = [&](int n, int k, int R) {
-    const long per_cu = (double)n * k * bpw < 24e6 ? 1 : 2;
-    const long wgs = (((long)n + R - 1) / R + 3) / 4;
-    return (int)std::max<long>(1, std::min(wgs, per_cu * cus));
-  };
-  m->lk_roles[0] = role(m->qkv_rows, H, 2);
-  m->lk_roles[1] = c.n_kv_heads * m->nsplit;
-  m->lk_roles[2] = role(H, qd, 2);
-  m->lk_roles[3] = (int)std::max<long>(1, std::min<long>((2L * F + 63) / 64, 2L * cus));
-  m->lk_roles[4] = role(H, F, 2);
-  size_t lds = attn_lds_bytes(c.head_dim, kv16);
-  lds = std::max(lds, gemv_lds_bytes(false, m->qkv_rows, H, 2, m->lk_roles[0]));
-  lds = std::max(lds, gemv_lds_bytes(false, H, qd, 2, m->lk_roles[2]));
-  lds = std::max(lds, gemv_lds_bytes(true, 2 * F, H, 2, m->lk_roles[3]));
-  lds = std::max(lds, gemv_lds_bytes(false, H, F, 2, m->lk_roles[4]));
-  m->lk_lds = lds;
-  int per_cu = 0;
-  hipFunction_t f = kernel(m->lk_name);
-  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 256, lds) != hipSuccess || per_cu < 1) {
-    (void)hipGetLastError();
-    return;
+  m->ao_name = std::string("attn_o_") + wt_tag(m->wt) + "_hd" + std::to_string(c.head_dim) +
+               (kv16 ? "_f16" : "_f32") + "_u" + std::to_string(uh);
+  m->mlp_name = std::string("mlp_") + wt_tag(m->wt) + "_h" + std::to_string(uh) + "f" + std::to_string(uf);
+  const GemvPlan po = gemv_plan(m->wt, "q8_resid", H, qd, cus);
+  const GemvPlan pg = gemv_plan(m->wt, "norm_silu", 2 * F, H, cus);
+  const GemvPlan pd = gemv_plan(m->wt, "q8_resid", H, F, cus);
+  // the fused roles use 2-row groups for O and down, 4-row for gate|up
+  if (po.name.find("_r2u") == std::string::npos || pd.name.find("_r2u") == std::string::npos) return;
+  m->lk_roles[0] = c.n_kv_heads * m->nsplit;
+  m->lk_roles[1] = (int)po.grid;
+  m->lk_roles[2] = (int)pg.grid;
+  m->lk_roles[3] = (int)pd.grid;
+  m->ao_lds = std::max(attn_lds_bytes(c.head_dim, kv16), po.lds);
+  m->mlp_lds = std::max(pg.lds, pd.lds);
+  for (auto [name, lds] : {std::make_pair(m->ao_name, m->ao_lds), std::make_pair(m->mlp_name, m->mlp_lds)}) {
+    int per_cu = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel(name), 256, lds) != hipSuccess ||
+        per_cu < 1) {
+      (void)hipGetLastError();
+      return;
+    }
   }
-  unsigned total = 0;
-  for (int r : m->lk_roles) total += (unsigned)r;
-  m->lk_grid = total;
-}
-
-// One cooperative launch running positions [pos0, pos0 + n_steps).
-void run_persistent(llmrs_model* m, size_t pos0, size_t n_steps, bool want_logits,
-                    unsigned long long* ts = nullptr) {
-  const llmrs_model_config& c = m->c;
-  hipStream_t s = ctx().stream;
-  LLMRS_HIP(hipMemsetAsync(m->bar, 0, 1024 * sizeof(unsigned), s));
-  LLMRS_HIP(hipMemsetAsync(m->bar_err, 0, sizeof(int), s));
-  DecodeArgs d{};
-  d.layers = m->layer_desc;
-  d.embed = m->embed;
-  d.final_norm = m->final_norm;
-  d.lm_w = m->lm_head.codes;
-  d.lm_s = m->lm_head.scales;
-  d.rope_cos = m->rope_cos;
-  d.rope_sin = m->rope_sin;
-  d.x = m->x;
-  d.h = m->h;
-  d.qkv = m->qkv;
-  d.ctx = m->ctxv;
-  d.ctx_q = m->ctx_q;
-  d.ctx_d = m->ctx_d;
-  d.mf = m->mf;
-  d.m_q = m->m_q;
-  d.m_d = m->m_d;
-  d.logits = want_logits ? m->logits : nullptr;
-  d.part_o = m->part_o;
-  d.part_ml = m->part_ml;
-  d.counters = m->counters;
-  d.part_val = m->part_val;
-  d.part_idx = m->part_idx;
-  d.bar = m->bar;
-  d.tokens = m->tokens;
-  d.gen = m->gen;
-  d.tokens_out = m->tokens;
-  d.pos_out = m->pos;
-  d.err = m->bar_err;
-  d.ts = ts;
-  d.n_layers = c.n_layers;
-  d.hidden = c.hidden;
-  d.nq = c.n_heads;
-  d.nkv = c.n_kv_heads;
-  d.hd = c.head_dim;
-  d.ffn = c.ffn;
-  d.vocab = c.vocab;
-  d.max_seq = c.max_seq;
-  d.qkv_rows = m->qkv_rows;
-  d.pos0 = (int)pos0;
-  d.n_steps = (int)n_steps;
-  d.n_prompt = m->host_n_prompt;
-  d.cap = m->cap;
-  d.nsplit = m->nsplit;
-  d.eps = c.rms_eps;
-  d.attn_scale = 1.0f / std::sqrt((float)c.head_dim);  // layer.rs:258
-  void* params[] = {&d};
-  LLMRS_HIP(hipModuleLaunchCooperativeKernel(kernel(m->pk_name), m->pk_grid, 1, 1, 256, 1, 1,
-                                             (unsigned)m->pk_lds, s, params));
+  m->ao_grid = (unsigned)(m->lk_roles[0] + m->lk_roles[1]);
+  m->mlp_grid = (unsigned)(m->lk_roles[2] + m->lk_roles[3]);
 }
 
 void check_barrier(llmrs_model* m) {
@@ -817,12 +708,11 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     m->logits = m->dalloc<float>(c.vocab);
     m->part_o = m->dalloc<float>((size_t)nq * m->nsplit * hd);
     m->part_ml = m->dalloc<float>((size_t)nq * m->nsplit * 2);
-    plan_persistent(m.get());
     plan_layer(m.get());
-    m->lk_flag_words = layer_flag_words(m->lk_roles[0], nkv, m->lk_roles[2], m->lk_roles[3]);
+    m->lk_flag_words = layer_flag_words(nkv, m->lk_roles[1], m->lk_roles[2]);
     m->lflags = m->dalloc<unsigned>((size_t)c.n_layers * m->lk_flag_words);
     m->epoch = m->dalloc<unsigned>(1);
-    const size_t nparts = std::max<size_t>((size_t)m->lm_grid, m->pk_grid);
+    const size_t nparts = (size_t)m->lm_grid;
     m->part_val = m->dalloc<float>(nparts);
     m->part_idx = m->dalloc<int>(nparts);
     m->counters = m->dalloc<int>((size_t)c.n_layers * nkv);
@@ -841,19 +731,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
       LLMRS_HIP(hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, cx.stream));
       LLMRS_HIP(hipMemcpyAsync(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, cx.stream));
     }
-    m->bar = m->dalloc<unsigned>(1024);
     m->bar_err = m->dalloc<int>(1);
-    {  // per-layer pointers for the persistent kernel
-      std::vector<LayerDesc> ld(c.n_layers);
-      for (int l = 0; l < c.n_layers; ++l) {
-        const LayerBufs& B = m->layers[l];
-        ld[l] = LayerDesc{B.qkv.codes, B.qkv.scales, B.o.codes, B.o.scales, B.gu.codes, B.gu.scales,
-                          B.down.codes, B.down.scales, B.norm[0], B.norm[1], B.kc, B.vc};
-      }
-      m->layer_desc = m->dalloc<LayerDesc>(ld.size());
-      LLMRS_HIP(hipMemcpyAsync(m->layer_desc, ld.data(), ld.size() * sizeof(LayerDesc),
-                               hipMemcpyHostToDevice, cx.stream));
-    }
     LLMRS_HIP(hipStreamSynchronize(cx.stream));
     // Resolve every kernel of the step now, so graph capture never has to.
     (void)kernel(gemv_plan(m->wt, "norm_store", m->qkv_rows, H, cx.num_cus).name);
@@ -1105,8 +983,6 @@ int llmrs_model_begin(llmrs_model* m, const int32_t* prompt, size_t n_prompt) {
     m->host_n_prompt = (int)n_prompt;
     if (n_prompt > 1 && prefill_enabled()) {
       run_prefill(m, 0, n_prompt, (int)n_prompt, false, nullptr);
-    } else if (m->pk_grid) {
-      run_persistent(m, 0, n_prompt, false);
     } else {
       for (size_t p = 0; p < n_prompt; ++p) {
         m->host_pos = p;
@@ -1122,11 +998,6 @@ int llmrs_model_decode_steps(llmrs_model* m, size_t n) {
   return guard([&] {
     LLMRS_REQUIRE(m && m->begun, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
     LLMRS_REQUIRE(m->host_pos + n <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
-    if (m->pk_grid) {
-      if (n) run_persistent(m, m->host_pos, n, false);
-      m->host_pos += n;
-      return;
-    }
     for (size_t i = 0; i < n; ++i) {
       replay_step(m);
       m->host_pos += 1;
@@ -1270,70 +1141,14 @@ int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
   return rc ? rc : count;
 }
 
-int llmrs_model_profile_phases(llmrs_model* m, size_t n_steps, double* us, int cap) {
-  int count = 0;
-  int rc = guard([&] {
-    LLMRS_REQUIRE(m && m->begun && us, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
-    LLMRS_REQUIRE(m->pk_grid, LLMRS_E_INVALID, "the persistent decode kernel is not in use");
-    LLMRS_REQUIRE(n_steps >= 1 && m->host_pos + n_steps <= (size_t)m->c.max_seq, LLMRS_E_RANGE,
-                  "decode beyond max_seq");
-    const size_t items = (size_t)m->c.n_kv_heads * m->nsplit;
-    const size_t nts = (size_t)m->c.n_layers * 10 + (size_t)m->pk_grid * 10 + items * 8;
-    unsigned long long* ts = nullptr;
-    LLMRS_HIP(hipMalloc(&ts, nts * sizeof(unsigned long long)));
-    LLMRS_HIP(hipMemsetAsync(ts, 0, nts * sizeof(unsigned long long), ctx().stream));
-    hipEvent_t e0, e1;
-    LLMRS_HIP(hipEventCreate(&e0));
-    LLMRS_HIP(hipEventCreate(&e1));
-    LLMRS_HIP(hipEventRecord(e0, ctx().stream));
-    run_persistent(m, m->host_pos, n_steps, false, ts);
-    LLMRS_HIP(hipEventRecord(e1, ctx().stream));
-    std::vector<unsigned long long> h(nts);
-    LLMRS_HIP(hipMemcpyAsync(h.data(), ts, nts * sizeof(unsigned long long), hipMemcpyDeviceToHost,
-                             ctx().stream));
-    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
-    float total_ms = 0.0f;
-    (void)hipEventElapsedTime(&total_ms, e0, e1);
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    (void)hipFree(ts);
-    m->host_pos += n_steps;
-    check_barrier(m);
-    // us[0] = launch wall time per step; then per layer 10 intervals (100 MHz ticks -> us):
-    // QKV work, wait, ATTN work, wait, O work, wait, GU work, wait, DOWN work, wait.
-    if (cap > 0) us[count++] = total_ms * 1e3 / (double)n_steps;
-    for (int l = 0; l < m->c.n_layers; ++l) {
-      const unsigned long long* t = h.data() + (size_t)l * 10;
-      const unsigned long long prev = l == 0 ? t[0] : h[(size_t)(l - 1) * 10 + 9];
-      for (int i = 0; i < 10 && count < cap; ++i) {
-        const unsigned long long a = i == 0 ? prev : t[i - 1];
-        us[count++] = (double)(t[i] - a) / 100.0;
-      }
-    }
-    // then, for layer 1, every workgroup's ten timestamps relative to the
-    // end of workgroup 0's layer-0 block
-    if (m->c.n_layers > 1) {
-      const unsigned long long t0 = h[9];
-      for (size_t w = 0; w < m->pk_grid; ++w)
-        for (int i = 0; i < 10 && count < cap; ++i)
-          us[count++] = ((double)h[(size_t)m->c.n_layers * 10 + w * 10 + i] - (double)t0) / 100.0;
-      // and the attention items' stage timestamps (8 each; 0 = not reached)
-      const size_t ab = (size_t)m->c.n_layers * 10 + (size_t)m->pk_grid * 10;
-      for (size_t i = 0; i < items * 8 && count < cap; ++i)
-        us[count++] = h[ab + i] ? ((double)h[ab + i] - (double)t0) / 100.0 : 0.0;
-    }
-  });
-  return rc ? rc : count;
-}
-
 int llmrs_model_profile_layer(llmrs_model* m, int layer, double* us, int cap) {
   int count = 0;
   int rc = guard([&] {
     LLMRS_REQUIRE(m && m->begun && us, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
-    LLMRS_REQUIRE(m->lk_grid, LLMRS_E_INVALID, "the fused layer kernel is not in use");
+    LLMRS_REQUIRE(m->ao_grid, LLMRS_E_INVALID, "the fused layer launches are not in use");
     LLMRS_REQUIRE(layer >= 0 && layer < m->c.n_layers, LLMRS_E_RANGE, "layer out of range");
     LLMRS_REQUIRE(m->host_pos + 1 <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
-    const size_t nts = (size_t)m->lk_grid * 4;
+    const size_t nts = ((size_t)m->ao_grid + m->mlp_grid) * 4;
     unsigned long long* ts = nullptr;
     LLMRS_HIP(hipMalloc(&ts, nts * sizeof(unsigned long long)));
     hipStream_t s = ctx().stream;
@@ -1342,7 +1157,10 @@ int llmrs_model_profile_layer(llmrs_model* m, int layer, double* us, int cap) {
     Launcher L{s};
     EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, c.hidden, c.vocab, m->epoch};
     L("embed_gather", 0.0, dim3((unsigned)((c.hidden + 255) / 256)), dim3(256), 0, e);
-    for (int li = 0; li < c.n_layers; ++li) enqueue_layer(m, L, li, li == layer ? ts : nullptr);
+    for (int li = 0; li < c.n_layers; ++li) {
+      enqueue_linear(m, L, li, LLMRS_W_Q);
+      enqueue_layer_tail(m, L, li, li == layer ? ts : nullptr);
+    }
     enqueue_head(m, L, false);
     std::vector<unsigned long long> h(nts);
     LLMRS_HIP(hipMemcpyAsync(h.data(), ts, nts * sizeof(unsigned long long), hipMemcpyDeviceToHost, s));
@@ -1350,13 +1168,16 @@ int llmrs_model_profile_layer(llmrs_model* m, int layer, double* us, int cap) {
     (void)hipFree(ts);
     m->host_pos += 1;
     check_barrier(m);
-    // us[0..4] = role sizes; then per workgroup 4 stamps in us relative to the
-    // earliest start (0 = not recorded)
-    unsigned long long t0 = ~0ull;
-    for (size_t i = 0; i < nts; i += 4)
-      if (h[i]) t0 = std::min(t0, h[i]);
-    for (int r = 0; r < 5 && count < cap; ++r) us[count++] = m->lk_roles[r];
-    for (size_t i = 0; i < nts && count < cap; ++i) us[count++] = h[i] ? (double)(h[i] - t0) / 100.0 : 0.0;
+    // us[0..3] = role sizes; then per workgroup of the two launches 4 stamps
+    // in us relative to that launch's earliest start (0 = not recorded)
+    for (int r = 0; r < 4 && count < cap; ++r) us[count++] = m->lk_roles[r];
+    for (int k = 0; k < 2; ++k) {
+      const size_t b = k == 0 ? 0 : (size_t)m->ao_grid * 4, e2 = k == 0 ? (size_t)m->ao_grid * 4 : nts;
+      unsigned long long t0 = ~0ull;
+      for (size_t i = b; i < e2; i += 4)
+        if (h[i]) t0 = std::min(t0, h[i]);
+      for (size_t i = b; i < e2 && count < cap; ++i) us[count++] = h[i] ? (double)(h[i] - t0) / 100.0 : 0.0;
+    }
   });
   return rc ? rc : count;
 }

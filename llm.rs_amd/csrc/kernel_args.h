@@ -181,7 +181,7 @@ constexpr size_t attn_lds_bytes(int hd, bool kv16) {
   return nw + 4 * 2 * (size_t)hd + 16;
 }
 
-// Persistent decode kernel (decode.hip): the per-layer weights and caches.
+// The weights, norms and caches of one decoder layer (layer.hip).
 struct LayerDesc {
   const uint8_t* qkv_w;
   const void* qkv_s;
@@ -197,10 +197,9 @@ struct LayerDesc {
   void* vc;
 };
 
-// One decoder layer of the batch-1 decode step in a single launch
-// (layer.hip).  The grid holds five roles in launch order - Q|K|V GEMV,
-// attention, O GEMV, gate|up GEMV, down GEMV - each a contiguous run of
-// workgroups; a role waits for its producer through a counter in `sync`.
+// Attention + O and gate|up + down of one decoder layer, one launch each
+// (layer.hip): producer-role workgroups first, consumer-role workgroups
+// after them, consumers waiting on the producers' completion flags.
 struct LayerArgs {
   LayerDesc w;               // this layer's weights, norms and caches
   float* x;                  // [hidden] layer input; the down role writes the output here
@@ -218,55 +217,20 @@ struct LayerArgs {
   float* part_o;             // attention partials [nq][nsplit][hd]
   float* part_ml;
   int* counters;             // [nkv] attention tickets of this layer, zero between uses
-  unsigned* flags;           // this layer's completion flags: Q|K|V, attention, O, gate|up
-                             // workgroups in that order (layer_flag_words entries)
+  unsigned* flags;           // this layer's completion flags: attention (one per KV head),
+                             // O, gate|up workgroups in that order (layer_flag_words entries)
   const unsigned* epoch;     // decode-step counter: a flag equal to it is set for this step
   int* err;                  // set when a wait exceeds its spin limit
   int hidden, nq, nkv, ffn, max_seq, qkv_rows, nsplit;
   float eps, attn_scale;
-  int n_qkv, n_attn, n_o, n_gu, n_down;  // workgroups per role
+  int n_attn, n_o, n_gu, n_down;  // workgroups per role
   unsigned long long* ts;    // profiling: 4 stamps per workgroup (start, released, done, end); null = off
 };
 
 // Completion-flag words per layer of the fused layer kernel.
-constexpr size_t layer_flag_words(int n_qkv, int n_attn_heads, int n_o, int n_gu) {
-  return (size_t)n_qkv + n_attn_heads + n_o + n_gu;
+constexpr size_t layer_flag_words(int n_attn_heads, int n_o, int n_gu) {
+  return (size_t)n_attn_heads + n_o + n_gu;
 }
 
-struct DecodeArgs {
-  const LayerDesc* layers;   // [n_layers], device memory
-  const float* embed;        // [vocab][hidden]
-  const float* final_norm;   // [hidden]
-  const uint8_t* lm_w;
-  const void* lm_s;
-  const float* rope_cos;     // [max_seq][hd/2]
-  const float* rope_sin;
-  // activations, exchanged between workgroups with device-scope loads/stores
-  float* x;
-  float* h;
-  float* qkv;
-  float* ctx;
-  int8_t* ctx_q;
-  float* ctx_d;
-  float* mf;
-  int8_t* m_q;
-  float* m_d;
-  float* logits;             // [vocab] of the last step, or null
-  float* part_o;             // attention partials [nq][nsplit][hd]
-  float* part_ml;            // [nq][nsplit][2]
-  int* counters;             // [n_layers][nkv] attention tickets, zero between uses
-  float* part_val;           // [grid] lm_head argmax partials
-  int* part_idx;
-  unsigned* bar;             // grid barrier words, zero at launch
-  const int* tokens;         // [cap] prompt ids (host-written)
-  int* gen;                  // [cap] argmax produced at position p, stored at p+1
-  int* tokens_out;           // [cap] generated ids stored at p+1 once past the prompt
-  int* pos_out;              // position after the launch
-  int* err;                  // non-zero: a barrier wait exceeded its spin limit
-  unsigned long long* ts;    // optional phase timestamps of workgroup 0 (100 MHz clock)
-  int n_layers, hidden, nq, nkv, hd, ffn, vocab, max_seq, qkv_rows;
-  int pos0, n_steps, n_prompt, cap, nsplit;
-  float eps, attn_scale;
-};
 
 }  // namespace llmrs

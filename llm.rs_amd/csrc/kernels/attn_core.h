@@ -1,6 +1,6 @@
 // attn_core.h - batch-1 decode attention over the KV cache for gfx950,
-// shared by the standalone kernels (attention.hip) and the persistent decode
-// kernel (decode.hip).
+// shared by the standalone kernels (attention.hip) and the fused attention +
+// O launch (layer.hip).
 //
 // Reference: LlamaAttention::forward, seq == 1 (layer.rs:175-299): per query
 // head, RoPE on q and k (layer.rs:216-217, cpu.rs:326-357), K/V append at
@@ -24,7 +24,8 @@
 // to the cache.  Partials (m, l, acc) go to global memory; the last
 // workgroup of a KV head (atomic ticket; partials move with device-scope
 // stores and loads) combines them and writes ctx as f32 and as Q8_0 codes
-// for the O projection.
+// for the O projection, also with device-scope stores, so a consumer in the
+// same launch (layer.hip) can read them once the item has completed.
 //
 // RoPE uses cos/sin tables [max_seq][hd/2] computed on the host with the
 // reference's own f32 formula and glibc, so rotation is bit-exact.
@@ -110,7 +111,7 @@ struct AttnLds {
 
 // One (KV head g, split) work item at decode position pos.  DEV = true moves
 // the projections, the cache, the partials and ctx with device-scope loads
-// and stores (producer and consumer in one persistent launch).
+// and stores (producer and consumer in one launch).
 struct NoWait {
   __device__ __forceinline__ bool operator()() const { return true; }
 };
@@ -498,12 +499,11 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
 #pragma unroll
     for (int e = 0; e < DPL; ++e) {
       const int dd = DPL * lane + e;
-      st_act<DEV>(a.ctx, (size_t)h * HD + dd, v[e]);
+      st_act<true>(a.ctx, (size_t)h * HD + dd, v[e]);
       const int8_t q = amax == 0.0f ? (int8_t)0 : (int8_t)q8_code(v[e], inv);
-      if (DEV) dev_st8(a.ctx_q, (int)((size_t)h * HD + dd), q);
-      else a.ctx_q[(size_t)h * HD + dd] = q;
+      dev_st8(a.ctx_q, (int)((size_t)h * HD + dd), q);
     }
-    if ((lane % LPB) == 0) st_act<DEV>(a.ctx_d, ((size_t)h * HD + DPL * lane) / 32, amax == 0.0f ? 0.0f : d);
+    if ((lane % LPB) == 0) st_act<true>(a.ctx_d, ((size_t)h * HD + DPL * lane) / 32, amax == 0.0f ? 0.0f : d);
   }
   if (tid == 0) dev_stu(a.counters, 4 * g, 0u);
   stamp(6);

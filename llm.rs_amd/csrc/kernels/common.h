@@ -103,7 +103,7 @@ __device__ __forceinline__ int q8_group32(float x, float* d_out) {
 
 // ---- device-coherent memory operations ---------------------------------
 // Data produced and consumed inside one launch by workgroups on different
-// XCDs (the persistent decode kernel) moves with device-scope (sc1) buffer
+// XCDs (the fused layer launches, the attention combine) moves with device-scope (sc1) buffer
 // loads and stores: they bypass the per-XCD L2 copies, so no L2 write-back
 // or invalidate is needed at barriers.  The base must be wave-uniform; the
 // descriptor covers 2 GiB from it.

@@ -1,5 +1,5 @@
 // gemv_core.h - the batch-1 dequant-GEMV machinery shared by the standalone
-// GEMV kernels (gemv.hip) and the persistent decode kernel (decode.hip).
+// GEMV kernels (gemv.hip) and the fused layer launches (layer.hip).
 //
 // y[row] = sum_b isum_b(row) * (d_w[row,b] * d_a[b]) where isum_b is the exact
 // int32 dot product of one 32-element block of weight codes with the Q8_0
@@ -18,10 +18,9 @@
 // b = base + 64*u + l (u < U), so every weight load instruction of a wave
 // reads 64 consecutive 16-byte blocks of one row (1 KB, fully coalesced).
 // Waves walk their units in order, two units in flight: the weights of unit
-// i+2 are requested right after unit i is consumed, and the first two units
-// are requested before the activation prologue (or, in the persistent
-// kernel, before the grid barrier that precedes the phase), so HBM latency
-// overlaps the prologue.  Row groups are dealt to the waves of `nwg`
+// i+2 are requested right after unit i is consumed, and the first units are
+// requested with the activation prologue (or, in a fused launch, before the
+// wait for the producer), so HBM latency overlaps the prologue.  Row groups are dealt to the waves of `nwg`
 // workgroups round-robin (whole 64-row tiles per workgroup for the SwiGLU
 // epilogue, which needs matching gate and up rows).
 //
@@ -36,7 +35,7 @@
 //              written as f32 and as Q8_0 codes for the down projection
 //   EPI_ARGMAX logits plus a per-workgroup (max, index) partial (lm_head)
 // DEV = true moves the activations, results and partials with device-scope
-// loads and stores (producer and consumer in one persistent launch).
+// loads and stores (producer and consumer in one launch).
 #pragma once
 #include "common.h"
 #include "../kernel_args.h"

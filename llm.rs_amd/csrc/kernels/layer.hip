@@ -1,4 +1,4 @@
-// layer.hip - one decoder layer of the batch-1 decode step in one launch.
+// layer.hip - the batch-1 decode layer in three launches instead of five.
 //
 // Reference: LlamaBlock::forward (layer.rs:373-406) at seq == 1:
 //   qkv = W_qkv . Q8(RMSNorm(x))                       (layer.rs:177-179, 377)
@@ -6,18 +6,20 @@
 //   h   = x + W_o . ctx                                 (layer.rs:329-332, 386)
 //   m   = silu(W_gate h') * (W_up h'), h' = Q8(RMSNorm(h))  (layer.rs:37-89, 393)
 //   x   = h + W_down . m                                (layer.rs:93-96, 403)
+// The Q|K|V GEMV stays a launch of its own (gemv.hip); attention + O and
+// gate|up + down are one launch each.
 //
-// Why one launch per layer: on MI355X every kernel boundary costs a launch
-// (~1.6 us in a graph) plus a ramp in which the new kernel's first weight
-// loads are still in flight, and a batch-1 layer has five dependent steps.
-// Here the grid is split into five roles, each a contiguous run of
-// workgroups in dependency order.  A consumer role first requests its first
-// weight units (weights never depend on activations), then waits on its
-// producer's completion flags, so weight streaming overlaps the producer's latency
-// (attention, prologues, tails) instead of following it.  Data produced and
-// consumed inside the launch moves with device-scope (sc1) loads and stores,
-// which bypass the per-XCD L2 copies; a producer workgroup waits for its
-// stores to complete before it sets its flag.
+// Why: on MI355X every kernel boundary costs a launch (~1.6 us in a graph)
+// plus a ramp in which the new kernel's first weight loads are still in
+// flight.  Inside one launch the grid is split into two roles, producer
+// workgroups first.  A consumer workgroup first requests its first weight
+// units (weights never depend on activations), then waits for its
+// producers' completion flags, so its weight stream overlaps the producer's
+// latency-bound tail (the attention chain, the gate|up tail) instead of
+// following it.  Data produced and consumed inside a launch moves with
+// device-scope (sc1) loads and stores, which bypass the per-XCD L2 copies; a
+// producer workgroup waits for its stores to complete before it sets its
+// flag.
 //
 // Progress: workgroups are dispatched in increasing index order, producers
 // before consumers, so a waiting consumer never holds a slot its producer
@@ -91,42 +93,22 @@ struct LayerStamps {
   }
 };
 
-template <int WT, int HD, bool KV16, int UH, int UF>
-__device__ __forceinline__ void layer_impl(const LayerArgs& L) {
+// Attention + O projection in one launch: the attention items first, then
+// the O workgroups, which request their weights, wait for every KV head's
+// combined ctx, and finish h = x + W_o . ctx.
+template <int WT, int HD, bool KV16, int UH>
+__device__ __forceinline__ void attn_o_impl(const LayerArgs& L) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ GemvShared sh;
   __shared__ unsigned s_word;
-  const int H = L.hidden, F = L.ffn;
+  const int H = L.hidden;
   int wg = blockIdx.x;
   const unsigned epoch = *L.epoch;
-  unsigned* f_qkv = L.flags;
-  unsigned* f_attn = f_qkv + L.n_qkv;
-  unsigned* f_o = f_attn + L.nkv;
-  unsigned* f_gu = f_o + L.n_o;
+  unsigned* f_attn = L.flags;
   LayerStamps st;
   st.dst = L.ts ? L.ts + 4 * (size_t)blockIdx.x : nullptr;
   st.rec(0);
 
-  // ---- Q|K|V: qkv = W_qkv . Q8(RMSNorm(x)) --------------------------------
-  if (wg < L.n_qkv) {
-    GemvArgs g{};
-    g.wq = L.w.qkv_w;
-    g.ws = L.w.qkv_s;
-    g.n = L.qkv_rows;
-    g.k = H;
-    g.x = L.x;
-    g.norm_w = L.w.norm_in;
-    g.eps = L.eps;
-    g.y = L.qkv;
-    UnitRegs<WT, 2, UH> ua, ub;
-    gemv_body<WT, PRO_NORM, EPI_STORE, 2, UH, true>(g, 0, wg, L.n_qkv, ua, ub, false, smem, sh);
-    st.rec(2);
-    set_flag(f_qkv + wg, epoch);
-    return;
-  }
-  wg -= L.n_qkv;
-
-  // ---- attention: one (KV head, split) item per workgroup ----------------
   if (wg < L.n_attn) {
     AttnArgs a{};
     a.qkv = L.qkv;
@@ -146,42 +128,46 @@ __device__ __forceinline__ void layer_impl(const LayerArgs& L) {
     a.nkv = L.nkv;
     a.nsplit = L.nsplit;
     a.scale = L.attn_scale;
-    const int pos = *L.pos_ptr;
-    auto wait_qkv = [&]() {
-      const bool ok = wait_flags(f_qkv, L.n_qkv, epoch, L.err, &s_word);
-      st.rec(1);
-      return ok;
-    };
-    const bool combined = attn_item<HD, KV16, true>(a, wg / L.nsplit, wg % L.nsplit, pos, smem, wait_qkv);
+    // q/k/v and the cache come from earlier launches: plain loads
+    const bool combined = attn_item<HD, KV16, false>(a, wg / L.nsplit, wg % L.nsplit, *L.pos_ptr, smem);
     st.rec(2);
     if (combined) set_flag(f_attn + wg / L.nsplit, epoch);
     return;
   }
   wg -= L.n_attn;
+  GemvArgs g{};
+  g.wq = L.w.o_w;
+  g.ws = L.w.o_s;
+  g.n = H;
+  g.k = L.nq * HD;
+  g.xq = L.ctx_q;
+  g.xd = L.ctx_d;
+  g.y = L.h;
+  g.res = L.x;
+  UnitRegs<WT, 2, UH> ua, ub;
+  Gemv<WT, EPI_RESID, 2, UH>(g, wg, L.n_o).prefetch(ua, ub);
+  if (!wait_flags(f_attn, L.nkv, epoch, L.err, &s_word)) return;
+  st.rec(1);
+  gemv_body<WT, PRO_Q8, EPI_RESID, 2, UH, true>(g, 0, wg, L.n_o, ua, ub, true, smem, sh);
+  st.rec(2);
+}
 
-  // ---- O + residual: h = x + W_o . ctx ------------------------------------
-  if (wg < L.n_o) {
-    GemvArgs g{};
-    g.wq = L.w.o_w;
-    g.ws = L.w.o_s;
-    g.n = H;
-    g.k = L.nq * HD;
-    g.xq = L.ctx_q;
-    g.xd = L.ctx_d;
-    g.y = L.h;
-    g.res = L.x;
-    UnitRegs<WT, 2, UH> ua, ub;
-    Gemv<WT, EPI_RESID, 2, UH>(g, wg, L.n_o).prefetch(ua, ub);
-    if (!wait_flags(f_attn, L.nkv, epoch, L.err, &s_word)) return;
-    st.rec(1);
-    gemv_body<WT, PRO_Q8, EPI_RESID, 2, UH, true>(g, 0, wg, L.n_o, ua, ub, true, smem, sh);
-    st.rec(2);
-    set_flag(f_o + wg, epoch);
-    return;
-  }
-  wg -= L.n_o;
+// gate|up + SwiGLU and down + residual in one launch: the gate|up
+// workgroups first, then the down workgroups, which request their weights,
+// wait for every gate|up workgroup and finish x = h + W_down . m.
+template <int WT, int UH, int UF>
+__device__ __forceinline__ void mlp_impl(const LayerArgs& L) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ GemvShared sh;
+  __shared__ unsigned s_word;
+  const int H = L.hidden, F = L.ffn;
+  int wg = blockIdx.x;
+  const unsigned epoch = *L.epoch;
+  unsigned* f_gu = L.flags + L.nkv + L.n_o;
+  LayerStamps st;
+  st.dst = L.ts ? L.ts + 4 * (size_t)blockIdx.x : nullptr;
+  st.rec(0);
 
-  // ---- gate|up + SwiGLU: m = silu(g) * u (+ Q8) --------------------------
   if (wg < L.n_gu) {
     GemvArgs g{};
     g.wq = L.w.gu_w;
@@ -194,51 +180,52 @@ __device__ __forceinline__ void layer_impl(const LayerArgs& L) {
     g.y = L.mf;
     g.yq = L.m_q;
     g.yd = L.m_d;
-    UnitRegs<WT, 2, UH> ua, ub;
-    Gemv<WT, EPI_SILU, 2, UH>(g, wg, L.n_gu).prefetch(ua, ub);
-    if (!wait_flags(f_o, L.n_o, epoch, L.err, &s_word)) return;
-    st.rec(1);
-    gemv_body<WT, PRO_NORM, EPI_SILU, 2, UH, true>(g, 0, wg, L.n_gu, ua, ub, true, smem, sh);
+    UnitRegs<WT, 4, UH> ua, ub;
+    gemv_body<WT, PRO_NORM, EPI_SILU, 4, UH, true, 1>(g, 0, wg, L.n_gu, ua, ub, false, smem, sh);
     st.rec(2);
     set_flag(f_gu + wg, epoch);
     return;
   }
   wg -= L.n_gu;
-
-  // ---- down + residual: x = h + W_down . m --------------------------------
-  {
-    GemvArgs g{};
-    g.wq = L.w.down_w;
-    g.ws = L.w.down_s;
-    g.n = H;
-    g.k = F;
-    g.xq = L.m_q;
-    g.xd = L.m_d;
-    g.y = L.x;
-    g.res = L.h;
-    UnitRegs<WT, 2, UF> ua, ub;
-    Gemv<WT, EPI_RESID, 2, UF>(g, wg, L.n_down).prefetch(ua, ub);
-    if (!wait_flags(f_gu, L.n_gu, epoch, L.err, &s_word)) return;
-    st.rec(1);
-    gemv_body<WT, PRO_Q8, EPI_RESID, 2, UF, true>(g, 0, wg, L.n_down, ua, ub, true, smem, sh);
-    st.rec(2);
-  }
+  GemvArgs g{};
+  g.wq = L.w.down_w;
+  g.ws = L.w.down_s;
+  g.n = H;
+  g.k = F;
+  g.xq = L.m_q;
+  g.xd = L.m_d;
+  g.y = L.x;
+  g.res = L.h;
+  UnitRegs<WT, 2, UF> ua, ub;
+  Gemv<WT, EPI_RESID, 2, UF>(g, wg, L.n_down).prefetch(ua, ub);
+  if (!wait_flags(f_gu, L.n_gu, epoch, L.err, &s_word)) return;
+  st.rec(1);
+  gemv_body<WT, PRO_Q8, EPI_RESID, 2, UF, true>(g, 0, wg, L.n_down, ua, ub, true, smem, sh);
+  st.rec(2);
 }
 
-#define LLMRS_LAYER(name, WT, HD, KV16, UH, UF)                                  \
-  extern "C" __global__ __launch_bounds__(kThreads) void name(LayerArgs L) {      \
-    layer_impl<WT, HD, KV16, UH, UF>(L);                                      \
+#define LLMRS_ATTN_O(name, WT, HD, KV16, UH)                                    \
+  extern "C" __global__ __launch_bounds__(kThreads) void name(LayerArgs L) {   \
+    attn_o_impl<WT, HD, KV16, UH>(L);                                         \
+  }
+#define LLMRS_MLP(name, WT, UH, UF)                                             \
+  extern "C" __global__ __launch_bounds__(kThreads) void name(LayerArgs L) {   \
+    mlp_impl<WT, UH, UF>(L);                                                  \
   }
 
-#define LLMRS_LAYER_FAMILY(tag, WT)                                          \
-  LLMRS_LAYER(layer_##tag##_hd64_f32_h1f2, WT, 64, false, 1, 2)              \
-  LLMRS_LAYER(layer_##tag##_hd64_f16_h1f2, WT, 64, true, 1, 2)               \
-  LLMRS_LAYER(layer_##tag##_hd128_f32_h1f2, WT, 128, false, 1, 2)            \
-  LLMRS_LAYER(layer_##tag##_hd128_f16_h1f2, WT, 128, true, 1, 2)             \
-  LLMRS_LAYER(layer_##tag##_hd64_f32_h2f1, WT, 64, false, 2, 1)              \
-  LLMRS_LAYER(layer_##tag##_hd64_f16_h2f1, WT, 64, true, 2, 1)               \
-  LLMRS_LAYER(layer_##tag##_hd128_f32_h2f1, WT, 128, false, 2, 1)            \
-  LLMRS_LAYER(layer_##tag##_hd128_f16_h2f1, WT, 128, true, 2, 1)
+#define LLMRS_LAYER_FAMILY(tag, WT)                                  \
+  LLMRS_ATTN_O(attn_o_##tag##_hd64_f32_u1, WT, 64, false, 1)         \
+  LLMRS_ATTN_O(attn_o_##tag##_hd64_f16_u1, WT, 64, true, 1)          \
+  LLMRS_ATTN_O(attn_o_##tag##_hd128_f32_u1, WT, 128, false, 1)       \
+  LLMRS_ATTN_O(attn_o_##tag##_hd128_f16_u1, WT, 128, true, 1)        \
+  LLMRS_ATTN_O(attn_o_##tag##_hd64_f32_u2, WT, 64, false, 2)         \
+  LLMRS_ATTN_O(attn_o_##tag##_hd64_f16_u2, WT, 64, true, 2)          \
+  LLMRS_ATTN_O(attn_o_##tag##_hd128_f32_u2, WT, 128, false, 2)       \
+  LLMRS_ATTN_O(attn_o_##tag##_hd128_f16_u2, WT, 128, true, 2)        \
+  LLMRS_MLP(mlp_##tag##_h1f1, WT, 1, 1)                              \
+  LLMRS_MLP(mlp_##tag##_h1f2, WT, 1, 2)                              \
+  LLMRS_MLP(mlp_##tag##_h2f1, WT, 2, 1)                              \
+  LLMRS_MLP(mlp_##tag##_h2f2, WT, 2, 2)
 
 LLMRS_LAYER_FAMILY(q4h, WT_Q4H)
 LLMRS_LAYER_FAMILY(q4f, WT_Q4F)

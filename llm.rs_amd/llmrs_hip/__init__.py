@@ -93,7 +93,6 @@ _SIGS = {
     "llmrs_model_decode_steps": (C.c_int, [C.c_void_p, C.c_size_t]),
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "llmrs_model_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
-    "llmrs_model_profile_phases": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_int]),
     "llmrs_model_profile_layer": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
     "llmrs_model_time_linear": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "llmrs_model_profile_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_char_p,
@@ -415,26 +414,13 @@ class HipModel:
         return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(wk[i]))
                 for i in range(n)]
 
-    def profile_phases(self, n_steps: int = 1, grid: int = 0):
-        """Persistent-kernel phase timing: (us per step, [layers][10] intervals)
-        and, with grid = the launch's workgroup count, ([grid][10] layer-1
-        timestamps, [items][8] attention stage timestamps)."""
-        cap = 1 + 10 * self.cfg.n_layers + (10 * grid + 8 * 4096 if grid else 0)
-        out = np.zeros(cap, np.float64)
-        n = _check(lib().llmrs_model_profile_phases(self._h, n_steps, _ptr(out), cap))
-        nl = 10 * self.cfg.n_layers
-        layers = out[1:1 + nl].reshape(-1, 10)
-        if grid:
-            wgs = out[1 + nl:1 + nl + 10 * grid].reshape(-1, 10)
-            return float(out[0]), layers, wgs, out[1 + nl + 10 * grid:n].reshape(-1, 8)
-        return float(out[0]), layers
-
     def profile_layer(self, layer: int = 1, cap: int = 1 << 16):
-        """Per-workgroup stamps of one fused layer launch: (role sizes,
-        [workgroups][4] = start, wait released, work done, end in us)."""
+        """Per-workgroup stamps of one layer's attention + O and gate|up +
+        down launches: (role sizes [attention, O, gate|up, down], [workgroups
+        of both launches][4] = start, wait released, work done, end in us)."""
         out = np.zeros(cap, np.float64)
         n = _check(lib().llmrs_model_profile_layer(self._h, layer, _ptr(out), cap))
-        return [int(v) for v in out[:5]], out[5:n].reshape(-1, 4)
+        return [int(v) for v in out[:4]], out[4:n].reshape(-1, 4)
 
     def weight_bytes(self) -> float:
         return float(lib().llmrs_model_weight_bytes(self._h))
