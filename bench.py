@@ -244,10 +244,14 @@ def main() -> int:
     spec = syn.with_sizes(base, prompt=n_prompt, decode=args.warmup + args.steps)
     lh.init(0)
     max_seq = spec.max_seq + args.profile_steps + 1
-    log(f"workload {spec.name}: prompt {n_prompt}, decode {args.warmup}+{args.steps}, max_seq {max_seq}")
+    pre = spec.prefilled  # cache positions filled with N(0,1) K/V before the prompt
+    log(f"workload {spec.name}: pre-filled {pre}, prompt {n_prompt}, decode {args.warmup}+{args.steps}, "
+        f"max_seq {max_seq}")
 
     t0 = time.perf_counter()
-    keep = not args.no_cpu_baseline
+    # The CPU sample of a pre-filled long-context workload would need the
+    # oracle's own copy of every weight and of the cache; it is not run.
+    keep = not args.no_cpu_baseline and not pre
     model = lh.HipModel(spec.config(max_seq))
     if keep:
         w = syn.make_weights(spec)
@@ -258,9 +262,15 @@ def main() -> int:
     log(f"weights generated and uploaded in {time.perf_counter() - t0:.1f}s "
         f"({model.weight_bytes() / 1e9:.3f} GB of linear weights)")
 
+    if pre:
+        t0 = time.perf_counter()
+        for layer in range(spec.n_layers):
+            for g in range(spec.n_kv_heads):
+                model.kv_write(layer, g, 0, *syn.prefill_kv(spec, layer, g))
+        log(f"K/V cache pre-filled ({pre} positions) in {time.perf_counter() - t0:.1f}s")
     prompt = syn.prompt(spec)
     t0 = time.perf_counter()
-    model.begin(prompt)
+    model.begin(prompt, start_pos=pre)
     lh.sync()
     prompt_s = time.perf_counter() - t0
     log(f"prompt of {n_prompt} tokens processed in {prompt_s * 1e3:.1f} ms")
@@ -279,7 +289,7 @@ def main() -> int:
     lh.sync()
     sync_all()
     dt = time.perf_counter() - t0
-    toks = model.tokens(n_prompt + args.warmup + args.steps + 1)
+    toks = model.tokens(pre + n_prompt + args.warmup + args.steps + 1)[pre:]
     assert toks.min() >= 0 and toks.max() < spec.vocab
     value = args.steps / dt
     log(f"decode: {value:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token)")
@@ -326,7 +336,7 @@ def main() -> int:
         "config": {"workload": f"{spec.name} decode", "layers": spec.n_layers, "hidden": spec.hidden,
                    "heads": spec.n_heads, "kv_heads": spec.n_kv_heads, "head_dim": spec.head_dim,
                    "ffn": spec.ffn, "vocab": spec.vocab, "weights": spec.weight.name,
-                   "kv_cache": spec.kv.name.lower(), "prompt": n_prompt,
+                   "kv_cache": spec.kv.name.lower(), "prefilled_positions": pre, "prompt": n_prompt,
                    "decode_steps": args.warmup + args.steps, "batch": 1},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -211,6 +211,11 @@ int llmrs_model_generate(llmrs_model* m, const int32_t* prompt,
 /* Benchmark helpers: start a greedy run (prompt processed, state resident),
  * then replay `n` more decode steps without host synchronisation. */
 int llmrs_model_begin(llmrs_model* m, const int32_t* prompt, size_t n_prompt);
+/* As llmrs_model_begin with the prompt at positions [start_pos, start_pos +
+ * n_prompt): the cache below start_pos is taken as already filled (the
+ * reference's chunk at cur_pos > 0, main.rs:134-138,313; llmrs_model_kv_write
+ * fills it). */
+int llmrs_model_begin_at(llmrs_model* m, const int32_t* prompt, size_t n_prompt, size_t start_pos);
 int llmrs_model_decode_steps(llmrs_model* m, size_t n);
 /* Tokens produced since llmrs_model_begin (count = n_prompt + steps). */
 int llmrs_model_tokens(llmrs_model* m, int32_t* out, size_t count);

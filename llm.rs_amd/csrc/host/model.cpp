@@ -66,7 +66,7 @@ struct llmrs_model {
   int8_t *ctx_q = nullptr, *m_q = nullptr;
   int *part_idx = nullptr, *counters = nullptr, *tokens = nullptr, *gen = nullptr;
   int *pos = nullptr, *n_prompt = nullptr, *err = nullptr;
-  int nsplit = 1, lm_grid = 1, cap = 0;
+  int nsplit = 1, attn_streams = 1, lm_grid = 1, cap = 0;
   size_t host_pos = 0;
   bool begun = false;
   hipGraph_t graph = nullptr;
@@ -154,6 +154,12 @@ double linear_weight_bytes(const llmrs_model* m, const DevLinear& L) {
 }
 
 void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits);
+
+// The decode-attention kernel of this model (attention.hip).
+std::string attn_kernel(const llmrs_model* m) {
+  return std::string("attn_decode_hd") + std::to_string(m->c.head_dim) +
+         (m->c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32") + (m->attn_streams > 1 ? "_s4" : "");
+}
 
 // The decode GEMV of one linear slot of layer li (LLMRS_W_Q = the stacked
 // Q|K|V rows, LLMRS_W_O, LLMRS_W_GATE = gate|up, LLMRS_W_DOWN) with its fused
@@ -295,8 +301,6 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
   }
 
   const float scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
-  const std::string attn = std::string("attn_decode_hd") + std::to_string(hd) +
-                           (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32");
   for (int li = 0; li < c.n_layers; ++li) {
     LayerBufs& Lb = m->layers[li];
     if (trace_dev)
@@ -323,7 +327,7 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
       a.nsplit = m->nsplit;
       a.scale = scale;
       const double kvb = 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
-      L(attn, kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(256), 0, a);
+      L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(256 * m->attn_streams), 0, a);
     }
     enqueue_linear(m, L, li, LLMRS_W_O);
     enqueue_linear(m, L, li, LLMRS_W_GATE);
@@ -536,7 +540,7 @@ void plan_layer(llmrs_model* m) {
   m->ao_grid = m->mlp_grid = 0;
   if (!env_int("LLMRS_FUSED", 0)) return;
   const int H = c.hidden, F = c.ffn, qd = c.n_heads * c.head_dim, cus = ctx().num_cus;
-  if (qd != H) return;
+  if (qd != H || m->attn_streams != 1) return;
   const int uh = (H / 32) % 128 == 0 ? 2 : 1, uf = (F / 32) % 128 == 0 ? 2 : 1;
   const bool kv16 = c.kv_dtype == LLMRS_F16;
   m->ao_name = std::string("attn_o_") + wt_tag(m->wt) + "_hd" + std::to_string(c.head_dim) +
@@ -678,8 +682,17 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
     m->qkv_rows = (nq + 2 * nkv) * hd;
     m->cap = c.max_seq + 1;
-    int splits = (c.max_seq + 63) / 64;
-    splits = std::min(splits, std::max(1, 2 * cx.num_cus / nkv));
+    // Attention splits: one 64-position tile per split up to two workgroups
+    // per CU; longer contexts run 4 tile streams per workgroup (one workgroup
+    // per CU) so the split combine stays short.
+    const int tiles = (c.max_seq + 63) / 64;
+    int splits = std::min(tiles, std::max(1, 2 * cx.num_cus / nkv));
+    m->attn_streams = 1;
+    const int es = env_int("LLMRS_ATTN_STREAMS", 0);  // 0 = by context length, 1 or 4 = forced
+    if (es == 4 || (es == 0 && tiles > splits)) {
+      m->attn_streams = 4;
+      splits = std::min((tiles + 3) / 4, std::max(1, cx.num_cus / nkv));
+    }
     m->nsplit = std::max(1, env_int("LLMRS_ATTN_SPLITS", splits));
     m->lm_grid = (int)gemv_plan(m->wt, "norm_argmax", c.vocab, H, cx.num_cus).grid;
     m->layers.resize(c.n_layers);
@@ -741,8 +754,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     (void)kernel(gemv_plan(m->wt, "norm_argmax", c.vocab, H, cx.num_cus).name);
     (void)kernel("embed_gather");
     (void)kernel("argmax_final");
-    (void)kernel(std::string("attn_decode_hd") + std::to_string(hd) +
-                 (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32"));
+    (void)kernel(attn_kernel(m.get()));
     *out = m.release();
   });
 }
@@ -973,25 +985,30 @@ int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n, size_t 
   });
 }
 
-int llmrs_model_begin(llmrs_model* m, const int32_t* prompt, size_t n_prompt) {
+int llmrs_model_begin_at(llmrs_model* m, const int32_t* prompt, size_t n_prompt, size_t start_pos) {
   return guard([&] {
     check_ready(m);
     LLMRS_REQUIRE(prompt && n_prompt > 0, LLMRS_E_INVALID, "empty prompt");
-    LLMRS_REQUIRE(n_prompt <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "prompt longer than max_seq");
-    upload_tokens(m, 0, prompt, n_prompt);
-    set_state(m, 0, (int)n_prompt);
-    m->host_n_prompt = (int)n_prompt;
+    LLMRS_REQUIRE(start_pos + n_prompt <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "prompt beyond max_seq");
+    const size_t end = start_pos + n_prompt;
+    upload_tokens(m, start_pos, prompt, n_prompt);
+    set_state(m, start_pos, (int)end);
+    m->host_n_prompt = (int)end;
     if (n_prompt > 1 && prefill_enabled()) {
-      run_prefill(m, 0, n_prompt, (int)n_prompt, false, nullptr);
+      run_prefill(m, start_pos, n_prompt, (int)end, false, nullptr);
     } else {
-      for (size_t p = 0; p < n_prompt; ++p) {
+      for (size_t p = start_pos; p < end; ++p) {
         m->host_pos = p;
         replay_step(m);
       }
     }
-    m->host_pos = n_prompt;
+    m->host_pos = end;
     m->begun = true;
   });
+}
+
+int llmrs_model_begin(llmrs_model* m, const int32_t* prompt, size_t n_prompt) {
+  return llmrs_model_begin_at(m, prompt, n_prompt, 0);
 }
 
 int llmrs_model_decode_steps(llmrs_model* m, size_t n) {

@@ -170,15 +170,15 @@ struct PrefillAttnArgs {
   float scale;           // fl(1 / fl(sqrt(hd)))
 };
 
-// LDS bytes of one decode-attention work item (attn_core.h: query heads,
-// padded K tile, V tile, the new row, the ticket).  Tiles are 64 positions
-// for an f16 cache and 32 for f32; at most 8 query heads per KV head.
-constexpr size_t attn_lds_bytes(int hd, bool kv16) {
+// LDS bytes of one decode-attention work item (attn_core.h: query heads, per
+// stream a padded K tile and a V tile, the new row, the ticket).  Tiles are
+// 64 positions for an f16 cache and 32 for f32; at most 8 query heads per KV
+// head; `streams` tile streams per workgroup.
+constexpr size_t attn_lds_bytes(int hd, bool kv16, int streams = 1) {
   const size_t es = kv16 ? 2 : 4, tile = kv16 ? 64 : 32, kstride = (size_t)hd + (kv16 ? 2 : 1);
-  const size_t k = 4 * 8 * (size_t)hd;
-  const size_t v = k + (es * tile * kstride + 15) / 16 * 16;
-  const size_t nw = v + es * tile * (size_t)hd;
-  return nw + 4 * 2 * (size_t)hd + 16;
+  const size_t kb = (es * tile * kstride + 15) / 16 * 16;
+  const size_t stream = kb + es * tile * (size_t)hd;
+  return 4 * 8 * (size_t)hd + (size_t)streams * stream + 4 * 2 * (size_t)hd + 16;
 }
 
 // The weights, norms and caches of one decoder layer (layer.hip).

@@ -7,18 +7,23 @@
 
 using namespace llmrs;
 
-template <int HD, bool KV16>
+template <int HD, bool KV16, int S>
 __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
-  __shared__ __align__(16) uint8_t lds[AttnLds<HD, KV16>::BYTES];
-  attn_item<HD, KV16, false>(a, blockIdx.y, blockIdx.x, *a.pos_ptr, lds);
+  __shared__ __align__(16) uint8_t lds[AttnLds<HD, KV16, S>::BYTES];
+  attn_item<HD, KV16, false, S>(a, blockIdx.y, blockIdx.x, *a.pos_ptr, lds);
 }
 
-#define LLMRS_ATTN(name, HD, KV16)                                           \
-  extern "C" __global__ __launch_bounds__(256) void name(AttnArgs a) {      \
-    attn_decode_impl<HD, KV16>(a);                                          \
+// Variant names: attn_decode_hd<HD>_<cache>[_s<streams>].
+#define LLMRS_ATTN(name, HD, KV16, S)                                              \
+  extern "C" __global__ __launch_bounds__(256 * S) void name(AttnArgs a) {        \
+    attn_decode_impl<HD, KV16, S>(a);                                             \
   }
 
-LLMRS_ATTN(attn_decode_hd64_f32, 64, false)
-LLMRS_ATTN(attn_decode_hd64_f16, 64, true)
-LLMRS_ATTN(attn_decode_hd128_f32, 128, false)
-LLMRS_ATTN(attn_decode_hd128_f16, 128, true)
+LLMRS_ATTN(attn_decode_hd64_f32, 64, false, 1)
+LLMRS_ATTN(attn_decode_hd64_f16, 64, true, 1)
+LLMRS_ATTN(attn_decode_hd128_f32, 128, false, 1)
+LLMRS_ATTN(attn_decode_hd128_f16, 128, true, 1)
+LLMRS_ATTN(attn_decode_hd64_f32_s4, 64, false, 4)
+LLMRS_ATTN(attn_decode_hd64_f16_s4, 64, true, 4)
+LLMRS_ATTN(attn_decode_hd128_f32_s4, 128, false, 4)
+LLMRS_ATTN(attn_decode_hd128_f16_s4, 128, true, 4)

@@ -94,24 +94,27 @@ struct AttnCfg {
   static_assert(CHUNKS % 256 == 0, "tile must split evenly over 256 threads");
 };
 
-// LDS carve-up of one work item (bytes): s_q, padded K tile, V tile, s_new,
-// ticket.
-template <int HD, bool KV16>
+// LDS carve-up of one work item (bytes): s_q, then per stream a padded K
+// tile and a V tile, s_new, ticket.
+template <int HD, bool KV16, int S = 1>
 struct AttnLds {
   typedef AttnCfg<HD, KV16> C;
   typedef typename C::kv_t kv_t;
   static constexpr size_t Q = 0;
-  static constexpr size_t K = Q + sizeof(float) * C::MAXREP * HD;
-  static constexpr size_t V = K + ((sizeof(kv_t) * C::TILE * C::KSTRIDE + 15) / 16) * 16;
-  static constexpr size_t NEW = V + sizeof(kv_t) * C::TILE * HD;
+  static constexpr size_t KBYTES = ((sizeof(kv_t) * C::TILE * C::KSTRIDE + 15) / 16) * 16;
+  static constexpr size_t STREAM = KBYTES + sizeof(kv_t) * C::TILE * HD;
+  static constexpr size_t K0 = Q + sizeof(float) * C::MAXREP * HD;
+  static constexpr size_t NEW = K0 + S * STREAM;
   static constexpr size_t TICKET = NEW + sizeof(float) * 2 * HD;
   static constexpr size_t BYTES = TICKET + 16;
-  static_assert(BYTES == attn_lds_bytes(HD, KV16), "host LDS size formula out of date");
+  static constexpr size_t K(int st) { return K0 + (size_t)st * STREAM; }
+  static constexpr size_t V(int st) { return K(st) + KBYTES; }
+  // stream merge area (reuses the tiles): per stream, head, dims + (m, l)
+  static constexpr size_t MERGE_BYTES = sizeof(float) * S * C::MAXREP * (HD + 2);
+  static_assert(S == 1 || MERGE_BYTES <= S * STREAM, "merge area fits in the tiles");
+  static_assert(BYTES == attn_lds_bytes(HD, KV16, S), "host LDS size formula out of date");
 };
 
-// One (KV head g, split) work item at decode position pos.  DEV = true moves
-// the projections, the cache, the partials and ctx with device-scope loads
-// and stores (producer and consumer in one launch).
 struct NoWait {
   __device__ __forceinline__ bool operator()() const { return true; }
 };
@@ -120,22 +123,30 @@ struct NoWait {
 // projections are read: a launch that also computes the projections waits
 // there for them (returning false abandons the item).  Returns true for the
 // workgroup that combined the splits of KV head g (ctx written).
-template <int HD, bool KV16, bool DEV, class Wait = NoWait>
+//
+// S > 1 runs S streams of 4 waves in one workgroup (256 * S threads): stream
+// st takes every S-th tile of the split, with its own online softmax, and
+// the streams merge through LDS before the partials are written, so a long
+// context needs S times fewer splits for the same parallelism (and the
+// combine reads S times fewer partials).
+template <int HD, bool KV16, bool DEV, int S = 1, class Wait = NoWait>
 __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, int pos, uint8_t* lds,
                                           const Wait& wait = Wait()) {
   typedef AttnCfg<HD, KV16> C;
-  typedef AttnLds<HD, KV16> LY;
+  typedef AttnLds<HD, KV16, S> LY;
   typedef typename C::kv_t kv_t;
   constexpr int TILE = C::TILE, MID = HD / 2, HPW = C::HPW, DPL = C::DPL;
   constexpr int ES = (int)sizeof(kv_t);
 
+  const int tid = threadIdx.x, lane = lane_id();
+  const int stm = wave_id() / 4, wave = wave_id() % 4;  // stream, wave within the stream
+  const int ltid = tid % 256;                           // thread within the stream
   float (*s_q)[HD] = (float (*)[HD])(lds + LY::Q);
-  kv_t* s_k = (kv_t*)(lds + LY::K);
-  kv_t* s_v = (kv_t*)(lds + LY::V);
+  kv_t* s_k = (kv_t*)(lds + LY::K(stm));
+  kv_t* s_v = (kv_t*)(lds + LY::V(stm));
   float (*s_new)[HD] = (float (*)[HD])(lds + LY::NEW);
   int& s_ticket = *(int*)(lds + LY::TICKET);
 
-  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   // Profiling stamps, kept in registers and stored when the item ends (a
   // store issued mid-kernel would make the next reuse of its data registers
   // wait for every outstanding load).
@@ -154,11 +165,10 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
   stamp(0);
   const int T = pos + 1;
   const int n_rep = a.nq / a.nkv;
-  // Splits are runs of whole tiles.
+  // Splits are runs of whole tiles, as even as the tile count allows.
   const int ntile = (T + TILE - 1) / TILE;
-  const int tps = (ntile + a.nsplit - 1) / a.nsplit;
-  const int start = min(T, split * tps * TILE);
-  const int end = min(T, start + tps * TILE);
+  const int start = min(T, (int)(((long)split * ntile) / a.nsplit) * TILE);
+  const int end = min(T, (int)(((long)(split + 1) * ntile) / a.nsplit) * TILE);
   const int qdim = a.nq * HD;
   const float* rc = a.rope_cos + (size_t)pos * MID;
   const float* rs = a.rope_sin + (size_t)pos * MID;
@@ -171,7 +181,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
   auto issue = [&](int t0) {
 #pragma unroll
     for (int i = 0; i < C::CPT; ++i) {
-      const int c = tid + 256 * i;
+      const int c = ltid + 256 * i;
       const int t = min(t0 + c / C::CPR, T - 1);  // clamped: rows past `end` are masked
       const int col = (c % C::CPR) * C::EPC;
       if (DEV) {
@@ -184,7 +194,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
       }
     }
   };
-  if (start < end) issue(start);
+  if (start + stm * TILE < end) issue(start + stm * TILE);
   if (!wait()) return false;
 
   // Rotated query heads of this group (cpu.rs:351-354) and, for the owner
@@ -192,6 +202,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
   // Every projection and table value is loaded first, in one batch, so the
   // section costs one memory round trip.
   const bool owner = pos >= start && pos < end;
+  const bool qthr = tid < 256;  // the projections are read by the first 256 threads
   constexpr int QPT = (C::MAXREP * MID + 255) / 256;  // query pairs per thread
   const size_t kr = qdim + (size_t)g * HD;
   const size_t vr = qdim + (size_t)a.nkv * HD + (size_t)g * HD;
@@ -206,7 +217,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     qc[u] = rc[j];
     qs[u] = rs[j];
   }
-  const bool kown = owner && tid < MID, vown = owner && tid < HD;
+  const bool kown = owner && tid < MID, vown = owner && tid < HD;  // tid < 256
   float kre = 0.0f, kim = 0.0f, kcs = 0.0f, ksn = 0.0f, vv = 0.0f;
   if (kown) {
     kre = ld_qkv<DEV>(a.qkv, kr + tid);
@@ -218,7 +229,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
     const int i = tid + 256 * u;
-    if (i < n_rep * MID) {
+    if (qthr && i < n_rep * MID) {
       const int hr = i / MID, j = i % MID;
       s_q[hr][j] = qre[u] * qc[u] - qim[u] * qs[u];
       s_q[hr][j + MID] = qre[u] * qs[u] + qim[u] * qc[u];
@@ -264,39 +275,44 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
   }
 
   stamp(1);
-  for (int t0 = start; t0 < end; t0 += TILE) {
+  for (int it = 0; start + it * S * TILE < end; ++it) {
+    const int t0 = start + (it * S + stm) * TILE;  // this stream's tile
+    const bool have = t0 < end;                    // uniform per stream
     __syncthreads();  // previous tile consumed; s_q / s_new written
-    // Stage the tile (already loaded into registers) into LDS: V rows with
-    // 16-byte stores, padded K rows with 4-byte stores.
+    if (have) {
+      // Stage the tile (already loaded into registers) into LDS: V rows with
+      // 16-byte stores, padded K rows with 4-byte stores.
 #pragma unroll
-    for (int i = 0; i < C::CPT; ++i) {
-      const int c = tid + 256 * i;
-      const int r = c / C::CPR, col = (c % C::CPR) * C::EPC;
-      u32x4 kw = pk[i], vw = pv[i];
-      if (t0 + r == pos) {  // owner only: the row it just wrote
-        kv_t* kp = (kv_t*)&kw;
-        kv_t* vp = (kv_t*)&vw;
+      for (int i = 0; i < C::CPT; ++i) {
+        const int c = ltid + 256 * i;
+        const int r = c / C::CPR, col = (c % C::CPR) * C::EPC;
+        u32x4 kw = pk[i], vw = pv[i];
+        if (t0 + r == pos) {  // owner only: the row it just wrote
+          kv_t* kp = (kv_t*)&kw;
+          kv_t* vp = (kv_t*)&vw;
 #pragma unroll
-        for (int e = 0; e < C::EPC; ++e) {
-          if constexpr (KV16) {
-            kp[e] = f2h(s_new[0][col + e]);
-            vp[e] = f2h(s_new[1][col + e]);
-          } else {
-            kp[e] = s_new[0][col + e];
-            vp[e] = s_new[1][col + e];
+          for (int e = 0; e < C::EPC; ++e) {
+            if constexpr (KV16) {
+              kp[e] = f2h(s_new[0][col + e]);
+              vp[e] = f2h(s_new[1][col + e]);
+            } else {
+              kp[e] = s_new[0][col + e];
+              vp[e] = s_new[1][col + e];
+            }
           }
         }
+        unsigned* kd = (unsigned*)(s_k + r * C::KSTRIDE + col);
+        kd[0] = kw.x;
+        kd[1] = kw.y;
+        kd[2] = kw.z;
+        kd[3] = kw.w;
+        *(u32x4*)(s_v + r * HD + col) = vw;
       }
-      unsigned* kd = (unsigned*)(s_k + r * C::KSTRIDE + col);
-      kd[0] = kw.x;
-      kd[1] = kw.y;
-      kd[2] = kw.z;
-      kd[3] = kw.w;
-      *(u32x4*)(s_v + r * HD + col) = vw;
     }
-    if (t0 + TILE < end) issue(t0 + TILE);  // next tile in flight during this one
+    if (t0 + S * TILE < end) issue(t0 + S * TILE);  // next tile in flight during this one
     __syncthreads();
-    if (t0 == start) stamp(2);
+    if (it == 0) stamp(2);
+    if (!have) continue;
 
     const int tvalid = min(TILE, end - t0);
 #pragma unroll
@@ -378,11 +394,57 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
   }
 
   stamp(3);
-  // Partials of this split.
+  if constexpr (S > 1) {
+    // Merge the streams into stream 0 (every stream covered the same heads
+    // with its own running max): through LDS, reusing the tiles.
+    float* mg = (float*)(lds + LY::K(0));
+    __syncthreads();  // tiles consumed
+    if (stm > 0) {
+#pragma unroll
+      for (int j = 0; j < HPW; ++j) {
+        const int hr = wave + 4 * j;
+        if (hr >= n_rep) continue;
+        float* dst = mg + ((size_t)stm * C::MAXREP + hr) * (HD + 2);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) dst[DPL * lane + e] = acc[j][e];
+        if (lane == 0) {
+          dst[HD] = m[j];
+          dst[HD + 1] = l[j];
+        }
+      }
+    }
+    __syncthreads();
+    if (stm == 0) {
+#pragma unroll
+      for (int j = 0; j < HPW; ++j) {
+        const int hr = wave + 4 * j;
+        if (hr >= n_rep) continue;
+        float M = m[j];
+        for (int q = 1; q < S; ++q) M = fmaxf(M, mg[((size_t)q * C::MAXREP + hr) * (HD + 2) + HD]);
+        const float c0 = m[j] == -INFINITY ? 0.0f : expf(m[j] - M);
+        float Ls = l[j] * c0, av[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) av[e] = acc[j][e] * c0;
+        for (int q = 1; q < S; ++q) {
+          const float* src = mg + ((size_t)q * C::MAXREP + hr) * (HD + 2);
+          const float mq = src[HD];
+          const float cq = mq == -INFINITY ? 0.0f : expf(mq - M);
+          Ls = Ls + src[HD + 1] * cq;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) av[e] = av[e] + src[DPL * lane + e] * cq;
+        }
+        m[j] = M;
+        l[j] = Ls;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[j][e] = av[e];
+      }
+    }
+  }
+  // Partials of this split (stream 0's waves).
 #pragma unroll
   for (int j = 0; j < HPW; ++j) {
     const int hr = wave + 4 * j;
-    if (hr < n_rep) {
+    if (stm == 0 && hr < n_rep) {
       const int h = g * n_rep + hr;
       const size_t idx = (size_t)h * a.nsplit + split;
       if (lane == 0) {
@@ -409,32 +471,34 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     return false;
   }
 
-  // Last workgroup of this KV head: combine the splits.
+  // Last workgroup of this KV head: combine the splits (stream 0's waves).
 #pragma unroll
   for (int j = 0; j < HPW; ++j) {
     const int hr = wave + 4 * j;
-    if (hr >= n_rep) continue;
+    if (stm != 0 || hr >= n_rep) continue;
     const int h = g * n_rep + hr;
     const size_t base = (size_t)h * a.nsplit;
-    // One batch of device-scope loads: (m, l) of split `lane` (8 bytes) and
-    // this lane's dims of the first PF splits' partial O, so a combine of up
-    // to PF splits costs one memory round trip (every split writes its
-    // partials; an empty one has m = -inf, l = 0, o = 0).  Splits beyond PF
-    // (and beyond 64, in further rounds) are loaded as they are used.
+    // Device-scope loads in batches: (m, l) of split `lane` (8 bytes) with
+    // this lane's dims of the first PF splits' partial O, then PF splits at a
+    // time, so a combine costs one memory round trip per PF splits (every
+    // split writes its partials; an empty one has m = -inf, l = 0, o = 0).
     constexpr int PF = 32;
     float opf[PF][DPL];
+    auto load_chunk = [&](int c0) {
 #pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int uu = min(u, a.nsplit - 1);  // clamped; weighted by 0 past nsplit
-      const int off = (int)(((base + uu) * HD + DPL * lane) * 4);
-      if constexpr (DPL == 2) {
-        const dev_u32x2 t = dev_ld8(a.part_o, off);
-        opf[u][0] = __uint_as_float(t.x);
-        opf[u][1] = __uint_as_float(t.y);
-      } else {
-        opf[u][0] = dev_ldf(a.part_o, off);
+      for (int u = 0; u < PF; ++u) {
+        const int uu = min(c0 + u, a.nsplit - 1);  // clamped; weighted by 0 past nsplit
+        const int off = (int)(((base + uu) * HD + DPL * lane) * 4);
+        if constexpr (DPL == 2) {
+          const dev_u32x2 t = dev_ld8(a.part_o, off);
+          opf[u][0] = __uint_as_float(t.x);
+          opf[u][1] = __uint_as_float(t.y);
+        } else {
+          opf[u][0] = dev_ldf(a.part_o, off);
+        }
       }
-    }
+    };
+    load_chunk(0);
     float ms, ls;
     {
       const int sp = min(lane, a.nsplit - 1);
@@ -444,43 +508,34 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     }
     float M = wave_max(ms);
     for (int s0 = LLMRS_WAVE; s0 < a.nsplit; s0 += LLMRS_WAVE) {
-      const int sp = s0 + lane;
-      const float mx = sp < a.nsplit ? ld_part<true>(a.part_ml, 2 * (base + sp)) : -INFINITY;
-      M = fmaxf(M, wave_max(mx));
+      const int sp = min(s0 + lane, a.nsplit - 1);
+      const dev_u32x2 t = dev_ld8(a.part_ml, (int)(2 * (base + sp) * 4));
+      M = fmaxf(M, wave_max(s0 + lane < a.nsplit ? __uint_as_float(t.x) : -INFINITY));
     }
     float L = 0.0f, o[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; ++e) o[e] = 0.0f;
     for (int s0 = 0; s0 < a.nsplit; s0 += LLMRS_WAVE) {
-      const int sp = s0 + lane;
       if (s0 > 0) {
-        ms = -INFINITY;
-        ls = 0.0f;
-        if (sp < a.nsplit) {
-          ms = ld_part<true>(a.part_ml, 2 * (base + sp));
-          ls = ld_part<true>(a.part_ml, 2 * (base + sp) + 1);
-        }
+        const int sp = min(s0 + lane, a.nsplit - 1);
+        const dev_u32x2 t = dev_ld8(a.part_ml, (int)(2 * (base + sp) * 4));
+        ms = s0 + lane < a.nsplit ? __uint_as_float(t.x) : -INFINITY;
+        ls = s0 + lane < a.nsplit ? __uint_as_float(t.y) : 0.0f;
       }
+      // w is 0 in lanes past nsplit, so clamped extra loads add 0
       const float w = ms == -INFINITY ? 0.0f : expf(ms - M);
       L = L + wave_sum(ls * w);
-      const int cnt = min(LLMRS_WAVE, a.nsplit - s0);
-      int u0 = 0;
-      if (s0 == 0) {
+#pragma unroll
+      for (int half = 0; half < LLMRS_WAVE / PF; ++half) {
+        const int c0 = s0 + PF * half;
+        if (c0 >= a.nsplit) break;
+        if (c0 > 0) load_chunk(c0);
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
-          // w is 0 in lanes past nsplit, so the clamped extra loads add 0
-          const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+          const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), PF * half + u));
 #pragma unroll
           for (int e = 0; e < DPL; ++e) o[e] = o[e] + opf[u][e] * wu;
         }
-        u0 = PF;
-      }
-#pragma unroll 8
-      for (int u = u0; u < cnt; ++u) {
-        const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
-#pragma unroll
-        for (int e = 0; e < DPL; ++e)
-          o[e] = o[e] + ld_part<true>(a.part_o, (base + s0 + u) * HD + DPL * lane + e) * wu;
       }
     }
     // ctx as f32 and as Q8_0 (32-dim blocks: 16 lanes x 2 dims, or 32 lanes x 1).

@@ -90,6 +90,7 @@ _SIGS = {
     "llmrs_model_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p]),
     "llmrs_model_generate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
     "llmrs_model_begin": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "llmrs_model_begin_at": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t]),
     "llmrs_model_decode_steps": (C.c_int, [C.c_void_p, C.c_size_t]),
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "llmrs_model_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
@@ -372,9 +373,11 @@ class HipModel:
         _check(lib().llmrs_model_generate(self._h, _ptr(ids), ids.size, n_steps, _ptr(out)))
         return out
 
-    def begin(self, prompt) -> None:
+    def begin(self, prompt, start_pos: int = 0) -> None:
+        """Process the prompt at [start_pos, start_pos + n) (the cache below
+        start_pos already filled) and keep the greedy state resident."""
         ids = np.ascontiguousarray(prompt, dtype=np.int32)
-        _check(lib().llmrs_model_begin(self._h, _ptr(ids), ids.size))
+        _check(lib().llmrs_model_begin_at(self._h, _ptr(ids), ids.size, start_pos))
 
     def decode_steps(self, n: int) -> None:
         _check(lib().llmrs_model_decode_steps(self._h, n))

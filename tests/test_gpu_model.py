@@ -159,8 +159,12 @@ def test_kv_contents_and_graph_vs_eager(hip, orc):
     assert list(ga) == eager
 
 
-def test_prefilled_kv_decode(hip, orc):
-    """Pre-filled N(0,1) K/V caches (the long-context workload's setup)."""
+@pytest.mark.parametrize("streams", ["0", "4"], ids=["auto", "streams4"])
+def test_prefilled_kv_decode(hip, orc, streams, monkeypatch):
+    """Pre-filled N(0,1) K/V caches (the long-context workload's setup),
+    with the attention layout chosen by context length and with four tile
+    streams per workgroup forced (the layout of the longest contexts)."""
+    monkeypatch.setenv("LLMRS_ATTN_STREAMS", streams)
     spec = syn.with_sizes(syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_heads=8, n_kv_heads=2),
                           prefilled=300, prompt=1, decode=40)
     gm, om, w = build(hip, orc, spec)
@@ -193,6 +197,15 @@ def test_prefilled_kv_decode(hip, orc):
     env, _ = oracle_envelope(orc, spec, w, tok, 0, prefill=prefill, start_pos=spec.prefilled, trials=3)
     assert err < max(1e-2, ENVELOPE * env), f"logits error {err:.3g}, jittered-oracle envelope {env:.3g}"
     check_stream(ids, oids, np.array(margins), min_steps=40)
+    # the resident greedy run from the same position (HIP-graph replay) gives
+    # the eager stream: the cache below start_pos is taken as pre-filled
+    for l in range(spec.n_layers):
+        for g in range(spec.n_kv_heads):
+            gm.kv_write(l, g, 0, *syn.prefill_kv(spec, l, g))
+    gm.begin(tok, start_pos=spec.prefilled)
+    gm.decode_steps(len(ids) - 1)
+    run = gm.tokens(spec.prefilled + len(ids) + 1)[spec.prefilled + 1:]
+    assert np.array_equal(run, np.array(ids)), f"graph run {run[:8]} vs eager {ids[:8]}"
 
 
 @pytest.mark.parametrize("index,prompt_len,steps", [(0, 32, 128), (1, 32, 128), (2, 16, 64)])
@@ -327,13 +340,15 @@ def test_error_paths(hip, orc):
 def test_attention_split_counts_agree(hip, orc, kv, monkeypatch):
     """Regression: a split whose tile runs past its end must not read the
     owner's new-token row (it once took stale LDS for it, so any split
-    count > 1 gave run-to-run different, wrong attention).  Every split count
+    count > 1 gave run-to-run different, wrong attention).  Every split count,
+    with one tile stream per workgroup or four (the long-context layout),
     gives the same tokens and logits within rounding, run after run."""
     spec = syn.tiny(DType.Q4_0, kv, head_dim=128, n_heads=8, n_kv_heads=2, ffn=1024)
     w = syn.make_weights(spec)
     toks = syn.prompt(spec)
     ref = None
-    for splits in (1, 2, 3, 8, 8):
+    for streams, splits in ((1, 1), (1, 2), (1, 3), (1, 8), (1, 8), (4, 1), (4, 2), (4, 3), (4, 3)):
+        monkeypatch.setenv("LLMRS_ATTN_STREAMS", str(streams))
         monkeypatch.setenv("LLMRS_ATTN_SPLITS", str(splits))
         gm = hip.HipModel(spec.config(96))
         syn.load_model(gm, w)
@@ -344,8 +359,8 @@ def test_attention_split_counts_agree(hip, orc, kv, monkeypatch):
             continue
         assert np.all(np.isfinite(tr))
         # only summation order differs: equal up to Q8 code steps
-        assert rel_norm_err(tr, ref[1]) < 1e-2, f"splits={splits}"
-        assert np.max(np.abs(lg - ref[0])) < 2e-2, f"splits={splits}"
+        assert rel_norm_err(tr, ref[1]) < 1e-2, f"streams={streams} splits={splits}"
+        assert np.max(np.abs(lg - ref[0])) < 2e-2, f"streams={streams} splits={splits}"
 
 
 FUSED = [
