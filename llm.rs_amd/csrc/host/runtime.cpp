@@ -77,16 +77,17 @@ GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
   if (eu && (std::atoi(eu) == 1 || std::atoi(eu) == 2)) U = std::atoi(eu);
   int R = 4;
   if (kind == "norm_store" || kind == "q8_resid") {
-    R = n <= 8192 ? 2 : 4;
+    R = 2;
     const char* er = std::getenv("LLMRS_GEMV_R");
     if (er && (std::atoi(er) == 2 || std::atoi(er) == 4)) R = std::atoi(er);
   }
-  // Workgroups per CU: 1 for matrices under 24 MB (Q|K|V and O of the 8B
-  // shape: fewer, longer-lived workgroups shorten the prologue queue), 2
-  // otherwise (measured on MI355X).
+  // Workgroups per CU (measured on MI355X): 1 for the RMSNorm-prologue
+  // store GEMV (Q|K|V: 8B 14 MB, 70B 47 MB) and for matrices under 24 MB -
+  // fewer, longer-lived workgroups keep the activation loads from queueing
+  // behind as many weight requests - and 2 otherwise.
   const double wbytes = (double)n * k * (wt == WT_Q8H ? 34.0 : wt == WT_Q4F ? 20.0 : 18.0) / 32.0;
   const char* ew = std::getenv("LLMRS_GEMV_WG_PER_CU");
-  const int per_cu = ew && *ew ? std::max(1, std::atoi(ew)) : (wbytes < 24e6 ? 1 : 2);
+  const int per_cu = ew && *ew ? std::max(1, std::atoi(ew)) : (kind == "norm_store" || wbytes < 24e6 ? 1 : 2);
   const long cap = (long)std::max(1, num_cus) * per_cu;
   GemvPlan p;
   p.name = std::string("gemv_") + wt_tag(wt) + "_" + kind + "_r" + std::to_string(R) + "u" +
