@@ -102,14 +102,20 @@ def test_gemm_bit_exact(hip, orc, rng, wtype, m, n, k):
         f"{got[bad[0][0], bad[1][0]]!r} vs {want[bad[0][0], bad[1][0]]!r}")
 
 
-def test_gemv_zero_and_special_inputs(hip, orc):
-    """amax == 0 blocks (d = 0) and a NaN input element (code 0)."""
+@pytest.mark.parametrize("k", [256, 4096])
+def test_gemv_zero_and_special_inputs(hip, orc, k):
+    """amax == 0 blocks (d = 0), a NaN input element (code 0) and, at
+    k = 4096 (eight lanes per block in the prologue), a block whose amax is
+    subnormal (d = amax/127 subnormal, 1/d = inf, codes clamp to +-127)."""
     be = hip.HipBackend()
-    n, k = 96, 256
+    n = 96
     qs, sc = hip.synth_q4(3, 4, n, k, 0.003, 0.006)
     x = np.zeros((1, k), F32)
     x[0, 40:70] = np.linspace(-2, 2, 30)
     x[0, 200] = np.nan
+    if k > 1024:
+        x[0, 1000:1032] = np.linspace(-1e-40, 1e-40, 32, dtype=F32)
+        x[0, 3000:3064] = np.linspace(-5, 3, 64)
     w = hip.Tensor.from_q4(qs, sc, n, k)
     got = be.matmul_transposed(hip.Tensor.from_numpy(x), w).data()
     want = orc.matmul_transposed_q4(x, qs, sc, n)
