@@ -253,7 +253,7 @@ void enqueue_layer_tail(llmrs_model* m, Launcher& L, int li, unsigned long long*
   a.pos_ptr = m->pos;
   a.part_o = m->part_o;
   a.part_ml = m->part_ml;
-  a.counters = m->counters + (size_t)li * c.n_kv_heads;
+  a.counters = m->counters + (size_t)li * c.n_kv_heads * llmrs::kTicketStride;
   a.flags = m->lflags + (size_t)li * m->lk_flag_words;
   a.epoch = m->epoch;
   a.err = m->bar_err;
@@ -317,7 +317,7 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
       a.rope_sin = m->rope_sin;
       a.part_o = m->part_o;
       a.part_ml = m->part_ml;
-      a.counters = m->counters + (size_t)li * nkv;
+      a.counters = m->counters + (size_t)li * nkv * llmrs::kTicketStride;
       a.ctx = m->ctxv;
       a.ctx_q = m->ctx_q;
       a.ctx_d = m->ctx_d;
@@ -682,10 +682,11 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
     m->qkv_rows = (nq + 2 * nkv) * hd;
     m->cap = c.max_seq + 1;
-    // Attention splits: one 64-position tile per split up to two workgroups
-    // per CU; longer contexts run 4 tile streams per workgroup (one workgroup
-    // per CU) so the split combine stays short.
-    const int tiles = (c.max_seq + 63) / 64;
+    // Attention splits: one tile per split up to two workgroups per CU;
+    // longer contexts run 4 tile streams per workgroup (one workgroup per CU)
+    // so the split combine stays short.
+    const int tile = llmrs::attn_tile(c.kv_dtype == LLMRS_F16);
+    const int tiles = (c.max_seq + tile - 1) / tile;
     int splits = std::min(tiles, std::max(1, 2 * cx.num_cus / nkv));
     m->attn_streams = 1;
     const int es = env_int("LLMRS_ATTN_STREAMS", 0);  // 0 = by context length, 1 or 4 = forced
@@ -728,7 +729,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     const size_t nparts = (size_t)m->lm_grid;
     m->part_val = m->dalloc<float>(nparts);
     m->part_idx = m->dalloc<int>(nparts);
-    m->counters = m->dalloc<int>((size_t)c.n_layers * nkv);
+    m->counters = m->dalloc<int>((size_t)c.n_layers * nkv * llmrs::kTicketStride);
     m->tokens = m->dalloc<int>(m->cap);
     m->gen = m->dalloc<int>(m->cap);
     m->pos = m->dalloc<int>(1);

@@ -66,7 +66,7 @@ struct AttnArgs {
   const float* rope_sin;
   float* part_o;           // [nq][nsplit][hd]
   float* part_ml;          // [nq][nsplit][2]
-  int* counters;           // [nkv] tickets, zero between launches
+  int* counters;           // [nkv][kTicketStride] tickets, zero between launches
   float* ctx;              // [nq*hd]
   int8_t* ctx_q;           // [nq*hd]
   float* ctx_d;            // [nq*hd/32]
@@ -174,8 +174,14 @@ struct PrefillAttnArgs {
 // stream a padded K tile and a V tile, the new row, the ticket).  Tiles are
 // 64 positions for an f16 cache and 32 for f32; at most 8 query heads per KV
 // head; `streams` tile streams per workgroup.
+// ints between the split tickets of two KV heads: each head's counter has a
+// 256-byte line of its own, so the heads' atomics do not queue on one line.
+constexpr int kTicketStride = 64;
+
+// Positions per decode-attention tile (attn_core.h: AttnCfg::TILE).
+constexpr int attn_tile(bool kv16) { return kv16 ? 32 : 32; }
 constexpr size_t attn_lds_bytes(int hd, bool kv16, int streams = 1) {
-  const size_t es = kv16 ? 2 : 4, tile = kv16 ? 64 : 32, kstride = (size_t)hd + (kv16 ? 2 : 1);
+  const size_t es = kv16 ? 2 : 4, tile = (size_t)attn_tile(kv16), kstride = (size_t)hd + (kv16 ? 2 : 1);
   const size_t kb = (es * tile * kstride + 15) / 16 * 16;
   const size_t stream = kb + es * tile * (size_t)hd;
   return 4 * 8 * (size_t)hd + (size_t)streams * stream + 4 * 2 * (size_t)hd + 16;
@@ -216,7 +222,7 @@ struct LayerArgs {
   const int* pos_ptr;        // device position of the token
   float* part_o;             // attention partials [nq][nsplit][hd]
   float* part_ml;
-  int* counters;             // [nkv] attention tickets of this layer, zero between uses
+  int* counters;             // [nkv][kTicketStride] attention tickets of this layer, zero between uses
   unsigned* flags;           // this layer's completion flags: attention (one per KV head),
                              // O, gate|up workgroups in that order (layer_flag_words entries)
   const unsigned* epoch;     // decode-step counter: a flag equal to it is set for this step

@@ -10,13 +10,16 @@
 // MI355X design: one workgroup per (KV head, sequence split), 4 waves.  The
 // group's n_rep query heads share every K/V tile (true GQA: the reference
 // instead duplicates K/V rows per query head, loader.rs:62-98, which gives
-// the same numbers).  A split is a run of whole 64-position tiles.  Per tile:
+// the same numbers).  A split is a run of whole 32-position tiles.  Per tile:
 //  - the K and V rows are requested with 16-byte loads for the whole tile at
 //    once (and the next tile's loads are issued before this tile is used),
 //    then staged through LDS, K rows padded so lane-per-position reads are
 //    conflict-free;
-//  - wave w owns query heads w, w+4: lane p forms the score of position p
-//    (q broadcast from LDS, f32 accumulate of f32 q times the stored K);
+//  - wave w owns query heads w, w+4: lanes p and p+32 form the score of
+//    position p over the first and second half of the head dims (q
+//    broadcast from LDS, f32 accumulate of f32 q times the stored K), so
+//    every lane works and a tile costs half the instructions of a 64-lane
+//    row walk over all dims;
 //  - softmax is online per head (running max and sum, DPP wave reductions);
 //  - for P.V lane l owns head dims 2l, 2l+1 (HD=128) or l (HD=64); the
 //    probabilities are broadcast from the lane that holds them.
@@ -82,7 +85,7 @@ __device__ __forceinline__ void st_kv(float* p, void* base, size_t idx, float v)
 template <int HD, bool KV16>
 struct AttnCfg {
   typedef typename KvType<KV16>::T kv_t;
-  static constexpr int TILE = KV16 ? 64 : 32;            // positions per tile
+  static constexpr int TILE = attn_tile(KV16);            // positions per tile (32)
   static constexpr int EPC = 16 / (int)sizeof(kv_t);      // elements per 16 B
   static constexpr int CPR = HD / EPC;                    // 16 B chunks per row
   static constexpr int CHUNKS = TILE * CPR;               // per tile, K or V
@@ -92,6 +95,7 @@ struct AttnCfg {
   static constexpr int HPW = MAXREP / 4;                  // heads per wave
   static constexpr int DPL = HD / LLMRS_WAVE;             // head dims per lane in P.V
   static_assert(CHUNKS % 256 == 0, "tile must split evenly over 256 threads");
+  static_assert(TILE == LLMRS_WAVE / 2, "two lanes (half rows) per position");
 };
 
 // LDS carve-up of one work item (bytes): s_q, then per stream a padded K
@@ -319,17 +323,22 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     for (int j = 0; j < HPW; ++j) {
       const int hr = wave + 4 * j;
       if (hr >= n_rep) continue;  // uniform per wave
-      // Score of position t0 + lane.  Four partial sums (d mod 4) instead of
-      // the reference's one sequential sum (cpu.rs:548): with one wave per
-      // SIMD nothing hides the latency of a single dependent FMA chain.
+      // Score of position t0 + (lane % 32): lanes 32..63 sum the second half
+      // of the head dims and the halves are added across the wave.  Four
+      // partial sums (d mod 4) per half instead of the reference's one
+      // sequential sum (cpu.rs:548): with one wave per SIMD nothing hides the
+      // latency of a single dependent FMA chain.  Lanes 32..63 then carry
+      // -inf, so each position enters the softmax once.
       float sc = -INFINITY;
-      if (lane < tvalid) {
+      {
+        const int prow = lane & (TILE - 1), dbase = (lane >> 5) * (HD / 2);
         float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-        // 32-bit LDS reads of the padded row: bank (lane*KSTRIDE/2 + i) mod 64
-        // differs across lanes, so the reads are conflict-free.
-        const unsigned* krow = (const unsigned*)(s_k + lane * C::KSTRIDE);
+        // 32-bit LDS reads of the padded row: bank (prow*KSTRIDE/2 + i) mod 32
+        // differs across the 32 lanes of each half.
+        const unsigned* krow = (const unsigned*)(s_k + prow * C::KSTRIDE);
 #pragma unroll 8
-        for (int d = 0; d < HD; d += 4) {
+        for (int i = 0; i < HD / 2; i += 4) {
+          const int d = dbase + i;
           const f32x4 q4 = *(const f32x4*)&s_q[hr][d];
           float k0, k1, k2, k3;
           if constexpr (KV16) {
@@ -349,7 +358,9 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
           s2 = __builtin_fmaf(q4.z, k2, s2);
           s3 = __builtin_fmaf(q4.w, k3, s3);
         }
-        sc = ((s0 + s1) + (s2 + s3)) * a.scale;
+        float sp = (s0 + s1) + (s2 + s3);
+        sp = sp + __shfl_xor(sp, 32);
+        if (lane < TILE && prow < tvalid) sc = sp * a.scale;
       }
       const float mnew = fmaxf(m[j], wave_max(sc));
       const float p = (sc == -INFINITY) ? 0.0f : expf(sc - mnew);
@@ -358,7 +369,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
       m[j] = mnew;
       // P.V over the tile's positions in four independent partial sums
       // (position mod 4); a full tile is unrolled so the LDS reads of
-      // successive rows overlap.
+      // successive rows overlap.  p of position u sits in lane u.
       float pt[4][DPL];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
@@ -377,7 +388,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
         }
       };
       if (tvalid == TILE) {
-#pragma unroll 16
+#pragma unroll
         for (int u = 0; u < TILE; u += 4) {
           pv_row(u, 0);
           pv_row(u + 1, 1);
@@ -463,7 +474,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   stamp(4);
-  if (tid == 0) s_ticket = atomicAdd(&a.counters[g], 1);
+  if (tid == 0) s_ticket = atomicAdd(&a.counters[g * kTicketStride], 1);
   __syncthreads();
   stamp(5);
   if (s_ticket != a.nsplit - 1) {
@@ -547,8 +558,8 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
       v[e] = o[e] / L;
       amax = fmaxf(amax, fabsf(v[e]));
     }
-#pragma unroll
-    for (int off = LPB / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, LPB));
+    amax = max16(amax);  // DPP within the 16-lane row
+    if (LPB == 32) amax = fmaxf(amax, __shfl_xor(amax, 16, 32));
     const float d = amax / 127.0f;
     const float inv = amax == 0.0f ? 0.0f : 1.0f / d;
 #pragma unroll
@@ -560,7 +571,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     }
     if ((lane % LPB) == 0) st_act<true>(a.ctx_d, ((size_t)h * HD + DPL * lane) / 32, amax == 0.0f ? 0.0f : d);
   }
-  if (tid == 0) dev_stu(a.counters, 4 * g, 0u);
+  if (tid == 0) dev_stu(a.counters, 4 * g * kTicketStride, 0u);
   stamp(6);
   flush_stamps();
   return true;

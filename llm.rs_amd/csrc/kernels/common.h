@@ -54,6 +54,14 @@ __device__ __forceinline__ float wave_sum(float v) {
   const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
   return ((r0 + r1) + r2) + r3;
 }
+// Maximum over each 16-lane row (quad exchanges, then the half-row and row
+// mirrors); every lane of the row holds the result.
+__device__ __forceinline__ float max16(float v) {
+  v = fmaxf(v, dpp_c<0xB1>(v));
+  v = fmaxf(v, dpp_c<0x4E>(v));
+  v = fmaxf(v, dpp_c<0x141>(v));
+  return fmaxf(v, dpp_c<0x140>(v));
+}
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_c<0xB1>(v));
   v = fmaxf(v, dpp_c<0x4E>(v));
