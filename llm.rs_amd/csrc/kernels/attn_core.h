@@ -482,11 +482,13 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     return false;
   }
 
-  // Last workgroup of this KV head: combine the splits (stream 0's waves).
+  // Last workgroup of this KV head: combine the splits, one query head per
+  // wave over all 4 * S waves of the workgroup (with 4 streams, 16 waves for
+  // at most 8 heads, so no wave combines two heads one after the other).
 #pragma unroll
-  for (int j = 0; j < HPW; ++j) {
-    const int hr = wave + 4 * j;
-    if (stm != 0 || hr >= n_rep) continue;
+  for (int j = 0; j < (HPW + S - 1) / S; ++j) {
+    const int hr = wave_id() + 4 * S * j;
+    if (hr >= n_rep) continue;
     const int h = g * n_rep + hr;
     const size_t base = (size_t)h * a.nsplit;
     // Device-scope loads in batches: (m, l) of split `lane` (8 bytes) with
