@@ -83,13 +83,17 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 }
 
 // One Q8_0 code for x with inverse scale inv (cpu.rs:736-740):
-// round-half-away-from-zero, clamp to [-127, 127], NaN -> 0.
+// round-half-away-from-zero, clamp to [-127, 127], NaN -> 0.  The rounding
+// is trunc(p + copysign(0.5 - 2^-25, p)): three instructions instead of the
+// six of roundf, and equal to roundf for every non-NaN float (checked
+// exhaustively over all 2^32 bit patterns; 0.5 - 2^-25 keeps p = 0.5 - 2^-25
+// from rounding up, and the sum of a half-integer and it rounds away from
+// zero).  The NaN case is a select, not a branch.
 __device__ __forceinline__ int q8_code(float x, float inv) {
-  float p = x * inv;
-  if (p != p) return 0;  // Rust's `NaN as i8` is 0
-  float r = __builtin_roundf(p);
+  const float p = x * inv;
+  float r = __builtin_truncf(p + __builtin_copysignf(0.49999997f, p));
   r = fminf(127.0f, fmaxf(-127.0f, r));
-  return (int)r;
+  return p != p ? 0 : (int)r;  // Rust's `NaN as i8` is 0
 }
 
 // Quantise 32 values held one per lane of a 32-lane group (lanes with the

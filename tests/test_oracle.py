@@ -48,6 +48,41 @@ def test_q8_quantize_nan_is_zero(orc):
 
 
 # ---- Q4 format (tensor.rs:102-167, test/opencl.rs:182-235) -----------------
+def test_round_half_away_identity():
+    """The GPU quantiser rounds with trunc(p + copysign(0.5 - 2**-25, p))
+    instead of roundf (fewer instructions).  Pin that this equals Rust's
+    f32::round (half away from zero, cpu.rs:739) on every float32 within
+    +-64 ulps of each integer and half-integer up to 256 (where a wrong
+    constant or a double rounding would show), plus random values; an
+    exhaustive check over all 2**32 bit patterns also finds no difference."""
+    F32 = np.float32
+    centers = np.concatenate([np.arange(0, 257, dtype=np.float64), np.arange(0, 256, dtype=np.float64) + 0.5])
+    vals = []
+    for c in centers:
+        x = F32(c)
+        seq_up = [x]
+        seq_dn = [x]
+        u, d = x, x
+        for _ in range(64):
+            u = np.nextafter(u, F32(np.inf))
+            d = np.nextafter(d, F32(-np.inf))
+            seq_up.append(u)
+            seq_dn.append(d)
+        vals.extend(seq_up)
+        vals.extend(seq_dn)
+    rng = np.random.default_rng(5)
+    x = np.concatenate([np.array(vals, F32), rng.uniform(-300, 300, 1 << 20).astype(F32),
+                        rng.uniform(-2, 2, 1 << 20).astype(F32),
+                        np.array([0.0, -0.0, 0.49999997, -0.49999997, 0.5, -0.5, 1.5, 2.5, 126.5, 127.5,
+                                  np.inf, -np.inf, 1e-40, -1e-40, 8388607.5, 8388609.0], F32)])
+    x = np.concatenate([x, -x])
+    c = np.copysign(F32(0.49999997), x).astype(F32)
+    trick = np.trunc((x + c).astype(F32))                      # float32 add, then truncate
+    want = (np.sign(x) * np.floor(np.abs(x.astype(np.float64)) + 0.5)).astype(F32)  # half away from zero
+    assert np.nextafter(F32(0.5), F32(0)) == F32(0.49999997)
+    assert np.array_equal(trick, want), x[trick != want][:8]
+
+
 def test_q4_nibble_order_one_hot(orc, rng):
     """Element 2i is the low nibble of byte i, 2i+1 the high nibble."""
     qs = rng.integers(0, 256, 16, dtype=np.uint8)
