@@ -644,9 +644,21 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
   ts.on = a.ts != nullptr;
   ts.rec(0);
 
+  // The residual of this lane's first output row is requested with the
+  // activations: loaded in the epilogue it would cost a whole memory round
+  // trip after the unit loop.  The row is clamped instead of tested, so the
+  // prologue has no branch at which the compiler would wait for the loads.
+  float res0 = 0.0f;
   {
     ActRegs<PRO> ar;
     issue_activation<PRO, DEV>(a, mrow, ar);
+    if (EPI == EPI_RESID) {
+      const int nv = (nunits / g.nchunk) * R;
+      const int v = min(lane, max(nv - 1, 0));
+      const int rg = max(g.row_group(v / R), 0);
+      const int row = min(rg * R + v % R, a.n - 1);
+      res0 = ld_act<DEV>(a.res, (size_t)mrow * a.n + row);
+    }
     if (!preloaded && PRE > 0) g.load(ua, nunits > 0 ? 0 : -1);
     if (!preloaded && PRE > 1) g.load(ub, nunits > 1 ? 1 : -1);
     finish_activation<PRO, G::Q4, DEV>(a, mrow, ar, s_q, s_d, s_off, sh.red, ts);
@@ -757,7 +769,11 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
       const int row = rg * R + v % R;
       if (rg >= 0 && row < a.n) {
         float out = s_out[wave * gmax * R + v];
-        if (EPI == EPI_RESID) out = out + ld_act<DEV>(a.res, ybase + row);  // layer.rs:386,403
+        if (EPI == EPI_RESID) {
+          float rv = res0;  // requested in the prologue for v0 == 0
+          if (v0 > 0) rv = ld_act<DEV>(a.res, ybase + row);
+          out = out + rv;  // layer.rs:386,403
+        }
         st_act<DEV>(a.y, ybase + row, out);
       }
     }
