@@ -10,7 +10,7 @@
 // MI355X design: one workgroup per (KV head, sequence split), 4 waves.  The
 // group's n_rep query heads share every K/V tile (true GQA: the reference
 // instead duplicates K/V rows per query head, loader.rs:62-98, which gives
-// the same numbers).  A split is a run of whole 32-position tiles.  Per tile:
+// the same numbers).  Splits take 32-position tiles round-robin.  Per tile:
 //  - the K and V rows are requested with 16-byte loads for the whole tile at
 //    once (and the next tile's loads are issued before this tile is used),
 //    then staged through LDS, K rows padded so lane-per-position reads are
@@ -167,15 +167,15 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     }
   };
   stamp(0);
-  const int T = pos + 1;
   const int n_rep = a.nq / a.nkv;
-  // Splits are runs of whole tiles, as even as the tile count allows.
-  const int ntile = (T + TILE - 1) / TILE;
-  const int start = min(T, (int)(((long)split * ntile) / a.nsplit) * TILE);
-  const int end = min(T, (int)(((long)(split + 1) * ntile) / a.nsplit) * TILE);
+  // Tiles are dealt to the splits round-robin: stream st of split s takes
+  // tiles (it * S + st) * nsplit + s, it = 0, 1, ...  The first tile of every
+  // stream is therefore known without the position, and its loads are
+  // requested before the position has arrived; rows past the context are
+  // clamped to the cache and masked.
+  const int first = (stm * a.nsplit + split) * TILE;  // this stream's first tile
+  const int stride = S * a.nsplit * TILE;             // and the distance to its next one
   const int qdim = a.nq * HD;
-  const float* rc = a.rope_cos + (size_t)pos * MID;
-  const float* rs = a.rope_sin + (size_t)pos * MID;
   const size_t gbase = (size_t)g * a.max_seq * HD;  // elements
   kv_t* kc = (kv_t*)a.kc + gbase;
   kv_t* vc = (kv_t*)a.vc + gbase;
@@ -186,7 +186,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
 #pragma unroll
     for (int i = 0; i < C::CPT; ++i) {
       const int c = ltid + 256 * i;
-      const int t = min(t0 + c / C::CPR, T - 1);  // clamped: rows past `end` are masked
+      const int t = min(t0 + c / C::CPR, a.max_seq - 1);  // clamped: rows past the context are masked
       const int col = (c % C::CPR) * C::EPC;
       if (DEV) {
         const int off = (int)((gbase + (size_t)t * HD + col) * ES);
@@ -198,14 +198,19 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
       }
     }
   };
-  if (start + stm * TILE < end) issue(start + stm * TILE);
+  issue(first);
+  // Keep the position's uses (and the wait for it) below the tile requests.
+  __builtin_amdgcn_sched_barrier(0);
+  const int T = pos + 1;
+  const float* rc = a.rope_cos + (size_t)pos * MID;
+  const float* rs = a.rope_sin + (size_t)pos * MID;
   if (!wait()) return false;
 
   // Rotated query heads of this group (cpu.rs:351-354) and, for the owner
   // of position pos, the rotated k and the v it appends (layer.rs:219-246).
   // Every projection and table value is loaded first, in one batch, so the
   // section costs one memory round trip.
-  const bool owner = pos >= start && pos < end;
+  const bool owner = (pos / TILE) % a.nsplit == split;  // holds the new position's tile
   const bool qthr = tid < 256;  // the projections are read by the first 256 threads
   constexpr int QPT = (C::MAXREP * MID + 255) / 256;  // query pairs per thread
   const size_t kr = qdim + (size_t)g * HD;
@@ -279,9 +284,9 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
   }
 
   stamp(1);
-  for (int it = 0; start + it * S * TILE < end; ++it) {
-    const int t0 = start + (it * S + stm) * TILE;  // this stream's tile
-    const bool have = t0 < end;                    // uniform per stream
+  for (int it = 0; (it * S * a.nsplit + split) * TILE < T; ++it) {
+    const int t0 = first + it * stride;  // this stream's tile
+    const bool have = t0 < T;            // uniform per stream
     __syncthreads();  // previous tile consumed; s_q / s_new written
     if (have) {
       // Stage the tile (already loaded into registers) into LDS: V rows with
@@ -313,12 +318,12 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
         *(u32x4*)(s_v + r * HD + col) = vw;
       }
     }
-    if (t0 + S * TILE < end) issue(t0 + S * TILE);  // next tile in flight during this one
+    if (t0 + stride < T) issue(t0 + stride);  // next tile in flight during this one
     __syncthreads();
     if (it == 0) stamp(2);
     if (!have) continue;
 
-    const int tvalid = min(TILE, end - t0);
+    const int tvalid = min(TILE, T - t0);
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
       const int hr = wave + 4 * j;
