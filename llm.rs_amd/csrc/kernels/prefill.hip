@@ -8,10 +8,13 @@
 // with isum_b the exact int32 dot product of one 32-element block.
 //
 // gemm_*: per 32-element block and 32 x 32 (token x row) tile, one
-// v_mfma_i32_32x32x32_i8 gives every isum_b exactly, and one
-// v_mfma_f32_32x32x2_f32 with the k = 1 operands zero gives every scale
-// s_b = d_w * d_a as a single IEEE product (round to nearest even, the same
-// value as the reference's f32 multiply).  The epilogue per element and
+// v_mfma_i32_32x32x32_i8 gives every isum_b exactly, and one two-block
+// v_mfma_f32_32x32x1_2b_f32 per token tile gives the scales
+// s_b = d_w * d_a of both row tiles, each as a single IEEE product (round to
+// nearest even, the same value as the reference's f32 multiply).  Lane
+// 32 blk + i supplies row / column i of block blk, and block blk's results
+// sit in registers 16 blk .. 16 blk + 15 in the layout of a one-block
+// 32 x 32 MFMA (checked on the device), so no operand is wasted.  The epilogue per element and
 // block is then the reference's own two roundings, total = total + isum * s,
 // in block order, so every output is bit-identical to the reference for
 // identical activation codes.  Three VALU operations per element and block
@@ -33,12 +36,10 @@ using namespace llmrs;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 namespace {
 
-#ifndef LLMRS_GEMM_SCALE_MFMA
-#define LLMRS_GEMM_SCALE_MFMA 1  // d_w * d_a on the f32 MFMA (else on the VALU)
-#endif
 #ifndef LLMRS_GEMM_WAVES
 #define LLMRS_GEMM_WAVES 2    // workgroups per CU the register budget allows
 #endif
@@ -79,13 +80,12 @@ struct GemmLoads {
   static constexpr int S_PER_T = kKB * kBN / 256;              // scales per thread (d_w and d_a)
 };
 
-// MFMA operands of one block for a wave's 2 x 2 tiles.
+// MFMA operands of one block for a wave's 2 x 2 tiles: codes, d_a of the
+// lane's token in each token tile, d_w of the lane's row in row tile
+// `half` (the two-block scale MFMA takes row tile blk from lanes 32 blk..).
 struct GemmOps {
   v4i A[2], B[2];
-  float da[2], dw[2];
-#if !LLMRS_GEMM_SCALE_MFMA
-  f32x4 dav[2][4];  // d_a of the lane's 16 tokens per token tile
-#endif
+  float da[2], dw;
 };
 
 }  // namespace
@@ -101,7 +101,6 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const int nb = a.K >> 5;
   const int nstage = (nb + kKB - 1) / kKB;
-  const unsigned kmask = half ? 0u : ~0u;  // lanes 32..63 hold the k = 1 scale operands
 
   // ---- staging: global -> registers -> LDS -------------------------------
   // activation chunk q: token q / (2 kKB), c = q % (2 kKB); weight chunk q:
@@ -172,14 +171,14 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds
 
   // ---- compute -------------------------------------------------------------
   // Per-lane LDS offsets of the operands (the block adds a constant).
-  int offA[2], offB[2], offDA[2], offDW[2];
+  int offA[2], offB[2], offDA[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     offA[t] = S::A + (half * kBM + wm + 32 * t) * 16;  // + (col ^ c) per block
     offB[t] = S::B + (half * kBN + wn + 32 * t) * 16;
     offDA[t] = S::DA + (wm + 32 * t + col) * 4;
-    offDW[t] = S::DW + (wn + 32 * t + col) * 4;
   }
+  const int offDW = S::DW + (wn + 32 * half + col) * 4;  // row tile `half` (two-block MFMA)
   auto load_ops = [&](const uint8_t* base, int b, GemmOps& o) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -188,17 +187,9 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds
       o.A[t] = v4i{va.x, va.y, va.z, va.w};
       const i32x4 vb = *(const i32x4*)(base + offB[t] + (b * (2 * kBN) + cx) * 16);
       o.B[t] = v4i{vb.x, vb.y, vb.z, vb.w};
-      // k = 1 operands of the scale product are zero
-#if LLMRS_GEMM_SCALE_MFMA
-      o.da[t] = __uint_as_float(*(const unsigned*)(base + offDA[t] + b * (S::SW * 4)) & kmask);
-      o.dw[t] = __uint_as_float(*(const unsigned*)(base + offDW[t] + b * (S::SW * 4)) & kmask);
-#else
-      o.dw[t] = *(const float*)(base + offDW[t] + b * (S::SW * 4));
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        o.dav[t][g] = *(const f32x4*)(base + S::DA + b * (S::SW * 4) + (wm + 32 * t + 8 * g + 4 * half) * 4);
-#endif
+      o.da[t] = *(const float*)(base + offDA[t] + b * (S::SW * 4));
     }
+    o.dw = *(const float*)(base + offDW + b * (S::SW * 4));
   };
 
   float acc[2][2][16];
@@ -208,21 +199,12 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds
     for (int r = 0; r < 2; ++r)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[t][r][i] = 0.0f;
-  auto epi = [&](int t, int r, const v16i& p, const v16f& sc) {
+  // sc: both row tiles' scales of token tile t (registers 16 r ..).
+  auto epi = [&](int t, int r, const v16i& p, const v32f& sc) {
 #pragma unroll
     for (int i = 0; i < 16; ++i)  // cpu.rs:913,932: total += isum * (d_w * d_a)
-      acc[t][r][i] = acc[t][r][i] + (float)p[i] * sc[i];
+      acc[t][r][i] = acc[t][r][i] + (float)p[i] * sc[16 * r + i];
   };
-#if !LLMRS_GEMM_SCALE_MFMA
-  auto epi_v = [&](int t, int r, const v16i& p, const GemmOps& o) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const f32x4 d4 = o.dav[t][i / 4];
-      const float da = (i % 4 == 0) ? d4.x : (i % 4 == 1) ? d4.y : (i % 4 == 2) ? d4.z : d4.w;
-      acc[t][r][i] = acc[t][r][i] + (float)p[i] * (o.dw[r] * da);
-    }
-  };
-#endif
 
   load_stage(0);
   store_stage(0);
@@ -237,46 +219,36 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds
       // the operands of block b+1 are read while block b is in flight.
       GemmOps o[2];
       v16i P[2];
-      v16f SC[2];
+      v32f SC;  // scales of the current (block, token tile) pair, both row tiles
       load_ops(base, 0, o[0]);
       P[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o[0].A[0], o[0].B[0], v16i{}, 0, 0, 0);
-#if LLMRS_GEMM_SCALE_MFMA
-      SC[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o[0].da[0], o[0].dw[0], v16f{}, 0, 0, 0);
-#endif
 #pragma unroll
       for (int k = 0; k < 4 * kKB; ++k) {
         const int b = k / 4, t = (k / 2) % 2, r = k % 2;
+        // The pair's scale MFMA at its r = 0 tile, then the next tile's
+        // integer MFMA, whose issue covers the scale MFMA's latency.
+        if (r == 0) SC = __builtin_amdgcn_mfma_f32_32x32x1f32(o[b % 2].da[t], o[b % 2].dw, v32f{}, 0, 0, 0);
         if (k % 4 == 0 && b + 1 < kKB) load_ops(base, b + 1, o[(b + 1) % 2]);
         if (k + 1 < 4 * kKB) {
           const int kn = k + 1;
           const GemmOps& on = o[(kn / 4) % 2];
           P[kn % 2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(on.A[(kn / 2) % 2], on.B[kn % 2], v16i{}, 0, 0, 0);
-#if LLMRS_GEMM_SCALE_MFMA
-          SC[kn % 2] = __builtin_amdgcn_mfma_f32_32x32x2f32(on.da[(kn / 2) % 2], on.dw[kn % 2], v16f{}, 0, 0, 0);
-#endif
         }
-#if LLMRS_GEMM_SCALE_MFMA
-        epi(t, r, P[k % 2], SC[k % 2]);
-#else
-        epi_v(t, r, P[k % 2], o[b % 2]);
-#endif
+        epi(t, r, P[k % 2], SC);
       }
     } else {
       for (int b = 0; b < kvalid; ++b) {
         GemmOps o;
         load_ops(base, b, o);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t) {
+          const v32f sc = __builtin_amdgcn_mfma_f32_32x32x1f32(o.da[t], o.dw, v32f{}, 0, 0, 0);
 #pragma unroll
           for (int r = 0; r < 2; ++r) {
             const v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.A[t], o.B[r], v16i{}, 0, 0, 0);
-#if LLMRS_GEMM_SCALE_MFMA
-            const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(o.da[t], o.dw[r], v16f{}, 0, 0, 0);
             epi(t, r, p, sc);
-#else
-            epi_v(t, r, p, o);
-#endif
           }
+        }
       }
     }
     if (st + 1 < nstage) store_stage((st + 1) & 1);
