@@ -159,14 +159,10 @@ def test_kv_contents_and_graph_vs_eager(hip, orc):
     assert list(ga) == eager
 
 
-@pytest.mark.parametrize("streams", ["0", "4"], ids=["auto", "streams4"])
-def test_prefilled_kv_decode(hip, orc, streams, monkeypatch):
-    """Pre-filled N(0,1) K/V caches (the long-context workload's setup),
-    with the attention layout chosen by context length and with four tile
-    streams per workgroup forced (the layout of the longest contexts)."""
-    monkeypatch.setenv("LLMRS_ATTN_STREAMS", streams)
-    spec = syn.with_sizes(syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_heads=8, n_kv_heads=2),
-                          prefilled=300, prompt=1, decode=40)
+def prefilled_decode(hip, orc, spec, steps):
+    """Decode `steps` tokens after N(0,1) K/V pre-filled below
+    spec.prefilled, eagerly against the oracle, then as a resident HIP-graph
+    run from the same position, which must repeat the eager stream."""
     gm, om, w = build(hip, orc, spec)
     for l in range(spec.n_layers):
         for g in range(spec.n_kv_heads):
@@ -176,11 +172,10 @@ def test_prefilled_kv_decode(hip, orc, streams, monkeypatch):
     tok = syn.prompt(spec)[:1]
     lg, _, _ = gm.forward(tok, spec.prefilled)
     olg, _ = om.forward(tok, spec.prefilled)
-    olg0 = olg
     err = float(np.max(np.abs(lg - olg)))
     ids, oids = [int(np.argmax(lg))], [orc.argmax(olg)[0]]
     margins = [orc.argmax(olg)[1]]
-    for s in range(1, 40):
+    for s in range(1, steps):
         pos = spec.prefilled + s
         lg, _, _ = gm.forward([ids[-1]], pos)
         olg, _ = om.forward([oids[-1]], pos)
@@ -196,7 +191,7 @@ def test_prefilled_kv_decode(hip, orc, streams, monkeypatch):
                 model.kv_write(l, g, 0, *syn.prefill_kv(spec, l, g))
     env, _ = oracle_envelope(orc, spec, w, tok, 0, prefill=prefill, start_pos=spec.prefilled, trials=3)
     assert err < max(1e-2, ENVELOPE * env), f"logits error {err:.3g}, jittered-oracle envelope {env:.3g}"
-    check_stream(ids, oids, np.array(margins), min_steps=40)
+    check_stream(ids, oids, np.array(margins), min_steps=steps)
     # the resident greedy run from the same position (HIP-graph replay) gives
     # the eager stream: the cache below start_pos is taken as pre-filled
     for l in range(spec.n_layers):
@@ -206,6 +201,33 @@ def test_prefilled_kv_decode(hip, orc, streams, monkeypatch):
     gm.decode_steps(len(ids) - 1)
     run = gm.tokens(spec.prefilled + len(ids) + 1)[spec.prefilled + 1:]
     assert np.array_equal(run, np.array(ids)), f"graph run {run[:8]} vs eager {ids[:8]}"
+
+
+@pytest.mark.parametrize("streams", ["0", "4"], ids=["auto", "streams4"])
+def test_prefilled_kv_decode(hip, orc, streams, monkeypatch):
+    """Pre-filled N(0,1) K/V caches (the long-context workload's setup),
+    with the attention layout chosen by context length and with four tile
+    streams per workgroup forced (the layout of the longest contexts)."""
+    monkeypatch.setenv("LLMRS_ATTN_STREAMS", streams)
+    spec = syn.with_sizes(syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_heads=8, n_kv_heads=2),
+                          prefilled=300, prompt=1, decode=40)
+    prefilled_decode(hip, orc, spec, 40)
+
+
+def test_70b_layer_shapes_long_context(hip, orc):
+    """One decoder layer at the 70B widths (hidden 8192, 64 query and 8 KV
+    heads of 128, FFN 28672: Q|K|V 10240 x 8192, O 8192 x 8192, gate|up
+    57344 x 8192, down 8192 x 28672) with a small vocabulary, decoding from
+    a 2100-position pre-filled f16 cache.  The 2113-position cache is 67
+    tiles of 32, more than the 64 splits of two workgroups per CU over 8 KV
+    heads, so the attention picks four tile streams per workgroup with 8
+    query heads per KV head (one combining wave per head across the
+    streams) - the long-context layout of the 70B workload, which the
+    full-size model otherwise reaches only in the benchmark."""
+    spec = syn.with_sizes(syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_layers=1, n_heads=64,
+                                   n_kv_heads=8, ffn=28672, vocab=1024, seed=20260004),
+                          prefilled=2100, prompt=1, decode=12)
+    prefilled_decode(hip, orc, spec, 12)
 
 
 @pytest.mark.parametrize("index,prompt_len,steps", [(0, 32, 128), (1, 32, 128), (2, 16, 64)])
