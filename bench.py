@@ -154,6 +154,7 @@ def bench_prefill(args, lh, syn) -> int:
     dom = max(gemm, key=lambda n: per[n][0])
     ms, fl, n = per[dom]
     achieved = fl / n / (ms / n / 1e3) / 1e12
+    traffic = hbm_traffic(f"{spec.name} prefill", dom)
 
     cpu = None
     if keep:
@@ -171,7 +172,8 @@ def bench_prefill(args, lh, syn) -> int:
                    "kv_cache": spec.kv.name.lower(), "prompt": M, "batch": 1},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1),
                      "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
-                     "flops_per_launch": round(fl / n), "avg_us": round(ms / n * 1e3, 2), "traffic": None},
+                     "flops_per_launch": round(fl / n), "avg_us": round(ms / n * 1e3, 2),
+                     "traffic": None if traffic is None else round(traffic)},
         "gemm_mfma_utilisation": round(g_fl / (g_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
         "gemm_share_of_prefill": round(g_ms / tot, 4),
         "cpu_baseline": cpu,
@@ -182,14 +184,17 @@ def bench_prefill(args, lh, syn) -> int:
 
 
 def traffic_probe(args, lh, syn) -> int:
-    """Dispatches for HBM-traffic counters: two eager decode steps (every
-    decode kernel once each) and a scale_f32 pass over 64 Mi floats, whose
+    """Dispatches for HBM-traffic counters: the workload's prompt as one
+    batched prefill (every prefill kernel once per layer at its real M),
+    four eager decode steps right after it (every decode kernel at the
+    prompt's context length) and a scale_f32 pass over 64 Mi floats, whose
     FETCH_SIZE / WRITE_SIZE readings calibrate the counters (each ideally
     256 MiB)."""
     import numpy as np
-    spec = syn.with_sizes(syn.WORKLOADS[args.workload], prompt=16, decode=8)
+    base = syn.WORKLOADS[args.workload]
+    spec = syn.with_sizes(base, prompt=args.prompt or base.prompt, decode=8)
     lh.init(0)
-    model = lh.HipModel(spec.config(64))
+    model = lh.HipModel(spec.config(spec.prompt + 16))
     syn.stream_model(model, spec)
     model.begin(syn.prompt(spec))
     model.decode_steps(2)
@@ -201,7 +206,8 @@ def traffic_probe(args, lh, syn) -> int:
     x = lh.Tensor.from_numpy(np.ones((n // 4096, 4096), np.float32))
     lh.HipBackend().scale(x, 1.0)
     lh.sync()
-    print(json.dumps({"probe": "traffic", "workload": spec.name, "calibration_kernel": "scale_f32",
+    print(json.dumps({"probe": "traffic", "workload": spec.name, "prompt": spec.prompt,
+                      "decode_context": [spec.prompt + 1, spec.prompt + 4], "calibration_kernel": "scale_f32",
                       "calibration_read_bytes": 4 * n, "calibration_write_bytes": 4 * n}), flush=True)
     return 0
 
@@ -217,7 +223,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
-                    help="for rocprofv3 --pmc runs: eager decode steps of the workload, then one "
+                    help="for rocprofv3 --pmc runs: the workload's prompt prefill, eager decode steps, then one "
                          "256 MiB scale_f32 pass (reads and writes 256 MiB) that calibrates the counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

@@ -95,6 +95,8 @@ void set_last_error(const std::string& msg);
 // Kernel weight types (must match the WT_* enumeration in gemv.hip).
 enum { WT_Q4H = 0, WT_Q4F = 1, WT_Q8H = 2 };
 const char* wt_tag(int wt);
+// PrefillGemmArgs::group_m for every prefill GEMM launch (LLMRS_GEMM_GROUP).
+int gemm_group_m();
 
 // Launch plan of one GEMV: kernel name, grid and dynamic LDS bytes.
 // `kind` is the prologue/epilogue pair of gemv.hip: quant_store,

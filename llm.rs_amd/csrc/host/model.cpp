@@ -441,7 +441,7 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
     }
     {  // Q|K|V
       PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.qkv.codes, Lb.qkv.scales, m->pf_qkv, nullptr,
-                        nullptr, nullptr, M, QR, H, QR};
+                        nullptr, nullptr, M, QR, H, QR, gemm_group_m()};
       L(gemm_kernel(m, "store"), flops(M, QR, H), gemm_grid(M, QR), blk, glds, g);
     }
     {  // RoPE + K/V append
@@ -461,7 +461,7 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
     }
     {  // O projection + residual (layer.rs:386)
       PrefillGemmArgs g{m->pf_ctx_q, m->pf_ctx_d, Lb.o.codes, Lb.o.scales, m->pf_h, m->pf_x,
-                        nullptr, nullptr, M, H, qd, H};
+                        nullptr, nullptr, M, H, qd, H, gemm_group_m()};
       L(gemm_kernel(m, "resid"), flops(M, H, qd), gemm_grid(M, H), blk, glds, g);
     }
     {  // post-attention RMSNorm + Q8_0
@@ -470,12 +470,12 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
     }
     {  // gate|up + SiLU + Q8_0 of m (layer.rs:40-89)
       PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.gu.codes, Lb.gu.scales, nullptr, nullptr,
-                        m->pf_m_q, m->pf_m_d, M, 2 * F, H, F};
+                        m->pf_m_q, m->pf_m_d, M, 2 * F, H, F, gemm_group_m()};
       L(gemm_kernel(m, "silu"), flops(M, 2 * F, H), gemm_grid(M, 2 * F), blk, glds, g);
     }
     {  // down projection + residual (layer.rs:403)
       PrefillGemmArgs g{m->pf_m_q, m->pf_m_d, Lb.down.codes, Lb.down.scales, m->pf_x, m->pf_h,
-                        nullptr, nullptr, M, H, F, H};
+                        nullptr, nullptr, M, H, F, H, gemm_group_m()};
       L(gemm_kernel(m, "resid"), flops(M, H, F), gemm_grid(M, H), blk, glds, g);
     }
   }

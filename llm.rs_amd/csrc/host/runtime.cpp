@@ -55,6 +55,17 @@ hipFunction_t kernel(const std::string& name) {
   fail(LLMRS_E_MODULE, "kernel not found in any loaded hsaco: " + name);
 }
 
+int gemm_group_m() {
+  // 4 token tiles per group: on the 8B shapes at M = 2048 this cuts the
+  // gate|up GEMM's L2 fetches 2.7x against row-major (8 is close, 2 and 16
+  // fetch 1.5x and 2.1x more than 4)
+  static const int g = [] {
+    const char* v = std::getenv("LLMRS_GEMM_GROUP");
+    return (v && *v) ? std::atoi(v) : 4;
+  }();
+  return g;
+}
+
 const char* wt_tag(int wt) {
   switch (wt) {
     case WT_Q4H: return "q4h";

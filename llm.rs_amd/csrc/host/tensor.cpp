@@ -204,7 +204,7 @@ int llmrs_matmul_transposed(const llmrs_tensor* a, const llmrs_tensor* b, llmrs_
       PrefillRowArgs r{(const float*)a->data, nullptr, xq, xd, (int)m, (int)k, 0.0f};
       launch("prefill_rows_q8", dim3((unsigned)m), dim3(kBlock), gemv_act_lds_host((int)k), s, r);
       PrefillGemmArgs g{xq, xd, (const uint8_t*)b->data, b->scales, (float*)o->data, nullptr,
-                        nullptr, nullptr, (int)m, (int)n, (int)k, (int)n};
+                        nullptr, nullptr, (int)m, (int)n, (int)k, (int)n, gemm_group_m()};
       launch(std::string("gemm_") + wt_tag(b->wt) + "_store",
              dim3((unsigned)((n + 127) / 128), (unsigned)((m + 127) / 128)), dim3(kBlock),
              gemm_lds_bytes(), s, g);

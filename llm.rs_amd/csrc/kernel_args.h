@@ -128,6 +128,12 @@ struct PrefillGemmArgs {
   int8_t* yq;            // SILU: [M][N/2] codes of m
   float* yd;             // SILU: [M][N/64] scales of m
   int M, N, K, ldy;
+  // Tile order (0 = row-major).  Workgroups reach the 8 XCDs round-robin in
+  // dispatch order; with group_m > 0 and a tile count divisible by 8, XCD x
+  // takes the x-th contiguous eighth of the tiles, walked group_m token tiles
+  // at a time, so the workgroups resident on one XCD share operand panels
+  // in its L2.
+  int group_m;
 };
 
 // Dynamic LDS of the prefill GEMM: two pipeline stages of 4 blocks, each

@@ -90,6 +90,24 @@ struct GemmOps {
 
 }  // namespace
 
+// First token and row of this workgroup's tile (PrefillGemmArgs::group_m).
+// Both steps are bijections on [0, tiles): the XCD deal when the tile count
+// is a multiple of 8, the grouped walk for any grid.
+__device__ __forceinline__ void gemm_tile(const PrefillGemmArgs& a, int& m0, int& n0) {
+  const int gx = gridDim.x, gy = gridDim.y, T = gx * gy;
+  if (a.group_m <= 0) {
+    m0 = blockIdx.y * kBM;
+    n0 = blockIdx.x * kBN;
+    return;
+  }
+  int t = blockIdx.x + blockIdx.y * gx;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  const int gsz = a.group_m * gx, g = t / gsz, fm = g * a.group_m;
+  const int gm = min(gy - fm, a.group_m), r = t - g * gsz;
+  m0 = (fm + r % gm) * kBM;
+  n0 = (r / gm) * kBN;
+}
+
 template <int WT, int EPI>
 __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds) {
   typedef GemmStage S;
@@ -97,7 +115,8 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds
   constexpr int BCH = G::BCH;
   const int lane = lane_id(), wave = wave_id(), tid = threadIdx.x;
   const int half = lane >> 5, col = lane & 31;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  int m0, n0;
+  gemm_tile(a, m0, n0);
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
   const int nb = a.K >> 5;
   const int nstage = (nb + kKB - 1) / kKB;
