@@ -670,6 +670,10 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     LLMRS_REQUIRE(c.hidden <= 32768 && c.ffn <= 32768 && c.n_heads * c.head_dim <= 32768,
                   LLMRS_E_INVALID, "GEMV input length is limited to 32768");
     LLMRS_REQUIRE(c.kv_dtype == LLMRS_F32 || c.kv_dtype == LLMRS_F16, LLMRS_E_INVALID, "kv_dtype");
+    // the attention kernels address one layer's K (or V) cache with 32-bit byte offsets
+    LLMRS_REQUIRE((double)c.n_kv_heads * c.max_seq * c.head_dim * (c.kv_dtype == LLMRS_F16 ? 2 : 4) <
+                      2147483648.0,
+                  LLMRS_E_INVALID, "one layer's K cache must stay below 2 GiB (n_kv_heads*max_seq*head_dim)");
     std::unique_ptr<llmrs_model> m(new llmrs_model());
     m->c = c;
     switch (c.weight_dtype) {
