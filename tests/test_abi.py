@@ -76,3 +76,20 @@ def test_synth_normal_and_tokens():
     t = lh.synth_tokens(20260002, 3, 512, 128256)
     assert t.min() >= 0 and t.max() < 128256 and len(set(t.tolist())) > 500
     assert np.array_equal(t, lh.synth_tokens(20260002, 3, 512, 128256))
+
+
+@pytest.mark.parametrize("field,value", [
+    ("max_seq", 1 << 20),   # 8 KV heads x 2^20 positions x 128 x 2 B: a 2 GiB K cache per layer
+    ("head_dim", 96),
+    ("n_kv_heads", 3),      # 8 query heads over 3 KV heads
+])
+def test_model_config_rejected_before_any_device_call(field, value):
+    """llmrs_model_create validates the configuration before touching a
+    device, so bad shapes fail with LLMRS_E_INVALID here, without a GPU."""
+    from llmrs_hip import DType, synthetic as syn
+    cfg = syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_heads=8, n_kv_heads=8).config(4096)
+    setattr(cfg, field, value)
+    h = C.c_void_p()
+    rc = lh.lib().llmrs_model_create(C.byref(cfg), C.byref(h))
+    assert rc == lh.E_INVALID, (rc, lh.lib().llmrs_last_error())
+    assert not h.value
