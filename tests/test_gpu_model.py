@@ -104,6 +104,8 @@ TINY = [
     syn.tiny(DType.Q8_0, DType.F16, head_dim=128, n_heads=4, n_kv_heads=1),
     syn.tiny(DType.Q8_0, DType.F32, head_dim=64, n_heads=8, n_kv_heads=8),
     syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_heads=16, n_kv_heads=2, ffn=2048),
+    # the reference's own Q4 storage (planar nibbles, f32 scales; tensor.rs:102-167)
+    syn.tiny(DType.Q4, DType.F16, head_dim=128, n_heads=8, n_kv_heads=2, ffn=1024, seed=11),
 ]
 
 
