@@ -41,7 +41,7 @@ def rng():
 
 
 def rel_close(got, want, rtol=1e-3, atol=1e-4):
-    """BASELINE per-kernel bar: |got - want| <= atol + rtol * |want| elementwise."""
+    """Per-kernel parity bar: |got - want| <= atol + rtol * |want| elementwise."""
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     err = np.abs(got - want)
