@@ -4,17 +4,22 @@ Default workload: the Llama-3-8B-shaped Q4_0 decoder with an f16 KV cache,
 a 512-token random prompt, then 256 greedy decode steps (warmup + timed).
 value = decode tok/s over the timed steps, weights resident in HBM.
 
-roofline: the dominant kernel (gate|up dequant-GEMV) - algorithmic bytes per
-launch over its mean launch duration, timed with HIP events on the model's
-stream around the gate|up GEMV of every layer launched back to back
-(llmrs_model_time_linear).  traffic: HBM bytes per launch from the committed
-rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.json), each
-counter scaled by its reading for a known 256 MiB scale_f32 pass.
+roofline: the dominant kernel (the gate|up dequant-GEMV): algorithmic bytes
+per launch over its mean launch duration inside eager decode steps, timed
+by the dispatches' own start/end timestamps (hipExtModuleLaunchKernel
+events on the model's stream) - the figure a rocprofv3 kernel trace of the
+same steps reports.  The same kernel launched back to back over every layer
+(llmrs_model_time_linear) is reported beside it.  traffic: HBM bytes per
+launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+(profiles/hbm_traffic.json), each counter scaled by its reading for a known
+256 MiB scale_f32 pass.
+prefill: the 2048-token prompt of the prefill workload through the same 8B
+model (batched prefill, int8 MFMA GEMMs), timed in the same run.
 cpu_baseline: the CPU oracle (C++ restatement of the reference CPU backend)
-on a bounded sample of the same workload, timed on this host.
+decoding at the GPU's context length on a bounded sample.
 
---workload 3: the 2048-token batched prefill of the same 8B model instead
-(prefill tok/s; roofline against the int8 MFMA peak).
+--workload 3: the 2048-token batched prefill alone (prefill tok/s; roofline
+against the int8 MFMA peak).
 --traffic-probe: the dispatches the rocprofv3 --pmc runs measure.
 """
 from __future__ import annotations
@@ -33,8 +38,25 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 METRIC = "decode tok/s (bs1, 8B-shape Q4_0) + Q4_0 GEMV HBM GB/s vs peak"
 PREFILL_METRIC = "prefill tok/s (8B-shape Q4_0, one 2048-token prompt) + GEMM MFMA utilisation"
+
+
+def metric_for(index: int, name: str) -> str:
+    """The headline metric for the 8B decode workload; the same measurement
+    named by its own workload otherwise."""
+    return METRIC if index == 2 else f"decode tok/s (bs1, {name}) + GEMV HBM GB/s vs peak"
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def log(msg: str) -> None:
@@ -52,21 +74,24 @@ def hbm_traffic(workload: str, kernel: str):
     return e["fetch_kib"] * 1024 * e["fetch_scale"] + e["write_kib"] * 1024 * e["write_scale"]
 
 
-def cpu_baseline(spec, w, seconds: float) -> dict:
-    """Oracle decode tok/s on a bounded sample: an 8-token prefix prefilled
-    (untimed), then as many decode steps as fit in about `seconds`."""
+def cpu_baseline(spec, w, context: int, seconds: float) -> dict:
+    """Oracle decode tok/s on a bounded sample at the GPU's context length:
+    the cache below `context` is filled with N(0,1) K/V rows (a decode
+    step's cost depends on the context length, not on the cached values),
+    then as many decode steps as fit in about `seconds` (at most 48)."""
     import numpy as np
 
     import oracle
-    oracle.set_threads(int(os.environ.get("ORACLE_THREADS", "0")))
-    om = oracle.OracleModel.from_spec(spec, max_seq=64)
-    om.load(w)
     from llmrs_hip import synthetic as syn
-    toks = syn.prompt(spec)[:8]
-    lg, _ = om.forward(toks, 0)
-    t = int(np.argmax(lg))
-    pos = len(toks)
-    steps, t0 = 0, time.perf_counter()
+    oracle.set_threads(int(os.environ.get("ORACLE_THREADS", str(min(16, os.cpu_count() or 1)))))
+    om = oracle.OracleModel.from_spec(spec, max_seq=context + 64)
+    om.load(w)
+    fill = syn.with_sizes(spec, prefilled=context)
+    for layer in range(spec.n_layers):
+        for g in range(spec.n_kv_heads):
+            om.kv_write(layer, g, 0, *syn.prefill_kv(fill, layer, g))
+    t = int(syn.prompt(spec)[-1])
+    pos, steps, t0 = context, 0, time.perf_counter()
     while steps < 48 and (time.perf_counter() - t0) < seconds:
         lg, _ = om.forward([t], pos)
         t = int(np.argmax(lg))
@@ -74,15 +99,17 @@ def cpu_baseline(spec, w, seconds: float) -> dict:
         steps += 1
     dt = time.perf_counter() - t0
     return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": oracle.threads(), "kind": "port",
-            "sample": f"{steps} decode steps of the same model after an 8-token prefill "
-                      f"(positions 8..{7 + steps}), oracle threads={oracle.threads()}"}
+            "cpu": cpu_model(),
+            "sample": f"{steps} decode steps of the same model at positions {context}..{context + steps - 1} "
+                      f"(the GPU's timed context; cache below {context} filled with N(0,1) K/V), "
+                      f"oracle threads={oracle.threads()}"}
 
 
 def cpu_prefill_baseline(spec, w, seconds: float) -> dict:
     """Oracle prefill tok/s on a bounded sample: one batched forward of a
     prompt prefix sized to take about `seconds`."""
     import oracle
-    oracle.set_threads(int(os.environ.get("ORACLE_THREADS", "0")))
+    oracle.set_threads(int(os.environ.get("ORACLE_THREADS", str(min(16, os.cpu_count() or 1)))))
     from llmrs_hip import synthetic as syn
     om = oracle.OracleModel.from_spec(spec, max_seq=256)
     om.load(w)
@@ -97,14 +124,67 @@ def cpu_prefill_baseline(spec, w, seconds: float) -> dict:
     om.forward(toks[:n2], 0)
     dt = time.perf_counter() - t0
     return {"value": round(n2 / dt, 3), "unit": "tok/s", "cores": oracle.threads(), "kind": "port",
+            "cpu": cpu_model(),
             "sample": f"one batched forward of the first {n2} prompt tokens of the same model, "
                       f"oracle threads={oracle.threads()}"}
 
 
+def measure_prefill(model, lh, prompt, warmup: int, steps: int, profile_steps: int, workload: str) -> dict:
+    """Batched prefill of `prompt` from position 0: tok/s over `steps` whole
+    prompts (each rewrites the KV cache), per-kernel rates from dispatch
+    timestamps, GEMM MFMA utilisation against the int8 and fp16 peaks."""
+    M = len(prompt)
+    for _ in range(warmup):
+        model.forward(prompt, 0, logits=False)
+    lh.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        model.forward(prompt, 0, logits=False)
+        log(f"prefill {i + 1}/{steps}")
+    lh.sync()
+    dt = time.perf_counter() - t0
+    value = steps * M / dt
+    log(f"prefill: {value:.1f} tok/s ({dt / steps * 1e3:.2f} ms per {M}-token prompt)")
+    per = defaultdict(lambda: [0.0, 0.0, 0])
+    for _ in range(profile_steps):
+        for k in model.profile_prefill(prompt):
+            e = per[k.name]
+            e[0] += k.ms
+            e[1] += k.bytes
+            e[2] += 1
+    P = max(1, profile_steps)
+    tot = sum(ms for ms, _, _ in per.values())
+    kernels = {}
+    for name, (ms, wk, n) in sorted(per.items(), key=lambda kv: -kv[1][0]):
+        avg_s = ms / n / 1e3
+        flop = name.startswith("gemm_") or name.startswith("attn_")
+        kernels[name] = {"launches": n // P, "avg_us": round(avg_s * 1e6, 2), "share": round(ms / tot, 4),
+                         ("tflop_s" if flop else "gb_s"): round(wk / n / avg_s / (1e12 if flop else 1e9), 1)}
+    gemm = [n for n in per if n.startswith("gemm_")]
+    g_ms = sum(per[n][0] for n in gemm)
+    g_fl = sum(per[n][1] for n in gemm)
+    dom = max(gemm, key=lambda n: per[n][0])
+    ms, fl, n = per[dom]
+    achieved = fl / n / (ms / n / 1e3) / 1e12
+    traffic = hbm_traffic(workload, dom)
+    gemm_rate = g_fl / (g_ms / 1e3) / 1e12
+    return {
+        "value": value, "ms": dt / steps * 1e3, "prompt": M,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1),
+                     "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
+                     "flops_per_launch": round(fl / n), "avg_us": round(ms / n * 1e3, 2),
+                     "traffic": None if traffic is None else round(traffic),
+                     "traffic_source": "profiles/hbm_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
+        "gemm_top_s": round(gemm_rate, 1),
+        "gemm_frac_int8_peak": round(gemm_rate / INT8_PEAK_TOPS, 4),
+        "gemm_frac_fp16_peak": round(gemm_rate / FP16_PEAK_TFLOPS, 4),
+        "gemm_share_of_prefill": round(g_ms / tot, 4),
+        "kernels": kernels,
+    }
+
+
 def bench_prefill(args, lh, syn) -> int:
-    """Batched prefill of the 2048-token prompt: tok/s over `steps` whole
-    prompts (each rewrites the KV cache from position 0), per-kernel FLOP
-    rates from HIP events, GEMM MFMA utilisation against the int8 peak."""
+    """The 2048-token prefill workload alone (one JSON line)."""
     spec = syn.WORKLOADS[args.workload]
     if args.prompt:
         spec = syn.with_sizes(spec, prompt=args.prompt, decode=0)
@@ -120,64 +200,28 @@ def bench_prefill(args, lh, syn) -> int:
         w = None
         syn.stream_model(model, spec)
     log(f"workload {spec.name}: weights uploaded in {time.perf_counter() - t0:.1f}s")
-    prompt = syn.prompt(spec)
-    for i in range(args.warmup):
-        model.forward(prompt, 0, logits=False)
-    lh.sync()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        model.forward(prompt, 0, logits=False)
-        log(f"prefill {i + 1}/{args.steps}")
-    lh.sync()
-    dt = time.perf_counter() - t0
-    value = args.steps * M / dt
-    log(f"prefill: {value:.1f} tok/s ({dt / args.steps * 1e3:.2f} ms per {M}-token prompt)")
-
-    per = defaultdict(lambda: [0.0, 0.0, 0])
-    for _ in range(args.profile_steps):
-        for k in model.profile_prefill(prompt):
-            e = per[k.name]
-            e[0] += k.ms
-            e[1] += k.bytes
-            e[2] += 1
-    P = max(1, args.profile_steps)
-    tot = sum(ms for ms, _, _ in per.values())
-    kernels = {}
-    for name, (ms, wk, n) in sorted(per.items(), key=lambda kv: -kv[1][0]):
-        avg_s = ms / n / 1e3
-        flop = name.startswith("gemm_") or name.startswith("attn_")
-        kernels[name] = {"launches": n // P, "avg_us": round(avg_s * 1e6, 2), "share": round(ms / tot, 4),
-                         ("tflop_s" if flop else "gb_s"): round(wk / n / avg_s / (1e12 if flop else 1e9), 1)}
-    gemm = [n for n in per if n.startswith("gemm_")]
-    g_ms = sum(per[n][0] for n in gemm)
-    g_fl = sum(per[n][1] for n in gemm)
-    dom = max(gemm, key=lambda n: per[n][0])
-    ms, fl, n = per[dom]
-    achieved = fl / n / (ms / n / 1e3) / 1e12
-    traffic = hbm_traffic(f"{spec.name} prefill", dom)
-
+    pf = measure_prefill(model, lh, syn.prompt(spec), args.warmup, args.steps, args.profile_steps,
+                         f"{spec.name} prefill")
     cpu = None
     if keep:
         log("timing the CPU oracle prefill on a bounded sample ...")
         cpu = cpu_prefill_baseline(spec, w, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads")
     line = {
-        "metric": PREFILL_METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 3),
+        "metric": PREFILL_METRIC, "value": round(pf["value"], 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(pf["ms"], 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8 MFMA (q4_0 x q8_0, exact block sums) + f32", "data": "synthetic",
         "config": {"workload": f"{spec.name} prefill", "layers": spec.n_layers, "hidden": spec.hidden,
                    "heads": spec.n_heads, "kv_heads": spec.n_kv_heads, "head_dim": spec.head_dim,
                    "ffn": spec.ffn, "vocab": spec.vocab, "weights": spec.weight.name,
                    "kv_cache": spec.kv.name.lower(), "prompt": M, "batch": 1},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 1),
-                     "peak": INT8_PEAK_TOPS, "unit": "TOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
-                     "flops_per_launch": round(fl / n), "avg_us": round(ms / n * 1e3, 2),
-                     "traffic": None if traffic is None else round(traffic)},
-        "gemm_mfma_utilisation": round(g_fl / (g_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
-        "gemm_share_of_prefill": round(g_ms / tot, 4),
+        "roofline": pf["roofline"],
+        "gemm_mfma_utilisation": pf["gemm_frac_int8_peak"],
+        "gemm_frac_fp16_peak": pf["gemm_frac_fp16_peak"],
+        "gemm_share_of_prefill": pf["gemm_share_of_prefill"],
         "cpu_baseline": cpu,
-        "kernels": kernels,
+        "kernels": pf["kernels"],
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -220,6 +264,8 @@ def main() -> int:
     ap.add_argument("--workload", type=int, default=2)
     ap.add_argument("--prompt", type=int, default=None, help="override the prompt length")
     ap.add_argument("--profile-steps", type=int, default=4)
+    ap.add_argument("--prefill-steps", type=int, default=3,
+                    help="timed 2048-token prefills in the decode run (0 = none)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -230,8 +276,6 @@ def main() -> int:
         print("bench.py: this backend runs on one GPU; multi-GPU figures are not produced "
               "(run with --gpus 1)", file=sys.stderr)
         return 2
-
-    import numpy as np
 
     import llmrs_hip as lh
     from llmrs_hip import synthetic as syn
@@ -249,8 +293,12 @@ def main() -> int:
     n_prompt = args.prompt or base.prompt
     spec = syn.with_sizes(base, prompt=n_prompt, decode=args.warmup + args.steps)
     lh.init(0)
-    max_seq = spec.max_seq + args.profile_steps + 1
     pre = spec.prefilled  # cache positions filled with N(0,1) K/V before the prompt
+    # The 8B decode run also measures the 2048-token prefill workload (its
+    # own model, so the decode model keeps the attention layout of its
+    # context length).
+    pf_spec = syn.WORKLOADS[3] if args.workload == 2 and args.prefill_steps > 0 else None
+    max_seq = spec.max_seq + args.profile_steps + 1
     log(f"workload {spec.name}: pre-filled {pre}, prompt {n_prompt}, decode {args.warmup}+{args.steps}, "
         f"max_seq {max_seq}")
 
@@ -283,10 +331,12 @@ def main() -> int:
 
     model.decode_steps(args.warmup)
     lh.sync()
+    # the benchmark contract brackets the timed steps with a device-wide
+    # synchronisation through torch as well as the library's own
     try:
         import torch
         sync_all = torch.cuda.synchronize if torch.cuda.is_available() else lh.sync
-    except Exception:  # torch is only the device-wide barrier here
+    except Exception:
         sync_all = lh.sync
     sync_all()
     lh.sync()
@@ -295,12 +345,13 @@ def main() -> int:
     lh.sync()
     sync_all()
     dt = time.perf_counter() - t0
-    toks = model.tokens(pre + n_prompt + args.warmup + args.steps + 1)[pre:]
+    first = pre + n_prompt + args.warmup  # position of the first timed step
+    toks = model.tokens(first + args.steps + 1)[pre:]
     assert toks.min() >= 0 and toks.max() < spec.vocab
     value = args.steps / dt
-    log(f"decode: {value:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token)")
+    log(f"decode: {value:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token), positions {first}..{first + args.steps - 1}")
 
-    # Per-kernel timing with HIP events on the model's stream (eager steps).
+    # Per-kernel durations inside eager decode steps (dispatch timestamps).
     per = defaultdict(lambda: [0.0, 0.0, 0])
     for _ in range(args.profile_steps):
         for k in model.profile_step():
@@ -318,41 +369,65 @@ def main() -> int:
     tot = sum(ms for ms, _, _ in per.values())
     for name, (ms, _, _) in per.items():
         kernels[name]["share"] = round(ms / tot, 4)
-    # The dominant kernel: the gate|up GEMV, timed back to back over all layers.
+    # The dominant kernel: the gate|up GEMV.
     dom = next(n for n in kernels if n.startswith("gemv_") and "_norm_silu_" in n)
-    gu_us, gu_bytes = model.time_linear(lh.W_GATE, reps=4)
-    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    ms, by, n = per[dom]
+    dom_us, dom_bytes = ms / n * 1e3, by / n
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    b2b_us, _ = model.time_linear(lh.W_GATE, reps=4)
     traffic = hbm_traffic(f"{spec.name} decode", dom)
-    log(f"{dom}: {gu_us:.2f} us per launch, {achieved:.0f} GB/s; HBM traffic per launch "
-        f"{traffic if traffic is None else round(traffic / 1e6, 2)} MB")
+    log(f"{dom}: {dom_us:.2f} us per launch in decode steps ({achieved:.0f} GB/s), {b2b_us:.2f} us back to "
+        f"back; HBM traffic per launch {traffic if traffic is None else round(traffic / 1e6, 2)} MB")
     wbytes = model.weight_bytes()
     roof_tok_s = HBM_PEAK_GBS * 1e9 / wbytes
+
+    prefill = None
+    if pf_spec:
+        t0 = time.perf_counter()
+        pf_model = lh.HipModel(pf_spec.config(pf_spec.prompt))
+        syn.stream_model(pf_model, pf_spec)
+        log(f"2048-token prefill model uploaded in {time.perf_counter() - t0:.1f}s")
+        pf = measure_prefill(pf_model, lh, syn.prompt(pf_spec), 1, args.prefill_steps, 2,
+                             f"{pf_spec.name} prefill")
+        pf_model.close()
+        prefill = {"workload": f"{pf_spec.name} prefill",
+                   "tok_s": round(pf["value"], 1), "ms": round(pf["ms"], 3), "prompt": pf["prompt"],
+                   "steps": args.prefill_steps, "roofline": pf["roofline"],
+                   "gemm_top_s": pf["gemm_top_s"], "gemm_frac_int8_peak": pf["gemm_frac_int8_peak"],
+                   "gemm_frac_fp16_peak": pf["gemm_frac_fp16_peak"],
+                   "gemm_share_of_prefill": pf["gemm_share_of_prefill"]}
 
     cpu = None
     if keep:
         log("timing the CPU oracle on a bounded sample ...")
-        cpu = cpu_baseline(spec, w, args.cpu_seconds)
+        cpu = cpu_baseline(spec, w, first, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads")
 
     line = {
-        "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "metric": metric_for(args.workload, spec.name), "value": round(value, 2), "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8 dot4 (q4_0 x q8_0) + f32", "data": "synthetic",
         "config": {"workload": f"{spec.name} decode", "layers": spec.n_layers, "hidden": spec.hidden,
                    "heads": spec.n_heads, "kv_heads": spec.n_kv_heads, "head_dim": spec.head_dim,
                    "ffn": spec.ffn, "vocab": spec.vocab, "weights": spec.weight.name,
                    "kv_cache": spec.kv.name.lower(), "prefilled_positions": pre, "prompt": n_prompt,
-                   "decode_steps": args.warmup + args.steps, "batch": 1},
+                   "decode_steps": args.warmup + args.steps, "timed_positions": [first, first + args.steps - 1],
+                   "batch": 1},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "bytes_per_launch": round(gu_bytes), "avg_us": round(gu_us, 2),
-                     "traffic": None if traffic is None else round(traffic)},
+                     "bytes_per_launch": round(dom_bytes), "avg_us": round(dom_us, 2),
+                     "timing": "mean duration of its launches inside eager decode steps (dispatch timestamps)",
+                     "back_to_back_us": round(b2b_us, 2),
+                     "back_to_back_frac": round(dom_bytes / (b2b_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None if traffic is None else round(traffic),
+                     "traffic_source": "profiles/hbm_traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
         "cpu_baseline": cpu,
         "decode_roofline_tok_s": round(roof_tok_s, 1),
         "frac_of_decode_roofline": round(value / roof_tok_s, 4),
         "weight_gb_per_token": round(wbytes / 1e9, 4),
         "prompt_ms": round(prompt_s * 1e3, 1),
+        "prefill": prefill,
         "kernels": kernels,
     }
     print(json.dumps(line), flush=True)

@@ -242,13 +242,42 @@ int llmrs_model_time_linear(llmrs_model* m, int slot, int reps, double* us_per_l
 int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
                                 size_t start_pos, char* names, float* ms,
                                 double* work, int cap);
-/* Profiling (no reference counterpart): one decode step in which `layer`'s
- * attention + O and gate|up + down launches record per-workgroup stamps.
- * us[0..3] = workgroups of the attention, O, gate|up and down roles, then 4
- * values per workgroup of the two launches in turn (start, producer wait
- * released, own work done, end) in us from that launch's earliest start
- * (0 = not recorded).  Returns the count written. */
-int llmrs_model_profile_layer(llmrs_model* m, int layer, double* us, int cap);
+/* ---- test probes (no reference counterpart) ------------------------------
+ * One layer's kernels run on inputs given by the host, with every
+ * intermediate the kernels produce copied back, so each kernel can be held to
+ * the reference arithmetic on its own inputs.  Every pointer of the probe
+ * may be NULL (not copied).  Decode rows are 1, prefill rows n. */
+typedef struct {
+  float* qkv;     /* [rows][(n_heads+2*n_kv_heads)*head_dim] Q|K|V before RoPE */
+  int8_t* xq;     /* [rows][hidden] Q8_0 codes of RMSNorm(x) (Q|K|V input) */
+  float* xd;      /* [rows][hidden/32] their scales */
+  float* ctx;     /* [rows][n_heads*head_dim] attention output */
+  int8_t* ctx_q;  /* [rows][n_heads*head_dim] its Q8_0 codes (O input) */
+  float* ctx_d;   /* [rows][n_heads*head_dim/32] */
+  float* h;       /* [rows][hidden] x + O.ctx (layer.rs:386) */
+  int8_t* hq;     /* [rows][hidden] Q8_0 codes of RMSNorm(h) (gate|up input) */
+  float* hd;      /* [rows][hidden/32] */
+  float* m;       /* [rows][ffn] silu(gate)*up (layer.rs:75-79) */
+  int8_t* m_q;    /* [rows][ffn] its Q8_0 codes (down input) */
+  float* m_d;     /* [rows][ffn/32] */
+  float* out;     /* [rows][hidden] h + down.m (layer.rs:403) */
+} llmrs_layer_probe;
+/* One decode step of `layer` at position `pos` on the row x[hidden]: the
+ * Q|K|V GEMV, the decode attention (which appends K/V at pos; the cache below
+ * pos is taken as filled), O, gate|up and down GEMVs, as in the decode loop. */
+int llmrs_model_probe_decode_layer(llmrs_model* m, int layer, size_t pos,
+                                   const float* x, llmrs_layer_probe* out);
+/* Final RMSNorm + lm_head GEMV + greedy argmax of the row x[hidden]: the
+ * prologue's Q8_0 operand (xq[hidden], xd[hidden/32]), the logits and the
+ * argmax (each may be NULL). */
+int llmrs_model_probe_head(llmrs_model* m, const float* x, int8_t* xq,
+                           float* xd, float* logits, int32_t* next);
+/* The batched prefill kernels of `layer` on rows x[n][hidden] at positions
+ * [start_pos, start_pos+n), n at most one prefill chunk. */
+int llmrs_model_probe_prefill_layer(llmrs_model* m, int layer, size_t start_pos,
+                                    size_t n, const float* x,
+                                    llmrs_layer_probe* out);
+
 /* Algorithmic weight bytes streamed per decode token (all linear weights). */
 double llmrs_model_weight_bytes(const llmrs_model* m);
 

@@ -13,6 +13,17 @@
 
 #include "llmrs_hip.h"
 
+// From libamdhip64 (declared in hip/hip_ext.h, whose C++ templates need the
+// HIP compiler): a module launch whose start and stop events are recorded by
+// the dispatch itself.
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX,
+                                               uint32_t globalWorkSizeY, uint32_t globalWorkSizeZ,
+                                               uint32_t localWorkSizeX, uint32_t localWorkSizeY,
+                                               uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void** kernelParams, void** extra,
+                                               hipEvent_t startEvent, hipEvent_t stopEvent,
+                                               uint32_t flags);
+
 namespace llmrs {
 
 // An error carried up to the C ABI, where it becomes a return code plus the
@@ -68,6 +79,19 @@ void launch(const std::string& name, dim3 grid, dim3 block, size_t shmem, hipStr
   void* params[] = {const_cast<Args*>(&args)};
   LLMRS_HIP(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
                                   (unsigned)shmem, stream, params, nullptr));
+}
+
+// A launch whose two events carry the dispatch packet's own start and end
+// timestamps (hipExtModuleLaunchKernel), so their elapsed time is the
+// kernel's execution time, as a kernel trace reports it, without the
+// event packets' own latency.
+template <class Args>
+void launch_timed(const std::string& name, dim3 grid, dim3 block, size_t shmem, hipStream_t stream,
+                  const Args& args, hipEvent_t start, hipEvent_t stop) {
+  hipFunction_t f = kernel(name);
+  void* params[] = {const_cast<Args*>(&args)};
+  LLMRS_HIP(hipExtModuleLaunchKernel(f, grid.x * block.x, grid.y * block.y, grid.z * block.z, block.x,
+                                     block.y, block.z, shmem, stream, params, nullptr, start, stop, 0));
 }
 
 // Runs `fn` and converts exceptions into a C return code.

@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <memory>
 #include <tuple>
 
@@ -72,16 +73,7 @@ struct llmrs_model {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   bool graph_failed = false;
-  int* bar_err = nullptr;            // set by a cross-workgroup wait that exceeded its spin limit
   int host_n_prompt = 0;
-  // attention + O and gate|up + down launches (layer.hip)
-  std::string ao_name, mlp_name;
-  unsigned ao_grid = 0, mlp_grid = 0;  // 0: one launch per GEMV / attention instead
-  size_t ao_lds = 0, mlp_lds = 0;
-  int lk_roles[4] = {0, 0, 0, 0};      // workgroups: attention, O, gate|up, down
-  size_t lk_flag_words = 0;          // completion flags per layer
-  unsigned* lflags = nullptr;        // [n_layers][lk_flag_words]
-  unsigned* epoch = nullptr;         // decode-step counter (embed_gather bumps it)
   // batched prompt (prefill) buffers for chunks of up to pf_cap rows,
   // allocated on first use
   int pf_cap = 0;
@@ -128,23 +120,22 @@ size_t kv_layer_elems(const llmrs_model* m) {
 }
 
 // Records a (name, algorithmic bytes, start, end) tuple per launch when
-// profiling; otherwise a plain launch.
+// profiling - the events take the dispatch's own start and end timestamps -
+// otherwise a plain launch.
 struct Launcher {
   hipStream_t s;
   std::vector<std::tuple<std::string, double, hipEvent_t, hipEvent_t>>* rec = nullptr;
   template <class A>
   void operator()(const std::string& name, double bytes, dim3 g, dim3 b, size_t lds, const A& args) {
+    if (!rec) {
+      launch(name, g, b, lds, s, args);
+      return;
+    }
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (rec) {
-      LLMRS_HIP(hipEventCreate(&e0));
-      LLMRS_HIP(hipEventCreate(&e1));
-      LLMRS_HIP(hipEventRecord(e0, s));
-    }
-    launch(name, g, b, lds, s, args);
-    if (rec) {
-      LLMRS_HIP(hipEventRecord(e1, s));
-      rec->emplace_back(name, bytes, e0, e1);
-    }
+    LLMRS_HIP(hipEventCreate(&e0));
+    LLMRS_HIP(hipEventCreate(&e1));
+    rec->emplace_back(name, bytes, e0, e1);
+    launch_timed(name, g, b, lds, s, args, e0, e1);
   }
 };
 
@@ -153,7 +144,8 @@ double linear_weight_bytes(const llmrs_model* m, const DevLinear& L) {
   return (double)L.n * nb * (block_code_bytes(m->wt) + block_scale_bytes(m->wt));
 }
 
-void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits);
+void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_xq = nullptr,
+                  float* probe_xd = nullptr);
 
 // The decode-attention kernel of this model (attention.hip).
 std::string attn_kernel(const llmrs_model* m) {
@@ -164,7 +156,10 @@ std::string attn_kernel(const llmrs_model* m) {
 // The decode GEMV of one linear slot of layer li (LLMRS_W_Q = the stacked
 // Q|K|V rows, LLMRS_W_O, LLMRS_W_GATE = gate|up, LLMRS_W_DOWN) with its fused
 // prologue and epilogue, on the decode activation buffers.
-void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot) {
+// `probe_xq` / `probe_xd` (test probes, may be null) receive the Q8_0
+// operand the GEMV's prologue built.
+void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot, int8_t* probe_xq = nullptr,
+                    float* probe_xd = nullptr) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, F = c.ffn;
   const int cus = ctx().num_cus;
@@ -226,109 +221,53 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot) {
     default:
       fail(LLMRS_E_INVALID, "enqueue_linear: slot must be Q, O, GATE or DOWN");
   }
+  g.probe_xq = probe_xq;
+  g.probe_xd = probe_xd;
   const GemvPlan p = gemv_plan(m->wt, kind, g.n, g.k, cus);
   L(p.name, bytes, dim3(p.grid), dim3(256), p.lds, g);
 }
 
-// Attention + O, then gate|up + down, of layer li (layer.hip); `ts` =
-// per-workgroup profiling stamps of both launches ([ao_grid + mlp_grid][4])
-// or null.
-void enqueue_layer_tail(llmrs_model* m, Launcher& L, int li, unsigned long long* ts = nullptr) {
+// Decode attention of layer li at the device position: RoPE of q and the new
+// k, K/V append, attention over the cache, ctx as f32 and Q8_0.
+void enqueue_attention(llmrs_model* m, Launcher& L, int li) {
   const llmrs_model_config& c = m->c;
-  const LayerBufs& B = m->layers[li];
-  LayerArgs a{};
-  a.w = LayerDesc{B.qkv.codes, B.qkv.scales, B.o.codes, B.o.scales, B.gu.codes, B.gu.scales,
-                  B.down.codes, B.down.scales, B.norm[0], B.norm[1], B.kc, B.vc};
-  a.x = m->x;
+  const int hd = c.head_dim, nkv = c.n_kv_heads;
+  LayerBufs& Lb = m->layers[li];
+  AttnArgs a{};
   a.qkv = m->qkv;
-  a.h = m->h;
+  a.pos_ptr = m->pos;
+  a.kc = (uint8_t*)Lb.kc;
+  a.vc = (uint8_t*)Lb.vc;
+  a.rope_cos = m->rope_cos;
+  a.rope_sin = m->rope_sin;
+  a.part_o = m->part_o;
+  a.part_ml = m->part_ml;
+  a.counters = m->counters + (size_t)li * nkv * llmrs::kTicketStride;
   a.ctx = m->ctxv;
   a.ctx_q = m->ctx_q;
   a.ctx_d = m->ctx_d;
-  a.mf = m->mf;
-  a.m_q = m->m_q;
-  a.m_d = m->m_d;
-  a.rope_cos = m->rope_cos;
-  a.rope_sin = m->rope_sin;
-  a.pos_ptr = m->pos;
-  a.part_o = m->part_o;
-  a.part_ml = m->part_ml;
-  a.counters = m->counters + (size_t)li * c.n_kv_heads * llmrs::kTicketStride;
-  a.flags = m->lflags + (size_t)li * m->lk_flag_words;
-  a.epoch = m->epoch;
-  a.err = m->bar_err;
-  a.hidden = c.hidden;
-  a.nq = c.n_heads;
-  a.nkv = c.n_kv_heads;
-  a.ffn = c.ffn;
   a.max_seq = c.max_seq;
-  a.qkv_rows = m->qkv_rows;
+  a.nq = c.n_heads;
+  a.nkv = nkv;
   a.nsplit = m->nsplit;
-  a.eps = c.rms_eps;
-  a.attn_scale = 1.0f / std::sqrt((float)c.head_dim);  // layer.rs:258
-  a.n_attn = m->lk_roles[0];
-  a.n_o = m->lk_roles[1];
-  a.n_gu = m->lk_roles[2];
-  a.n_down = m->lk_roles[3];
-  a.ts = ts;
-  const double kvb = 2.0 * c.n_kv_heads * (double)(m->host_pos + 1) * c.head_dim * kv_elem_bytes(m);
-  L(m->ao_name, linear_weight_bytes(m, B.o) + kvb, dim3(m->ao_grid), dim3(256), m->ao_lds, a);
-  a.ts = ts ? ts + 4 * (size_t)m->ao_grid : nullptr;
-  L(m->mlp_name, linear_weight_bytes(m, B.gu) + linear_weight_bytes(m, B.down), dim3(m->mlp_grid),
-    dim3(256), m->mlp_lds, a);
+  a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
+  const double kvb = 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
+  L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(256 * m->attn_streams), 0, a);
 }
 
 void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
   const llmrs_model_config& c = m->c;
-  const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
+  const int H = c.hidden;
 
-  EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, H, c.vocab, m->epoch};
+  EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, H, c.vocab};
   L("embed_gather", 8.0 * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
 
-  if (m->ao_grid) {
-    for (int li = 0; li < c.n_layers; ++li) {
-      if (trace_dev)
-        LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)li * H, m->x, H * sizeof(float),
-                                 hipMemcpyDeviceToDevice, L.s));
-      enqueue_linear(m, L, li, LLMRS_W_Q);
-      enqueue_layer_tail(m, L, li);
-    }
-    if (trace_dev)
-      LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)c.n_layers * H, m->x, H * sizeof(float),
-                               hipMemcpyDeviceToDevice, L.s));
-    enqueue_head(m, L, write_logits);
-    return;
-  }
-
-  const float scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
   for (int li = 0; li < c.n_layers; ++li) {
-    LayerBufs& Lb = m->layers[li];
     if (trace_dev)
       LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)li * H, m->x, H * sizeof(float),
                                hipMemcpyDeviceToDevice, L.s));
     enqueue_linear(m, L, li, LLMRS_W_Q);
-    {  // attention
-      AttnArgs a{};
-      a.qkv = m->qkv;
-      a.pos_ptr = m->pos;
-      a.kc = (uint8_t*)Lb.kc;
-      a.vc = (uint8_t*)Lb.vc;
-      a.rope_cos = m->rope_cos;
-      a.rope_sin = m->rope_sin;
-      a.part_o = m->part_o;
-      a.part_ml = m->part_ml;
-      a.counters = m->counters + (size_t)li * nkv * llmrs::kTicketStride;
-      a.ctx = m->ctxv;
-      a.ctx_q = m->ctx_q;
-      a.ctx_d = m->ctx_d;
-      a.max_seq = c.max_seq;
-      a.nq = nq;
-      a.nkv = nkv;
-      a.nsplit = m->nsplit;
-      a.scale = scale;
-      const double kvb = 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
-      L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(256 * m->attn_streams), 0, a);
-    }
+    enqueue_attention(m, L, li);
     enqueue_linear(m, L, li, LLMRS_W_O);
     enqueue_linear(m, L, li, LLMRS_W_GATE);
     enqueue_linear(m, L, li, LLMRS_W_DOWN);
@@ -341,7 +280,7 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
 
 // Final RMSNorm + lm_head GEMV of the row in m->x, then the greedy step
 // bookkeeping at the device position (model.rs:39-47, main.rs:185-190).
-void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits) {
+void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_xq, float* probe_xd) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden;
   const int cus = ctx().num_cus;
@@ -357,6 +296,8 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits) {
     g.y = write_logits ? m->logits : nullptr;
     g.part_val = m->part_val;
     g.part_idx = m->part_idx;
+    g.probe_xq = probe_xq;
+    g.probe_xd = probe_xd;
     const GemvPlan p = gemv_plan(m->wt, "norm_argmax", g.n, g.k, cus);
     LLMRS_REQUIRE((int)p.grid == m->lm_grid, LLMRS_E_INVALID, "lm_head grid changed since model creation");
     L(p.name, linear_weight_bytes(m, m->lm_head) + 8.0 * H, dim3(p.grid), dim3(256), p.lds, g);
@@ -400,29 +341,31 @@ std::string gemm_kernel(const llmrs_model* m, const char* epi) {
 
 dim3 gemm_grid(int M, int N) { return dim3((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128)); }
 
-// One chunk of M <= pf_cap rows at positions [start, start+M): embeddings,
-// every layer, and (head) the lm_head of the last row with the greedy step
-// at the device position.  The recorded figure per launch is its FLOPs for
-// the GEMMs and attention, bytes for the rest.  trace_dev, when set, is
-// [M][n_layers+1][hidden].
-void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head, bool write_logits,
-                     float* trace_dev) {
+// Device buffers a test probe adds to one prefill layer: ctx and the SwiGLU
+// product m as f32 (the production path keeps only their Q8_0 codes).
+struct PrefillProbe {
+  float* ctx = nullptr;  // [M][nq*hd]
+  float* mf = nullptr;   // [M][ffn]
+  std::function<void(int)> after;  // called after stage s (0..6) has been enqueued
+};
+
+// Layer li of one chunk of M rows at positions [start, start+M), in place on
+// pf_x (the residual stream).  Stages: 0 RMSNorm+Q8, 1 Q|K|V GEMM, 2 RoPE +
+// K/V append, 3 causal attention, 4 O GEMM + residual, 5 RMSNorm+Q8,
+// 6 gate|up GEMM + SwiGLU + Q8, 7 down GEMM + residual.  The recorded figure
+// per launch is its FLOPs for the GEMMs and attention, bytes for the rest.
+void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, int M,
+                           const PrefillProbe* probe = nullptr) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
   const int qd = nq * hd, QR = m->qkv_rows;
   const bool kv16 = c.kv_dtype == LLMRS_F16;
   const dim3 blk(256);
-  auto trace = [&](int li) {
-    if (trace_dev)
-      LLMRS_HIP(hipMemcpy2DAsync(trace_dev + (size_t)li * H, (size_t)(c.n_layers + 1) * H * sizeof(float),
-                                 m->pf_x, H * sizeof(float), H * sizeof(float), M,
-                                 hipMemcpyDeviceToDevice, L.s));
-  };
   auto flops = [](double a, double b, double k) { return 2.0 * a * b * k; };
+  auto after = [&](int stage) {
+    if (probe && probe->after) probe->after(stage);
+  };
   const size_t glds = gemm_lds_bytes();
-
-  EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab, nullptr};
-  L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), blk, 0, e);
   const float scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
   // f16 caches use the matrix-core kernel (LLMRS_PREFILL_ATTN=valu selects the
   // vector kernel, which also serves f32 caches)
@@ -432,52 +375,79 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
                                      : "attn_prefill_hd" + std::to_string(hd) + (kv16 ? "_f16" : "_f32");
   // causal score and P.V products over the chunk
   const double attn_flops = 4.0 * nq * hd * ((double)M * start + (double)M * (M + 1) / 2.0);
+  LayerBufs& Lb = m->layers[li];
+  {  // RMSNorm + Q8_0 of each row (layer.rs:378; cpu.rs:90-93)
+    PrefillRowArgs r{m->pf_x, Lb.norm[0], m->pf_aq, m->pf_ad, M, H, c.rms_eps};
+    L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
+  }
+  after(0);
+  {  // Q|K|V
+    PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.qkv.codes, Lb.qkv.scales, m->pf_qkv, nullptr,
+                      nullptr, nullptr, M, QR, H, QR, gemm_group_m()};
+    L(gemm_kernel(m, "store"), flops(M, QR, H), gemm_grid(M, QR), blk, glds, g);
+  }
+  after(1);
+  {  // RoPE + K/V append
+    PrefillRopeArgs r{m->pf_qkv, m->pf_q, Lb.kc, Lb.vc, m->rope_cos, m->rope_sin, M, nq, nkv, hd,
+                      c.max_seq, (int)start, QR, kv16 ? 1 : 0};
+    const long total = (long)M * (nq + 2 * nkv) * (hd / 2);
+    const unsigned grid = (unsigned)std::min<long>((total + 255) / 256, 8192);
+    L("prefill_rope_kv", 4.0 * QR * M * 2, dim3(grid), blk, 0, r);
+  }
+  after(2);
+  {  // causal attention
+    PrefillAttnArgs a{m->pf_q, Lb.kc, Lb.vc, probe ? probe->ctx : nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq,
+                      nkv, c.max_seq, (int)start, scale};
+    if (mfma_attn)
+      L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nkv), dim3(512), 0, a);
+    else
+      L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nq), blk, 0, a);
+  }
+  after(3);
+  {  // O projection + residual (layer.rs:386)
+    PrefillGemmArgs g{m->pf_ctx_q, m->pf_ctx_d, Lb.o.codes, Lb.o.scales, m->pf_h, m->pf_x,
+                      nullptr, nullptr, M, H, qd, H, gemm_group_m()};
+    L(gemm_kernel(m, "resid"), flops(M, H, qd), gemm_grid(M, H), blk, glds, g);
+  }
+  after(4);
+  {  // post-attention RMSNorm + Q8_0
+    PrefillRowArgs r{m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, M, H, c.rms_eps};
+    L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
+  }
+  after(5);
+  {  // gate|up + SiLU + Q8_0 of m (layer.rs:40-89)
+    PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.gu.codes, Lb.gu.scales, probe ? probe->mf : nullptr, nullptr,
+                      m->pf_m_q, m->pf_m_d, M, 2 * F, H, F, gemm_group_m()};
+    L(gemm_kernel(m, "silu"), flops(M, 2 * F, H), gemm_grid(M, 2 * F), blk, glds, g);
+  }
+  after(6);
+  {  // down projection + residual (layer.rs:403)
+    PrefillGemmArgs g{m->pf_m_q, m->pf_m_d, Lb.down.codes, Lb.down.scales, m->pf_x, m->pf_h,
+                      nullptr, nullptr, M, H, F, H, gemm_group_m()};
+    L(gemm_kernel(m, "resid"), flops(M, H, F), gemm_grid(M, H), blk, glds, g);
+  }
+  after(7);
+}
+
+// One chunk of M <= pf_cap rows at positions [start, start+M): embeddings,
+// every layer, and (head) the lm_head of the last row with the greedy step
+// at the device position.  trace_dev, when set, is
+// [M][n_layers+1][hidden].
+void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head, bool write_logits,
+                     float* trace_dev) {
+  const llmrs_model_config& c = m->c;
+  const int H = c.hidden;
+  auto trace = [&](int li) {
+    if (trace_dev)
+      LLMRS_HIP(hipMemcpy2DAsync(trace_dev + (size_t)li * H, (size_t)(c.n_layers + 1) * H * sizeof(float),
+                                 m->pf_x, H * sizeof(float), H * sizeof(float), M,
+                                 hipMemcpyDeviceToDevice, L.s));
+  };
+  EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab};
+  L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), dim3(256), 0, e);
   for (int li = 0; li < c.n_layers; ++li) {
-    LayerBufs& Lb = m->layers[li];
     trace(li);
-    {  // RMSNorm + Q8_0 of each row (layer.rs:378; cpu.rs:90-93)
-      PrefillRowArgs r{m->pf_x, Lb.norm[0], m->pf_aq, m->pf_ad, M, H, c.rms_eps};
-      L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
-    }
-    {  // Q|K|V
-      PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.qkv.codes, Lb.qkv.scales, m->pf_qkv, nullptr,
-                        nullptr, nullptr, M, QR, H, QR, gemm_group_m()};
-      L(gemm_kernel(m, "store"), flops(M, QR, H), gemm_grid(M, QR), blk, glds, g);
-    }
-    {  // RoPE + K/V append
-      PrefillRopeArgs r{m->pf_qkv, m->pf_q, Lb.kc, Lb.vc, m->rope_cos, m->rope_sin, M, nq, nkv, hd,
-                        c.max_seq, (int)start, QR, kv16 ? 1 : 0};
-      const long total = (long)M * (nq + 2 * nkv) * (hd / 2);
-      const unsigned grid = (unsigned)std::min<long>((total + 255) / 256, 8192);
-      L("prefill_rope_kv", 4.0 * QR * M * 2, dim3(grid), blk, 0, r);
-    }
-    {  // causal attention
-      PrefillAttnArgs a{m->pf_q, Lb.kc, Lb.vc, nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq, nkv,
-                        c.max_seq, (int)start, scale};
-      if (mfma_attn)
-        L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nkv), dim3(512), 0, a);
-      else
-        L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nq), blk, 0, a);
-    }
-    {  // O projection + residual (layer.rs:386)
-      PrefillGemmArgs g{m->pf_ctx_q, m->pf_ctx_d, Lb.o.codes, Lb.o.scales, m->pf_h, m->pf_x,
-                        nullptr, nullptr, M, H, qd, H, gemm_group_m()};
-      L(gemm_kernel(m, "resid"), flops(M, H, qd), gemm_grid(M, H), blk, glds, g);
-    }
-    {  // post-attention RMSNorm + Q8_0
-      PrefillRowArgs r{m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, M, H, c.rms_eps};
-      L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
-    }
-    {  // gate|up + SiLU + Q8_0 of m (layer.rs:40-89)
-      PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.gu.codes, Lb.gu.scales, nullptr, nullptr,
-                        m->pf_m_q, m->pf_m_d, M, 2 * F, H, F, gemm_group_m()};
-      L(gemm_kernel(m, "silu"), flops(M, 2 * F, H), gemm_grid(M, 2 * F), blk, glds, g);
-    }
-    {  // down projection + residual (layer.rs:403)
-      PrefillGemmArgs g{m->pf_m_q, m->pf_m_d, Lb.down.codes, Lb.down.scales, m->pf_x, m->pf_h,
-                        nullptr, nullptr, M, H, F, H, gemm_group_m()};
-      L(gemm_kernel(m, "resid"), flops(M, H, F), gemm_grid(M, H), blk, glds, g);
-    }
+    enqueue_prefill_layer(m, L, li, start, M);
   }
   trace(c.n_layers);
   if (head) {
@@ -526,54 +496,6 @@ void run_prefill(llmrs_model* m, size_t start, size_t n, int n_prompt, bool writ
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));
     (void)hipFree(tdev);
   }
-}
-
-// The attention + O and gate|up + down launches for this model (opt-in with
-// LLMRS_FUSED=1; the O input length must equal the hidden size): role sizes
-// follow the standalone GEMV plans, LDS is the larger role's.  Measured on
-// the 8B decode they are slower than one launch per GEMV and attention (645
-// vs 706 tok/s): a consumer sees its producers' completion flags 1.5-3.5 us
-// after the last one is set, more than a kernel boundary costs in a graph,
-// and the consumers' early weight requests slow the producers' own loads.
-void plan_layer(llmrs_model* m) {
-  const llmrs_model_config& c = m->c;
-  m->ao_grid = m->mlp_grid = 0;
-  if (!env_int("LLMRS_FUSED", 0)) return;
-  const int H = c.hidden, F = c.ffn, qd = c.n_heads * c.head_dim, cus = ctx().num_cus;
-  if (qd != H || m->attn_streams != 1) return;
-  const int uh = (H / 32) % 128 == 0 ? 2 : 1, uf = (F / 32) % 128 == 0 ? 2 : 1;
-  const bool kv16 = c.kv_dtype == LLMRS_F16;
-  m->ao_name = std::string("attn_o_") + wt_tag(m->wt) + "_hd" + std::to_string(c.head_dim) +
-               (kv16 ? "_f16" : "_f32") + "_u" + std::to_string(uh);
-  m->mlp_name = std::string("mlp_") + wt_tag(m->wt) + "_h" + std::to_string(uh) + "f" + std::to_string(uf);
-  const GemvPlan po = gemv_plan(m->wt, "q8_resid", H, qd, cus);
-  const GemvPlan pg = gemv_plan(m->wt, "norm_silu", 2 * F, H, cus);
-  const GemvPlan pd = gemv_plan(m->wt, "q8_resid", H, F, cus);
-  // the fused roles use 2-row groups for O and down, 4-row for gate|up
-  if (po.name.find("_r2u") == std::string::npos || pd.name.find("_r2u") == std::string::npos) return;
-  m->lk_roles[0] = c.n_kv_heads * m->nsplit;
-  m->lk_roles[1] = (int)po.grid;
-  m->lk_roles[2] = (int)pg.grid;
-  m->lk_roles[3] = (int)pd.grid;
-  m->ao_lds = std::max(attn_lds_bytes(c.head_dim, kv16), po.lds);
-  m->mlp_lds = std::max(pg.lds, pd.lds);
-  for (auto [name, lds] : {std::make_pair(m->ao_name, m->ao_lds), std::make_pair(m->mlp_name, m->mlp_lds)}) {
-    int per_cu = 0;
-    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel(name), 256, lds) != hipSuccess ||
-        per_cu < 1) {
-      (void)hipGetLastError();
-      return;
-    }
-  }
-  m->ao_grid = (unsigned)(m->lk_roles[0] + m->lk_roles[1]);
-  m->mlp_grid = (unsigned)(m->lk_roles[2] + m->lk_roles[3]);
-}
-
-void check_barrier(llmrs_model* m) {
-  int e = 0;
-  LLMRS_HIP(hipMemcpyAsync(&e, m->bar_err, sizeof(int), hipMemcpyDeviceToHost, ctx().stream));
-  LLMRS_HIP(hipStreamSynchronize(ctx().stream));
-  if (e) fail(LLMRS_E_HIP, "decode: a cross-workgroup wait exceeded its spin limit");
 }
 
 void check_ready(const llmrs_model* m) {
@@ -726,10 +648,6 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     m->logits = m->dalloc<float>(c.vocab);
     m->part_o = m->dalloc<float>((size_t)nq * m->nsplit * hd);
     m->part_ml = m->dalloc<float>((size_t)nq * m->nsplit * 2);
-    plan_layer(m.get());
-    m->lk_flag_words = layer_flag_words(nkv, m->lk_roles[1], m->lk_roles[2]);
-    m->lflags = m->dalloc<unsigned>((size_t)c.n_layers * m->lk_flag_words);
-    m->epoch = m->dalloc<unsigned>(1);
     const size_t nparts = (size_t)m->lm_grid;
     m->part_val = m->dalloc<float>(nparts);
     m->part_idx = m->dalloc<int>(nparts);
@@ -749,7 +667,6 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
       LLMRS_HIP(hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, cx.stream));
       LLMRS_HIP(hipMemcpyAsync(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, cx.stream));
     }
-    m->bar_err = m->dalloc<int>(1);
     LLMRS_HIP(hipStreamSynchronize(cx.stream));
     // Resolve every kernel of the step now, so graph capture never has to.
     (void)kernel(gemv_plan(m->wt, "norm_store", m->qkv_rows, H, cx.num_cus).name);
@@ -984,7 +901,6 @@ int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n, size_t 
     if (next) LLMRS_HIP(hipMemcpyAsync(next, m->gen + start_pos + n, sizeof(int32_t), hipMemcpyDeviceToHost, s));
     LLMRS_HIP(hipStreamSynchronize(s));
     check_err(m);
-    check_barrier(m);
     m->host_pos = start_pos + n;
     m->begun = false;
   });
@@ -1034,7 +950,6 @@ int llmrs_model_tokens(llmrs_model* m, int32_t* out, size_t count) {
     LLMRS_HIP(hipMemcpyAsync(out, m->tokens, count * sizeof(int32_t), hipMemcpyDeviceToHost, ctx().stream));
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));
     check_err(m);
-    check_barrier(m);
   });
 }
 
@@ -1163,47 +1078,6 @@ int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
   return rc ? rc : count;
 }
 
-int llmrs_model_profile_layer(llmrs_model* m, int layer, double* us, int cap) {
-  int count = 0;
-  int rc = guard([&] {
-    LLMRS_REQUIRE(m && m->begun && us, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
-    LLMRS_REQUIRE(m->ao_grid, LLMRS_E_INVALID, "the fused layer launches are not in use");
-    LLMRS_REQUIRE(layer >= 0 && layer < m->c.n_layers, LLMRS_E_RANGE, "layer out of range");
-    LLMRS_REQUIRE(m->host_pos + 1 <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
-    const size_t nts = ((size_t)m->ao_grid + m->mlp_grid) * 4;
-    unsigned long long* ts = nullptr;
-    LLMRS_HIP(hipMalloc(&ts, nts * sizeof(unsigned long long)));
-    hipStream_t s = ctx().stream;
-    LLMRS_HIP(hipMemsetAsync(ts, 0, nts * sizeof(unsigned long long), s));
-    const llmrs_model_config& c = m->c;
-    Launcher L{s};
-    EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, c.hidden, c.vocab, m->epoch};
-    L("embed_gather", 0.0, dim3((unsigned)((c.hidden + 255) / 256)), dim3(256), 0, e);
-    for (int li = 0; li < c.n_layers; ++li) {
-      enqueue_linear(m, L, li, LLMRS_W_Q);
-      enqueue_layer_tail(m, L, li, li == layer ? ts : nullptr);
-    }
-    enqueue_head(m, L, false);
-    std::vector<unsigned long long> h(nts);
-    LLMRS_HIP(hipMemcpyAsync(h.data(), ts, nts * sizeof(unsigned long long), hipMemcpyDeviceToHost, s));
-    LLMRS_HIP(hipStreamSynchronize(s));
-    (void)hipFree(ts);
-    m->host_pos += 1;
-    check_barrier(m);
-    // us[0..3] = role sizes; then per workgroup of the two launches 4 stamps
-    // in us relative to that launch's earliest start (0 = not recorded)
-    for (int r = 0; r < 4 && count < cap; ++r) us[count++] = m->lk_roles[r];
-    for (int k = 0; k < 2; ++k) {
-      const size_t b = k == 0 ? 0 : (size_t)m->ao_grid * 4, e2 = k == 0 ? (size_t)m->ao_grid * 4 : nts;
-      unsigned long long t0 = ~0ull;
-      for (size_t i = b; i < e2; i += 4)
-        if (h[i]) t0 = std::min(t0, h[i]);
-      for (size_t i = b; i < e2 && count < cap; ++i) us[count++] = h[i] ? (double)(h[i] - t0) / 100.0 : 0.0;
-    }
-  });
-  return rc ? rc : count;
-}
-
 double llmrs_model_weight_bytes(const llmrs_model* m) {
   if (!m) return 0.0;
   double b = linear_weight_bytes(m, m->lm_head);
@@ -1211,6 +1085,160 @@ double llmrs_model_weight_bytes(const llmrs_model* m) {
     b += linear_weight_bytes(m, L.qkv) + linear_weight_bytes(m, L.o) + linear_weight_bytes(m, L.gu) +
          linear_weight_bytes(m, L.down);
   return b;
+}
+
+}  // extern "C"
+
+// ---- test probes: one layer's kernels on given inputs ----------------------
+
+namespace {
+
+void check_layer_ready(const llmrs_model* m, int layer) {
+  LLMRS_REQUIRE(m, LLMRS_E_INVALID, "null model");
+  LLMRS_REQUIRE(layer >= 0 && layer < m->c.n_layers, LLMRS_E_RANGE, "layer out of range");
+  LLMRS_REQUIRE(m->layers[layer].set_mask == 0x37f, LLMRS_E_INVALID,
+                "layer " + std::to_string(layer) + " weights incomplete");
+}
+
+// Copies `bytes` from device `src` to host `dst` when dst is set (the stream
+// is synchronised by the caller).
+void probe_copy(void* dst, const void* src, size_t bytes) {
+  if (dst) LLMRS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx().stream));
+}
+
+// Device scratch of a probe call, freed on every exit path.
+struct ProbeBuf {
+  std::vector<void*> ptrs;
+  template <class T>
+  T* get(size_t count) {
+    void* p = nullptr;
+    LLMRS_HIP(hipMalloc(&p, std::max<size_t>(count * sizeof(T), 256)));
+    ptrs.push_back(p);
+    return (T*)p;
+  }
+  ~ProbeBuf() {
+    (void)hipStreamSynchronize(ctx().stream);
+    for (void* p : ptrs) (void)hipFree(p);
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+int llmrs_model_probe_decode_layer(llmrs_model* m, int layer, size_t pos, const float* x,
+                                   llmrs_layer_probe* out) {
+  return guard([&] {
+    check_layer_ready(m, layer);
+    LLMRS_REQUIRE(x && out, LLMRS_E_INVALID, "null argument");
+    LLMRS_REQUIRE(pos < (size_t)m->c.max_seq, LLMRS_E_RANGE, "position beyond max_seq");
+    const llmrs_model_config& c = m->c;
+    const size_t H = c.hidden, F = c.ffn, qd = (size_t)c.n_heads * c.head_dim;
+    hipStream_t s = ctx().stream;
+    ProbeBuf pb;
+    int8_t* xq = pb.get<int8_t>(H);
+    float* xd = pb.get<float>(H / 32);
+    set_state(m, pos, INT_MAX);
+    m->host_pos = pos;
+    LLMRS_HIP(hipMemcpyAsync(m->x, x, H * sizeof(float), hipMemcpyHostToDevice, s));
+    Launcher L{s};
+    auto sync = [&] { LLMRS_HIP(hipStreamSynchronize(s)); };
+    enqueue_linear(m, L, layer, LLMRS_W_Q, xq, xd);
+    probe_copy(out->qkv, m->qkv, m->qkv_rows * sizeof(float));
+    probe_copy(out->xq, xq, H);
+    probe_copy(out->xd, xd, H / 32 * sizeof(float));
+    sync();
+    enqueue_attention(m, L, layer);
+    probe_copy(out->ctx, m->ctxv, qd * sizeof(float));
+    probe_copy(out->ctx_q, m->ctx_q, qd);
+    probe_copy(out->ctx_d, m->ctx_d, qd / 32 * sizeof(float));
+    sync();
+    enqueue_linear(m, L, layer, LLMRS_W_O);
+    probe_copy(out->h, m->h, H * sizeof(float));
+    sync();
+    enqueue_linear(m, L, layer, LLMRS_W_GATE, xq, xd);
+    probe_copy(out->hq, xq, H);
+    probe_copy(out->hd, xd, H / 32 * sizeof(float));
+    probe_copy(out->m, m->mf, F * sizeof(float));
+    probe_copy(out->m_q, m->m_q, F);
+    probe_copy(out->m_d, m->m_d, F / 32 * sizeof(float));
+    sync();
+    enqueue_linear(m, L, layer, LLMRS_W_DOWN);
+    probe_copy(out->out, m->x, H * sizeof(float));
+    sync();
+    m->begun = false;
+  });
+}
+
+int llmrs_model_probe_head(llmrs_model* m, const float* x, int8_t* xq, float* xd, float* logits,
+                           int32_t* next) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && x, LLMRS_E_INVALID, "null argument");
+    LLMRS_REQUIRE(m->final_set && m->lm_set, LLMRS_E_INVALID, "final norm / lm_head not set");
+    const size_t H = m->c.hidden;
+    hipStream_t s = ctx().stream;
+    ProbeBuf pb;
+    int8_t* dq = pb.get<int8_t>(H);
+    float* dd = pb.get<float>(H / 32);
+    set_state(m, 0, INT_MAX);
+    LLMRS_HIP(hipMemcpyAsync(m->x, x, H * sizeof(float), hipMemcpyHostToDevice, s));
+    Launcher L{s};
+    enqueue_head(m, L, logits != nullptr, dq, dd);
+    probe_copy(xq, dq, H);
+    probe_copy(xd, dd, H / 32 * sizeof(float));
+    probe_copy(logits, m->logits, (size_t)m->c.vocab * sizeof(float));
+    probe_copy(next, m->gen + 1, sizeof(int32_t));
+    LLMRS_HIP(hipStreamSynchronize(s));
+    m->begun = false;
+  });
+}
+
+int llmrs_model_probe_prefill_layer(llmrs_model* m, int layer, size_t start_pos, size_t n,
+                                    const float* x, llmrs_layer_probe* out) {
+  return guard([&] {
+    check_layer_ready(m, layer);
+    LLMRS_REQUIRE(x && out && n > 0, LLMRS_E_INVALID, "null argument or no rows");
+    LLMRS_REQUIRE(start_pos + n <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "positions beyond max_seq");
+    ensure_prefill(m);
+    LLMRS_REQUIRE(n <= (size_t)m->pf_cap, LLMRS_E_RANGE, "more rows than one prefill chunk");
+    const llmrs_model_config& c = m->c;
+    const size_t H = c.hidden, F = c.ffn, qd = (size_t)c.n_heads * c.head_dim, M = n;
+    hipStream_t s = ctx().stream;
+    ProbeBuf pb;
+    PrefillProbe p;
+    p.ctx = pb.get<float>(M * qd);
+    p.mf = pb.get<float>(M * F);
+    LLMRS_HIP(hipMemcpyAsync(m->pf_x, x, M * H * sizeof(float), hipMemcpyHostToDevice, s));
+    p.after = [&](int stage) {
+      switch (stage) {
+        case 0:
+          probe_copy(out->xq, m->pf_aq, M * H);
+          probe_copy(out->xd, m->pf_ad, M * H / 32 * sizeof(float));
+          break;
+        case 1: probe_copy(out->qkv, m->pf_qkv, M * m->qkv_rows * sizeof(float)); break;
+        case 3:
+          probe_copy(out->ctx, p.ctx, M * qd * sizeof(float));
+          probe_copy(out->ctx_q, m->pf_ctx_q, M * qd);
+          probe_copy(out->ctx_d, m->pf_ctx_d, M * qd / 32 * sizeof(float));
+          break;
+        case 4: probe_copy(out->h, m->pf_h, M * H * sizeof(float)); break;
+        case 5:
+          probe_copy(out->hq, m->pf_aq, M * H);
+          probe_copy(out->hd, m->pf_ad, M * H / 32 * sizeof(float));
+          break;
+        case 6:
+          probe_copy(out->m, p.mf, M * F * sizeof(float));
+          probe_copy(out->m_q, m->pf_m_q, M * F);
+          probe_copy(out->m_d, m->pf_m_d, M * F / 32 * sizeof(float));
+          break;
+        case 7: probe_copy(out->out, m->pf_x, M * H * sizeof(float)); break;
+      }
+      LLMRS_HIP(hipStreamSynchronize(s));
+    };
+    Launcher L{s};
+    enqueue_prefill_layer(m, L, layer, start_pos, (int)M, &p);
+    m->begun = false;
+  });
 }
 
 }  // extern "C"

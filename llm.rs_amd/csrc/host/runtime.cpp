@@ -271,7 +271,7 @@ int llmrs_init(int device_ordinal, const char* hsaco_dir) {
       c->num_cus = prop.multiProcessorCount;
       LLMRS_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
       std::string dir = hsaco_dir ? std::string(hsaco_dir) : library_dir();
-      for (const char* name : {"gemv", "attention", "ops", "prefill", "layer"}) {
+      for (const char* name : {"gemv", "attention", "ops", "prefill"}) {
         std::string path = dir + "/" + name + ".hsaco";
         LLMRS_REQUIRE(std::filesystem::exists(path), LLMRS_E_MODULE, "missing code object " + path);
         hipModule_t m = nullptr;

@@ -28,6 +28,8 @@ struct GemvArgs {
   float* part_val;       // [gridDim.x] (EPI_ARGMAX)
   int* part_idx;         // [gridDim.x] (EPI_ARGMAX)
   unsigned long long* ts;  // profiling: 4 stamps per workgroup (null = off)
+  int8_t* probe_xq;      // [k] when set: workgroup 0 copies the Q8_0 activation codes of
+  float* probe_xd;       // its prologue and [k/32] their scales here (test probes)
 };
 
 // Dynamic LDS of a decode GEMV (gemv_core.h): the quantised activation row
@@ -113,7 +115,6 @@ struct EmbedArgs {
   float* x;             // [hidden]
   int* err;             // set to 1 on an out-of-range id
   int hidden, vocab;
-  unsigned* epoch;      // decode-step counter, incremented once per launch (may be null)
 };
 
 // Prefill GEMM (prefill.hip): Y[t][r] = sum_b isum_b(t, r) * (d_w[r,b] * d_a[t,b])
@@ -192,57 +193,5 @@ constexpr size_t attn_lds_bytes(int hd, bool kv16, int streams = 1) {
   const size_t stream = kb + es * tile * (size_t)hd;
   return 4 * 8 * (size_t)hd + (size_t)streams * stream + 4 * 2 * (size_t)hd + 16;
 }
-
-// The weights, norms and caches of one decoder layer (layer.hip).
-struct LayerDesc {
-  const uint8_t* qkv_w;
-  const void* qkv_s;
-  const uint8_t* o_w;
-  const void* o_s;
-  const uint8_t* gu_w;
-  const void* gu_s;
-  const uint8_t* down_w;
-  const void* down_s;
-  const float* norm_in;
-  const float* norm_post;
-  void* kc;
-  void* vc;
-};
-
-// Attention + O and gate|up + down of one decoder layer, one launch each
-// (layer.hip): producer-role workgroups first, consumer-role workgroups
-// after them, consumers waiting on the producers' completion flags.
-struct LayerArgs {
-  LayerDesc w;               // this layer's weights, norms and caches
-  float* x;                  // [hidden] layer input; the down role writes the output here
-  float* qkv;                // [qkv_rows]
-  float* h;                  // [hidden] x + O . ctx
-  float* ctx;                // [nq*hd]
-  int8_t* ctx_q;
-  float* ctx_d;
-  float* mf;                 // [ffn] silu(g)*u (may be null)
-  int8_t* m_q;
-  float* m_d;
-  const float* rope_cos;
-  const float* rope_sin;
-  const int* pos_ptr;        // device position of the token
-  float* part_o;             // attention partials [nq][nsplit][hd]
-  float* part_ml;
-  int* counters;             // [nkv][kTicketStride] attention tickets of this layer, zero between uses
-  unsigned* flags;           // this layer's completion flags: attention (one per KV head),
-                             // O, gate|up workgroups in that order (layer_flag_words entries)
-  const unsigned* epoch;     // decode-step counter: a flag equal to it is set for this step
-  int* err;                  // set when a wait exceeds its spin limit
-  int hidden, nq, nkv, ffn, max_seq, qkv_rows, nsplit;
-  float eps, attn_scale;
-  int n_attn, n_o, n_gu, n_down;  // workgroups per role
-  unsigned long long* ts;    // profiling: 4 stamps per workgroup (start, released, done, end); null = off
-};
-
-// Completion-flag words per layer of the fused layer kernel.
-constexpr size_t layer_flag_words(int n_attn_heads, int n_o, int n_gu) {
-  return (size_t)n_attn_heads + n_o + n_gu;
-}
-
 
 }  // namespace llmrs

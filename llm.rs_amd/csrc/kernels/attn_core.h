@@ -1,6 +1,5 @@
-// attn_core.h - batch-1 decode attention over the KV cache for gfx950,
-// shared by the standalone kernels (attention.hip) and the fused attention +
-// O launch (layer.hip).
+// attn_core.h - batch-1 decode attention over the KV cache for gfx950
+// (instantiated by attention.hip).
 //
 // Reference: LlamaAttention::forward, seq == 1 (layer.rs:175-299): per query
 // head, RoPE on q and k (layer.rs:216-217, cpu.rs:326-357), K/V append at
@@ -27,8 +26,7 @@
 // to the cache.  Partials (m, l, acc) go to global memory; the last
 // workgroup of a KV head (atomic ticket; partials move with device-scope
 // stores and loads) combines them and writes ctx as f32 and as Q8_0 codes
-// for the O projection, also with device-scope stores, so a consumer in the
-// same launch (layer.hip) can read them once the item has completed.
+// for the O projection.
 //
 // RoPE uses cos/sin tables [max_seq][hd/2] computed on the host with the
 // reference's own f32 formula and glibc, so rotation is bit-exact.

@@ -1,5 +1,5 @@
-// gemv_core.h - the batch-1 dequant-GEMV machinery shared by the standalone
-// GEMV kernels (gemv.hip) and the fused layer launches (layer.hip).
+// gemv_core.h - the batch-1 dequant-GEMV machinery of the decode GEMV
+// kernels (gemv.hip).
 //
 // y[row] = sum_b isum_b(row) * (d_w[row,b] * d_a[b]) where isum_b is the exact
 // int32 dot product of one 32-element block of weight codes with the Q8_0
@@ -19,8 +19,8 @@
 // reads 64 consecutive 16-byte blocks of one row (1 KB, fully coalesced).
 // Waves walk their units in order, two units in flight: the weights of unit
 // i+2 are requested right after unit i is consumed, and the first units are
-// requested with the activation prologue (or, in a fused launch, before the
-// wait for the producer), so HBM latency overlaps the prologue.  Row groups are dealt to the waves of `nwg`
+// requested with the activation prologue, so HBM latency overlaps the
+// prologue.  Row groups are dealt to the waves of `nwg`
 // workgroups round-robin (whole 64-row tiles per workgroup for the SwiGLU
 // epilogue, which needs matching gate and up rows).
 //
@@ -35,7 +35,8 @@
 //              written as f32 and as Q8_0 codes for the down projection
 //   EPI_ARGMAX logits plus a per-workgroup (max, index) partial (lm_head)
 // DEV = true moves the activations, results and partials with device-scope
-// loads and stores (producer and consumer in one launch).
+// loads and stores (for a producer and consumer in one launch; the decode
+// kernels use DEV = false).
 #pragma once
 #include "common.h"
 #include "../kernel_args.h"
@@ -798,6 +799,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
   }
   ts.rec(3);
   if (ts.on && tid == 0) ts.write(a.ts + 8 * ((size_t)mrow * nwg + wg));
+  // Test probe: the prologue's operand, copied after every load has been
+  // consumed so the unit pipeline is unaffected.
+  if (a.probe_xq && wg == 0 && mrow == 0) {
+    for (int i = tid; i < k; i += kThreads) a.probe_xq[i] = s_q[i];
+    for (int b = tid; b < nb; b += kThreads) a.probe_xd[b] = s_d[b];
+  }
 }
 
 }  // namespace llmrs

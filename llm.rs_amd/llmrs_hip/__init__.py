@@ -94,11 +94,15 @@ _SIGS = {
     "llmrs_model_decode_steps": (C.c_int, [C.c_void_p, C.c_size_t]),
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "llmrs_model_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
-    "llmrs_model_profile_layer": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int]),
     "llmrs_model_time_linear": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "llmrs_model_profile_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_char_p,
                                                C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_weight_bytes": (C.c_double, [C.c_void_p]),
+    "llmrs_model_probe_decode_layer": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p]),
+    "llmrs_model_probe_head": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                          C.c_void_p]),
+    "llmrs_model_probe_prefill_layer": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_size_t, C.c_void_p,
+                                                   C.c_void_p]),
     "llmrs_synth_q4": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_synth_q8": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_synth_normal": (C.c_int, [C.c_uint64, C.c_uint64, C.c_size_t, C.c_float, C.c_float, C.c_void_p, C.c_int]),
@@ -305,6 +309,23 @@ class KernelTiming:
     bytes: float
 
 
+class LayerProbe(C.Structure):
+    """llmrs_layer_probe: host buffers for one layer's intermediates."""
+    _fields_ = [(n, C.c_void_p) for n in
+                ("qkv", "xq", "xd", "ctx", "ctx_q", "ctx_d", "h", "hq", "hd", "m", "m_q", "m_d", "out")]
+
+
+def _probe_arrays(cfg, rows: int) -> dict:
+    H, F = cfg.hidden, cfg.ffn
+    qd = cfg.n_heads * cfg.head_dim
+    qr = (cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim
+    f, i8 = np.float32, np.int8
+    shapes = {"qkv": (qr, f), "xq": (H, i8), "xd": (H // 32, f), "ctx": (qd, f), "ctx_q": (qd, i8),
+              "ctx_d": (qd // 32, f), "h": (H, f), "hq": (H, i8), "hd": (H // 32, f), "m": (F, f),
+              "m_q": (F, i8), "m_d": (F // 32, f), "out": (H, f)}
+    return {k: np.zeros((rows, n), t) for k, (n, t) in shapes.items()}
+
+
 class HipModel:
     """The resident decode model (llmrs_model_*)."""
 
@@ -417,13 +438,35 @@ class HipModel:
         return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(wk[i]))
                 for i in range(n)]
 
-    def profile_layer(self, layer: int = 1, cap: int = 1 << 16):
-        """Per-workgroup stamps of one layer's attention + O and gate|up +
-        down launches: (role sizes [attention, O, gate|up, down], [workgroups
-        of both launches][4] = start, wait released, work done, end in us)."""
-        out = np.zeros(cap, np.float64)
-        n = _check(lib().llmrs_model_profile_layer(self._h, layer, _ptr(out), cap))
-        return [int(v) for v in out[:4]], out[4:n].reshape(-1, 4)
+    def probe_decode_layer(self, layer: int, pos: int, x: np.ndarray) -> dict:
+        """One decode step of `layer` at `pos` on the row x (test probe):
+        every intermediate of its kernels, as 1-D arrays (LayerProbe)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = _probe_arrays(self.cfg, 1)
+        pr = LayerProbe(**{k: v.ctypes.data for k, v in out.items()})
+        _check(lib().llmrs_model_probe_decode_layer(self._h, layer, pos, _ptr(x), C.byref(pr)))
+        return {k: v[0] for k, v in out.items()}
+
+    def probe_head(self, x: np.ndarray):
+        """Final RMSNorm + lm_head + argmax of the row x (test probe):
+        (Q8_0 codes, scales, logits, next id)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        H = self.cfg.hidden
+        xq, xd = np.zeros(H, np.int8), np.zeros(H // 32, np.float32)
+        lg = np.zeros(self.cfg.vocab, np.float32)
+        nxt = np.zeros(1, np.int32)
+        _check(lib().llmrs_model_probe_head(self._h, _ptr(x), _ptr(xq), _ptr(xd), _ptr(lg), _ptr(nxt)))
+        return xq, xd, lg, int(nxt[0])
+
+    def probe_prefill_layer(self, layer: int, start_pos: int, x: np.ndarray) -> dict:
+        """The batched prefill kernels of `layer` on rows x [n][hidden] at
+        positions start_pos.. (test probe): every intermediate, [n][...]."""
+        x = np.ascontiguousarray(x, np.float32)
+        n = x.shape[0]
+        out = _probe_arrays(self.cfg, n)
+        pr = LayerProbe(**{k: v.ctypes.data for k, v in out.items()})
+        _check(lib().llmrs_model_probe_prefill_layer(self._h, layer, start_pos, n, _ptr(x), C.byref(pr)))
+        return out
 
     def weight_bytes(self) -> float:
         return float(lib().llmrs_model_weight_bytes(self._h))

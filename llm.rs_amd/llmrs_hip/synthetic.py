@@ -111,10 +111,13 @@ def linear(spec: Spec, tid: int, slot: int, threads: int = 0):
     return synth_q4(spec.seed, tid, n, k, *Q4_SCALE, threads=threads)
 
 
-def make_weights(spec: Spec, threads: int = 0) -> Weights:
+def make_weights(spec: Spec, threads: int = 0, embed: bool = True) -> Weights:
+    """Every tensor of `spec` (embed=False leaves the embedding table out:
+    None, for probes that feed layer inputs directly)."""
     H = spec.hidden
     w = Weights(spec,
-                embed=synth_normal(spec.seed, 0, spec.vocab * H, 0.0, 0.02, threads).reshape(spec.vocab, H),
+                embed=(synth_normal(spec.seed, 0, spec.vocab * H, 0.0, 0.02, threads).reshape(spec.vocab, H)
+                       if embed else None),
                 final_norm=synth_normal(spec.seed, 1, H, 1.0, 0.02, threads),
                 lm_head=linear(spec, 2, W_LM_HEAD, threads))
     for l in range(spec.n_layers):
@@ -140,7 +143,8 @@ def prefill_kv(spec: Spec, layer: int, kv_head: int, threads: int = 0):
 def load_model(model, w: Weights) -> None:
     """Upload every tensor of `w` into a HipModel."""
     spec = w.spec
-    model.set_embedding(w.embed)
+    if w.embed is not None:
+        model.set_embedding(w.embed)
     model.set_norm(-1, N_FINAL, w.final_norm)
     put = model.set_linear_q8_0 if spec.weight == DType.Q8_0 else model.set_linear_q4
     put(-1, W_LM_HEAD, *w.lm_head)

@@ -21,7 +21,13 @@ _P = C.c_void_p
 _SIGS = {
     "orc_set_threads": (None, [C.c_int]),
     "orc_get_threads": (C.c_int, []),
-    "orc_set_jitter": (None, [C.c_uint64, C.c_int]),
+    "orc_set_arch": (None, [C.c_int]),
+    "orc_get_arch": (C.c_int, []),
+    "orc_record_codes": (None, [C.c_int]),
+    "orc_set_attn_f64": (None, [C.c_int]),
+    "orc_recorded_codes": (_I64, [_P, _I64]),
+    "orc_gemv_codes": (None, [_P, _P, _I64, _I64, _P, _P, _I64, C.c_int, _P]),
+    "orc_model_attention": (C.c_int, [_P, C.c_int, _P, _I64, _I64, _P]),
     "orc_quantize_row_q8_0": (None, [_P, _I64, _P, _P]),
     "orc_quantize_q4": (None, [_P, _I64, _P, _P]),
     "orc_dequantize_q4": (None, [_P, _P, _I64, _P]),
@@ -80,11 +86,44 @@ def set_threads(n: int) -> None:
     lib().orc_set_threads(n)
 
 
-def set_jitter(seed: int, ulps: int = 1) -> None:
-    """Test-only: seed != 0 moves every linear-layer input by a pseudo-random
-    whole number of ulps in [-ulps, ulps] before the reference arithmetic
-    (seed 0 = off, the default)."""
-    lib().orc_set_jitter(seed, ulps)
+def set_arch(arch: int) -> None:
+    """Test-only: restate the reference's x86-64 build (0, the default) or
+    its aarch64 build (1: NEON summation orders of the Q4 GEMV, f32 dot and
+    saxpy, cpu.rs:461-619,747-886)."""
+    lib().orc_set_arch(arch)
+
+
+def set_attn_f64(on: bool) -> None:
+    """Test-only: the attention's scores, softmax and P.V summed in float64
+    (rounded to f32 once), the rest of the arithmetic unchanged."""
+    lib().orc_set_attn_f64(1 if on else 0)
+
+
+def record_codes(on: bool) -> None:
+    """Test-only: start (clearing) or stop recording every Q8_0 code."""
+    lib().orc_record_codes(1 if on else 0)
+
+
+def recorded_codes() -> np.ndarray:
+    n = lib().orc_recorded_codes(None, 0)
+    out = np.empty(n, np.int8)
+    lib().orc_recorded_codes(_p(out), n)
+    return out
+
+
+def gemv_codes(xq, xd, w, scales, n, q8w=False):
+    """The reference block loop over already-quantised activation rows
+    (xq [m][k] int8, xd [m][k/32]) for Q4 (reference nibble order) or Q8
+    weight codes: [m][n]."""
+    xq = np.ascontiguousarray(xq, np.int8)
+    if xq.ndim == 1:
+        xq = xq[None]
+    m, k = xq.shape
+    xd = _f32(xd).reshape(m, k // 32)
+    w = np.ascontiguousarray(w, np.int8 if q8w else np.uint8)
+    out = np.empty((m, n), np.float32)
+    lib().orc_gemv_codes(_p(xq), _p(xd), m, k, _p(w), _p(_f32(scales)), n, 1 if q8w else 0, _p(out))
+    return out
 
 
 def threads() -> int:
@@ -280,6 +319,19 @@ class OracleModel:
         assert lib().orc_model_kv_read(self._h, layer, kv_head, pos0, n, _p(k), _p(v)) == 0
         return k, v
 
+    def attention(self, layer, qkv, start_pos):
+        """Attention of `layer` given Q|K|V projections [seq][(nq+2nkv)hd]
+        (before RoPE) at positions start_pos..: appends K/V, returns ctx."""
+        qkv = _f32(qkv)
+        if qkv.ndim == 1:
+            qkv = qkv[None]
+        seq = qkv.shape[0]
+        ctx = np.empty((seq, self.cfg.n_heads * self.cfg.head_dim), np.float32)
+        rc = lib().orc_model_attention(self._h, layer, _p(qkv), seq, start_pos, _p(ctx))
+        if rc:
+            raise ValueError("oracle attention failed")
+        return ctx
+
     def forward(self, tokens, start_pos, all_rows=False, trace=False):
         ids = np.ascontiguousarray(tokens, np.int32)
         n = ids.size
@@ -303,7 +355,8 @@ class OracleModel:
         """Borrow every tensor of a synthetic.Weights."""
         from llmrs_hip import DType  # noqa: WPS433 (lazy: package path set by caller)
         spec = w.spec
-        self.set_embedding(w.embed)
+        if w.embed is not None:
+            self.set_embedding(w.embed)
         self.set_norm(-1, 2, w.final_norm)
         put = self.set_linear_q8 if spec.weight == DType.Q8_0 else self.set_linear_q4
         put(-1, 7, *w.lm_head)

@@ -118,27 +118,19 @@ class Pool {
   int nthreads_ = 1;
 };
 
-// Test-only noise model (orc_set_jitter): when the seed is non-zero, every
-// input of a linear layer is moved element-wise by a pseudo-random whole
-// number of ulps in [-ulps, +ulps] before the reference arithmetic runs.  It
-// measures how far the reference's own output moves under rounding-level
-// input changes - the envelope a different f32 summation order can reach.
-// Off (seed 0) by default.
-std::atomic<uint64_t> g_jitter_seed{0};
-std::atomic<uint64_t> g_jitter_calls{0};
-std::atomic<int> g_jitter_ulps{1};
-
-inline uint64_t jitter_mix(uint64_t z) {
-  z += 0x9E3779B97F4A7C15ull;
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-  return z ^ (z >> 31);
-}
-
 Pool& pool() {
   static Pool p(0);
   return p;
 }
+
+// Which build of the reference the arithmetic restates (orc_set_arch):
+// 0 = x86-64 (the default; the timed host), 1 = aarch64, the reference's
+// primary target (Android), whose NEON paths sum in other orders: the Q4
+// GEMV adds four blocks before the running total (kernel_neon_sdot,
+// cpu.rs:747-886), simd_dot_f32 keeps 32 fused multiply-add lanes
+// (cpu.rs:461-544) and simd_saxpy fuses (cpu.rs:558-619).  Test-only: it
+// measures how far the reference's own two builds disagree.
+std::atomic<int> g_arch{0};
 
 // Rust's `iter().zip().map(|(x, y)| x * y).sum()`: sequential from zero
 // (cpu.rs:546-549, the non-aarch64 simd_dot_f32).
@@ -147,6 +139,53 @@ inline float dot_seq(const float* a, const float* b, int64_t n) {
   for (int64_t i = 0; i < n; ++i) s = s + a[i] * b[i];
   return s;
 }
+
+// simd_dot_f32 on aarch64 (cpu.rs:461-544): eight 4-lane accumulators over
+// 32-element steps with fused multiply-add, combined as
+// ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)) lane-wise, 4-element leftovers fused
+// into that, the lanes summed pairwise ((l0+l1)+(l2+l3), vaddvq_f32), then
+// scalar leftovers unfused.
+inline float dot_neon(const float* a, const float* b, int64_t n) {
+  float acc[8][4] = {};
+  int64_t i = 0;
+  for (; i + 32 <= n; i += 32)
+    for (int j = 0; j < 8; ++j)
+      for (int l = 0; l < 4; ++l) acc[j][l] = std::fma(a[i + 4 * j + l], b[i + 4 * j + l], acc[j][l]);
+  float v[4];
+  for (int l = 0; l < 4; ++l)
+    v[l] = ((acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l])) +
+           ((acc[4][l] + acc[5][l]) + (acc[6][l] + acc[7][l]));
+  for (; i + 4 <= n; i += 4)
+    for (int l = 0; l < 4; ++l) v[l] = std::fma(a[i + l], b[i + l], v[l]);
+  float sum = (v[0] + v[1]) + (v[2] + v[3]);
+  for (; i < n; ++i) sum = sum + a[i] * b[i];
+  return sum;
+}
+
+// simd_dot_f32 of the selected build.
+inline float dot_ref(const float* a, const float* b, int64_t n) {
+  return g_arch.load(std::memory_order_relaxed) ? dot_neon(a, b, n) : dot_seq(a, b, n);
+}
+
+// simd_saxpy of the selected build (y += alpha * x): unfused on x86
+// (cpu.rs:620-625); on aarch64 fused over whole 32-element steps and unfused
+// for the leftovers (cpu.rs:558-619).
+inline void saxpy_ref(float alpha, const float* x, float* y, int64_t n) {
+  int64_t i = 0;
+  if (g_arch.load(std::memory_order_relaxed))
+    for (const int64_t n32 = n / 32 * 32; i < n32; ++i) y[i] = std::fma(alpha, x[i], y[i]);
+  for (; i < n; ++i) y[i] = y[i] + alpha * x[i];
+}
+
+// Test-only: attention sums in float64 (orc_set_attn_f64), to measure how
+// far the reference's own f32 attention sums move its results.
+std::atomic<int> g_attn_f64{0};
+
+// Test-only record of every Q8_0 code quantize_row_q8_0 produces, in call
+// order (orc_record_codes), so two runs can be compared code by code.
+std::atomic<int> g_record{0};
+std::mutex g_record_mu;
+std::vector<int8_t> g_recorded;
 
 // Exact integer sum over one Q4 block: sum_i (q_i - 8) * a_i, with the
 // reference nibble order (element 2i = low nibble of byte i, element 2i+1 =
@@ -183,28 +222,39 @@ inline int32_t q8_isum_avx2(const int8_t* w, const int8_t* a) {
   return _mm_cvtsi128_si32(s);
 }
 
-// One Q4 output row: cpu.rs:903-938 (kernel_avx2).  The f32 accumulation is
-// sequential over blocks from 0.0: total += isum * (d_w * d_a).
-inline float q4_row(const uint8_t* qrow, const float* srow, const int8_t* aq,
-                    const float* ad, int64_t nb) {
+// The f32 block accumulation of one output row from its exact block sums.
+// x86 (kernel_avx2, cpu.rs:903-938): sequential over blocks from 0.0,
+// total += isum * (d_w * d_a).  aarch64 (kernel_neon_sdot, cpu.rs:771-877):
+// four blocks at a time, total += ((p0 + p1) + p2) + p3 with p = isum *
+// (d_a * d_w), then the remaining blocks one by one.
+template <class ISum>
+inline float block_row(const float* srow, const float* ad, int64_t nb, ISum isum) {
   float total = 0.0f;
-  for (int64_t b = 0; b < nb; ++b) {
+  int64_t b = 0;
+  if (g_arch.load(std::memory_order_relaxed)) {
+    for (; b + 4 <= nb; b += 4) {
+      float p[4];
+      for (int j = 0; j < 4; ++j) p[j] = (float)isum(b + j) * (ad[b + j] * srow[b + j]);
+      total = total + (((p[0] + p[1]) + p[2]) + p[3]);
+    }
+  }
+  for (; b < nb; ++b) {
     float scale = srow[b] * ad[b];
-    float blk = (float)q4_isum_avx2(qrow + 16 * b, aq + 32 * b);
+    float blk = (float)isum(b);
     total = total + blk * scale;
   }
   return total;
 }
 
+// One Q4 output row (cpu.rs:903-938, or the aarch64 order).
+inline float q4_row(const uint8_t* qrow, const float* srow, const int8_t* aq,
+                    const float* ad, int64_t nb) {
+  return block_row(srow, ad, nb, [&](int64_t b) { return q4_isum_avx2(qrow + 16 * b, aq + 32 * b); });
+}
+
 inline float q8_row(const int8_t* wrow, const float* srow, const int8_t* aq,
                     const float* ad, int64_t nb) {
-  float total = 0.0f;
-  for (int64_t b = 0; b < nb; ++b) {
-    float scale = srow[b] * ad[b];
-    float blk = (float)q8_isum_avx2(wrow + 32 * b, aq + 32 * b);
-    total = total + blk * scale;
-  }
-  return total;
+  return block_row(srow, ad, nb, [&](int64_t b) { return q8_isum_avx2(wrow + 32 * b, aq + 32 * b); });
 }
 
 // f32 -> binary16, IEEE round-to-nearest-even (F16C).
@@ -217,11 +267,24 @@ extern "C" {
 
 void orc_set_threads(int n) { pool().resize(n); }
 
-void orc_set_jitter(uint64_t seed, int ulps) {
-  g_jitter_ulps.store(ulps < 1 ? 1 : ulps);
-  g_jitter_seed.store(seed);
-  g_jitter_calls.store(0);
+void orc_set_arch(int arch) { g_arch.store(arch ? 1 : 0); }
+int orc_get_arch(void) { return g_arch.load(); }
+
+void orc_set_attn_f64(int on) { g_attn_f64.store(on ? 1 : 0); }
+
+void orc_record_codes(int on) {
+  std::lock_guard<std::mutex> lk(g_record_mu);
+  g_record.store(on ? 1 : 0);
+  if (on) g_recorded.clear();
 }
+
+int64_t orc_recorded_codes(int8_t* out, int64_t cap) {
+  std::lock_guard<std::mutex> lk(g_record_mu);
+  const int64_t n = (int64_t)g_recorded.size();
+  if (out) std::memcpy(out, g_recorded.data(), (size_t)std::min(n, cap));
+  return n;
+}
+
 int orc_get_threads(void) { return pool().size(); }
 
 // cpu.rs:724-743 (x86 path of quantize_row_q8_0).  amax by strict '>' fold
@@ -250,6 +313,10 @@ void orc_quantize_row_q8_0(const float* x, int64_t k, int8_t* q, float* d) {
         qb[i] = (int8_t)r;
       }
     }
+  }
+  if (g_record.load(std::memory_order_relaxed)) {
+    std::lock_guard<std::mutex> lk(g_record_mu);
+    g_recorded.insert(g_recorded.end(), q, q + nb * 32);
   }
 }
 
@@ -305,22 +372,19 @@ int32_t orc_q4_block_isum_scalar(const uint8_t* q4, const int8_t* a) {
 // row of `a` to Q8 (cpu.rs:79,98-100), then one sequential block loop per
 // output column (kernel_avx2 cpu.rs:888-941), columns in 512 chunks
 // (cpu.rs:74,81).
+//
+// Loop order: every output is one q4_row call, whatever the order, so the
+// values equal the reference's row-parallel loop (cpu.rs:91-110).  The
+// rows are quantised first, then 512-column chunks run in parallel, each
+// taking every row in turn while its weights stay in cache.
 void orc_matmul_transposed_q4(const float* a, int64_t m, int64_t k,
                               const uint8_t* qs, const float* scales,
                               int64_t n, float* out) {
   const int64_t nb = k / 32;
-  std::vector<int8_t> aq(k);
-  std::vector<float> ad(nb);
-  for (int64_t i = 0; i < m; ++i) {
-    orc_quantize_row_q8_0(a + i * k, k, aq.data(), ad.data());
-    float* res = out + i * n;
-    const int64_t chunks = (n + 511) / 512;
-    pool().run(chunks, [&](int64_t c) {
-      int64_t j0 = c * 512, j1 = std::min(n, j0 + 512);
-      for (int64_t j = j0; j < j1; ++j)
-        res[j] = q4_row(qs + j * (k / 2), scales + j * nb, aq.data(), ad.data(), nb);
-    });
-  }
+  std::vector<int8_t> aq(m * k);
+  std::vector<float> ad(m * nb);
+  for (int64_t i = 0; i < m; ++i) orc_quantize_row_q8_0(a + i * k, k, &aq[i * k], &ad[i * nb]);
+  orc_gemv_codes(aq.data(), ad.data(), m, k, qs, scales, n, 0, out);
 }
 
 // Q8_0-weight GEMV: no reference function (the reference has only F32 and
@@ -330,25 +394,17 @@ void orc_matmul_transposed_q8w(const float* a, int64_t m, int64_t k,
                                const int8_t* qs, const float* scales,
                                int64_t n, float* out) {
   const int64_t nb = k / 32;
-  std::vector<int8_t> aq(k);
-  std::vector<float> ad(nb);
-  for (int64_t i = 0; i < m; ++i) {
-    orc_quantize_row_q8_0(a + i * k, k, aq.data(), ad.data());
-    float* res = out + i * n;
-    const int64_t chunks = (n + 511) / 512;
-    pool().run(chunks, [&](int64_t c) {
-      int64_t j0 = c * 512, j1 = std::min(n, j0 + 512);
-      for (int64_t j = j0; j < j1; ++j)
-        res[j] = q8_row(qs + j * k, scales + j * nb, aq.data(), ad.data(), nb);
-    });
-  }
+  std::vector<int8_t> aq(m * k);
+  std::vector<float> ad(m * nb);
+  for (int64_t i = 0; i < m; ++i) orc_quantize_row_q8_0(a + i * k, k, &aq[i * k], &ad[i * nb]);
+  orc_gemv_codes(aq.data(), ad.data(), m, k, qs, scales, n, 1, out);
 }
 
 // matmul_transposed, f32 branch (cpu.rs:114-146): sequential dot per output.
 void orc_matmul_transposed_f32(const float* a, int64_t m, int64_t k,
                                const float* b, int64_t n, float* out) {
   pool().run(m, [&](int64_t i) {
-    for (int64_t j = 0; j < n; ++j) out[i * n + j] = dot_seq(a + i * k, b + j * k, k);
+    for (int64_t j = 0; j < n; ++j) out[i * n + j] = dot_ref(a + i * k, b + j * k, k);
   });
 }
 
@@ -362,8 +418,7 @@ void orc_matmul(const float* a, int64_t m, int64_t k, const float* b,
     for (int64_t p = 0; p < k; ++p) {
       float val = a[i * k + p];
       if (val == 0.0f) continue;
-      const float* brow = b + p * n;
-      for (int64_t j = 0; j < n; ++j) res[j] = res[j] + val * brow[j];
+      saxpy_ref(val, b + p * n, res, n);
     }
   });
 }
@@ -372,7 +427,7 @@ void orc_matmul(const float* a, int64_t m, int64_t k, const float* b,
 void orc_matmul_slice(const float* a, int64_t m, int64_t k,
                       const float* other, int64_t rows, float* out) {
   pool().run(m, [&](int64_t i) {
-    for (int64_t j = 0; j < rows; ++j) out[i * rows + j] = dot_seq(a + i * k, other + j * k, k);
+    for (int64_t j = 0; j < rows; ++j) out[i * rows + j] = dot_ref(a + i * k, other + j * k, k);
   });
 }
 
@@ -498,20 +553,6 @@ namespace {
 
 void linear_forward(const orc_model* m, const OrcLinear& w, const float* x,
                     int64_t rows, float* out) {
-  std::vector<float> jittered;
-  const uint64_t seed = g_jitter_seed.load();
-  if (seed) {
-    const uint64_t call = g_jitter_calls.fetch_add(1);
-    jittered.assign(x, x + rows * w.k);
-    const int ulps = g_jitter_ulps.load();
-    for (int64_t i = 0; i < rows * w.k; ++i) {
-      const uint64_t h = jitter_mix(seed ^ jitter_mix(call * 0x100000001B3ull + (uint64_t)i));
-      const int steps = (int)(h % (uint64_t)(2 * ulps + 1)) - ulps;
-      for (int s = 0; s < steps; ++s) jittered[i] = std::nextafter(jittered[i], INFINITY);
-      for (int s = 0; s > steps; --s) jittered[i] = std::nextafter(jittered[i], -INFINITY);
-    }
-    x = jittered.data();
-  }
   if (m->c.weight_dtype == 4)
     orc_matmul_transposed_q8w(x, rows, w.k, w.q8, w.scales, w.n, out);
   else
@@ -534,18 +575,18 @@ inline void kv_store(OrcLayer& L, bool f16, bool is_k, int64_t idx, float v) {
 // per KV head.  The reference duplicates K/V projection rows per query head
 // (loader.rs:62-98), so query head h reads KV head h / n_rep; the duplicated
 // rows produce identical cache contents, hence identical results.
-void attention_forward(orc_model* m, int li, const float* hn, int64_t seq,
-                       int64_t start_pos, float* ctx_out) {
+// The attention of layer li given the projections of `seq` rows (q_all
+// [seq][nq*hd], k_all / v_all [seq][nkv*hd], before RoPE): RoPE, K/V append
+// at start_pos.., scores, softmax and P.V (layer.rs:216-326).  ctx_out rows
+// have stride ctx_stride.
+void attention_core(orc_model* m, int li, const float* q_all, const float* k_all, const float* v_all,
+                    int64_t seq, int64_t start_pos, float* ctx_out, int64_t ctx_stride) {
   const orc_config& c = m->c;
   OrcLayer& L = m->layers[li];
-  const int64_t H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
+  const int64_t hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
   const int64_t qdim = nq * hd, kvdim = nkv * hd, ms = c.max_seq;
   const int64_t n_rep = nq / nkv;
   const bool f16 = c.kv_dtype == 1;
-  std::vector<float> q_all(seq * qdim), k_all(seq * kvdim), v_all(seq * kvdim);
-  linear_forward(m, L.w[0], hn, seq, q_all.data());  // layer.rs:177
-  linear_forward(m, L.w[1], hn, seq, k_all.data());  // layer.rs:178
-  linear_forward(m, L.w[2], hn, seq, v_all.data());  // layer.rs:179
   const int64_t total = start_pos + seq;
 
   // KV update (layer.rs:219-246): rope k per head (layer.rs:217), store k
@@ -578,6 +619,29 @@ void attention_forward(orc_model* m, int li, const float* hn, int64_t seq,
         kr[t * hd + d] = kv_load(L, f16, true, (g * ms + t) * hd + d);
         vr[t * hd + d] = kv_load(L, f16, false, (g * ms + t) * hd + d);
       }
+    if (g_attn_f64.load(std::memory_order_relaxed)) {
+      // Test-only: the same attention with every sum in float64 (scores,
+      // softmax, P.V), rounded to f32 once at the end.
+      std::vector<double> sc(total);
+      for (int64_t i = 0; i < seq; ++i) {
+        const int64_t last = seq > 1 ? start_pos + i : total - 1;
+        double mx = -INFINITY;
+        for (int64_t t = 0; t <= last; ++t) {
+          double d = 0.0;
+          for (int64_t e = 0; e < hd; ++e) d += (double)qh[i * hd + e] * (double)kr[t * hd + e];
+          sc[t] = d * (double)inv_sqrt;
+          mx = std::max(mx, sc[t]);
+        }
+        double sum = 0.0;
+        for (int64_t t = 0; t <= last; ++t) sum += (sc[t] = std::exp(sc[t] - mx));
+        for (int64_t e = 0; e < hd; ++e) {
+          double acc = 0.0;
+          for (int64_t t = 0; t <= last; ++t) acc += sc[t] * (double)vr[t * hd + e];
+          ctx_out[i * ctx_stride + h * hd + e] = (float)(acc / sum);
+        }
+      }
+      return;
+    }
     std::vector<float> scores(seq * total), probs(seq * total);
     orc_matmul_slice(qh.data(), seq, hd, kr.data(), total, scores.data());  // layer.rs:257
     for (auto& s : scores) s = s * inv_sqrt;                                 // layer.rs:258
@@ -602,13 +666,25 @@ void attention_forward(orc_model* m, int li, const float* hn, int64_t seq,
         for (int64_t p = 0; p < total; ++p) {
           float val = probs[i * total + p];
           if (val == 0.0f) continue;
-          for (int64_t d = 0; d < hd; ++d) res[d] = res[d] + val * vr[p * hd + d];
+          saxpy_ref(val, &vr[p * hd], res, hd);
         }
       }
       for (int64_t i = 0; i < seq; ++i)
-        std::memcpy(&ctx_out[i * H + h * hd], &ctx[i * hd], hd * sizeof(float));
+        std::memcpy(&ctx_out[i * ctx_stride + h * hd], &ctx[i * hd], hd * sizeof(float));
     }
   });
+}
+
+void attention_forward(orc_model* m, int li, const float* hn, int64_t seq,
+                       int64_t start_pos, float* ctx_out) {
+  const orc_config& c = m->c;
+  OrcLayer& L = m->layers[li];
+  const int64_t qdim = (int64_t)c.n_heads * c.head_dim, kvdim = (int64_t)c.n_kv_heads * c.head_dim;
+  std::vector<float> q_all(seq * qdim), k_all(seq * kvdim), v_all(seq * kvdim);
+  linear_forward(m, L.w[0], hn, seq, q_all.data());  // layer.rs:177
+  linear_forward(m, L.w[1], hn, seq, k_all.data());  // layer.rs:178
+  linear_forward(m, L.w[2], hn, seq, v_all.data());  // layer.rs:179
+  attention_core(m, li, q_all.data(), k_all.data(), v_all.data(), seq, start_pos, ctx_out, qdim);
 }
 
 }  // namespace
@@ -718,6 +794,48 @@ int orc_model_kv_read(orc_model* m, int layer, int kv_head, int64_t pos0,
       k[i * c.head_dim + d] = kv_load(L, f16, true, idx);
       v[i * c.head_dim + d] = kv_load(L, f16, false, idx);
     }
+  return 0;
+}
+
+// Test probes: one kernel's arithmetic on given inputs.
+// The block loop of matmul_transposed (kernel_avx2 cpu.rs:888-941, or the
+// aarch64 order) over `m` rows of already-quantised activations: xq [m][k]
+// codes, xd [m][k/32] scales; weights Q4 (q8w == 0: reference nibble order)
+// or Q8 codes.
+void orc_gemv_codes(const int8_t* xq, const float* xd, int64_t m, int64_t k, const void* w,
+                    const float* scales, int64_t n, int q8w, float* out) {
+  const int64_t nb = k / 32;
+  const int64_t chunks = (n + 511) / 512;
+  pool().run(chunks, [&](int64_t c) {
+    const int64_t j0 = c * 512, j1 = std::min(n, j0 + 512);
+    for (int64_t i = 0; i < m; ++i) {
+      const int8_t* aq = xq + i * k;
+      const float* ad = xd + i * nb;
+      float* res = out + i * n;
+      for (int64_t j = j0; j < j1; ++j)
+        res[j] = q8w ? q8_row((const int8_t*)w + j * k, scales + j * nb, aq, ad, nb)
+                     : q4_row((const uint8_t*)w + j * (k / 2), scales + j * nb, aq, ad, nb);
+    }
+  });
+}
+
+// The attention of `layer` for `seq` rows given their Q|K|V projections
+// qkv [seq][(nq + 2 nkv) hd] (before RoPE), at positions start_pos..: the K/V
+// rows are appended to the oracle's cache, ctx [seq][nq hd] is written.
+int orc_model_attention(orc_model* m, int layer, const float* qkv, int64_t seq, int64_t start_pos,
+                        float* ctx) {
+  const orc_config& c = m->c;
+  if (layer < 0 || layer >= c.n_layers || seq <= 0 || start_pos < 0 || start_pos + seq > c.max_seq)
+    return -1;
+  const int64_t qdim = (int64_t)c.n_heads * c.head_dim, kvdim = (int64_t)c.n_kv_heads * c.head_dim;
+  const int64_t rows = qdim + 2 * kvdim;
+  std::vector<float> q_all(seq * qdim), k_all(seq * kvdim), v_all(seq * kvdim);
+  for (int64_t i = 0; i < seq; ++i) {
+    std::memcpy(&q_all[i * qdim], qkv + i * rows, qdim * sizeof(float));
+    std::memcpy(&k_all[i * kvdim], qkv + i * rows + qdim, kvdim * sizeof(float));
+    std::memcpy(&v_all[i * kvdim], qkv + i * rows + qdim + kvdim, kvdim * sizeof(float));
+  }
+  attention_core(m, layer, q_all.data(), k_all.data(), v_all.data(), seq, start_pos, ctx, qdim);
   return 0;
 }
 

@@ -40,10 +40,17 @@ extern "C" {
 
 void orc_set_threads(int n);
 int orc_get_threads(void);
-/* Test-only noise model: seed != 0 moves every linear-layer input by a
- * pseudo-random whole number of ulps in [-ulps, ulps] (per element and call)
- * before the reference arithmetic; seed 0 turns it off (the default). */
-void orc_set_jitter(uint64_t seed, int ulps);
+/* Test-only: which build of the reference the arithmetic restates, 0 = x86-64
+ * (default), 1 = aarch64 (NEON orders of cpu.rs:461-544,558-619,747-886). */
+void orc_set_arch(int arch);
+int orc_get_arch(void);
+/* Test-only: attention scores, softmax and P.V summed in float64 (on != 0),
+ * the rest of the reference arithmetic unchanged. */
+void orc_set_attn_f64(int on);
+/* Test-only: record every Q8_0 code produced (on != 0 clears the record);
+ * orc_recorded_codes copies up to `cap` of them and returns the count. */
+void orc_record_codes(int on);
+int64_t orc_recorded_codes(int8_t* out, int64_t cap);
 
 /* ---- cpu.rs primitives -------------------------------------------------- */
 void orc_quantize_row_q8_0(const float* x, int64_t k, int8_t* q, float* d);
@@ -104,6 +111,13 @@ int orc_model_kv_read(orc_model* m, int layer, int kv_head, int64_t pos0,
 int orc_model_forward(orc_model* m, const int32_t* tokens, int64_t n,
                       int64_t start_pos, float* logits, int all_rows,
                       float* trace);
+/* Test probes: the block loop over already-quantised activation rows
+ * (xq [m][k], xd [m][k/32]) with Q4 (q8w = 0) or Q8 weight codes; and the
+ * attention of one layer given the Q|K|V projections of `seq` rows. */
+void orc_gemv_codes(const int8_t* xq, const float* xd, int64_t m, int64_t k, const void* w,
+                    const float* scales, int64_t n, int q8w, float* out);
+int orc_model_attention(orc_model* m, int layer, const float* qkv, int64_t seq,
+                        int64_t start_pos, float* ctx);
 /* Greedy token loop (main.rs:128-327 with argmax).  out: n_steps ids;
  * margins: top1-top2 logit gap per step (may be NULL). */
 int orc_model_generate(orc_model* m, const int32_t* prompt, int64_t n_prompt,

@@ -23,7 +23,8 @@ def pytest_configure(config):
 def orc():
     import oracle
     oracle.lib()
-    oracle.set_threads(int(os.environ.get("ORACLE_THREADS", "0")))
+    # the GPU hosts give one GPU's job 16 cores, whatever os.cpu_count() says
+    oracle.set_threads(int(os.environ.get("ORACLE_THREADS", str(min(16, os.cpu_count() or 1)))))
     return oracle
 
 

@@ -14,11 +14,12 @@ from conftest import rel_close
 pytestmark = pytest.mark.gpu
 F32 = np.float32
 
-# (n, k): every decode GEMV shape of the 1B and 8B workloads (q, k|v, o,
-# gate|up, down, lm_head) plus the reference's own test shapes.
+# (n, k): every decode GEMV shape of the 1B, 8B and 70B workloads (q, k|v,
+# o, gate|up, down, lm_head) plus the reference's own test shapes.
 GEMV_SHAPES = [
     (64, 128), (128, 256), (2048, 2048), (512, 2048), (16384, 2048), (2048, 8192),
     (128256, 2048), (4096, 4096), (1024, 4096), (28672, 4096), (4096, 14336), (128256, 4096),
+    (8192, 8192), (1024, 8192), (57344, 8192), (8192, 28672), (128256, 8192),
 ]
 
 

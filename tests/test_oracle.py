@@ -248,3 +248,93 @@ def test_argmax_lowest_index_on_ties(orc):
     assert i == 1 and m == 0.0
     i, m = orc.argmax(np.array([3, 1, 2], F32))
     assert i == 0 and m == 1.0
+
+
+# ---- the aarch64 restatement (orc_set_arch(1)) ------------------------------
+# Known answers worked out by hand from the NEON code's order, on inputs whose
+# products are exact, so that only the order of additions (and fusing)
+# decides the result; the x86 build gives a different value on each.
+
+def _with_arch(orc, arch, fn):
+    orc.set_arch(arch)
+    try:
+        return fn()
+    finally:
+        orc.set_arch(0)
+
+
+def test_neon_dot_pairs_accumulators(orc):
+    """simd_dot_f32 on aarch64 (cpu.rs:518-521, 535): elements 0, 8 and 12
+    sit in accumulators 0, 2 and 3 (lane 0); (s0 + s1) + (s2 + s3) adds the
+    two ones before they meet 2^24, so the sum is 2^24 + 2.  In sequence
+    each +1 on 2^24 rounds back to 2^24."""
+    a = np.zeros((1, 32), F32)
+    a[0, 0], a[0, 8], a[0, 12] = 2.0 ** 24, 1.0, 1.0
+    b = np.ones((1, 32), F32)
+    neon = _with_arch(orc, 1, lambda: orc.matmul_slice(a, b, 1))[0, 0]
+    x86 = orc.matmul_slice(a, b, 1)[0, 0]
+    assert neon == 2.0 ** 24 + 2 and x86 == 2.0 ** 24
+
+
+def test_neon_dot_fuses_multiply_add(orc):
+    """vfmaq_f32 (cpu.rs:481): elements 0 and 32 share accumulator 0 lane 0;
+    -1 + (1 + 2^-12)^2 fused keeps the 2^-24 term (2^-11 + 2^-24), unfused
+    the product rounds it away (2^-11)."""
+    a = np.zeros((1, 64), F32)
+    b = np.zeros((1, 64), F32)
+    a[0, 0], b[0, 0] = -1.0, 1.0
+    a[0, 32] = b[0, 32] = 1.0 + 2.0 ** -12
+    neon = _with_arch(orc, 1, lambda: orc.matmul_slice(a, b, 1))[0, 0]
+    x86 = orc.matmul_slice(a, b, 1)[0, 0]
+    assert neon == 2.0 ** -11 + 2.0 ** -24 and x86 == 2.0 ** -11
+
+
+def test_neon_q4_gemv_adds_four_blocks_first(orc):
+    """kernel_neon_sdot (cpu.rs:850): blocks 4 and 5 (one group) are summed
+    before the running total 2^24 from block 0, giving 2^24 + 2; the x86
+    block loop (cpu.rs:932) adds them one at a time and stays at 2^24.
+    Block sums are 1 (one weight code 9 against activation code 1), scales
+    d_w * d_a = 2^24 for block 0 and 1 otherwise."""
+    nb = 8
+    xq = np.zeros((1, 32 * nb), np.int8)
+    for b in (0, 4, 5):
+        xq[0, 32 * b] = 1
+    xd = np.ones((1, nb), F32)
+    xd[0, 0] = 2.0 ** 12
+    qs = np.full(16 * nb, 0x88, np.uint8)    # every code 8: (q - 8) = 0
+    qs[16 * np.arange(nb)] = 0x89            # element 0 of each block: code 9
+    sc = np.ones(nb, F32)
+    sc[0] = 2.0 ** 12
+    neon = _with_arch(orc, 1, lambda: orc.gemv_codes(xq, xd, qs, sc, 1))[0, 0]
+    x86 = orc.gemv_codes(xq, xd, qs, sc, 1)[0, 0]
+    assert neon == 2.0 ** 24 + 2 and x86 == 2.0 ** 24
+
+
+def test_neon_saxpy_fuses_over_whole_steps(orc):
+    """simd_saxpy on aarch64 (cpu.rs:570): y = fma(alpha, x, y) over
+    32-element steps, unfused for the leftovers (cpu.rs:610-615): through
+    matmul (cpu.rs:198), y[0] = -1 + (1 + 2^-12)^2 keeps 2^-24 when fused;
+    element 32 (a leftover of n = 33) does not."""
+    a = np.array([[1.0, 1.0 + 2.0 ** -12]], F32)
+    b = np.zeros((2, 33), F32)
+    b[0, 0] = b[0, 32] = -1.0
+    b[1, 0] = b[1, 32] = 1.0 + 2.0 ** -12
+    neon = _with_arch(orc, 1, lambda: orc.matmul(a, b))[0]
+    x86 = orc.matmul(a, b)[0]
+    assert neon[0] == 2.0 ** -11 + 2.0 ** -24 and neon[32] == 2.0 ** -11
+    assert x86[0] == 2.0 ** -11 and x86[32] == 2.0 ** -11
+
+
+def test_gemv_codes_matches_matmul_transposed(orc, rng):
+    """The probe entry (block loop on given codes) equals matmul_transposed,
+    which quantises first, bit for bit."""
+    m, n, k = 3, 40, 256
+    a = rng.normal(0, 1, (m, k)).astype(F32)
+    qs = rng.integers(0, 256, n * k // 2).astype(np.uint8)
+    sc = rng.uniform(0.003, 0.006, n * k // 32).astype(F32)
+    xq, xd = zip(*(orc.quantize_row_q8_0(a[i]) for i in range(m)))
+    got = orc.gemv_codes(np.stack(xq), np.stack(xd), qs, sc, n)
+    assert np.array_equal(got, orc.matmul_transposed_q4(a, qs, sc, n))
+    w8 = rng.integers(-127, 128, n * k).astype(np.int8)
+    got8 = orc.gemv_codes(np.stack(xq), np.stack(xd), w8, sc, n, q8w=True)
+    assert np.array_equal(got8, orc.matmul_transposed_q8w(a, w8, sc, n))
