@@ -132,6 +132,17 @@ int llmrs_scale(const llmrs_tensor* x, float value, llmrs_tensor** out);
 /* Backend::copy_from (backend.rs:39). */
 int llmrs_copy_from(const llmrs_tensor* t, llmrs_tensor** out);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): Backend::matmul_transposed (backend.rs:24) into `out`,
+ * an f32 tensor of shape [m, n] the caller allocated beforehand, with no
+ * device allocation.  Quantised b with m > 1 stages each row's Q8_0 codes in
+ * a fixed per-device scratch of 16 MiB: m*k + 4*m*k/32 bytes must fit
+ * (else LLMRS_E_RANGE).  Calls that overlap on one device race on that
+ * scratch.  Results equal llmrs_matmul_transposed's. */
+int llmrs_matmul_transposed_noalloc(const llmrs_tensor* a, const llmrs_tensor* b,
+                                    llmrs_tensor* out);
+
 /* ---- resident decode model (no trait counterpart) ----------------------- */
 /* Mirrors LlamaConfig (src/core/config.rs:3-17) plus what the reference
  * hard-codes: head_dim (loader.rs:164 derives hidden/num_heads), max_seq

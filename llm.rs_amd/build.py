@@ -18,6 +18,7 @@ PKG = Path(__file__).resolve().parent
 REPO = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "lib"
+BUILD = PKG / "_build"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 
@@ -31,6 +32,10 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
+HOST_HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
 HOST_FLAGS = [
     "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-mf16c",
     "-Wall", "-Wextra", "-Wno-unused-parameter", "-D__HIP_PLATFORM_AMD__",
@@ -43,8 +48,8 @@ def _run_all(cmds: list[list[str]]) -> None:
     failed = []
     for cmd, p in procs:
         out, _ = p.communicate()
-        noise = "unknown target feature"
-        lines = [ln for ln in (out or "").splitlines() if noise not in ln and ln.strip()]
+        noise = ("unknown target feature", "is not a recognized feature for this target")
+        lines = [ln for ln in (out or "").splitlines() if not any(n in ln for n in noise) and ln.strip()]
         if p.returncode != 0:
             failed.append((cmd, "\n".join(lines)))
         elif lines:
@@ -65,18 +70,29 @@ def build(verbose: bool = False) -> Path:
         tmp = out.with_suffix(".hsaco.tmp")
         cmds.append([hipcc, *HIP_FLAGS, f"-I{CSRC}", "-o", str(tmp), str(src)])
         outs.append((tmp, out))
+    # Host sources with device data of their own (csrc/host/*.hip) are
+    # compiled by hipcc into objects linked into the host library.
+    BUILD.mkdir(exist_ok=True)
+    host_objs = []
+    obj_cmds = []
+    for src in sorted((CSRC / "host").glob("*.hip")):
+        obj = BUILD / f"{src.stem}.o"
+        obj_cmds.append([hipcc, *HOST_HIP_FLAGS, f"-I{REPO / 'include'}", f"-I{CSRC}", "-c", "-o", str(obj),
+                         str(src)])
+        host_objs.append(str(obj))
     so = LIB / "libllmrs_hip.so"
     so_tmp = LIB / "libllmrs_hip.so.tmp"
-    cmds.append([
+    link = [
         os.environ.get("CXX", "g++"), *HOST_FLAGS, f"-I{ROCM / 'include'}", f"-I{REPO / 'include'}",
-        f"-I{CSRC}", "-o", str(so_tmp), *map(str, sorted((CSRC / "host").glob("*.cpp"))),
+        f"-I{CSRC}", "-o", str(so_tmp), *map(str, sorted((CSRC / "host").glob("*.cpp"))), *host_objs,
         f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}", "-ldl", "-lpthread",
-    ])
+    ]
     outs.append((so_tmp, so))
     if verbose:
-        for c in cmds:
+        for c in cmds + obj_cmds + [link]:
             print("$", " ".join(c))
-    _run_all(cmds)
+    _run_all(cmds + obj_cmds)
+    _run_all([link])
     for tmp, out in outs:
         tmp.replace(out)
     return LIB

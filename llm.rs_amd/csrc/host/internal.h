@@ -59,10 +59,18 @@ class Allocator {
   std::map<void*, size_t> live_;
 };
 
+// Device scratch of llmrs_matmul_transposed_noalloc (noalloc.hip): a fixed
+// array of the library's own code object, one per device.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+// Its device address on the current device (hipGetSymbolAddress).
+void* noalloc_scratch_address();
+
 struct Context {
   int device = -1;
   hipStream_t stream = nullptr;
   int num_cus = 0;
+  void* noalloc_scratch = nullptr;  // device address of the scratch on `device`
+  std::string noalloc_error;        // why it is null
   std::vector<hipModule_t> modules;
   std::map<std::string, hipFunction_t> kernels;
   Allocator alloc;

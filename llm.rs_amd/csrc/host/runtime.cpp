@@ -270,6 +270,14 @@ int llmrs_init(int device_ordinal, const char* hsaco_dir) {
       LLMRS_HIP(hipGetDeviceProperties(&prop, device_ordinal));
       c->num_cus = prop.multiProcessorCount;
       LLMRS_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+      // the no-allocation entry point's scratch, resolved with the device
+      // current; a failure is reported by that entry point, not by init
+      try {
+        c->noalloc_scratch = noalloc_scratch_address();
+      } catch (const Error& e) {
+        c->noalloc_scratch = nullptr;
+        c->noalloc_error = e.what();
+      }
       std::string dir = hsaco_dir ? std::string(hsaco_dir) : library_dir();
       for (const char* name : {"gemv", "attention", "ops", "prefill"}) {
         std::string path = dir + "/" + name + ".hsaco";

@@ -71,6 +71,7 @@ _SIGS = {
     "llmrs_tensor_free": (C.c_int, [C.c_void_p]),
     "llmrs_matmul": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]),
     "llmrs_matmul_transposed": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]),
+    "llmrs_matmul_transposed_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "llmrs_matmul_slice": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.POINTER(C.c_void_p)]),
     "llmrs_add_assign": (C.c_int, [C.c_void_p, C.c_void_p]),
     "llmrs_silu_mul": (C.c_int, [C.c_void_p, C.c_void_p]),
@@ -259,6 +260,12 @@ class HipBackend:
 
     def matmul_transposed(self, a: Tensor, b: Tensor) -> Tensor:  # backend.rs:24
         return _out_tensor(lib().llmrs_matmul_transposed, a.handle, b.handle)
+
+    def matmul_transposed_noalloc(self, a: Tensor, b: Tensor, out: Tensor) -> None:
+        """matmul_transposed into a pre-allocated [m, n] f32 tensor, with no
+        device allocation (fixed per-device scratch; no reference
+        counterpart)."""
+        _check(lib().llmrs_matmul_transposed_noalloc(a.handle, b.handle, out.handle))
 
     def matmul_slice(self, a: Tensor, other_data, rows: int, cols: int) -> Tensor:  # backend.rs:28
         od = np.ascontiguousarray(other_data, dtype=np.float32)
