@@ -370,7 +370,7 @@ def main() -> int:
     for name, (ms, _, _) in per.items():
         kernels[name]["share"] = round(ms / tot, 4)
     # The dominant kernel: the gate|up GEMV.
-    dom = next(n for n in kernels if n.startswith("gemv_") and "_norm_silu_" in n)
+    dom = next(n for n in kernels if n.startswith("gemv_") and "_silu_" in n)
     ms, by, n = per[dom]
     dom_us, dom_bytes = ms / n * 1e3, by / n
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9

@@ -289,6 +289,15 @@ int llmrs_model_probe_prefill_layer(llmrs_model* m, int layer, size_t start_pos,
                                     size_t n, const float* x,
                                     llmrs_layer_probe* out);
 
+/* Profiling (no reference counterpart): one eager decode step in which the
+ * decode GEMV of `slot` (LLMRS_W_Q = Q|K|V, LLMRS_W_O, LLMRS_W_GATE =
+ * gate|up, LLMRS_W_DOWN) of `layer` records per-workgroup stamps.  Per
+ * workgroup 9 values: start, operand ready, unit loop done, end, input
+ * arrived, norm factor known, operand quantised (us from the launch's
+ * earliest start; -1 = not recorded), the XCC id and the HW_ID register.
+ * Returns the count written. */
+int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
+                               int cap);
 /* Algorithmic weight bytes streamed per decode token (all linear weights). */
 double llmrs_model_weight_bytes(const llmrs_model* m);
 

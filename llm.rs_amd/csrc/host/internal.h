@@ -136,6 +136,7 @@ int gemm_group_m();
 struct GemvPlan {
   std::string name;
   unsigned grid = 1;
+  unsigned threads = 256;
   size_t lds = 0;
 };
 GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus);

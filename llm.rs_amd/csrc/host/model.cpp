@@ -65,6 +65,12 @@ struct llmrs_model {
   float *logits = nullptr, *ctx_d = nullptr, *m_d = nullptr, *part_o = nullptr, *part_ml = nullptr;
   float *part_val = nullptr, *rope_cos = nullptr, *rope_sin = nullptr, *trace = nullptr;
   int8_t *ctx_q = nullptr, *m_q = nullptr;
+  // RMSNorm operands from the producers (gemv_core.h PRO_NQ): codes of x*w,
+  // d' and sums of squares per block, of x (Q|K|V and lm_head input) and of
+  // h (gate|up input)
+  int8_t *x_q = nullptr, *h_q = nullptr;
+  float *x_d = nullptr, *x_ss = nullptr, *h_d = nullptr, *h_ss = nullptr;
+  bool nq = true;  // false: RMSNorm + Q8_0 inside the consumers (LLMRS_NQ=0)
   int *part_idx = nullptr, *counters = nullptr, *tokens = nullptr, *gen = nullptr;
   int *pos = nullptr, *n_prompt = nullptr, *err = nullptr;
   int nsplit = 1, attn_streams = 1, lm_grid = 1, cap = 0;
@@ -153,13 +159,36 @@ std::string attn_kernel(const llmrs_model* m) {
          (m->c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32") + (m->attn_streams > 1 ? "_s4" : "");
 }
 
+// x = the embedding of the token at the device position, or (x_in set) the
+// row x_in; with the consumers' RMSNorm folded into the producers, also the
+// first RMSNorm's operand of x with weight norm_w (PRO_NQ of gemv_core.h).
+void enqueue_embed(llmrs_model* m, Launcher& L, const float* x_in, const float* norm_w) {
+  const int H = m->c.hidden;
+  EmbedArgs e{};
+  e.table = m->embed;
+  e.tokens = m->tokens;
+  e.pos_ptr = m->pos;
+  e.x = m->x;
+  e.err = m->err;
+  e.hidden = H;
+  e.vocab = m->c.vocab;
+  if (m->nq) {
+    e.norm_w = norm_w;
+    e.xq = m->x_q;
+    e.xd = m->x_d;
+    e.xss = m->x_ss;
+  }
+  e.x_in = x_in;
+  L("embed_gather", (m->nq ? 9.25 : 8.0) * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
+}
+
 // The decode GEMV of one linear slot of layer li (LLMRS_W_Q = the stacked
 // Q|K|V rows, LLMRS_W_O, LLMRS_W_GATE = gate|up, LLMRS_W_DOWN) with its fused
 // prologue and epilogue, on the decode activation buffers.
 // `probe_xq` / `probe_xd` (test probes, may be null) receive the Q8_0
 // operand the GEMV's prologue built.
 void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot, int8_t* probe_xq = nullptr,
-                    float* probe_xd = nullptr) {
+                    float* probe_xd = nullptr, unsigned long long* stamps = nullptr) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, F = c.ffn;
   const int cus = ctx().num_cus;
@@ -173,12 +202,20 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot, int8_t* probe
       g.ws = Lb.qkv.scales;
       g.n = Lb.qkv.n;
       g.k = H;
-      g.x = m->x;
-      g.norm_w = Lb.norm[0];
       g.eps = c.rms_eps;
       g.y = m->qkv;
-      kind = "norm_store";
-      bytes = linear_weight_bytes(m, Lb.qkv) + 8.0 * H + 4.0 * g.n;
+      if (m->nq) {
+        g.xq = m->x_q;
+        g.xd = m->x_d;
+        g.xss = m->x_ss;
+        kind = "nq_store";
+        bytes = linear_weight_bytes(m, Lb.qkv) + 1.125 * H + 4.0 * g.n;
+      } else {
+        g.x = m->x;
+        g.norm_w = Lb.norm[0];
+        kind = "norm_store";
+        bytes = linear_weight_bytes(m, Lb.qkv) + 8.0 * H + 4.0 * g.n;
+      }
       break;
     case LLMRS_W_O:  // O projection + residual (layer.rs:386)
       g.wq = Lb.o.codes;
@@ -191,20 +228,36 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot, int8_t* probe
       g.res = m->x;
       kind = "q8_resid";
       bytes = linear_weight_bytes(m, Lb.o) + 1.125 * g.k + 8.0 * H;
+      if (m->nq) {  // and the post-attention RMSNorm's operand (layer.rs:393)
+        g.norm_next = Lb.norm[1];
+        g.yq = m->h_q;
+        g.yd = m->h_d;
+        g.yss = m->h_ss;
+        kind = "q8_nq";
+        bytes += 5.25 * H;
+      }
       break;
     case LLMRS_W_GATE:  // gate|up + SiLU (layer.rs:40-89, 400)
       g.wq = Lb.gu.codes;
       g.ws = Lb.gu.scales;
       g.n = 2 * F;
       g.k = H;
-      g.x = m->h;
-      g.norm_w = Lb.norm[1];
       g.eps = c.rms_eps;
       g.y = m->mf;
       g.yq = m->m_q;
       g.yd = m->m_d;
-      kind = "norm_silu";
-      bytes = linear_weight_bytes(m, Lb.gu) + 8.0 * H + 5.125 * F;
+      if (m->nq) {
+        g.xq = m->h_q;
+        g.xd = m->h_d;
+        g.xss = m->h_ss;
+        kind = "nq_silu";
+        bytes = linear_weight_bytes(m, Lb.gu) + 1.125 * H + 5.125 * F;
+      } else {
+        g.x = m->h;
+        g.norm_w = Lb.norm[1];
+        kind = "norm_silu";
+        bytes = linear_weight_bytes(m, Lb.gu) + 8.0 * H + 5.125 * F;
+      }
       break;
     case LLMRS_W_DOWN:  // down projection + residual (layer.rs:403)
       g.wq = Lb.down.codes;
@@ -217,14 +270,36 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot, int8_t* probe
       g.res = m->h;
       kind = "q8_resid";
       bytes = linear_weight_bytes(m, Lb.down) + 1.125 * F + 8.0 * H;
+      if (m->nq) {  // and the next RMSNorm's operand: next layer's input norm or the final norm
+        g.norm_next = li + 1 < c.n_layers ? m->layers[li + 1].norm[0] : m->final_norm;
+        g.yq = m->x_q;
+        g.yd = m->x_d;
+        g.yss = m->x_ss;
+        kind = "q8_nq";
+        bytes += 5.25 * H;
+      }
       break;
     default:
       fail(LLMRS_E_INVALID, "enqueue_linear: slot must be Q, O, GATE or DOWN");
   }
   g.probe_xq = probe_xq;
   g.probe_xd = probe_xd;
+  g.ts = stamps;
   const GemvPlan p = gemv_plan(m->wt, kind, g.n, g.k, cus);
-  L(p.name, bytes, dim3(p.grid), dim3(256), p.lds, g);
+  L(p.name, bytes, dim3(p.grid), dim3(p.threads), p.lds, g);
+}
+
+// Workgroups of the decode GEMV of a linear slot (for stamp buffers).
+unsigned linear_grid(llmrs_model* m, int slot) {
+  const llmrs_model_config& c = m->c;
+  const int H = c.hidden, F = c.ffn, qd = c.n_heads * c.head_dim, cus = ctx().num_cus;
+  switch (slot) {
+    case LLMRS_W_Q: return gemv_plan(m->wt, m->nq ? "nq_store" : "norm_store", m->qkv_rows, H, cus).grid;
+    case LLMRS_W_O: return gemv_plan(m->wt, m->nq ? "q8_nq" : "q8_resid", H, qd, cus).grid;
+    case LLMRS_W_GATE: return gemv_plan(m->wt, m->nq ? "nq_silu" : "norm_silu", 2 * F, H, cus).grid;
+    case LLMRS_W_DOWN: return gemv_plan(m->wt, m->nq ? "q8_nq" : "q8_resid", H, F, cus).grid;
+  }
+  fail(LLMRS_E_INVALID, "slot must be Q, O, GATE or DOWN");
 }
 
 // Decode attention of layer li at the device position: RoPE of q and the new
@@ -259,8 +334,7 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
   const llmrs_model_config& c = m->c;
   const int H = c.hidden;
 
-  EmbedArgs e{m->embed, m->tokens, m->pos, m->x, m->err, H, c.vocab};
-  L("embed_gather", 8.0 * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
+  enqueue_embed(m, L, nullptr, m->layers[0].norm[0]);
 
   for (int li = 0; li < c.n_layers; ++li) {
     if (trace_dev)
@@ -290,17 +364,23 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
     g.ws = m->lm_head.scales;
     g.n = c.vocab;
     g.k = H;
-    g.x = m->x;
-    g.norm_w = m->final_norm;
     g.eps = c.rms_eps;
+    if (m->nq) {
+      g.xq = m->x_q;
+      g.xd = m->x_d;
+      g.xss = m->x_ss;
+    } else {
+      g.x = m->x;
+      g.norm_w = m->final_norm;
+    }
     g.y = write_logits ? m->logits : nullptr;
     g.part_val = m->part_val;
     g.part_idx = m->part_idx;
     g.probe_xq = probe_xq;
     g.probe_xd = probe_xd;
-    const GemvPlan p = gemv_plan(m->wt, "norm_argmax", g.n, g.k, cus);
+    const GemvPlan p = gemv_plan(m->wt, m->nq ? "nq_argmax" : "norm_argmax", g.n, g.k, cus);
     LLMRS_REQUIRE((int)p.grid == m->lm_grid, LLMRS_E_INVALID, "lm_head grid changed since model creation");
-    L(p.name, linear_weight_bytes(m, m->lm_head) + 8.0 * H, dim3(p.grid), dim3(256), p.lds, g);
+    L(p.name, linear_weight_bytes(m, m->lm_head) + (m->nq ? 1.125 : 8.0) * H, dim3(p.grid), dim3(256), p.lds, g);
   }
   ArgmaxFinalArgs f{m->part_val, m->part_idx, m->lm_grid, m->pos, m->n_prompt, m->tokens, m->gen, m->cap};
   L("argmax_final", 8.0 * m->lm_grid, dim3(1), dim3(256), 0, f);
@@ -443,7 +523,8 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
                                  m->pf_x, H * sizeof(float), H * sizeof(float), M,
                                  hipMemcpyDeviceToDevice, L.s));
   };
-  EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab};
+  EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab, nullptr, nullptr, nullptr,
+              nullptr, nullptr};
   L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), dim3(256), 0, e);
   for (int li = 0; li < c.n_layers; ++li) {
     trace(li);
@@ -451,8 +532,12 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
   }
   trace(c.n_layers);
   if (head) {
-    LLMRS_HIP(hipMemcpyAsync(m->x, m->pf_x + (size_t)(M - 1) * H, H * sizeof(float),
-                             hipMemcpyDeviceToDevice, L.s));
+    if (m->nq) {
+      enqueue_embed(m, L, m->pf_x + (size_t)(M - 1) * H, m->final_norm);
+    } else {
+      LLMRS_HIP(hipMemcpyAsync(m->x, m->pf_x + (size_t)(M - 1) * H, H * sizeof(float),
+                               hipMemcpyDeviceToDevice, L.s));
+    }
     enqueue_head(m, L, write_logits);
   }
 }
@@ -621,7 +706,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
       splits = std::min((tiles + 3) / 4, std::max(1, cx.num_cus / nkv));
     }
     m->nsplit = std::max(1, env_int("LLMRS_ATTN_SPLITS", splits));
-    m->lm_grid = (int)gemv_plan(m->wt, "norm_argmax", c.vocab, H, cx.num_cus).grid;
+    m->lm_grid = (int)gemv_plan(m->wt, "nq_argmax", c.vocab, H, cx.num_cus).grid;
     m->layers.resize(c.n_layers);
     for (auto& L : m->layers) {
       m->alloc_linear(L.qkv, m->qkv_rows, H);
@@ -643,6 +728,18 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     m->ctx_q = m->dalloc<int8_t>((size_t)nq * hd);
     m->ctx_d = m->dalloc<float>((size_t)nq * hd / 32);
     m->mf = m->dalloc<float>(F);
+    // Producer-side RMSNorm operands when the producers' 32-row tiles fill
+    // the GPU (measured on 256 CUs: hidden 8192, 70B shape, 103.9 -> 110.2
+    // tok/s; hidden 4096, 8B shape, the 128-tile O and down GEMVs lose more
+    // than the consumers' prologues gain, 724 -> 707); LLMRS_NQ=0/1 forces.
+    const int nqe = env_int("LLMRS_NQ", -1);
+    m->nq = H / 32 <= 256 && (nqe >= 0 ? nqe != 0 : H / 32 >= cx.num_cus);
+    m->x_q = m->dalloc<int8_t>(H);
+    m->h_q = m->dalloc<int8_t>(H);
+    m->x_d = m->dalloc<float>(H / 32);
+    m->h_d = m->dalloc<float>(H / 32);
+    m->x_ss = m->dalloc<float>(H / 32);
+    m->h_ss = m->dalloc<float>(H / 32);
     m->m_q = m->dalloc<int8_t>(F);
     m->m_d = m->dalloc<float>(F / 32);
     m->logits = m->dalloc<float>(c.vocab);
@@ -669,11 +766,12 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     }
     LLMRS_HIP(hipStreamSynchronize(cx.stream));
     // Resolve every kernel of the step now, so graph capture never has to.
-    (void)kernel(gemv_plan(m->wt, "norm_store", m->qkv_rows, H, cx.num_cus).name);
-    (void)kernel(gemv_plan(m->wt, "q8_resid", H, nq * hd, cx.num_cus).name);
-    (void)kernel(gemv_plan(m->wt, "norm_silu", 2 * F, H, cx.num_cus).name);
-    (void)kernel(gemv_plan(m->wt, "q8_resid", H, F, cx.num_cus).name);
-    (void)kernel(gemv_plan(m->wt, "norm_argmax", c.vocab, H, cx.num_cus).name);
+    const bool nqk = m->nq;
+    (void)kernel(gemv_plan(m->wt, nqk ? "nq_store" : "norm_store", m->qkv_rows, H, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, nqk ? "q8_nq" : "q8_resid", H, nq * hd, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, nqk ? "nq_silu" : "norm_silu", 2 * F, H, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, nqk ? "q8_nq" : "q8_resid", H, F, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, nqk ? "nq_argmax" : "norm_argmax", c.vocab, H, cx.num_cus).name);
     (void)kernel("embed_gather");
     (void)kernel("argmax_final");
     (void)kernel(attn_kernel(m.get()));
@@ -1078,6 +1176,55 @@ int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
   return rc ? rc : count;
 }
 
+int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out, int cap) {
+  int count = 0;
+  int rc = guard([&] {
+    LLMRS_REQUIRE(m && m->begun && out, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
+    LLMRS_REQUIRE(layer >= 0 && layer < m->c.n_layers, LLMRS_E_RANGE, "layer out of range");
+    LLMRS_REQUIRE(m->host_pos + 1 <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
+    const unsigned nwg = linear_grid(m, slot);
+    unsigned long long* ts = nullptr;
+    LLMRS_HIP(hipMalloc(&ts, (size_t)nwg * 8 * sizeof(unsigned long long)));
+    hipStream_t s = ctx().stream;
+    std::vector<unsigned long long> h((size_t)nwg * 8);
+    try {
+      LLMRS_HIP(hipMemsetAsync(ts, 0, h.size() * sizeof(unsigned long long), s));
+      const llmrs_model_config& c = m->c;
+      Launcher L{s};
+      enqueue_embed(m, L, nullptr, m->layers[0].norm[0]);
+      for (int li = 0; li < c.n_layers; ++li) {
+        enqueue_linear(m, L, li, LLMRS_W_Q, nullptr, nullptr, li == layer && slot == LLMRS_W_Q ? ts : nullptr);
+        enqueue_attention(m, L, li);
+        enqueue_linear(m, L, li, LLMRS_W_O, nullptr, nullptr, li == layer && slot == LLMRS_W_O ? ts : nullptr);
+        enqueue_linear(m, L, li, LLMRS_W_GATE, nullptr, nullptr,
+                       li == layer && slot == LLMRS_W_GATE ? ts : nullptr);
+        enqueue_linear(m, L, li, LLMRS_W_DOWN, nullptr, nullptr,
+                       li == layer && slot == LLMRS_W_DOWN ? ts : nullptr);
+      }
+      enqueue_head(m, L, false);
+      LLMRS_HIP(hipMemcpyAsync(h.data(), ts, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost, s));
+      LLMRS_HIP(hipStreamSynchronize(s));
+    } catch (...) {
+      (void)hipStreamSynchronize(s);
+      (void)hipFree(ts);
+      throw;
+    }
+    (void)hipFree(ts);
+    m->host_pos += 1;
+    // per workgroup: stamps 0-6 in us from the launch's earliest start (-1 =
+    // not recorded), then the XCC id and the HW_ID word
+    unsigned long long t0 = ~0ull;
+    for (unsigned w = 0; w < nwg; ++w)
+      if (h[8 * w]) t0 = std::min(t0, h[8 * w]);
+    for (unsigned w = 0; w < nwg && count + 9 <= cap; ++w) {
+      for (int i = 0; i < 7; ++i) out[count++] = h[8 * w + i] ? (double)(h[8 * w + i] - t0) / 100.0 : -1.0;
+      out[count++] = (double)(h[8 * w + 7] >> 32);
+      out[count++] = (double)(h[8 * w + 7] & 0xFFFFFFFFull);
+    }
+  });
+  return rc ? rc : count;
+}
+
 double llmrs_model_weight_bytes(const llmrs_model* m) {
   if (!m) return 0.0;
   double b = linear_weight_bytes(m, m->lm_head);
@@ -1138,11 +1285,13 @@ int llmrs_model_probe_decode_layer(llmrs_model* m, int layer, size_t pos, const 
     ProbeBuf pb;
     int8_t* xq = pb.get<int8_t>(H);
     float* xd = pb.get<float>(H / 32);
+    float* xin = pb.get<float>(H);
     set_state(m, pos, INT_MAX);
     m->host_pos = pos;
-    LLMRS_HIP(hipMemcpyAsync(m->x, x, H * sizeof(float), hipMemcpyHostToDevice, s));
+    LLMRS_HIP(hipMemcpyAsync(xin, x, H * sizeof(float), hipMemcpyHostToDevice, s));
     Launcher L{s};
     auto sync = [&] { LLMRS_HIP(hipStreamSynchronize(s)); };
+    enqueue_embed(m, L, xin, m->layers[layer].norm[0]);
     enqueue_linear(m, L, layer, LLMRS_W_Q, xq, xd);
     probe_copy(out->qkv, m->qkv, m->qkv_rows * sizeof(float));
     probe_copy(out->xq, xq, H);
@@ -1180,9 +1329,11 @@ int llmrs_model_probe_head(llmrs_model* m, const float* x, int8_t* xq, float* xd
     ProbeBuf pb;
     int8_t* dq = pb.get<int8_t>(H);
     float* dd = pb.get<float>(H / 32);
+    float* xin = pb.get<float>(H);
     set_state(m, 0, INT_MAX);
-    LLMRS_HIP(hipMemcpyAsync(m->x, x, H * sizeof(float), hipMemcpyHostToDevice, s));
+    LLMRS_HIP(hipMemcpyAsync(xin, x, H * sizeof(float), hipMemcpyHostToDevice, s));
     Launcher L{s};
+    enqueue_embed(m, L, xin, m->final_norm);
     enqueue_head(m, L, logits != nullptr, dq, dd);
     probe_copy(xq, dq, H);
     probe_copy(xd, dd, H / 32 * sizeof(float));

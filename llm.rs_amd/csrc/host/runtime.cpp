@@ -87,10 +87,15 @@ GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
   const char* eu = std::getenv("LLMRS_GEMV_U");
   if (eu && (std::atoi(eu) == 1 || std::atoi(eu) == 2)) U = std::atoi(eu);
   int R = 4;
-  if (kind == "norm_store" || kind == "q8_resid") {
+  if (kind == "norm_store" || kind == "q8_resid" || kind == "nq_store") {
     R = 2;
     const char* er = std::getenv("LLMRS_GEMV_R");
     if (er && (std::atoi(er) == 2 || std::atoi(er) == 4)) R = std::atoi(er);
+  }
+  int waves = 4;
+  if (kind == "q8_nq") {  // 32-row tiles, one per 8-wave workgroup (gemv_w8.hip)
+    R = 2;
+    waves = 8;
   }
   // Workgroups per CU (measured on MI355X): 1 for the RMSNorm-prologue
   // store GEMV (Q|K|V: 8B 14 MB, 70B 47 MB) and for matrices under 24 MB -
@@ -98,20 +103,24 @@ GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
   // behind as many weight requests - and 2 otherwise.
   const double wbytes = (double)n * k * (wt == WT_Q8H ? 34.0 : wt == WT_Q4F ? 20.0 : 18.0) / 32.0;
   const char* ew = std::getenv("LLMRS_GEMV_WG_PER_CU");
-  const int per_cu = ew && *ew ? std::max(1, std::atoi(ew)) : (kind == "norm_store" || wbytes < 24e6 ? 1 : 2);
+  const bool store = kind == "norm_store" || kind == "nq_store";
+  const int per_cu = ew && *ew ? std::max(1, std::atoi(ew)) : (store || wbytes < 24e6 ? 1 : 2);
   const long cap = (long)std::max(1, num_cus) * per_cu;
   GemvPlan p;
   p.name = std::string("gemv_") + wt_tag(wt) + "_" + kind + "_r" + std::to_string(R) + "u" +
-           std::to_string(U);
+           std::to_string(U) + (waves == 8 ? "_w8" : "");
+  p.threads = 64 * waves;
+  // tiled epilogues: whole 64-row SwiGLU tiles or 32-row next-norm tiles
+  const int tile = (kind == "norm_silu" || kind == "nq_silu") ? 64 : kind == "q8_nq" ? 32 : 0;
   long wgs;
-  if (kind == "norm_silu") {
-    wgs = (n + 63) / 64;
+  if (tile) {
+    wgs = (n + tile - 1) / tile;
   } else {
     const long nrg = (n + R - 1) / R;
-    wgs = (nrg + 3) / 4;
+    wgs = (nrg + waves - 1) / waves;
   }
   p.grid = (unsigned)std::max<long>(1, std::min(wgs, cap));
-  p.lds = llmrs::gemv_lds_bytes(kind == "norm_silu", n, k, R, (int)p.grid);
+  p.lds = llmrs::gemv_lds_bytes(tile, n, k, R, (int)p.grid, waves);
   return p;
 }
 
@@ -279,7 +288,7 @@ int llmrs_init(int device_ordinal, const char* hsaco_dir) {
         c->noalloc_error = e.what();
       }
       std::string dir = hsaco_dir ? std::string(hsaco_dir) : library_dir();
-      for (const char* name : {"gemv", "attention", "ops", "prefill"}) {
+      for (const char* name : {"gemv", "gemv_w8", "attention", "ops", "prefill"}) {
         std::string path = dir + "/" + name + ".hsaco";
         LLMRS_REQUIRE(std::filesystem::exists(path), LLMRS_E_MODULE, "missing code object " + path);
         hipModule_t m = nullptr;

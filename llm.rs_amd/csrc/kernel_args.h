@@ -19,12 +19,15 @@ struct GemvArgs {
   const float* x;        // [m][k] input rows (PRO_QUANT, PRO_NORM)
   const float* norm_w;   // [k] RMSNorm weight (PRO_NORM)
   float eps;
-  const int8_t* xq;      // [k] activation codes (PRO_Q8)
-  const float* xd;       // [k/32] activation scales (PRO_Q8)
+  const int8_t* xq;      // [k] activation codes (PRO_Q8, PRO_NQ: codes of x*w)
+  const float* xd;       // [k/32] activation scales (PRO_Q8; PRO_NQ: d' before the RMSNorm factor)
+  const float* xss;      // [k/32] per-block sums of x^2 (PRO_NQ)
   float* y;              // [m][n]; EPI_SILU: [n/2] (may be null); EPI_ARGMAX: logits (may be null)
-  const float* res;      // [m][n] residual (EPI_RESID; may alias y)
-  int8_t* yq;            // [n/2] codes of silu(g)*u (EPI_SILU)
-  float* yd;             // [n/64] scales of silu(g)*u (EPI_SILU)
+  const float* res;      // [m][n] residual (EPI_RESID, EPI_NQ; may alias y)
+  const float* norm_next;  // [n] weight of the RMSNorm the output feeds (EPI_NQ)
+  int8_t* yq;            // EPI_SILU: [n/2] codes of silu(g)*u; EPI_NQ: [n] codes of y*norm_next
+  float* yd;             // EPI_SILU: [n/64] scales; EPI_NQ: [n/32] d' = amax(y*norm_next)/127
+  float* yss;            // [n/32] per-block sums of y^2 (EPI_NQ)
   float* part_val;       // [gridDim.x] (EPI_ARGMAX)
   int* part_idx;         // [gridDim.x] (EPI_ARGMAX)
   unsigned long long* ts;  // profiling: 4 stamps per workgroup (null = off)
@@ -35,15 +38,16 @@ struct GemvArgs {
 // Dynamic LDS of a decode GEMV (gemv_core.h): the quantised activation row
 // (k codes, k/32 scales, k/32 Q4 offsets; 16-byte aligned), then the row
 // results parked until the unit loop ends: per wave (4 per workgroup) R
-// values of each of its row groups, or for the SwiGLU epilogue 64 values per
+// values of each of its row groups, or for a tiled epilogue (`tile` rows:
+// 64 for SwiGLU, 32 for the residual + next-norm codes) `tile` values per
 // tile of the workgroup.  nwg = workgroups of the launch.
 constexpr size_t gemv_act_bytes(int k) { return (size_t)k + 8 * (size_t)(k / 32); }
-constexpr size_t gemv_out_floats(bool silu, int n, int r, int nwg) {
-  return silu ? (size_t)(((n + 63) / 64 + nwg - 1) / nwg) * 64
-              : (size_t)((((size_t)n + r - 1) / r + (size_t)nwg * 4 - 1) / ((size_t)nwg * 4)) * r * 4;
+constexpr size_t gemv_out_floats(int tile, int n, int r, int nwg, int waves = 4) {
+  return tile ? (size_t)(((n + tile - 1) / tile + nwg - 1) / nwg) * tile
+              : (size_t)((((size_t)n + r - 1) / r + (size_t)nwg * waves - 1) / ((size_t)nwg * waves)) * r * waves;
 }
-constexpr size_t gemv_lds_bytes(bool silu, int n, int k, int r, int nwg) {
-  return (gemv_act_bytes(k) + 15) / 16 * 16 + 4 * gemv_out_floats(silu, n, r, nwg);
+constexpr size_t gemv_lds_bytes(int tile, int n, int k, int r, int nwg, int waves = 4) {
+  return (gemv_act_bytes(k) + 15) / 16 * 16 + 4 * gemv_out_floats(tile, n, r, nwg, waves);
 }
 
 // lm_head partial reduction + greedy bookkeeping (gemv.hip: argmax_final).
@@ -115,6 +119,15 @@ struct EmbedArgs {
   float* x;             // [hidden]
   int* err;             // set to 1 on an out-of-range id
   int hidden, vocab;
+  // One row only: when norm_w is set, the first RMSNorm's operand of the
+  // row (the PRO_NQ prologue of gemv_core.h): Q8_0 codes of x*w, d' =
+  // amax/127 and the sum of x^2 per 32-element block.  x_in set: the row is
+  // x_in (copied to x) instead of an embedding.
+  const float* norm_w;
+  int8_t* xq;
+  float* xd;
+  float* xss;
+  const float* x_in;
 };
 
 // Prefill GEMM (prefill.hip): Y[t][r] = sum_b isum_b(t, r) * (d_w[r,b] * d_a[t,b])

@@ -9,13 +9,19 @@
 
 using namespace llmrs;
 
+// Weight units requested before the activation prologue: one for the
+// SwiGLU GEMV with the RMSNorm prologue (earlier weight requests delay its
+// 32 KB of activation loads), two otherwise.
+template <int PRO, int EPI>
+constexpr int pre_units() { return EPI == EPI_SILU && PRO == PRO_NORM ? 1 : 2; }
+
 template <int WT, int PRO, int EPI, int R, int U>
 __device__ __forceinline__ void gemv_impl(const GemvArgs& a) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ GemvShared sh;
   UnitRegs<WT, R, U> ua, ub;
-  gemv_body<WT, PRO, EPI, R, U, false, EPI == EPI_SILU ? 1 : 2>(a, blockIdx.y, blockIdx.x, gridDim.x, ua, ub,
-                                                                false, smem, sh);
+  gemv_body<WT, PRO, EPI, R, U, false, pre_units<PRO, EPI>()>(a, blockIdx.y, blockIdx.x, gridDim.x, ua, ub,
+                                                               false, smem, sh);
 }
 
 #define LLMRS_GEMV(name, WT, PRO, EPI, R, U)                                       \
@@ -31,7 +37,10 @@ __device__ __forceinline__ void gemv_impl(const GemvArgs& a) {
   LLMRS_GEMV(gemv_##tag##_q8_resid_r2u##U, WT, PRO_Q8, EPI_RESID, 2, U)                   \
   LLMRS_GEMV(gemv_##tag##_q8_resid_r4u##U, WT, PRO_Q8, EPI_RESID, 4, U)                   \
   LLMRS_GEMV(gemv_##tag##_norm_silu_r4u##U, WT, PRO_NORM, EPI_SILU, 4, U)                 \
-  LLMRS_GEMV(gemv_##tag##_norm_argmax_r4u##U, WT, PRO_NORM, EPI_ARGMAX, 4, U)
+  LLMRS_GEMV(gemv_##tag##_norm_argmax_r4u##U, WT, PRO_NORM, EPI_ARGMAX, 4, U)               \
+  LLMRS_GEMV(gemv_##tag##_nq_store_r2u##U, WT, PRO_NQ, EPI_STORE, 2, U)                   \
+  LLMRS_GEMV(gemv_##tag##_nq_silu_r4u##U, WT, PRO_NQ, EPI_SILU, 4, U)                     \
+  LLMRS_GEMV(gemv_##tag##_nq_argmax_r4u##U, WT, PRO_NQ, EPI_ARGMAX, 4, U)
 
 LLMRS_GEMV_FAMILY(q4h, WT_Q4H, 1)
 LLMRS_GEMV_FAMILY(q4h, WT_Q4H, 2)

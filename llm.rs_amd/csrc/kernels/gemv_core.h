@@ -26,14 +26,31 @@
 //
 // The activation vector is quantised once per workgroup into LDS (prologue):
 //   PRO_QUANT  Q8_0 of an f32 row                     (matmul_transposed)
-//   PRO_NORM   RMSNorm then Q8_0                        (QKV, gate|up, lm_head)
+//   PRO_NORM   RMSNorm then Q8_0 of an f32 row
 //   PRO_Q8     already-quantised codes from global      (O, down)
+//   PRO_NQ     codes of RMSNorm(x) from the producer    (QKV, gate|up, lm_head):
+//              Q8_0 codes of x*w with per-block scales d' = amax(x*w)/127 and
+//              per-block sums of x^2; the prologue adds the sums, forms
+//              s = 1/sqrt(ss/k + eps) and uses d = d' * s
 // and each row group is finished in an epilogue:
 //   EPI_STORE  y = acc
-//   EPI_RESID  y = acc + res                            (O + residual, down + residual)
+//   EPI_RESID  y = acc + res
 //   EPI_SILU   gate|up rows interleaved in tiles of 32+32; m = silu(g)*u,
 //              written as f32 and as Q8_0 codes for the down projection
 //   EPI_ARGMAX logits plus a per-workgroup (max, index) partial (lm_head)
+//   EPI_NQ     y = acc + res in tiles of 32 rows, then the PRO_NQ operand of
+//              the next RMSNorm (weight norm_next): codes, d' and sum of y^2
+//              per 32-row block (O + residual, down + residual)
+//
+// Why PRO_NQ / EPI_NQ: RMSNorm then Q8_0 (cpu.rs:381-389, 724-743) computes
+// y = (x*s)*w, d = amax(y)/127, q = round(y/d).  The codes do not depend on
+// the positive factor s (it scales y and d alike), so the producer, which
+// holds x but not s (a sum over the whole vector), quantises x*w; the
+// consumer applies s to the 32x fewer scales.  Only the rounding differs from
+// the reference's order (a code moves only where x*w/d' sits within a few ulps
+// of a rounding midpoint), and every consumer workgroup loads k + k/8 bytes
+// instead of 8k bytes of f32 input and norm weights, with no quantiser
+// arithmetic in its prologue.
 // DEV = true moves the activations, results and partials with device-scope
 // loads and stores (for a producer and consumer in one launch; the decode
 // kernels use DEV = false).
@@ -48,12 +65,24 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum { WT_Q4H = 0, WT_Q4F = 1, WT_Q8H = 2 };
-enum { PRO_QUANT = 0, PRO_NORM = 1, PRO_Q8 = 2 };
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
+enum { PRO_QUANT = 0, PRO_NORM = 1, PRO_Q8 = 2, PRO_NQ = 3 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3, EPI_NQ = 4 };
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / LLMRS_WAVE;
+// Waves per workgroup: 4, or 8 for a code object built with
+// LLMRS_GEMV_WAVES=8 (gemv_w8.hip: the 32-row-tile producers, which run one
+// workgroup per tile on half the CUs at the 8B width and need twice the
+// loads in flight per CU).
+#ifndef LLMRS_GEMV_WAVES
+#define LLMRS_GEMV_WAVES 4
+#endif
+constexpr int kThreads = LLMRS_GEMV_WAVES * LLMRS_WAVE;
+constexpr int kWaves = LLMRS_GEMV_WAVES;
 constexpr int kSiluTile = 64;  // rows per SwiGLU tile: 32 gate + 32 up
+constexpr int kNqTile = 32;    // rows per EPI_NQ tile: one Q8_0 block of y
+// Rows per tile of the tiled epilogues (0: row groups dealt singly).
+__host__ __device__ constexpr int epi_tile(int epi) {
+  return epi == EPI_SILU ? kSiluTile : epi == EPI_NQ ? kNqTile : 0;
+}
 
 // Raw scale bits: the conversion happens at use, so a load never has to
 // complete before the next one is issued.
@@ -168,7 +197,19 @@ template <int PRO, bool Q4, bool DEV>
 __device__ __forceinline__ void load_activation(const GemvArgs& a, int mrow, int8_t* s_q,
                                                 float* s_d, int* s_off, float* s_red) {
   const int k = a.k, nb = k >> 5, tid = threadIdx.x;
-  if (PRO == PRO_Q8) {
+  if (PRO == PRO_Q8 || PRO == PRO_NQ) {
+    float scale = 1.0f;
+    if (PRO == PRO_NQ) {  // s from the per-block sums of squares
+      float ss = 0.0f;
+      for (int b = tid; b < nb; b += kThreads) ss = ss + ld_act<DEV>(a.xss, b);
+      ss = wave_sum(ss);
+      if (lane_id() == 0) s_red[wave_id()] = ss;
+      __syncthreads();
+      float tot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) tot = tot + s_red[w];
+      scale = 1.0f / sqrtf(tot / (float)k + a.eps);
+    }
     for (int b = tid; b < nb; b += kThreads) {
       i32x4 c0, c1;
       if (DEV) {
@@ -183,7 +224,7 @@ __device__ __forceinline__ void load_activation(const GemvArgs& a, int mrow, int
       i32x4* dst = (i32x4*)(s_q + 32 * b);
       dst[0] = c0;
       dst[1] = c1;
-      s_d[b] = ld_act<DEV>(a.xd, b);
+      s_d[b] = PRO == PRO_NQ ? ld_act<DEV>(a.xd, b) * scale : ld_act<DEV>(a.xd, b);
       if (Q4) {
         int s = 0;
         s = dot4(c0.x, 0x01010101, s);
@@ -303,11 +344,13 @@ constexpr int kQ8Blocks = 4;
 
 template <int PRO>
 struct ActRegs {
-  f32x4 x[PRO == PRO_Q8 ? 1 : 8];
+  static constexpr bool CODES = PRO == PRO_Q8 || PRO == PRO_NQ;
+  f32x4 x[CODES ? 1 : 8];
   f32x4 w[PRO == PRO_NORM ? 8 : 1];
-  i32x4 c0[PRO == PRO_Q8 ? kQ8Blocks : 1];
-  i32x4 c1[PRO == PRO_Q8 ? kQ8Blocks : 1];
-  float d[PRO == PRO_Q8 ? kQ8Blocks : 1];
+  i32x4 c0[CODES ? kQ8Blocks : 1];
+  i32x4 c1[CODES ? kQ8Blocks : 1];
+  float d[CODES ? kQ8Blocks : 1];
+  float ss;  // PRO_NQ: this thread's block sum of squares
 };
 
 // Elements per thread when the whole input spreads evenly over the
@@ -319,16 +362,17 @@ __device__ __forceinline__ int act_ept(int k) {
 template <int PRO>
 __device__ __forceinline__ bool act_in_regs(int k) {
   const int nb = k >> 5;
-  return PRO == PRO_Q8 ? nb <= kQ8Blocks * kThreads : nb <= kThreads;
+  return PRO == PRO_Q8 ? nb <= kQ8Blocks * kThreads : nb <= kThreads;  // PRO_NQ: one block per thread
 }
 
 template <int PRO, bool DEV>
 __device__ __forceinline__ void issue_activation(const GemvArgs& a, int mrow, ActRegs<PRO>& r) {
   const int k = a.k, nb = k >> 5, tid = threadIdx.x;
   if (!act_in_regs<PRO>(k)) return;
-  if (PRO == PRO_Q8) {
+  if (PRO == PRO_Q8 || PRO == PRO_NQ) {
+    if (PRO == PRO_NQ) r.ss = ld_act<DEV>(a.xss, min(tid, nb - 1));  // clamped; masked at use
 #pragma unroll
-    for (int i = 0; i < kQ8Blocks; ++i) {
+    for (int i = 0; i < (PRO == PRO_NQ ? 1 : kQ8Blocks); ++i) {
       const int b = min(tid + kThreads * i, nb - 1);  // clamped; extra ones unused
       if (kThreads * i < nb) {
         if (DEV) {
@@ -366,7 +410,7 @@ __device__ __forceinline__ void issue_activation(const GemvArgs& a, int mrow, Ac
 // stored once at the end of the kernel: a store issued mid-kernel would make
 // the next reuse of its data registers wait for every outstanding load.
 // 0 start, 1 operand ready, 2 loop done, 3 end, 4 input arrived, 5 norm
-// scale known, 6 operand quantised.
+// scale known, 6 operand quantised, 7 where it ran: XCC id << 32 | HW_ID.
 struct Stamps {
   bool on;
   unsigned long long t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -433,15 +477,31 @@ __device__ __forceinline__ void finish_activation(const GemvArgs& a, int mrow, A
     load_activation<PRO, Q4, DEV>(a, mrow, s_q, s_d, s_off, s_red);
     return;
   }
-  if (PRO == PRO_Q8) {
+  if (PRO == PRO_Q8 || PRO == PRO_NQ) {
+    float scale = 1.0f;
+    if (PRO == PRO_NQ) {
+      // RMSNorm factor (cpu.rs:381-383) from the producer's block sums of
+      // squares: rms = sqrt(ss/n + eps), s = 1/rms; the scales become d' * s.
+      float ss = tid < nb ? r.ss : 0.0f;
+      ts.rec(4);
+      ss = wave_sum(ss);
+      if (lane_id() == 0) s_red[wave_id()] = ss;
+      __syncthreads();
+      float tot = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kQ8Blocks; ++i) {
+      for (int w = 0; w < kWaves; ++w) tot = tot + s_red[w];
+      const float rms = sqrtf(tot / (float)k + a.eps);
+      scale = 1.0f / rms;
+      ts.rec(5);
+    }
+#pragma unroll
+    for (int i = 0; i < (PRO == PRO_NQ ? 1 : kQ8Blocks); ++i) {
       const int b = tid + kThreads * i;
       if (kThreads * i < nb && b < nb) {
         i32x4* dst = (i32x4*)(s_q + 32 * b);
         dst[0] = r.c0[i];
         dst[1] = r.c1[i];
-        s_d[b] = r.d[i];
+        s_d[b] = PRO == PRO_NQ ? r.d[i] * scale : r.d[i];
         if (Q4) {
           int s = 0;
           s = dot4(r.c0[i].x, 0x01010101, s);
@@ -483,8 +543,9 @@ struct Gemv {
   static constexpr bool Q4 = (WT != WT_Q8H);
   static constexpr int BS = Q4 ? 16 : 32;       // code bytes per block
   static constexpr int BPU = LLMRS_WAVE * U;    // blocks per unit
-  static constexpr int SILU_RG = kSiluTile / R / kWaves;  // row groups per wave per tile
-  static_assert(EPI != EPI_SILU || (kSiluTile % (R * kWaves) == 0), "SwiGLU tile must split evenly");
+  static constexpr int TILE = epi_tile(EPI);             // rows per tile (tiled epilogues)
+  static constexpr int TRG = TILE ? TILE / R / kWaves : 1;  // row groups per wave per tile
+  static_assert(TILE == 0 || (TILE % (R * kWaves) == 0), "a tile must split evenly over the waves");
 
   const GemvArgs& a;
   int nb, nchunk, nrg, lane, wave, wg, nwg, nunits;
@@ -499,10 +560,10 @@ struct Gemv {
     // the SwiGLU epilogue every wave of a workgroup walks the same number of
     // tiles, so the per-tile barriers are uniform.
     int ngroups;
-    if (EPI == EPI_SILU) {
-      const int ntiles = (a.n + kSiluTile - 1) / kSiluTile;
+    if (TILE) {
+      const int ntiles = (a.n + TILE - 1) / TILE;
       const int my_tiles = wg < ntiles ? (ntiles - 1 - wg) / nwg + 1 : 0;
-      ngroups = my_tiles * SILU_RG;
+      ngroups = my_tiles * TRG;
     } else {
       const int first = wg * kWaves + wave;
       const int stride = nwg * kWaves;
@@ -513,9 +574,9 @@ struct Gemv {
 
   // Row group of the j-th group this wave processes (-1 past the end).
   __device__ __forceinline__ int row_group(int j) const {
-    if (EPI == EPI_SILU) {
-      const int tile = wg + (j / SILU_RG) * nwg;
-      const int rg = tile * (kSiluTile / R) + wave * SILU_RG + (j % SILU_RG);
+    if (TILE) {
+      const int tile = wg + (j / TRG) * nwg;
+      const int rg = tile * (TILE / R) + wave * TRG + (j % TRG);
       return rg < nrg ? rg : -1;
     }
     const int rg = wg * kWaves + wave + j * nwg * kWaves;
@@ -609,7 +670,7 @@ struct GemvShared {
 
 // Bytes of the activation area in LDS for an input of length k.
 __host__ __device__ constexpr size_t gemv_act_lds(int k) { return gemv_act_bytes(k); }
-static_assert(kThreads == 4 * LLMRS_WAVE && kSiluTile == 64, "gemv_lds_bytes assumes 4 waves, 64-row tiles");
+static_assert(kWaves == 4 || kWaves == 8, "gemv_lds_bytes takes the wave count");
 
 // One GEMV over the waves of workgroup `wg` of `nwg`: prologue, pipelined
 // unit loop, epilogues.  `ua`/`ub` hold the first two units already when
@@ -644,12 +705,15 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
   Stamps ts;
   ts.on = a.ts != nullptr;
   ts.rec(0);
+  if (ts.on)
+    ts.t[7] = ((unsigned long long)__builtin_amdgcn_s_getreg((15 << 11) | 20) << 32) |
+              (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);
 
   // The residual of this lane's first output row is requested with the
   // activations: loaded in the epilogue it would cost a whole memory round
   // trip after the unit loop.  The row is clamped instead of tested, so the
   // prologue has no branch at which the compiler would wait for the loads.
-  float res0 = 0.0f;
+  float res0 = 0.0f, wn0 = 0.0f;
   {
     ActRegs<PRO> ar;
     issue_activation<PRO, DEV>(a, mrow, ar);
@@ -659,6 +723,11 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
       const int rg = max(g.row_group(v / R), 0);
       const int row = min(rg * R + v % R, a.n - 1);
       res0 = ld_act<DEV>(a.res, (size_t)mrow * a.n + row);
+    }
+    if (EPI == EPI_NQ) {  // residual and next-norm weight of the first 8 tiles' rows
+      const int row = min((wg + (tid / 32) * nwg) * kNqTile + tid % 32, a.n - 1);
+      res0 = ld_act<DEV>(a.res, (size_t)mrow * a.n + row);
+      wn0 = a.norm_next[row];
     }
     if (!preloaded && PRE > 0) g.load(ua, nunits > 0 ? 0 : -1);
     if (!preloaded && PRE > 1) g.load(ub, nunits > 1 ? 1 : -1);
@@ -702,8 +771,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
     for (int r = 0; r < R; ++r)
       if (lane == r) out = vals[r];
     int slot;
-    if (EPI == EPI_SILU)
-      slot = (j / G::SILU_RG) * kSiluTile + wave * (G::SILU_RG * R) + (j % G::SILU_RG) * R;
+    if (G::TILE)
+      slot = (j / G::TRG) * G::TILE + wave * (G::TRG * R) + (j % G::TRG) * R;
     else
       slot = (wave * gmax + j) * R;
     if (lane < R) s_out[slot + lane] = out;
@@ -759,6 +828,34 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
         if (DEV) dev_st8(a.yq, idx, (int8_t)qc);
         else a.yq[idx] = (int8_t)qc;
         if (e == 0) st_act<DEV>(a.yd, tile, d);
+      }
+    }
+  } else if (EPI == EPI_NQ) {
+    __syncthreads();
+    const int ntiles = (a.n + kNqTile - 1) / kNqTile;
+    const int my_tiles = wg < ntiles ? (ntiles - 1 - wg) / nwg + 1 : 0;
+    // 32 threads per tile: y = acc + res (layer.rs:386,403), then the next
+    // RMSNorm's operand: Q8_0 of y*w (d' = amax/127, cpu.rs:724-743) and the
+    // block's sum of y^2.
+    for (int q0 = 0; q0 < my_tiles; q0 += kThreads / 32) {
+      const int q = q0 + tid / 32, e = tid % 32;
+      if (q < my_tiles) {  // uniform per 32-lane half-wave
+        const int tile = wg + q * nwg;
+        const int row = tile * kNqTile + e;
+        const bool ok = row < a.n;
+        const float rv = q0 == 0 ? res0 : (ok ? ld_act<DEV>(a.res, ybase + row) : 0.0f);
+        const float wv = q0 == 0 ? wn0 : (ok ? a.norm_next[row] : 0.0f);
+        const float yv = s_out[q * kNqTile + e] + rv;
+        if (ok) st_act<DEV>(a.y, ybase + row, yv);
+        const float z = ok ? yv * wv : 0.0f;
+        float d;
+        const int qc = q8_group32(z, &d);
+        const float ss = group_sum<32>(ok ? yv * yv : 0.0f);
+        if (ok) a.yq[row] = (int8_t)qc;
+        if (e == 0) {
+          a.yd[tile] = d;
+          a.yss[tile] = ss;
+        }
       }
     }
   } else if (EPI == EPI_STORE || EPI == EPI_RESID || (EPI == EPI_ARGMAX && a.y)) {

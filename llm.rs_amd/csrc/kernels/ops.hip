@@ -128,16 +128,41 @@ extern "C" __global__ __launch_bounds__(256) void matmul_t_f32(MatArgs g) {
 }
 
 
-// Embedding gather (main.rs:159-167) for the token at the device position.
+// Embedding gather (main.rs:159-167) for the token at the device position,
+// or a given row; with norm_w set, also the first RMSNorm's operand: per
+// 32-element block (one half-wave), Q8_0 codes of x*w with d' = amax/127
+// (cpu.rs:724-743) and the block's sum of x^2 (cpu.rs:381, summed per block).
 extern "C" __global__ __launch_bounds__(256) void embed_gather(EmbedArgs e) {
-  // Row blockIdx.y of a chunk starting at *pos_ptr (one row when decoding).
-  int tok = e.tokens[*e.pos_ptr + blockIdx.y];
-  if (tok < 0 || tok >= e.vocab) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) *e.err = 1;
-    tok = 0;
+  const float* row;
+  if (e.x_in) {
+    row = e.x_in;
+  } else {
+    // Row blockIdx.y of a chunk starting at *pos_ptr (one row when decoding).
+    int tok = e.tokens[*e.pos_ptr + blockIdx.y];
+    if (tok < 0 || tok >= e.vocab) {
+      if (threadIdx.x == 0 && blockIdx.x == 0) *e.err = 1;
+      tok = 0;
+    }
+    row = e.table + (size_t)tok * e.hidden;
   }
-  const float* row = e.table + (size_t)tok * e.hidden;
   float* x = e.x + (size_t)blockIdx.y * e.hidden;
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < e.hidden; i += gridDim.x * blockDim.x)
-    x[i] = row[i];
+  for (int i0 = blockIdx.x * blockDim.x; i0 < e.hidden; i0 += gridDim.x * blockDim.x) {
+    const int i = i0 + threadIdx.x;
+    const bool ok = i < e.hidden;  // hidden is a multiple of 32: whole half-waves
+    const float v = ok ? row[i] : 0.0f;
+    if (ok) x[i] = v;
+    if (e.norm_w) {
+      const float z = ok ? v * e.norm_w[i] : 0.0f;
+      float d;
+      const int q = q8_group32(z, &d);
+      const float ss = group_sum<32>(v * v);
+      if (ok) {
+        e.xq[i] = (int8_t)q;
+        if ((i & 31) == 0) {
+          e.xd[i / 32] = d;
+          e.xss[i / 32] = ss;
+        }
+      }
+    }
+  }
 }

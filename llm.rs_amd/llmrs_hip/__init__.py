@@ -99,6 +99,7 @@ _SIGS = {
     "llmrs_model_profile_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_char_p,
                                                C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_weight_bytes": (C.c_double, [C.c_void_p]),
+    "llmrs_model_profile_stamps": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int]),
     "llmrs_model_probe_decode_layer": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p]),
     "llmrs_model_probe_head": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                           C.c_void_p]),
@@ -474,6 +475,14 @@ class HipModel:
         pr = LayerProbe(**{k: v.ctypes.data for k, v in out.items()})
         _check(lib().llmrs_model_probe_prefill_layer(self._h, layer, start_pos, n, _ptr(x), C.byref(pr)))
         return out
+
+    def profile_stamps(self, layer: int, slot: int, cap: int = 1 << 16) -> np.ndarray:
+        """Per-workgroup stamps of one decode GEMV in an eager step: rows of
+        (start, operand ready, loop done, end, input arrived, norm factor,
+        quantised [us], XCC id, HW_ID)."""
+        out = np.zeros(cap, np.float64)
+        n = _check(lib().llmrs_model_profile_stamps(self._h, layer, slot, _ptr(out), cap))
+        return out[:n].reshape(-1, 9)
 
     def weight_bytes(self) -> float:
         return float(lib().llmrs_model_weight_bytes(self._h))

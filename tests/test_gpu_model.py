@@ -471,3 +471,34 @@ def test_error_paths(hip, orc):
     incomplete = hip.HipModel(spec.config(16))
     with pytest.raises(hip.LlmrsError):
         incomplete.forward([1], 0)
+
+
+@pytest.mark.parametrize("spec", [TINY[1], TINY[2], TINY[5]], ids=lambda s: s.name)
+def test_producer_side_norm_operands(hip, orc, spec, monkeypatch):
+    """LLMRS_NQ=1 forces the RMSNorm operands to be produced by the O and
+    down GEMV epilogues and the embedding gather (the default above hidden
+    8192 / 256 CUs): residual trace, logits and greedy stream against the
+    oracle, and logits within rounding of the consumer-side path."""
+    w = syn.make_weights(spec)
+    toks = syn.prompt(spec)
+    om = orc.OracleModel.from_spec(spec, max_seq=96)
+    om.load(w)
+    olg, otr = om.forward(toks, 0, all_rows=False, trace=True)
+    out = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("LLMRS_NQ", mode)
+        monkeypatch.setenv("LLMRS_PREFILL", "0")  # every prompt row through the decode kernels
+        gm = hip.HipModel(spec.config(96))
+        syn.load_model(gm, w)
+        lg, nxt, tr = gm.forward(toks, 0, trace=True)
+        for li in range(1, spec.n_layers + 1):
+            e = rel_norm_err(tr[:, li], otr[:, li])
+            assert e < 1e-2, f"NQ={mode}: layer {li} residual relative error {e:.3g}"
+        assert np.max(np.abs(lg - olg)) < 1e-2, f"NQ={mode}"
+        monkeypatch.delenv("LLMRS_PREFILL")
+        gtoks = gm.generate(toks, 40)
+        otoks, margins = om.generate(toks, 40)
+        check_stream(gtoks, otoks, margins, min_steps=40)
+        out[mode] = lg
+        gm.close()
+    assert np.max(np.abs(out["1"] - out["0"])) < 1e-2
