@@ -291,10 +291,13 @@ int llmrs_model_probe_prefill_layer(llmrs_model* m, int layer, size_t start_pos,
 
 /* Profiling (no reference counterpart): one eager decode step in which the
  * decode GEMV of `slot` (LLMRS_W_Q = Q|K|V, LLMRS_W_O, LLMRS_W_GATE =
- * gate|up, LLMRS_W_DOWN) of `layer` records per-workgroup stamps.  Per
- * workgroup 9 values: start, operand ready, unit loop done, end, input
- * arrived, norm factor known, operand quantised (us from the launch's
- * earliest start; -1 = not recorded), the XCC id and the HW_ID register.
+ * gate|up, LLMRS_W_DOWN), or with slot -2 the decode attention, of `layer`
+ * records per-workgroup stamps.  Per workgroup 9 values: 7 stamps in us from
+ * the launch's earliest start (-1 = not recorded; GEMV: start, operand
+ * ready, unit loop done, end, input arrived, norm factor known, operand
+ * quantised; attention, items (KV head, split) in head-major order:
+ * start, projections loaded, first tile staged, tiles done, partials
+ * written, ticket taken, splits combined), the XCC id and HW_ID.
  * Returns the count written. */
 int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
                                int cap);

@@ -304,7 +304,7 @@ unsigned linear_grid(llmrs_model* m, int slot) {
 
 // Decode attention of layer li at the device position: RoPE of q and the new
 // k, K/V append, attention over the cache, ctx as f32 and Q8_0.
-void enqueue_attention(llmrs_model* m, Launcher& L, int li) {
+void enqueue_attention(llmrs_model* m, Launcher& L, int li, unsigned long long* stamps = nullptr) {
   const llmrs_model_config& c = m->c;
   const int hd = c.head_dim, nkv = c.n_kv_heads;
   LayerBufs& Lb = m->layers[li];
@@ -326,6 +326,7 @@ void enqueue_attention(llmrs_model* m, Launcher& L, int li) {
   a.nkv = nkv;
   a.nsplit = m->nsplit;
   a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
+  a.ts = stamps;
   const double kvb = 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
   L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(256 * m->attn_streams), 0, a);
 }
@@ -1182,7 +1183,7 @@ int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
     LLMRS_REQUIRE(m && m->begun && out, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
     LLMRS_REQUIRE(layer >= 0 && layer < m->c.n_layers, LLMRS_E_RANGE, "layer out of range");
     LLMRS_REQUIRE(m->host_pos + 1 <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
-    const unsigned nwg = linear_grid(m, slot);
+    const unsigned nwg = slot == -2 ? (unsigned)(m->nsplit * m->c.n_kv_heads) : linear_grid(m, slot);
     unsigned long long* ts = nullptr;
     LLMRS_HIP(hipMalloc(&ts, (size_t)nwg * 8 * sizeof(unsigned long long)));
     hipStream_t s = ctx().stream;
@@ -1194,7 +1195,7 @@ int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
       enqueue_embed(m, L, nullptr, m->layers[0].norm[0]);
       for (int li = 0; li < c.n_layers; ++li) {
         enqueue_linear(m, L, li, LLMRS_W_Q, nullptr, nullptr, li == layer && slot == LLMRS_W_Q ? ts : nullptr);
-        enqueue_attention(m, L, li);
+        enqueue_attention(m, L, li, li == layer && slot == -2 ? ts : nullptr);
         enqueue_linear(m, L, li, LLMRS_W_O, nullptr, nullptr, li == layer && slot == LLMRS_W_O ? ts : nullptr);
         enqueue_linear(m, L, li, LLMRS_W_GATE, nullptr, nullptr,
                        li == layer && slot == LLMRS_W_GATE ? ts : nullptr);

@@ -165,6 +165,9 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     }
   };
   stamp(0);
+  if (prof)  // where it ran: XCC id << 32 | HW_ID
+    st[7] = ((unsigned long long)__builtin_amdgcn_s_getreg((15 << 11) | 20) << 32) |
+            (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);
   const int n_rep = a.nq / a.nkv;
   // Tiles are dealt to the splits round-robin: stream st of split s takes
   // tiles (it * S + st) * nsplit + s, it = 0, 1, ...  The first tile of every

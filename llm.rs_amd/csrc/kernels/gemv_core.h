@@ -560,7 +560,7 @@ struct Gemv {
     // the SwiGLU epilogue every wave of a workgroup walks the same number of
     // tiles, so the per-tile barriers are uniform.
     int ngroups;
-    if (TILE) {
+    if constexpr (TILE > 0) {
       const int ntiles = (a.n + TILE - 1) / TILE;
       const int my_tiles = wg < ntiles ? (ntiles - 1 - wg) / nwg + 1 : 0;
       ngroups = my_tiles * TRG;
@@ -574,7 +574,7 @@ struct Gemv {
 
   // Row group of the j-th group this wave processes (-1 past the end).
   __device__ __forceinline__ int row_group(int j) const {
-    if (TILE) {
+    if constexpr (TILE > 0) {
       const int tile = wg + (j / TRG) * nwg;
       const int rg = tile * (TILE / R) + wave * TRG + (j % TRG);
       return rg < nrg ? rg : -1;

@@ -204,12 +204,14 @@ ATTN_LAYOUTS = [(1, 1), (1, 2), (1, 3), (4, 1), (4, 2)]
 
 @pytest.mark.parametrize("kv", [DType.F16, DType.F32], ids=["f16", "f32"])
 @pytest.mark.parametrize("head_dim", [128, 64])
+@pytest.mark.parametrize("nkv", [2, 8], ids=["kv2", "kv8"])
 @pytest.mark.parametrize("streams,splits", ATTN_LAYOUTS, ids=lambda v: str(v))
-def test_decode_attention_layouts(hip, orc, kv, head_dim, streams, splits, monkeypatch):
+def test_decode_attention_layouts(hip, orc, kv, head_dim, nkv, streams, splits, monkeypatch):
+    """Query heads per KV head: 2 (nkv = 8) and 8 (nkv = 2)."""
     monkeypatch.setenv("LLMRS_ATTN_STREAMS", str(streams))
     monkeypatch.setenv("LLMRS_ATTN_SPLITS", str(splits))
     pos = 700
-    spec = syn.tiny(DType.Q4_0, kv, head_dim=head_dim, n_layers=1, n_heads=8, n_kv_heads=2, ffn=512,
+    spec = syn.tiny(DType.Q4_0, kv, head_dim=head_dim, n_layers=1, n_heads=16, n_kv_heads=nkv, ffn=512,
                     seed=31 + head_dim)
     gm, om, _ = layer_models(hip, orc, spec, pos + 3)
     fill_cache(gm, om, spec, pos)
