@@ -65,6 +65,12 @@ constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
 // Its device address on the current device (hipGetSymbolAddress).
 void* noalloc_scratch_address();
 
+// A loaded kernel and the most threads per workgroup it accepts.
+struct KernelInfo {
+  hipFunction_t f = nullptr;
+  int max_threads = 0;
+};
+
 struct Context {
   int device = -1;
   hipStream_t stream = nullptr;
@@ -72,18 +78,20 @@ struct Context {
   void* noalloc_scratch = nullptr;  // device address of the scratch on `device`
   std::string noalloc_error;        // why it is null
   std::vector<hipModule_t> modules;
-  std::map<std::string, hipFunction_t> kernels;
+  std::map<std::string, KernelInfo> kernels;
   Allocator alloc;
 };
 
 Context& ctx();  // fails with LLMRS_E_NOINIT before llmrs_init
 std::recursive_mutex& api_mutex();
-hipFunction_t kernel(const std::string& name);
+// The kernel `name`; fails (LLMRS_E_INVALID) when `block` exceeds the
+// threads per workgroup it was compiled for (its launch bounds).
+hipFunction_t kernel(const std::string& name, dim3 block = dim3(1));
 
 template <class Args>
 void launch(const std::string& name, dim3 grid, dim3 block, size_t shmem, hipStream_t stream,
             const Args& args) {
-  hipFunction_t f = kernel(name);
+  hipFunction_t f = kernel(name, block);
   void* params[] = {const_cast<Args*>(&args)};
   LLMRS_HIP(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
                                   (unsigned)shmem, stream, params, nullptr));
@@ -96,7 +104,7 @@ void launch(const std::string& name, dim3 grid, dim3 block, size_t shmem, hipStr
 template <class Args>
 void launch_timed(const std::string& name, dim3 grid, dim3 block, size_t shmem, hipStream_t stream,
                   const Args& args, hipEvent_t start, hipEvent_t stop) {
-  hipFunction_t f = kernel(name);
+  hipFunction_t f = kernel(name, block);
   void* params[] = {const_cast<Args*>(&args)};
   LLMRS_HIP(hipExtModuleLaunchKernel(f, grid.x * block.x, grid.y * block.y, grid.z * block.z, block.x,
                                      block.y, block.z, shmem, stream, params, nullptr, start, stop, 0));

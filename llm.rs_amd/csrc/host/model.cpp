@@ -73,7 +73,11 @@ struct llmrs_model {
   bool nq = true;  // false: RMSNorm + Q8_0 inside the consumers (LLMRS_NQ=0)
   int *part_idx = nullptr, *counters = nullptr, *tokens = nullptr, *gen = nullptr;
   int *pos = nullptr, *n_prompt = nullptr, *err = nullptr;
-  int nsplit = 1, attn_streams = 1, lm_grid = 1, cap = 0;
+  int nsplit = 1, lm_grid = 1, cap = 0;
+  // decode attention layout: tile streams per workgroup of the vector kernel
+  // (f32 caches, 256 threads each), tile waves per 256-thread workgroup of
+  // the matrix-core kernel (f16 caches)
+  int attn_streams = 1, attn_waves = 1;
   size_t host_pos = 0;
   bool begun = false;
   hipGraph_t graph = nullptr;
@@ -121,8 +125,10 @@ struct llmrs_model {
 namespace {
 
 size_t kv_elem_bytes(const llmrs_model* m) { return m->c.kv_dtype == LLMRS_F16 ? 2 : 4; }
+// Cache rows per KV head: max_seq rounded up to whole attention tiles.
+int kv_rows(const llmrs_model* m) { return llmrs::kv_rows(m->c.max_seq); }
 size_t kv_layer_elems(const llmrs_model* m) {
-  return (size_t)m->c.n_kv_heads * m->c.max_seq * m->c.head_dim;
+  return (size_t)m->c.n_kv_heads * kv_rows(m) * m->c.head_dim;
 }
 
 // Records a (name, algorithmic bytes, start, end) tuple per launch when
@@ -155,8 +161,13 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
 
 // The decode-attention kernel of this model (attention.hip).
 std::string attn_kernel(const llmrs_model* m) {
-  return std::string("attn_decode_hd") + std::to_string(m->c.head_dim) +
-         (m->c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32") + (m->attn_streams > 1 ? "_s4" : "");
+  if (m->c.kv_dtype == LLMRS_F16)
+    return "attn_decode_mfma_hd" + std::to_string(m->c.head_dim) + "_w" + std::to_string(m->attn_waves);
+  return "attn_decode_hd" + std::to_string(m->c.head_dim) + "_f32" + (m->attn_streams > 1 ? "_s4" : "");
+}
+// Its threads per workgroup.
+unsigned attn_threads(const llmrs_model* m) {
+  return m->c.kv_dtype == LLMRS_F16 ? 256u : 256u * (unsigned)m->attn_streams;
 }
 
 // x = the embedding of the token at the device position, or (x_in set) the
@@ -321,14 +332,14 @@ void enqueue_attention(llmrs_model* m, Launcher& L, int li, unsigned long long* 
   a.ctx = m->ctxv;
   a.ctx_q = m->ctx_q;
   a.ctx_d = m->ctx_d;
-  a.max_seq = c.max_seq;
+  a.max_seq = kv_rows(m);
   a.nq = c.n_heads;
   a.nkv = nkv;
   a.nsplit = m->nsplit;
   a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
   a.ts = stamps;
   const double kvb = 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
-  L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(256 * m->attn_streams), 0, a);
+  L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(attn_threads(m)), 0, a);
 }
 
 void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
@@ -470,7 +481,7 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
   after(1);
   {  // RoPE + K/V append
     PrefillRopeArgs r{m->pf_qkv, m->pf_q, Lb.kc, Lb.vc, m->rope_cos, m->rope_sin, M, nq, nkv, hd,
-                      c.max_seq, (int)start, QR, kv16 ? 1 : 0};
+                      kv_rows(m), (int)start, QR, kv16 ? 1 : 0};
     const long total = (long)M * (nq + 2 * nkv) * (hd / 2);
     const unsigned grid = (unsigned)std::min<long>((total + 255) / 256, 8192);
     L("prefill_rope_kv", 4.0 * QR * M * 2, dim3(grid), blk, 0, r);
@@ -478,7 +489,7 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
   after(2);
   {  // causal attention
     PrefillAttnArgs a{m->pf_q, Lb.kc, Lb.vc, probe ? probe->ctx : nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq,
-                      nkv, c.max_seq, (int)start, scale};
+                      nkv, kv_rows(m), (int)start, scale};
     if (mfma_attn)
       L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nkv), dim3(512), 0, a);
     else
@@ -679,7 +690,8 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
                   LLMRS_E_INVALID, "GEMV input length is limited to 32768");
     LLMRS_REQUIRE(c.kv_dtype == LLMRS_F32 || c.kv_dtype == LLMRS_F16, LLMRS_E_INVALID, "kv_dtype");
     // the attention kernels address one layer's K (or V) cache with 32-bit byte offsets
-    LLMRS_REQUIRE((double)c.n_kv_heads * c.max_seq * c.head_dim * (c.kv_dtype == LLMRS_F16 ? 2 : 4) <
+    LLMRS_REQUIRE((double)c.n_kv_heads * llmrs::kv_rows(c.max_seq) * c.head_dim *
+                          (c.kv_dtype == LLMRS_F16 ? 2 : 4) <
                       2147483648.0,
                   LLMRS_E_INVALID, "one layer's K cache must stay below 2 GiB (n_kv_heads*max_seq*head_dim)");
     std::unique_ptr<llmrs_model> m(new llmrs_model());
@@ -694,19 +706,32 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
     m->qkv_rows = (nq + 2 * nkv) * hd;
     m->cap = c.max_seq + 1;
-    // Attention splits: one tile per split up to two workgroups per CU;
-    // longer contexts run 4 tile streams per workgroup (one workgroup per CU)
-    // so the split combine stays short.
-    const int tile = llmrs::attn_tile(c.kv_dtype == LLMRS_F16);
-    const int tiles = (c.max_seq + tile - 1) / tile;
-    int splits = std::min(tiles, std::max(1, 2 * cx.num_cus / nkv));
+    // Attention splits over the tiles of max_seq.  f16 caches (matrix-core
+    // kernel; attn_waves = its tile waves per workgroup): one tile per
+    // workgroup up to two workgroups per CU (and the combine's 64 splits),
+    // beyond that four tile waves per workgroup and up to one workgroup per
+    // CU.  f32 caches (vector kernel): one tile per split up to two
+    // workgroups per CU; longer contexts run 4 tile streams per workgroup
+    // (one workgroup per CU) so the split combine stays short.
+    const int tiles = llmrs::kv_rows(c.max_seq) / llmrs::kAttnTile;
+    int splits;
     m->attn_streams = 1;
-    const int es = env_int("LLMRS_ATTN_STREAMS", 0);  // 0 = by context length, 1 or 4 = forced
-    if (es == 4 || (es == 0 && tiles > splits)) {
-      m->attn_streams = 4;
-      splits = std::min((tiles + 3) / 4, std::max(1, cx.num_cus / nkv));
+    if (c.kv_dtype == LLMRS_F16) {
+      const int ew = env_int("LLMRS_ATTN_WAVES", 0);  // 0 = by context length, 1 or 4 = forced
+      const bool one = ew == 1 || (ew == 0 && tiles <= std::min(llmrs::kMfmaAttnMaxSplits, 2 * cx.num_cus / nkv));
+      m->attn_waves = one ? 1 : 4;
+      splits = one ? tiles : std::min((tiles + 3) / 4, std::max(1, cx.num_cus / nkv));
+      splits = std::min(env_int("LLMRS_ATTN_SPLITS", splits), llmrs::kMfmaAttnMaxSplits);
+    } else {
+      splits = std::min(tiles, std::max(1, 2 * cx.num_cus / nkv));
+      const int es = env_int("LLMRS_ATTN_STREAMS", 0);  // 0 = by context length, 1 or 4 = forced
+      if (es == 4 || (es == 0 && tiles > splits)) {
+        m->attn_streams = 4;
+        splits = std::min((tiles + 3) / 4, std::max(1, cx.num_cus / nkv));
+      }
+      splits = env_int("LLMRS_ATTN_SPLITS", splits);
     }
-    m->nsplit = std::max(1, env_int("LLMRS_ATTN_SPLITS", splits));
+    m->nsplit = std::max(1, splits);
     m->lm_grid = (int)gemv_plan(m->wt, "nq_argmax", c.vocab, H, cx.num_cus).grid;
     m->layers.resize(c.n_layers);
     for (auto& L : m->layers) {
@@ -745,7 +770,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     m->m_d = m->dalloc<float>(F / 32);
     m->logits = m->dalloc<float>(c.vocab);
     m->part_o = m->dalloc<float>((size_t)nq * m->nsplit * hd);
-    m->part_ml = m->dalloc<float>((size_t)nq * m->nsplit * 2);
+    m->part_ml = m->dalloc<float>((size_t)nq * llmrs::ml_stride(m->nsplit) * 2);
     const size_t nparts = (size_t)m->lm_grid;
     m->part_val = m->dalloc<float>(nparts);
     m->part_idx = m->dalloc<int>(nparts);
@@ -775,7 +800,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     (void)kernel(gemv_plan(m->wt, nqk ? "nq_argmax" : "norm_argmax", c.vocab, H, cx.num_cus).name);
     (void)kernel("embed_gather");
     (void)kernel("argmax_final");
-    (void)kernel(attn_kernel(m.get()));
+    (void)kernel(attn_kernel(m.get()), dim3(attn_threads(m.get())));
     *out = m.release();
   });
 }
@@ -921,22 +946,32 @@ int llmrs_model_kv_write(llmrs_model* m, int layer, int kv_head, size_t pos0, si
     LLMRS_REQUIRE(layer >= 0 && layer < c.n_layers && kv_head >= 0 && kv_head < c.n_kv_heads,
                   LLMRS_E_INVALID, "layer / kv_head out of range");
     LLMRS_REQUIRE(pos0 + n <= (size_t)c.max_seq, LLMRS_E_RANGE, "positions beyond max_seq");
-    const size_t cnt = n * c.head_dim, eb = kv_elem_bytes(m);
-    const size_t off = ((size_t)kv_head * c.max_seq + pos0) * c.head_dim * eb;
-    std::vector<uint8_t> kb(cnt * eb), vb(cnt * eb);
+    const int hd = c.head_dim;
+    const size_t cnt = n * hd, eb = kv_elem_bytes(m), head = (size_t)kv_head * kv_rows(m) * hd;
+    LayerBufs& Lb = m->layers[layer];
+    std::vector<uint8_t> kb(cnt * eb);
+    std::vector<uint16_t> vb;  // alive until the copies below have completed
     if (eb == 2) {
-      for (size_t i = 0; i < cnt; ++i) {
-        uint16_t hk = host_f2h(k[i]), hv = host_f2h(v[i]);
-        std::memcpy(&kb[2 * i], &hk, 2);
-        std::memcpy(&vb[2 * i], &hv, 2);
-      }
+      // K rows as they are; the f16 V cache is blocked (v_offset): read the
+      // 8-position blocks that [pos0, pos0 + n) touches, merge, write back.
+      const size_t b0 = pos0 / 8, b1 = (pos0 + n + 7) / 8;
+      vb.resize((b1 - b0) * 8 * hd);
+      uint16_t* vdev = (uint16_t*)Lb.vc + head + b0 * 8 * hd;
+      LLMRS_HIP(hipMemcpyAsync(vb.data(), vdev, vb.size() * 2, hipMemcpyDeviceToHost, ctx().stream));
+      LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+      for (size_t t = 0; t < n; ++t)
+        for (int d = 0; d < hd; ++d) {
+          const uint16_t hk = host_f2h(k[t * hd + d]);
+          std::memcpy(&kb[2 * (t * hd + d)], &hk, 2);
+          vb[llmrs::v_offset(pos0 + t, d, hd, true) - b0 * 8 * hd] = host_f2h(v[t * hd + d]);
+        }
+      LLMRS_HIP(hipMemcpyAsync(vdev, vb.data(), vb.size() * 2, hipMemcpyHostToDevice, ctx().stream));
     } else {
       std::memcpy(kb.data(), k, cnt * 4);
-      std::memcpy(vb.data(), v, cnt * 4);
+      LLMRS_HIP(hipMemcpyAsync((float*)Lb.vc + head + pos0 * hd, v, cnt * 4, hipMemcpyHostToDevice, ctx().stream));
     }
-    LayerBufs& Lb = m->layers[layer];
-    LLMRS_HIP(hipMemcpyAsync((uint8_t*)Lb.kc + off, kb.data(), kb.size(), hipMemcpyHostToDevice, ctx().stream));
-    LLMRS_HIP(hipMemcpyAsync((uint8_t*)Lb.vc + off, vb.data(), vb.size(), hipMemcpyHostToDevice, ctx().stream));
+    LLMRS_HIP(hipMemcpyAsync((uint8_t*)Lb.kc + (head + pos0 * hd) * eb, kb.data(), kb.size(),
+                             hipMemcpyHostToDevice, ctx().stream));
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));
   });
 }
@@ -949,24 +984,29 @@ int llmrs_model_kv_read(llmrs_model* m, int layer, int kv_head, size_t pos0, siz
     LLMRS_REQUIRE(layer >= 0 && layer < c.n_layers && kv_head >= 0 && kv_head < c.n_kv_heads,
                   LLMRS_E_INVALID, "layer / kv_head out of range");
     LLMRS_REQUIRE(pos0 + n <= (size_t)c.max_seq, LLMRS_E_RANGE, "positions beyond max_seq");
-    const size_t cnt = n * c.head_dim, eb = kv_elem_bytes(m);
-    const size_t off = ((size_t)kv_head * c.max_seq + pos0) * c.head_dim * eb;
-    std::vector<uint8_t> kb(cnt * eb), vb(cnt * eb);
+    const int hd = c.head_dim;
+    const size_t cnt = n * hd, eb = kv_elem_bytes(m), head = (size_t)kv_head * kv_rows(m) * hd;
     LayerBufs& Lb = m->layers[layer];
-    LLMRS_HIP(hipMemcpyAsync(kb.data(), (uint8_t*)Lb.kc + off, kb.size(), hipMemcpyDeviceToHost, ctx().stream));
-    LLMRS_HIP(hipMemcpyAsync(vb.data(), (uint8_t*)Lb.vc + off, vb.size(), hipMemcpyDeviceToHost, ctx().stream));
-    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
-    for (size_t i = 0; i < cnt; ++i) {
-      if (eb == 2) {
-        uint16_t hk, hv;
-        std::memcpy(&hk, &kb[2 * i], 2);
-        std::memcpy(&hv, &vb[2 * i], 2);
-        k[i] = host_h2f(hk);
-        v[i] = host_h2f(hv);
-      } else {
-        std::memcpy(&k[i], &kb[4 * i], 4);
-        std::memcpy(&v[i], &vb[4 * i], 4);
-      }
+    std::vector<uint8_t> kb(cnt * eb);
+    LLMRS_HIP(hipMemcpyAsync(kb.data(), (uint8_t*)Lb.kc + (head + pos0 * hd) * eb, kb.size(),
+                             hipMemcpyDeviceToHost, ctx().stream));
+    if (eb == 2) {  // blocked f16 V (v_offset): the 8-position blocks of the range
+      const size_t b0 = pos0 / 8, b1 = (pos0 + n + 7) / 8;
+      std::vector<uint16_t> vb((b1 - b0) * 8 * hd);
+      LLMRS_HIP(hipMemcpyAsync(vb.data(), (uint16_t*)Lb.vc + head + b0 * 8 * hd, vb.size() * 2,
+                               hipMemcpyDeviceToHost, ctx().stream));
+      LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+      for (size_t t = 0; t < n; ++t)
+        for (int d = 0; d < hd; ++d) {
+          uint16_t hk;
+          std::memcpy(&hk, &kb[2 * (t * hd + d)], 2);
+          k[t * hd + d] = host_h2f(hk);
+          v[t * hd + d] = host_h2f(vb[llmrs::v_offset(pos0 + t, d, hd, true) - b0 * 8 * hd]);
+        }
+    } else {
+      LLMRS_HIP(hipMemcpyAsync(v, (float*)Lb.vc + head + pos0 * hd, cnt * 4, hipMemcpyDeviceToHost, ctx().stream));
+      LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+      std::memcpy(k, kb.data(), cnt * 4);
     }
   });
 }

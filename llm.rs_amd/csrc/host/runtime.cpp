@@ -40,19 +40,28 @@ Context& ctx() {
   return *g_ctx;
 }
 
-hipFunction_t kernel(const std::string& name) {
+hipFunction_t kernel(const std::string& name, dim3 block) {
   Context& c = ctx();
   auto it = c.kernels.find(name);
-  if (it != c.kernels.end()) return it->second;
-  for (hipModule_t m : c.modules) {
-    hipFunction_t f = nullptr;
-    if (hipModuleGetFunction(&f, m, name.c_str()) == hipSuccess && f) {
-      c.kernels[name] = f;
-      return f;
+  if (it == c.kernels.end()) {
+    for (hipModule_t m : c.modules) {
+      KernelInfo k;
+      if (hipModuleGetFunction(&k.f, m, name.c_str()) == hipSuccess && k.f) {
+        LLMRS_HIP(hipFuncGetAttribute(&k.max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, k.f));
+        it = c.kernels.emplace(name, k).first;
+        break;
+      }
+    }
+    if (it == c.kernels.end()) {
+      (void)hipGetLastError();
+      fail(LLMRS_E_MODULE, "kernel not found in any loaded hsaco: " + name);
     }
   }
-  (void)hipGetLastError();
-  fail(LLMRS_E_MODULE, "kernel not found in any loaded hsaco: " + name);
+  const long threads = (long)block.x * block.y * block.z;
+  LLMRS_REQUIRE(threads <= it->second.max_threads, LLMRS_E_INVALID,
+                name + ": " + std::to_string(threads) + " threads per workgroup, compiled for at most " +
+                    std::to_string(it->second.max_threads));
+  return it->second.f;
 }
 
 int gemm_group_m() {

@@ -67,16 +67,16 @@ struct AttnArgs {
   const float* qkv;        // [nq*hd | nkv*hd | nkv*hd] projections of this token
   const int* pos_ptr;      // device position (the new token's index)
   void* kc;                // this layer's K cache [nkv][max_seq][hd]
-  void* vc;                // this layer's V cache [nkv][max_seq][hd]
+  void* vc;                // this layer's V cache [nkv][max_seq rows] (v_offset)
   const float* rope_cos;   // [max_seq][hd/2]
   const float* rope_sin;
   float* part_o;           // [nq][nsplit][hd]
-  float* part_ml;          // [nq][nsplit][2]
+  float* part_ml;          // [nq][ml_stride(nsplit)][2]
   int* counters;           // [nkv][kTicketStride] tickets, zero between launches
   float* ctx;              // [nq*hd]
   int8_t* ctx_q;           // [nq*hd]
   float* ctx_d;            // [nq*hd/32]
-  int max_seq, nq, nkv, nsplit;
+  int max_seq, nq, nkv, nsplit;  // max_seq: cache rows per KV head (kv_rows)
   float scale;             // fl(1 / fl(sqrt(hd))), layer.rs:258
   unsigned long long* ts;  // profiling: 8 stage timestamps per item (null = off)
 };
@@ -190,18 +190,37 @@ struct PrefillAttnArgs {
   float scale;           // fl(1 / fl(sqrt(hd)))
 };
 
-// LDS bytes of one decode-attention work item (attn_core.h: query heads, per
-// stream a padded K tile and a V tile, the new row, the ticket).  Tiles are
-// 64 positions for an f16 cache and 32 for f32; at most 8 query heads per KV
-// head; `streams` tile streams per workgroup.
 // ints between the split tickets of two KV heads: each head's counter has a
 // 256-byte line of its own, so the heads' atomics do not queue on one line.
 constexpr int kTicketStride = 64;
 
-// Positions per decode-attention tile (attn_core.h: AttnCfg::TILE).
-constexpr int attn_tile(bool kv16) { return kv16 ? 32 : 32; }
+// Positions per decode-attention tile (attn_core.h, attn_mfma.h).
+constexpr int kAttnTile = 32;
+constexpr int attn_tile(bool) { return kAttnTile; }
+// Splits of one matrix-core decode-attention launch at most (its combine
+// stages every split's (max, sum) of the group in LDS).
+constexpr int kMfmaAttnMaxSplits = 64;
+// (max, sum) pairs per query head in the decode-attention partials: the
+// split count rounded up to even, so the matrix-core combine reads them two
+// per 16-byte load.
+constexpr int ml_stride(int nsplit) { return (nsplit + 1) & ~1; }
+// Positions allocated per KV head in a layer's cache: max_seq rounded up to
+// whole tiles, so a tile load never leaves the buffer.
+constexpr int kv_rows(int max_seq) { return (max_seq + kAttnTile - 1) / kAttnTile * kAttnTile; }
+// Element offset of (position p, dim d) in one KV head's rows.  K, and a V
+// cache in f32, are row-major [p][hd]; a V cache in f16 is blocked and
+// transposed, [p/8][hd][p%8]: the 8 positions of a block are 16 contiguous
+// bytes per dim, one matrix-core operand (attn_mfma.h).
+constexpr size_t v_offset(size_t p, int d, int hd, bool f16) {
+  return f16 ? ((p / 8) * (size_t)hd + (size_t)d) * 8 + p % 8 : p * (size_t)hd + (size_t)d;
+}
+
+// LDS bytes of one vector-ALU decode-attention work item (attn_core.h, f32
+// caches: query heads, per stream a padded K tile and a V tile, the new row,
+// the ticket); at most 8 query heads per KV head; `streams` tile streams per
+// workgroup.
 constexpr size_t attn_lds_bytes(int hd, bool kv16, int streams = 1) {
-  const size_t es = kv16 ? 2 : 4, tile = (size_t)attn_tile(kv16), kstride = (size_t)hd + (kv16 ? 2 : 1);
+  const size_t es = kv16 ? 2 : 4, tile = (size_t)kAttnTile, kstride = (size_t)hd + (kv16 ? 2 : 1);
   const size_t kb = (es * tile * kstride + 15) / 16 * 16;
   const size_t stream = kb + es * tile * (size_t)hd;
   return 4 * 8 * (size_t)hd + (size_t)streams * stream + 4 * 2 * (size_t)hd + 16;

@@ -1,29 +1,43 @@
 // attention.hip - standalone batch-1 decode attention kernels for gfx950.
 //
-// One launch per layer: grid (nsplit, nkv), one work item of attn_core.h
-// (which documents the algorithm) per workgroup.  Reference:
-// LlamaAttention::forward with seq == 1 (layer.rs:175-299).
+// One launch per layer, one work item per workgroup, grid (nsplit, nkv).
+// f16 caches run on the matrix cores (attn_mfma.h, which documents the
+// algorithm and the blocked V layout); f32 caches on the vector ALUs
+// (attn_core.h).  Reference: LlamaAttention::forward with seq == 1
+// (layer.rs:175-299).
 #include "attn_core.h"
+#include "attn_mfma.h"
 
 using namespace llmrs;
 
-template <int HD, bool KV16, int S>
+template <int HD, int S>
 __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
-  __shared__ __align__(16) uint8_t lds[AttnLds<HD, KV16, S>::BYTES];
-  attn_item<HD, KV16, false, S>(a, blockIdx.y, blockIdx.x, *a.pos_ptr, lds);
+  __shared__ __align__(16) uint8_t lds[AttnLds<HD, false, S>::BYTES];
+  attn_item<HD, false, false, S>(a, blockIdx.y, blockIdx.x, *a.pos_ptr, lds);
 }
 
-// Variant names: attn_decode_hd<HD>_<cache>[_s<streams>].
-#define LLMRS_ATTN(name, HD, KV16, S)                                              \
-  extern "C" __global__ __launch_bounds__(256 * S) void name(AttnArgs a) {        \
-    attn_decode_impl<HD, KV16, S>(a);                                             \
-  }
+template <int HD, int TW>
+__device__ __forceinline__ void attn_decode_mfma_impl(const AttnArgs& a) {
+  __shared__ __align__(16) uint8_t lds[MfmaAttnLds<HD, TW>::BYTES];
+  attn_mfma_item<HD, TW>(a, *a.pos_ptr, lds);
+}
 
-LLMRS_ATTN(attn_decode_hd64_f32, 64, false, 1)
-LLMRS_ATTN(attn_decode_hd64_f16, 64, true, 1)
-LLMRS_ATTN(attn_decode_hd128_f32, 128, false, 1)
-LLMRS_ATTN(attn_decode_hd128_f16, 128, true, 1)
-LLMRS_ATTN(attn_decode_hd64_f32_s4, 64, false, 4)
-LLMRS_ATTN(attn_decode_hd64_f16_s4, 64, true, 4)
-LLMRS_ATTN(attn_decode_hd128_f32_s4, 128, false, 4)
-LLMRS_ATTN(attn_decode_hd128_f16_s4, 128, true, 4)
+// Variant names: attn_decode_hd<HD>_f32[_s<streams>].
+#define LLMRS_ATTN(name, HD, S)                                                    \
+  extern "C" __global__ __launch_bounds__(256 * S) void name(AttnArgs a) {        \
+    attn_decode_impl<HD, S>(a);                                                   \
+  }
+LLMRS_ATTN(attn_decode_hd64_f32, 64, 1)
+LLMRS_ATTN(attn_decode_hd128_f32, 128, 1)
+LLMRS_ATTN(attn_decode_hd64_f32_s4, 64, 4)
+LLMRS_ATTN(attn_decode_hd128_f32_s4, 128, 4)
+
+// attn_decode_mfma_hd<HD>_w<tile waves>
+#define LLMRS_ATTN_MFMA(name, HD, TW)                                              \
+  extern "C" __global__ __launch_bounds__(256) void name(AttnArgs a) {            \
+    attn_decode_mfma_impl<HD, TW>(a);                                             \
+  }
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w1, 64, 1)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w4, 64, 4)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w1, 128, 1)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w4, 128, 4)

@@ -74,6 +74,19 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// The value held by lane l ^ 32 (l ^ 16): with both operands v, gfx950's
+// v_permlane32_swap (v_permlane16_swap) returns the lower and the upper half
+// (the even and the odd 16-lane row) of v side by side, in VALU time rather
+// than an LDS permute's round trip.
+__device__ __forceinline__ float xor32(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(lane_id() < 32 ? p[1] : p[0]);
+}
+__device__ __forceinline__ float xor16(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((lane_id() & 16) ? p[0] : p[1]);
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) {
   return __half2float(__ushort_as_half(h));
 }

@@ -388,9 +388,10 @@ extern "C" __global__ __launch_bounds__(256) void prefill_rope_kv(PrefillRopeArg
     } else {
       const int g = h - r.nq - r.nkv;
       const size_t o = ((size_t)g * r.max_seq + pos) * r.hd;
-      if (r.kv16) {
-        ((uint16_t*)r.vc)[o + j] = f2h(src[j]);
-        ((uint16_t*)r.vc)[o + j + mid] = f2h(src[j + mid]);
+      if (r.kv16) {  // blocked V layout (v_offset)
+        const size_t hb = (size_t)g * r.max_seq * r.hd;
+        ((uint16_t*)r.vc)[hb + v_offset(pos, j, r.hd, true)] = f2h(src[j]);
+        ((uint16_t*)r.vc)[hb + v_offset(pos, j + mid, r.hd, true)] = f2h(src[j + mid]);
       } else {
         ((float*)r.vc)[o + j] = src[j];
         ((float*)r.vc)[o + j + mid] = src[j + mid];
@@ -447,7 +448,7 @@ __device__ __forceinline__ void attn_prefill_impl(const PrefillAttnArgs& a) {
       const int r = i / HD, d = i % HD;
       const int t = min(k0 + r, kend - 1);
       s_k[r][d] = kc[(size_t)t * HD + d];
-      s_v[r][d] = vc[(size_t)t * HD + d];
+      s_v[r][d] = vc[v_offset(t, d, HD, KV16)];
     }
     __syncthreads();
     float sc[2][KPT];
@@ -628,8 +629,9 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
     float m = -INFINITY, l = 0.0f;  // m in the log2 domain
 
     // K rows [key][HD] and V^T [HD][key] of tile pair (2i, 2i+1): thread
-    // chunk c < 2 * 32 * HD / 8 = (tile c / (32 HD / 8), key, part); keys
-    // clamped (those past kend are masked below).  Loaded a pair ahead.
+    // chunk c < 2 * 32 * HD / 8 = (tile c / (32 HD / 8), then key and 8-dim
+    // part of K, or dim and 8-key block of the blocked V); keys clamped
+    // (those past kend are masked below).  Loaded a pair ahead.
     constexpr int CPT = 2 * KT * HD / 8 / 512;
     u32x4 rk[CPT], rv[CPT];
     auto fetch = [&](int pr) {
@@ -638,9 +640,9 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
         const int c = tid + 512 * j;
         const int t = c / (KT * HD / 8), cc = c % (KT * HD / 8);
         const int key = cc / (HD / 8), part = cc % (HD / 8);
-        const size_t src = (size_t)min((2 * pr + t) * KT + key, kend - 1) * HD + part * 8;
-        rk[j] = *(const u32x4*)(kc + src);
-        rv[j] = *(const u32x4*)(vc + src);
+        rk[j] = *(const u32x4*)(kc + (size_t)min((2 * pr + t) * KT + key, kend - 1) * HD + part * 8);
+        const int vb = cc / HD, vd = cc % HD;
+        rv[j] = *(const u32x4*)(vc + v_offset(min((2 * pr + t) * KT + 8 * vb, kend - 1) & ~7, vd, HD, true));
       }
     };
     fetch(0);
@@ -653,11 +655,10 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
         const int key = cc / (HD / 8), part = cc % (HD / 8);
         uint8_t* tb = lds + t * LY::TILE;
         *(u32x4*)(tb + LY::K + key * LY::KROW + part * 16) = rk[j];
-        const unsigned vw[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          *(uint16_t*)(tb + LY::V + (part * 8 + e) * LY::VROW + key * 2) =
-              (uint16_t)(vw[e / 2] >> (16 * (e % 2)));
+        const int vb = cc / HD, vd = cc % HD;  // keys 8 vb .. 8 vb + 7 of dim vd
+        uint2* vdst = (uint2*)(tb + LY::V + vd * LY::VROW + vb * 16);
+        vdst[0] = make_uint2(rv[j].x, rv[j].y);
+        vdst[1] = make_uint2(rv[j].z, rv[j].w);
       }
       __syncthreads();
       if (pr + 1 < npair) fetch(pr + 1);

@@ -26,6 +26,8 @@ _SIGS = {
     "orc_record_codes": (None, [C.c_int]),
     "orc_set_attn_f64": (None, [C.c_int]),
     "orc_recorded_codes": (_I64, [_P, _I64]),
+    "orc_inject_codes": (None, [_P, _I64, C.c_float]),
+    "orc_injected_stats": (None, [_P, _P, _P, _P]),
     "orc_gemv_codes": (None, [_P, _P, _I64, _I64, _P, _P, _I64, C.c_int, _P]),
     "orc_model_attention": (C.c_int, [_P, C.c_int, _P, _I64, _I64, _P]),
     "orc_quantize_row_q8_0": (None, [_P, _I64, _P, _P]),
@@ -109,6 +111,28 @@ def recorded_codes() -> np.ndarray:
     out = np.empty(n, np.int8)
     lib().orc_recorded_codes(_p(out), n)
     return out
+
+
+def inject_codes(codes, tol: float = 0.0) -> None:
+    """Test-only: replay forward passes with these Q8_0 codes (in the call
+    order of quantize_row_q8_0) instead of the oracle's own rounding; None
+    stops.  Differing codes are checked against `tol` (injected_stats)."""
+    if codes is None:
+        lib().orc_inject_codes(None, 0, 0.0)
+        return
+    codes = np.ascontiguousarray(codes, np.int8)
+    inject_codes._held = codes
+    lib().orc_inject_codes(_p(codes), codes.size, float(tol))
+
+
+def injected_stats() -> dict:
+    """Codes taken, codes differing from the oracle's own, differing codes
+    not one step away at a rounding midpoint (within tol, or past the end of
+    the given codes), and the largest midpoint distance of a differing code."""
+    t, d, b = (C.c_int64(), C.c_int64(), C.c_int64())
+    m = C.c_float()
+    lib().orc_injected_stats(C.byref(t), C.byref(d), C.byref(b), C.byref(m))
+    return {"taken": t.value, "differ": d.value, "bad": b.value, "max_dist": m.value}
 
 
 def gemv_codes(xq, xd, w, scales, n, q8w=False):

@@ -187,6 +187,13 @@ std::atomic<int> g_record{0};
 std::mutex g_record_mu;
 std::vector<int8_t> g_recorded;
 
+// Test-only substitution of Q8_0 codes (orc_inject_codes), guarded by
+// g_record_mu.
+std::atomic<int> g_inject{0};
+std::vector<int8_t> g_inject_codes;
+int64_t g_inject_pos = 0, g_inject_differ = 0, g_inject_bad = 0;
+float g_inject_tol = 0.0f, g_inject_max_dist = 0.0f;
+
 // Exact integer sum over one Q4 block: sum_i (q_i - 8) * a_i, with the
 // reference nibble order (element 2i = low nibble of byte i, element 2i+1 =
 // high nibble; tensor.rs:125-131).  Any evaluation order gives the same
@@ -318,6 +325,45 @@ void orc_quantize_row_q8_0(const float* x, int64_t k, int8_t* q, float* d) {
     std::lock_guard<std::mutex> lk(g_record_mu);
     g_recorded.insert(g_recorded.end(), q, q + nb * 32);
   }
+  if (g_inject.load(std::memory_order_relaxed)) {
+    std::lock_guard<std::mutex> lk(g_record_mu);
+    for (int64_t b = 0; b < nb; ++b) {
+      const float inv = d[b] == 0.0f ? 0.0f : 1.0f / d[b];
+      for (int i = 0; i < 32; ++i) {
+        const int64_t e = 32 * b + i;
+        if (g_inject_pos >= (int64_t)g_inject_codes.size()) {
+          ++g_inject_bad;  // more codes asked for than given
+          continue;
+        }
+        const int8_t c = g_inject_codes[g_inject_pos++];
+        if (c == q[e]) continue;
+        ++g_inject_differ;
+        // midpoint between the two codes, in code units
+        const float p = x[e] * inv, mid = 0.5f * ((float)c + (float)q[e]);
+        const float dist = std::fabs(p - mid);
+        g_inject_max_dist = std::max(g_inject_max_dist, dist);
+        if (std::abs((int)c - (int)q[e]) != 1 || !(dist <= g_inject_tol)) ++g_inject_bad;
+        q[e] = c;
+      }
+    }
+  }
+}
+
+void orc_inject_codes(const int8_t* codes, int64_t n, float tol) {
+  std::lock_guard<std::mutex> lk(g_record_mu);
+  g_inject_codes.assign(codes ? codes : nullptr, codes ? codes + n : nullptr);
+  g_inject_pos = g_inject_differ = g_inject_bad = 0;
+  g_inject_tol = tol;
+  g_inject_max_dist = 0.0f;
+  g_inject.store(codes ? 1 : 0);
+}
+
+void orc_injected_stats(int64_t* taken, int64_t* differ, int64_t* bad, float* max_dist) {
+  std::lock_guard<std::mutex> lk(g_record_mu);
+  *taken = g_inject_pos;
+  *differ = g_inject_differ;
+  *bad = g_inject_bad;
+  *max_dist = g_inject_max_dist;
 }
 
 // Tensor::quantize_q4 (tensor.rs:102-167): d = amax/7, q = trunc(clamp(x/d +

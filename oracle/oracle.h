@@ -51,6 +51,16 @@ void orc_set_attn_f64(int on);
  * orc_recorded_codes copies up to `cap` of them and returns the count. */
 void orc_record_codes(int on);
 int64_t orc_recorded_codes(int8_t* out, int64_t cap);
+/* Test-only: while `codes` is set (null stops), quantize_row_q8_0 takes its
+ * codes from it in call order instead of its own rounding - so a forward
+ * pass can be replayed with another implementation's activation codes - and
+ * checks each taken code against its own: a differing code must be one step
+ * away with the product x*inv within `tol` (code units) of the rounding
+ * midpoint between the two.  orc_injected_stats reports codes taken,
+ * codes that differ, differing codes failing that check, and the largest
+ * midpoint distance of a differing code. */
+void orc_inject_codes(const int8_t* codes, int64_t n, float tol);
+void orc_injected_stats(int64_t* taken, int64_t* differ, int64_t* bad, float* max_dist);
 
 /* ---- cpu.rs primitives -------------------------------------------------- */
 void orc_quantize_row_q8_0(const float* x, int64_t k, int8_t* q, float* d);

@@ -146,7 +146,7 @@ def check_decode_attention(gm, om, orc, spec, pr, pos):
 # (workload, pre-filled positions): the 1B Q4_0/f32-KV and Q8_0/f16-KV, 8B
 # and 70B layer widths with every GEMV shape of the workloads, the full
 # 128256-row lm_head included.  The 70B case decodes at position 8192, where
-# the attention runs 32 splits x 4 tile streams with 2-3 tiles per stream
+# the matrix-core attention runs 32 splits x 4 waves with 2-3 tiles per wave
 # (the long-context layout of the 70B workload).
 DECODE_CASES = [(0, 300), (1, 300), (2, 700), (4, 8192)]
 
@@ -199,7 +199,12 @@ def test_decode_layer_kernels(hip, orc, index, pos):
 # all run.  Two steps in a row, and the second step repeated: equal inputs
 # give bit-identical outputs (a split that read stale LDS once made them
 # differ run to run).
-ATTN_LAYOUTS = [(1, 1), (1, 2), (1, 3), (4, 1), (4, 2)]
+# (tile streams or waves, splits): tile streams per workgroup of the vector
+# kernel (f32 caches), tile waves per workgroup of the matrix-core kernel
+# (f16).  At position 700 (22 tiles) one tile wave runs 22, 11 or 8 tiles
+# with 1, 2 or 3 splits, four run 6 or 3 per wave with 1 or 2 splits, and 7
+# or 64 splits leave waves and whole splits without a tile.
+ATTN_LAYOUTS = [(1, 1), (1, 2), (1, 3), (4, 1), (4, 2), (1, 7), (1, 64), (4, 7)]
 
 
 @pytest.mark.parametrize("kv", [DType.F16, DType.F32], ids=["f16", "f32"])
@@ -208,7 +213,7 @@ ATTN_LAYOUTS = [(1, 1), (1, 2), (1, 3), (4, 1), (4, 2)]
 @pytest.mark.parametrize("streams,splits", ATTN_LAYOUTS, ids=lambda v: str(v))
 def test_decode_attention_layouts(hip, orc, kv, head_dim, nkv, streams, splits, monkeypatch):
     """Query heads per KV head: 2 (nkv = 8) and 8 (nkv = 2)."""
-    monkeypatch.setenv("LLMRS_ATTN_STREAMS", str(streams))
+    monkeypatch.setenv("LLMRS_ATTN_STREAMS" if kv == DType.F32 else "LLMRS_ATTN_WAVES", str(streams))
     monkeypatch.setenv("LLMRS_ATTN_SPLITS", str(splits))
     pos = 700
     spec = syn.tiny(DType.Q4_0, kv, head_dim=head_dim, n_layers=1, n_heads=16, n_kv_heads=nkv, ffn=512,

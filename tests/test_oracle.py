@@ -338,3 +338,39 @@ def test_gemv_codes_matches_matmul_transposed(orc, rng):
     w8 = rng.integers(-127, 128, n * k).astype(np.int8)
     got8 = orc.gemv_codes(np.stack(xq), np.stack(xd), w8, sc, n, q8w=True)
     assert np.array_equal(got8, orc.matmul_transposed_q8w(a, w8, sc, n))
+
+
+def test_code_replay_checks_midpoints(orc):
+    """orc_inject_codes: the oracle takes the given codes; a differing code
+    passes only one step away from its own with x*inv at the rounding
+    midpoint (within tol).  One block with amax 127 (d = 1, inv = 1): 2.5
+    sits on the 2|3 midpoint, 2.2 does not."""
+    x = np.zeros(32, np.float32)
+    x[0], x[1], x[2] = 127.0, 2.5, 2.2
+    own, d = orc.quantize_row_q8_0(x)
+    assert own[1] == 3 and own[2] == 2 and d[0] == 1.0
+    try:
+        orc.inject_codes(own, 1e-3)  # its own codes: nothing differs
+        q, _ = orc.quantize_row_q8_0(x)
+        st = orc.injected_stats()
+        assert np.array_equal(q, own) and st == {"taken": 32, "differ": 0, "bad": 0, "max_dist": 0.0}
+        mid = own.copy()
+        mid[1] = 2  # the other side of the 2.5 midpoint: taken, not bad
+        orc.inject_codes(mid, 1e-3)
+        q, _ = orc.quantize_row_q8_0(x)
+        st = orc.injected_stats()
+        assert q[1] == 2 and st["differ"] == 1 and st["bad"] == 0 and st["max_dist"] == 0.0
+        for i, c in ((2, 3), (1, 1)):  # 2.2 is 0.3 from a midpoint; 1 is two steps from 3
+            bad = own.copy()
+            bad[i] = c
+            orc.inject_codes(bad, 1e-3)
+            q, _ = orc.quantize_row_q8_0(x)
+            st = orc.injected_stats()
+            assert q[i] == c and st["differ"] == 1 and st["bad"] == 1
+        orc.inject_codes(own[:16], 1e-3)  # fewer codes than asked for
+        orc.quantize_row_q8_0(x)
+        assert orc.injected_stats()["bad"] == 16
+    finally:
+        orc.inject_codes(None)
+    q, _ = orc.quantize_row_q8_0(x)
+    assert np.array_equal(q, own)
