@@ -167,7 +167,7 @@ std::string attn_kernel(const llmrs_model* m) {
 }
 // Its threads per workgroup.
 unsigned attn_threads(const llmrs_model* m) {
-  return m->c.kv_dtype == LLMRS_F16 ? 256u : 256u * (unsigned)m->attn_streams;
+  return m->c.kv_dtype == LLMRS_F16 ? 64u * (unsigned)std::max(4, m->attn_waves) : 256u * (unsigned)m->attn_streams;
 }
 
 // x = the embedding of the token at the device position, or (x_in set) the
@@ -709,7 +709,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     // Attention splits over the tiles of max_seq.  f16 caches (matrix-core
     // kernel; attn_waves = its tile waves per workgroup): one tile per
     // workgroup up to two workgroups per CU (and the combine's 64 splits),
-    // beyond that four tile waves per workgroup and up to one workgroup per
+    // beyond that eight tile waves per workgroup and up to one workgroup per
     // CU.  f32 caches (vector kernel): one tile per split up to two
     // workgroups per CU; longer contexts run 4 tile streams per workgroup
     // (one workgroup per CU) so the split combine stays short.
@@ -717,10 +717,11 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     int splits;
     m->attn_streams = 1;
     if (c.kv_dtype == LLMRS_F16) {
-      const int ew = env_int("LLMRS_ATTN_WAVES", 0);  // 0 = by context length, 1 or 4 = forced
-      const bool one = ew == 1 || (ew == 0 && tiles <= std::min(llmrs::kMfmaAttnMaxSplits, 2 * cx.num_cus / nkv));
-      m->attn_waves = one ? 1 : 4;
-      splits = one ? tiles : std::min((tiles + 3) / 4, std::max(1, cx.num_cus / nkv));
+      int ew = env_int("LLMRS_ATTN_WAVES", 0);  // 0 = by context length; 1, 4 or 8 = forced
+      if (ew != 1 && ew != 4 && ew != 8)
+        ew = tiles <= std::min(llmrs::kMfmaAttnMaxSplits, 2 * cx.num_cus / nkv) ? 1 : 8;
+      m->attn_waves = ew;
+      splits = ew == 1 ? tiles : std::min((tiles + ew - 1) / ew, std::max(1, cx.num_cus / nkv));
       splits = std::min(env_int("LLMRS_ATTN_SPLITS", splits), llmrs::kMfmaAttnMaxSplits);
     } else {
       splits = std::min(tiles, std::max(1, 2 * cx.num_cus / nkv));

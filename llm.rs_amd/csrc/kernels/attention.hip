@@ -32,12 +32,14 @@ LLMRS_ATTN(attn_decode_hd128_f32, 128, 1)
 LLMRS_ATTN(attn_decode_hd64_f32_s4, 64, 4)
 LLMRS_ATTN(attn_decode_hd128_f32_s4, 128, 4)
 
-// attn_decode_mfma_hd<HD>_w<tile waves>
-#define LLMRS_ATTN_MFMA(name, HD, TW)                                              \
-  extern "C" __global__ __launch_bounds__(256) void name(AttnArgs a) {            \
-    attn_decode_mfma_impl<HD, TW>(a);                                             \
+// attn_decode_mfma_hd<HD>_w<tile waves>: max(4, tile waves) waves
+#define LLMRS_ATTN_MFMA(name, HD, TW)                                                   \
+  extern "C" __global__ __launch_bounds__(64 * (TW > 4 ? TW : 4)) void name(AttnArgs a) { \
+    attn_decode_mfma_impl<HD, TW>(a);                                                  \
   }
 LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w1, 64, 1)
 LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w4, 64, 4)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w8, 64, 8)
 LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w1, 128, 1)
 LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w4, 128, 4)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w8, 128, 8)

@@ -8,11 +8,12 @@
 // head h reads KV head h / n_rep (the reference duplicates the K/V rows per
 // query head, loader.rs:62-98, which gives the same numbers).
 //
-// One workgroup of 4 waves per (KV head g, split); TW of them (1 or 4) take
-// tiles.  The KV head's tiles of 32 positions are dealt over (split, tile
-// wave): tile (i * TW + wave) * nsplit + split for i = 0, 1, ...  TW = 1
-// spreads a short context's tiles over the most CUs (a tile's 16 KB of loads
-// per CU); TW = 4 keeps four tiles in flight per CU for long contexts.  A
+// One workgroup of max(4, TW) waves per (KV head g, split); TW of them (1,
+// 4 or 8) take tiles.  The KV head's tiles of 32 positions are dealt over
+// (split, tile wave): tile (i * TW + wave) * nsplit + split for i = 0, 1,
+// ...  TW = 1 spreads a short context's tiles over the most CUs (a tile's
+// 16 KB of loads per CU); TW = 4 or 8 keeps that many tiles in flight per CU
+// for long contexts.  A
 // wave takes a whole tile for all n_rep query heads of the group with
 // v_mfma_f32_16x16x32_f16 (A 16 x 32, B 32 x 16; the 16 columns are query
 // heads, at most 16):
@@ -33,8 +34,7 @@
 // current one is computed.  The tile waves' (max, sum, O) merge through LDS
 // into the split's partials; the last workgroup of the KV head (atomic
 // ticket; partials move with device-scope stores and loads) combines the
-// splits with all four waves and writes ctx as f32 and as Q8_0 codes for the
-// O projection.
+// splits and writes ctx as f32 and as Q8_0 codes for the O projection.
 //
 // v_mfma_f32_16x16x32_f16 lane layout: lane l holds A[l%16][8(l/16) + e],
 // B[8(l/16) + e][l%16] (e = 0..7) and D[4(l/16) + i][l%16] (i = 0..3).
@@ -82,7 +82,7 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   constexpr float kP = 16384.0f;  // p is scaled by 2^14 before its hi/lo split
   typedef MfmaAttnLds<HD, TW> LY;
   static_assert(TILE == 32, "two 16-position blocks per tile");
-  static_assert(TW == 1 || TW == 4, "one or four tile waves");
+  static_assert(TW == 1 || TW == 4 || TW == 8, "one, four or eight tile waves");
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int c = lane & 15, r = lane >> 4;  // MFMA column (query head of the group), lane group
   const int g = blockIdx.y, split = blockIdx.x;
@@ -379,26 +379,38 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
 #pragma unroll
     for (int b = 0; b < NB; ++b) o[b] = mfma16(as_h16x8(op.v[b]), pl, o[b]);
   };
-  // Tiles of this wave, two register sets in turn.
+  // Tiles of this wave: with up to four tile waves, two register sets in
+  // turn (the next tile loads while one is computed); with eight, two waves
+  // per SIMD share the registers, so one set, and a wave rarely has a second
+  // tile.
   int t0 = first;
-  while (t0 < T) {
-    int t1 = t0 + stride;
-    if (t1 < T) fetch(B, t1);
-    if (owner && t0 == town) patch(A);
-    process(A, t0);
-    if (t0 == first) stamp(2);
-    t0 = t1;
-    if (t0 >= T) break;
-    t1 = t0 + stride;
-    if (t1 < T) fetch(A, t1);
-    if (owner && t0 == town) patch(B);
-    process(B, t0);
-    t0 = t1;
+  if constexpr (TW <= 4) {
+    while (t0 < T) {
+      int t1 = t0 + stride;
+      if (t1 < T) fetch(B, t1);
+      if (owner && t0 == town) patch(A);
+      process(A, t0);
+      if (t0 == first) stamp(2);
+      t0 = t1;
+      if (t0 >= T) break;
+      t1 = t0 + stride;
+      if (t1 < T) fetch(A, t1);
+      if (owner && t0 == town) patch(B);
+      process(B, t0);
+      t0 = t1;
+    }
+  } else {
+    for (; t0 < T; t0 += stride) {
+      if (t0 != first) fetch(A, t0);
+      if (owner && t0 == town) patch(A);
+      process(A, t0);
+      if (t0 == first) stamp(2);
+    }
   }
   stamp(3);
 
   // The split's partials: with one tile wave its own (max, sum, O); with
-  // four, merged through LDS, wave w writing O blocks w, w + 4, ...
+  // more, merged through LDS, wave w writing O blocks w, w + TW, ...
   const size_t pidx = (size_t)(g * n_rep + c) * a.nsplit + split;
   const size_t midx = (size_t)(g * n_rep + c) * ml_stride(a.nsplit) + split;
   if constexpr (TW == 1) {
@@ -436,7 +448,7 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
       L = L + cw[w] * sml[(w * 16 + c) * 2 + 1];
     }
 #pragma unroll
-    for (int b = wave; b < NB; b += 4) {
+    for (int b = wave; b < NB; b += TW) {
       f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int w = 0; w < TW; ++w)

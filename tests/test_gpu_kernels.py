@@ -200,11 +200,12 @@ def test_decode_layer_kernels(hip, orc, index, pos):
 # give bit-identical outputs (a split that read stale LDS once made them
 # differ run to run).
 # (tile streams or waves, splits): tile streams per workgroup of the vector
-# kernel (f32 caches), tile waves per workgroup of the matrix-core kernel
-# (f16).  At position 700 (22 tiles) one tile wave runs 22, 11 or 8 tiles
-# with 1, 2 or 3 splits, four run 6 or 3 per wave with 1 or 2 splits, and 7
-# or 64 splits leave waves and whole splits without a tile.
-ATTN_LAYOUTS = [(1, 1), (1, 2), (1, 3), (4, 1), (4, 2), (1, 7), (1, 64), (4, 7)]
+# kernel (f32 caches: 1 or 4), tile waves per workgroup of the matrix-core
+# kernel (f16: 1, 4 or 8).  At position 700 (22 tiles) one tile wave runs
+# 22, 11 or 8 tiles with 1, 2 or 3 splits, four run 6 or 3 per wave with 1
+# or 2 splits, eight run 3 or 1-2 with 1 or 2 splits, and 7 or 64 splits
+# leave waves and whole splits without a tile.
+ATTN_LAYOUTS = [(1, 1), (1, 2), (1, 3), (4, 1), (4, 2), (1, 7), (1, 64), (4, 7), (8, 1), (8, 2), (8, 7)]
 
 
 @pytest.mark.parametrize("kv", [DType.F16, DType.F32], ids=["f16", "f32"])
@@ -213,6 +214,8 @@ ATTN_LAYOUTS = [(1, 1), (1, 2), (1, 3), (4, 1), (4, 2), (1, 7), (1, 64), (4, 7)]
 @pytest.mark.parametrize("streams,splits", ATTN_LAYOUTS, ids=lambda v: str(v))
 def test_decode_attention_layouts(hip, orc, kv, head_dim, nkv, streams, splits, monkeypatch):
     """Query heads per KV head: 2 (nkv = 8) and 8 (nkv = 2)."""
+    if kv == DType.F32 and streams == 8:
+        pytest.skip("the vector kernel runs 1 or 4 tile streams")
     monkeypatch.setenv("LLMRS_ATTN_STREAMS" if kv == DType.F32 else "LLMRS_ATTN_WAVES", str(streams))
     monkeypatch.setenv("LLMRS_ATTN_SPLITS", str(splits))
     pos = 700
