@@ -46,6 +46,7 @@ extern "C" {
 #define LLMRS_E_MODULE (-5)     /* hsaco missing or kernel not found */
 #define LLMRS_E_RANGE (-6)      /* position beyond max_seq, id beyond vocab */
 #define LLMRS_E_OOM (-7)        /* device allocation failed */
+#define LLMRS_E_FORMAT (-8)     /* unreadable or unsupported weight file */
 
 /* ---- devices (src/backend.rs:7-12 plus the new Hip variant) ------------- */
 #define LLMRS_DEVICE_CPU 0
@@ -179,6 +180,8 @@ typedef struct {
 
 int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out);
 int llmrs_model_free(llmrs_model* m);
+/* The configuration a model was created with (e.g. by a loader). */
+int llmrs_model_get_config(const llmrs_model* m, llmrs_model_config* out);
 /* embed_tokens (loader.rs:105): f32 [vocab][hidden]. */
 int llmrs_model_set_embedding(llmrs_model* m, const float* table);
 int llmrs_model_set_norm(llmrs_model* m, int layer, int slot, const float* w);
@@ -191,6 +194,31 @@ int llmrs_model_set_linear_q4(llmrs_model* m, int layer, int slot,
 /* A linear weight in Q8_0 (weight_dtype LLMRS_Q8_0): int8 [n][k] + scales. */
 int llmrs_model_set_linear_q8_0(llmrs_model* m, int layer, int slot,
                                 const int8_t* qs, const float* scales);
+/* Loading a model from weight files (Loader::load_model, loader.rs:100-198).
+ * max_seq <= 0 takes the reference's 2048 positions (KVCache::new,
+ * loader.rs:162-166); weight_dtype 0 takes the file's own (else it must
+ * match); a NULL options pointer means {2048, LLMRS_F16, 0}. */
+typedef struct {
+  int32_t max_seq;
+  int32_t kv_dtype;     /* LLMRS_F16 | LLMRS_F32 */
+  int32_t weight_dtype; /* 0 | LLMRS_Q4 | LLMRS_Q4_0 | LLMRS_Q8_0 */
+} llmrs_load_options;
+/* A Hugging Face checkpoint: `path` is a directory holding config.json and
+ * model.safetensors (or model.safetensors.index.json with its shards), or
+ * a .safetensors file with config.json beside it.  F32/BF16 tensors (F16
+ * too); every linear weight quantised with Tensor::quantize_q4
+ * (tensor.rs:102-167) into LLMRS_Q4; lm_head, or the tied embedding when
+ * the checkpoint has none (loader.rs:186-190).  Replaces Loader::new +
+ * Loader::load_model (loader.rs:19-23,100-198). */
+int llmrs_model_load_safetensors(const char* path, const llmrs_load_options* opt,
+                                 llmrs_model** out);
+/* A GGUF file of the llama architecture (no reference counterpart): Q4_0
+ * and Q8_0 linear weights are uploaded as they are, in the model weight
+ * dtype of the same name (all linear weights must share one), F32/F16/BF16
+ * ones quantised as above; Q and K rows are put back from llama.cpp's
+ * interleaved RoPE order into the rotate-half order; output.weight, or the
+ * tied token_embd.weight, as lm_head. */
+int llmrs_model_load_gguf(const char* path, const llmrs_load_options* opt, llmrs_model** out);
 /* Write already-rotated K and V rows for positions [pos0, pos0+n) of one
  * layer and KV head (pre-filled caches); k, v are f32 [n][head_dim], stored
  * in the model's kv_dtype. */

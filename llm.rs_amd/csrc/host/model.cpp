@@ -1267,6 +1267,13 @@ int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
   return rc ? rc : count;
 }
 
+int llmrs_model_get_config(const llmrs_model* m, llmrs_model_config* out) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && out, LLMRS_E_INVALID, "null argument");
+    *out = m->c;
+  });
+}
+
 double llmrs_model_weight_bytes(const llmrs_model* m) {
   if (!m) return 0.0;
   double b = linear_weight_bytes(m, m->lm_head);

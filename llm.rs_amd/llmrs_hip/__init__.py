@@ -82,6 +82,9 @@ _SIGS = {
     "llmrs_copy_from": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
     "llmrs_model_create": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
     "llmrs_model_free": (C.c_int, [C.c_void_p]),
+    "llmrs_model_get_config": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "llmrs_model_load_safetensors": (C.c_int, [C.c_char_p, C.c_void_p, C.POINTER(C.c_void_p)]),
+    "llmrs_model_load_gguf": (C.c_int, [C.c_char_p, C.c_void_p, C.POINTER(C.c_void_p)]),
     "llmrs_model_set_embedding": (C.c_int, [C.c_void_p, C.c_void_p]),
     "llmrs_model_set_norm": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "llmrs_model_set_linear_q4": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
@@ -306,6 +309,12 @@ class ModelConfig(C.Structure):
     ]
 
 
+class LoadOptions(C.Structure):
+    """llmrs_load_options: KV capacity (<= 0: 2048), KV storage, weight
+    storage (0: the file's own)."""
+    _fields_ = [("max_seq", C.c_int32), ("kv_dtype", C.c_int32), ("weight_dtype", C.c_int32)]
+
+
 W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN, W_LM_HEAD = range(8)
 N_INPUT, N_POST, N_FINAL = range(3)
 
@@ -343,6 +352,34 @@ class HipModel:
         h = C.c_void_p()
         _check(lib().llmrs_model_create(C.byref(cfg), C.byref(h)))
         self._h = h
+
+    @classmethod
+    def _adopt(cls, h: C.c_void_p) -> "HipModel":
+        self = cls.__new__(cls)
+        self._h = h
+        self.cfg = ModelConfig()
+        _check(lib().llmrs_model_get_config(h, C.byref(self.cfg)))
+        return self
+
+    @classmethod
+    def load_safetensors(cls, path, max_seq: int = 0, kv: DType = DType.F16, device: int = 0) -> "HipModel":
+        """A Hugging Face checkpoint (directory with config.json and
+        model.safetensors or its shards): llmrs_model_load_safetensors."""
+        init(device)
+        opt = LoadOptions(int(max_seq), int(kv), 0)
+        h = C.c_void_p()
+        _check(lib().llmrs_model_load_safetensors(str(path).encode(), C.byref(opt), C.byref(h)))
+        return cls._adopt(h)
+
+    @classmethod
+    def load_gguf(cls, path, max_seq: int = 0, kv: DType = DType.F16, weight: int = 0,
+                  device: int = 0) -> "HipModel":
+        """A llama-architecture GGUF file: llmrs_model_load_gguf."""
+        init(device)
+        opt = LoadOptions(int(max_seq), int(kv), int(weight))
+        h = C.c_void_p()
+        _check(lib().llmrs_model_load_gguf(str(path).encode(), C.byref(opt), C.byref(h)))
+        return cls._adopt(h)
 
     def close(self) -> None:
         if self._h and self._h.value:

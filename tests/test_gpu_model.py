@@ -35,11 +35,10 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import rel_close
+from conftest import NEAR_TIE, check_stream, rel_close
 from llmrs_hip import DType, synthetic as syn
 
 pytestmark = pytest.mark.gpu
-NEAR_TIE = 2e-3
 
 
 def reference_builds(orc, spec, w, toks, steps=0, max_seq=None, prefill=None, start_pos=0):
@@ -101,19 +100,6 @@ def rel_norm_err(got, want):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
-
-
-def check_stream(gpu, ref, margins, min_steps=64):
-    gpu, ref = np.asarray(gpu), np.asarray(ref)
-    mism = np.nonzero(gpu != ref)[0]
-    if mism.size == 0:
-        return len(ref)
-    i = int(mism[0])
-    assert margins[i] < NEAR_TIE, (
-        f"greedy stream diverged at step {i} with oracle margin {margins[i]:.4g}: "
-        f"gpu {gpu[max(0, i - 2):i + 3]} oracle {ref[max(0, i - 2):i + 3]}")
-    assert i >= min(min_steps, len(ref)) or margins[i] < NEAR_TIE
-    return i
 
 
 TINY = [
