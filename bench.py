@@ -381,6 +381,27 @@ def main() -> int:
     wbytes = model.weight_bytes()
     roof_tok_s = HBM_PEAK_GBS * 1e9 / wbytes
 
+    # Sampled decoding (the reference token loop's defaults: penalty 1.2 over
+    # 64 ids, temperature 0.8, top_p 0.9; no end-of-sequence stop) from the
+    # same prompt, and the sampler's own duration in an eager step.
+    samp = lh.Sampling.make(seed=2026, eos=())
+    model.set_sampling(samp)
+    sampled_steps = min(64, args.steps)
+    model.begin(prompt, start_pos=pre)
+    model.decode_steps(min(4, args.warmup))
+    lh.sync()
+    t0 = time.perf_counter()
+    model.decode_steps(sampled_steps)
+    lh.sync()
+    sdt = time.perf_counter() - t0
+    sampler = [k for k in model.profile_step() if k.name.startswith("sample_")]
+    model.set_sampling(None)
+    sampled = {"tok_s": round(sampled_steps / sdt, 1), "steps": sampled_steps,
+               "sampler_us": round(sum(k.ms for k in sampler) * 1e3, 2) if sampler else None,
+               "sampler_launches": len(sampler),
+               "temperature": 0.8, "top_p": 0.9, "repeat_penalty": 1.2, "penalty_window": 64}
+    log(f"sampled decode: {sampled['tok_s']} tok/s, sampler {sampled['sampler_us']} us per token")
+
     prefill = None
     if pf_spec:
         t0 = time.perf_counter()
@@ -428,6 +449,7 @@ def main() -> int:
         "weight_gb_per_token": round(wbytes / 1e9, 4),
         "prompt_ms": round(prompt_s * 1e3, 1),
         "prefill": prefill,
+        "sampled_decode": sampled,
         "kernels": kernels,
     }
     print(json.dumps(line), flush=True)

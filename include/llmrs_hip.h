@@ -247,7 +247,43 @@ int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n,
  * decode position runs as one replay of a captured HIP graph. */
 int llmrs_model_generate(llmrs_model* m, const int32_t* prompt,
                          size_t n_prompt, size_t n_steps, int32_t* out_tokens);
-/* Benchmark helpers: start a greedy run (prompt processed, state resident),
+/* ---- sampling (src/main.rs:192-305) ------------------------------------
+ * The token loop's sampling in place of the greedy argmax: repetition
+ * penalty, temperature, softmax, then nucleus (top_p < 1) or roulette
+ * sampling, and the end-of-sequence stop.  The reference draws U from an
+ * unseeded thread RNG (main.rs:123, rng.random::<f32>()); here the draw after
+ * the token at position p uses U = (output p+1 of the SplitMix64 stream
+ * seeded with `seed`) >> 40, times 2^-24 - 24 random bits, as the
+ * reference's f32 draw - so a run repeats. */
+#define LLMRS_MAX_EOS 8
+typedef struct {
+  float temperature;      /* logits / t unless |t - 1| <= 1e-6 (main.rs:214-220); finite, > 0 */
+  float top_p;            /* < 1: nucleus over p > 1e-5 (main.rs:249-283); >= 1: roulette (main.rs:284-294) */
+  float repeat_penalty;   /* > 1: the ids of the history window penalised (main.rs:193-212) */
+  int32_t penalty_window; /* ids of the history penalised; <= 0: all of it */
+  uint64_t seed;
+  int32_t n_eos;          /* end-of-sequence ids (main.rs:121), up to LLMRS_MAX_EOS */
+  int32_t eos[LLMRS_MAX_EOS];
+} llmrs_sampling;
+/* Sets (s != NULL) or clears (NULL: greedy argmax) the sampling of the
+ * model's decode steps: llmrs_model_begin, decode_steps and generate, and
+ * llmrs_model_forward's `next`.  The penalty history is the prompt plus the
+ * ids produced.  A drawn end-of-sequence id ends the sequence (main.rs:
+ * 308-310): it is not appended, and later steps leave the tokens as they are.
+ * llmrs_model_generate then fills the rest of out_tokens with -1.
+ * Vocabularies up to 262144 ids. */
+int llmrs_model_set_sampling(llmrs_model* m, const llmrs_sampling* s);
+/* Tokens produced since llmrs_model_begin (the first comes from the prompt's
+ * last position) and whether an end-of-sequence id stopped the run. */
+int llmrs_model_produced(llmrs_model* m, size_t* n, int32_t* stopped);
+/* The sampler alone (test probe, no reference counterpart): the logits of
+ * one step, the history the penalty window reads (input_ids, main.rs:
+ * 195-203) and the position that selects U.  Writes the drawn id and U
+ * (either may be NULL). */
+int llmrs_sample_logits(const float* logits, int32_t vocab, const int32_t* history,
+                        size_t n_history, const llmrs_sampling* s, uint64_t position,
+                        int32_t* token, float* u);
+/* Benchmark helpers: start a run (prompt processed, state resident),
  * then replay `n` more decode steps without host synchronisation. */
 int llmrs_model_begin(llmrs_model* m, const int32_t* prompt, size_t n_prompt);
 /* As llmrs_model_begin with the prompt at positions [start_pos, start_pos +

@@ -84,6 +84,13 @@ struct llmrs_model {
   hipGraphExec_t exec = nullptr;
   bool graph_failed = false;
   int host_n_prompt = 0;
+  // sampling in place of the greedy argmax (llmrs_model_set_sampling)
+  bool sampling = false;
+  llmrs_sampling samp{};
+  float* probs = nullptr;      // [vocab] sampler scratch, allocated on first use
+  llmrs::SampleState* samp_state = nullptr;
+  int* eos = nullptr;          // [LLMRS_MAX_EOS]
+  int* stopped = nullptr;      // an end-of-sequence id was drawn
   // batched prompt (prefill) buffers for chunks of up to pf_cap rows,
   // allocated on first use
   int pf_cap = 0;
@@ -173,6 +180,44 @@ unsigned attn_threads(const llmrs_model* m) {
 // x = the embedding of the token at the device position, or (x_in set) the
 // row x_in; with the consumers' RMSNorm folded into the producers, also the
 // first RMSNorm's operand of x with weight norm_w (PRO_NQ of gemv_core.h).
+// Kernel arguments of the sampling parameters; the caller fills the buffers.
+SampleArgs sample_args(const llmrs_sampling& s, int vocab) {
+  SampleArgs a{};
+  a.vocab = vocab;
+  a.groups = llmrs::sample_groups(vocab);
+  a.penalty = s.repeat_penalty;
+  a.temperature = s.temperature;
+  a.top_p = s.top_p;
+  a.window = s.penalty_window;
+  a.seed = s.seed;
+  a.n_eos = s.n_eos;
+  a.step_override = -1;
+  return a;
+}
+
+void check_sampling(const llmrs_sampling& s, int vocab) {
+  LLMRS_REQUIRE(std::isfinite(s.temperature) && s.temperature > 0.0f, LLMRS_E_INVALID,
+                "temperature must be finite and > 0");
+  LLMRS_REQUIRE(std::isfinite(s.top_p), LLMRS_E_INVALID, "top_p must be finite");
+  LLMRS_REQUIRE(std::isfinite(s.repeat_penalty) && s.repeat_penalty > 0.0f, LLMRS_E_INVALID,
+                "repeat_penalty must be finite and > 0");
+  LLMRS_REQUIRE(s.n_eos >= 0 && s.n_eos <= LLMRS_MAX_EOS, LLMRS_E_INVALID, "n_eos must be in [0, 8]");
+  LLMRS_REQUIRE(vocab > 0 && vocab <= llmrs::kSampleMaxVocab, LLMRS_E_INVALID,
+                "sampling supports vocabularies up to 262144 ids");
+}
+
+// The sampler's launch chain (sample.hip): prep, probs, the refine levels
+// (top-p only), pick.  Work figures: bytes of the launch's vocabulary passes.
+void enqueue_sample(Launcher& L, const SampleArgs& a) {
+  const dim3 grid((unsigned)a.groups), block((unsigned)llmrs::kSampleThreads);
+  const double V = a.vocab;
+  L("sample_prep", 8.0 * V, grid, block, 0, a);
+  L("sample_probs", 8.0 * V, grid, block, 0, a);
+  if (a.top_p < 1.0f)
+    for (int i = 0; i < llmrs::kSampleRefines; ++i) L("sample_refine", 4.0 * V, grid, block, 0, a);
+  L("sample_pick", 4.0 * V, grid, block, 0, a);
+}
+
 void enqueue_embed(llmrs_model* m, Launcher& L, const float* x_in, const float* norm_w) {
   const int H = m->c.hidden;
   EmbedArgs e{};
@@ -385,7 +430,7 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
       g.x = m->x;
       g.norm_w = m->final_norm;
     }
-    g.y = write_logits ? m->logits : nullptr;
+    g.y = write_logits || m->sampling ? m->logits : nullptr;
     g.part_val = m->part_val;
     g.part_idx = m->part_idx;
     g.probe_xq = probe_xq;
@@ -393,6 +438,21 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
     const GemvPlan p = gemv_plan(m->wt, m->nq ? "nq_argmax" : "norm_argmax", g.n, g.k, cus);
     LLMRS_REQUIRE((int)p.grid == m->lm_grid, LLMRS_E_INVALID, "lm_head grid changed since model creation");
     L(p.name, linear_weight_bytes(m, m->lm_head) + (m->nq ? 1.125 : 8.0) * H, dim3(p.grid), dim3(256), p.lds, g);
+  }
+  if (m->sampling) {
+    SampleArgs a = sample_args(m->samp, c.vocab);
+    a.logits = m->logits;
+    a.probs = m->probs;
+    a.st = m->samp_state;
+    a.pos = m->pos;
+    a.n_prompt = m->n_prompt;
+    a.tokens = m->tokens;
+    a.gen = m->gen;
+    a.cap = m->cap;
+    a.eos = m->eos;
+    a.stopped = m->stopped;
+    enqueue_sample(L, a);
+    return;
   }
   ArgmaxFinalArgs f{m->part_val, m->part_idx, m->lm_grid, m->pos, m->n_prompt, m->tokens, m->gen, m->cap};
   L("argmax_final", 8.0 * m->lm_grid, dim3(1), dim3(256), 0, f);
@@ -617,9 +677,10 @@ void check_err(llmrs_model* m) {
 }
 
 void set_state(llmrs_model* m, size_t pos, int n_prompt) {
-  int v[2] = {(int)pos, n_prompt};
+  int v[3] = {(int)pos, n_prompt, 0};
   LLMRS_HIP(hipMemcpyAsync(m->pos, &v[0], sizeof(int), hipMemcpyHostToDevice, ctx().stream));
   LLMRS_HIP(hipMemcpyAsync(m->n_prompt, &v[1], sizeof(int), hipMemcpyHostToDevice, ctx().stream));
+  LLMRS_HIP(hipMemcpyAsync(m->stopped, &v[2], sizeof(int), hipMemcpyHostToDevice, ctx().stream));
   LLMRS_HIP(hipStreamSynchronize(ctx().stream));
 }
 
@@ -781,6 +842,8 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     m->pos = m->dalloc<int>(1);
     m->n_prompt = m->dalloc<int>(1);
     m->err = m->dalloc<int>(1);
+    m->stopped = m->dalloc<int>(1);
+    m->eos = m->dalloc<int>(LLMRS_MAX_EOS);
     m->trace = m->dalloc<float>((size_t)(c.n_layers + 1) * H);
     {  // RoPE tables for every position (cpu.rs:345-349)
       const size_t mid = hd / 2;
@@ -801,6 +864,8 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     (void)kernel(gemv_plan(m->wt, nqk ? "nq_argmax" : "norm_argmax", c.vocab, H, cx.num_cus).name);
     (void)kernel("embed_gather");
     (void)kernel("argmax_final");
+    for (const char* k : {"sample_prep", "sample_probs", "sample_refine", "sample_pick"})
+      (void)kernel(k, dim3(llmrs::kSampleThreads));
     (void)kernel(attn_kernel(m.get()), dim3(attn_threads(m.get())));
     *out = m.release();
   });
@@ -1100,11 +1165,105 @@ int llmrs_model_generate(llmrs_model* m, const int32_t* prompt, size_t n_prompt,
   if (n_steps == 0) return LLMRS_OK;
   rc = llmrs_model_decode_steps(m, n_steps - 1);
   if (rc) return rc;
-  std::vector<int32_t> all(n_prompt + n_steps);
-  rc = llmrs_model_tokens(m, all.data(), all.size());
+  size_t produced = n_steps;
+  int32_t stopped = 0;
+  rc = llmrs_model_produced(m, &produced, &stopped);
   if (rc) return rc;
-  std::memcpy(out_tokens, all.data() + n_prompt, n_steps * sizeof(int32_t));
+  produced = std::min(produced, n_steps);
+  std::vector<int32_t> all(n_prompt + n_steps);
+  rc = llmrs_model_tokens(m, all.data(), n_prompt + produced);
+  if (rc) return rc;
+  std::memcpy(out_tokens, all.data() + n_prompt, produced * sizeof(int32_t));
+  for (size_t i = produced; i < n_steps; ++i) out_tokens[i] = -1;
   return LLMRS_OK;
+}
+
+int llmrs_model_produced(llmrs_model* m, size_t* n, int32_t* stopped) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && m->begun, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
+    int v[2] = {0, 0};
+    LLMRS_HIP(hipMemcpyAsync(&v[0], m->pos, sizeof(int), hipMemcpyDeviceToHost, ctx().stream));
+    LLMRS_HIP(hipMemcpyAsync(&v[1], m->stopped, sizeof(int), hipMemcpyDeviceToHost, ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    // the device position is that of the last token produced (the prompt's
+    // last before any)
+    if (n) *n = (size_t)std::max(0, v[0] + 1 - m->host_n_prompt);
+    if (stopped) *stopped = v[1];
+  });
+}
+
+int llmrs_model_set_sampling(llmrs_model* m, const llmrs_sampling* s) {
+  return guard([&] {
+    LLMRS_REQUIRE(m, LLMRS_E_INVALID, "null model");
+    if (s) {
+      check_sampling(*s, m->c.vocab);
+      if (!m->probs) {
+        m->probs = m->dalloc<float>(m->c.vocab);
+        m->samp_state = (llmrs::SampleState*)m->dalloc<uint8_t>(sizeof(llmrs::SampleState));
+      }
+      int ids[LLMRS_MAX_EOS] = {};
+      std::memcpy(ids, s->eos, sizeof(ids));
+      LLMRS_HIP(hipMemcpyAsync(m->eos, ids, sizeof(ids), hipMemcpyHostToDevice, ctx().stream));
+      LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+      m->samp = *s;
+    }
+    m->sampling = s != nullptr;
+    // the captured step ends with the argmax or the sampler: capture anew
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+    m->graph_failed = false;
+  });
+}
+
+int llmrs_sample_logits(const float* logits, int32_t vocab, const int32_t* history, size_t n_history,
+                        const llmrs_sampling* s, uint64_t position, int32_t* token, float* u) {
+  return guard([&] {
+    LLMRS_REQUIRE(logits && s && (history || n_history == 0), LLMRS_E_INVALID, "null argument");
+    check_sampling(*s, vocab);
+    LLMRS_REQUIRE(n_history < (size_t)INT_MAX && position < (uint64_t)LLONG_MAX, LLMRS_E_RANGE,
+                  "history or position too large");
+    hipStream_t st = ctx().stream;
+    const size_t V = (size_t)vocab;
+    // one allocation: sampler state, logits, probs, history, eos, token, u
+    const size_t off_l = align_up(sizeof(llmrs::SampleState), 256);
+    const size_t off_p = off_l + V * 4, off_h = off_p + V * 4, off_e = off_h + std::max<size_t>(n_history, 1) * 4;
+    const size_t off_t = off_e + LLMRS_MAX_EOS * 4, bytes = off_t + 8;
+    uint8_t* d = nullptr;
+    LLMRS_HIP(hipMalloc(&d, bytes));
+    try {
+      LLMRS_HIP(hipMemsetAsync(d, 0, off_l, st));
+      LLMRS_HIP(hipMemcpyAsync(d + off_l, logits, V * 4, hipMemcpyHostToDevice, st));
+      if (n_history)
+        LLMRS_HIP(hipMemcpyAsync(d + off_h, history, n_history * 4, hipMemcpyHostToDevice, st));
+      LLMRS_HIP(hipMemcpyAsync(d + off_e, s->eos, LLMRS_MAX_EOS * 4, hipMemcpyHostToDevice, st));
+      SampleArgs a = sample_args(*s, vocab);
+      a.st = (llmrs::SampleState*)d;
+      a.logits = (const float*)(d + off_l);
+      a.probs = (float*)(d + off_p);
+      a.hist = (const int*)(d + off_h);
+      a.n_hist = (int)n_history;
+      a.eos = (const int*)(d + off_e);
+      a.step_override = (long long)position;
+      a.out_token = (int*)(d + off_t);
+      a.out_u = (float*)(d + off_t + 4);
+      Launcher L{st};
+      enqueue_sample(L, a);
+      int32_t t = 0;
+      float uu = 0.0f;
+      LLMRS_HIP(hipMemcpyAsync(&t, d + off_t, 4, hipMemcpyDeviceToHost, st));
+      LLMRS_HIP(hipMemcpyAsync(&uu, d + off_t + 4, 4, hipMemcpyDeviceToHost, st));
+      LLMRS_HIP(hipStreamSynchronize(st));
+      if (token) *token = t;
+      if (u) *u = uu;
+    } catch (...) {
+      (void)hipStreamSynchronize(st);
+      (void)hipFree(d);
+      throw;
+    }
+    LLMRS_HIP(hipFree(d));
+  });
 }
 
 }  // extern "C"

@@ -62,6 +62,66 @@ struct ArgmaxFinalArgs {
   int cap;
 };
 
+// Sampling of the next token (sample.hip): a chain of launches over
+// workgroups of kSampleThreads threads, each owning kSampleSlice consecutive
+// ids.  Vocabularies up to kSampleMaxVocab ids.
+constexpr int kSampleMaxVocab = 262144;
+constexpr int kSampleThreads = 256;
+constexpr int kSamplePerThread = 2;
+constexpr int kSampleSlice = kSampleThreads * kSamplePerThread;
+constexpr int kSampleMaxGroups = kSampleMaxVocab / kSampleSlice;
+// First-level bins: bits 30..20 of a probability's pattern, plus one bin for
+// the part of 1e-5's bin below the candidate threshold; refine levels: bits
+// 19..10, then 9..0 inside the selected bin.
+constexpr int kSampleL1Bins = 2049;
+constexpr int kSampleRBins = 1024;
+constexpr int kSampleRefines = 4;  // two levels for the top-p cut, two for the draw
+constexpr int sample_groups(int vocab) { return (vocab + kSampleSlice - 1) / kSampleSlice; }
+
+// Device state of one sampler, zero before its first use; every launch
+// leaves the counters and histograms it consumed at zero again.
+struct SampleState {
+  unsigned ticket[4];            // last-workgroup tickets: prep, probs, refine, pick
+  float M, S;                    // softmax max and sum
+  int mode;                      // selection in progress: 0 none, 1 the top-p cut, 2 the draw
+  int level;                     // next refine level (1 or 2)
+  int bin1;                      // first-level bin of the selection
+  unsigned digit2;               // its second-level digit, once known
+  int cut_rank;                  // first-level rank of the cut bin (-1: no cut)
+  int pick;                      // workgroup holding the drawn id (-1: none, id 0)
+  unsigned vcut, ktie, vsel, ksel;
+  unsigned long long target, above, cut_base, cut_above, total, r, pick_base;
+  float wg_max[kSampleMaxGroups], wg_sum[kSampleMaxGroups];
+  unsigned long long wg_fix[kSampleMaxGroups];
+  unsigned l1_n[kSampleL1Bins + 3];
+  unsigned long long l1_s[kSampleL1Bins + 3];
+  unsigned r_n[kSampleRBins];
+  unsigned long long r_s[kSampleRBins];
+};
+
+struct SampleArgs {
+  const float* logits;   // [vocab] of the step
+  float* probs;          // [vocab] scratch
+  SampleState* st;
+  int vocab, groups;     // groups = sample_groups(vocab)
+  int* pos;              // device position (null: probe, no bookkeeping)
+  const int* n_prompt;
+  int* tokens;           // [cap] ids per position (the penalty history)
+  int* gen;              // [cap] drawn id at position p, stored at p+1
+  int cap;
+  const int* eos;        // end-of-sequence ids
+  int n_eos;
+  int* stopped;          // set once one is drawn (null: probe)
+  float penalty, temperature, top_p;
+  int window;            // penalty window (<= 0: the whole history)
+  unsigned long long seed;
+  long long step_override;  // >= 0: the draw's position (probe), else *pos
+  const int* hist;       // probe: explicit history [n_hist] (null: tokens[0..pos])
+  int n_hist;
+  int* out_token;        // probe outputs (may be null)
+  float* out_u;
+};
+
 // Decode attention (attention.hip).
 struct AttnArgs {
   const float* qkv;        // [nq*hd | nkv*hd | nkv*hd] projections of this token

@@ -97,6 +97,10 @@ _SIGS = {
     "llmrs_model_begin_at": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t]),
     "llmrs_model_decode_steps": (C.c_int, [C.c_void_p, C.c_size_t]),
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "llmrs_model_set_sampling": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "llmrs_model_produced": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t), C.POINTER(C.c_int32)]),
+    "llmrs_sample_logits": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_size_t, C.c_void_p, C.c_uint64,
+                                      C.c_void_p, C.c_void_p]),
     "llmrs_model_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_time_linear": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "llmrs_model_profile_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_char_p,
@@ -315,6 +319,41 @@ class LoadOptions(C.Structure):
     _fields_ = [("max_seq", C.c_int32), ("kv_dtype", C.c_int32), ("weight_dtype", C.c_int32)]
 
 
+MAX_EOS = 8
+LLAMA3_EOS = (128001, 128009)  # main.rs:121
+
+
+class Sampling(C.Structure):
+    """llmrs_sampling: the token loop's sampling parameters (main.rs:42-58
+    defaults: penalty 1.2 over the last 64 ids, temperature 0.8, top_p 0.9)
+    and the seed that makes its draws repeat."""
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("repeat_penalty", C.c_float),
+                ("penalty_window", C.c_int32), ("seed", C.c_uint64), ("n_eos", C.c_int32),
+                ("eos", C.c_int32 * MAX_EOS)]
+
+    @classmethod
+    def make(cls, temperature=0.8, top_p=0.9, repeat_penalty=1.2, penalty_window=64, seed=0,
+             eos=LLAMA3_EOS) -> "Sampling":
+        eos = tuple(eos)
+        if len(eos) > MAX_EOS:
+            raise ValueError(f"at most {MAX_EOS} end-of-sequence ids")
+        s = cls(float(temperature), float(top_p), float(repeat_penalty), int(penalty_window), int(seed), len(eos))
+        for i, e in enumerate(eos):
+            s.eos[i] = int(e)
+        return s
+
+
+def sample_logits(logits, history, sampling: Sampling, position: int) -> tuple[int, float]:
+    """The device sampler alone on one step's logits: (drawn id, U)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    h = np.ascontiguousarray(history, dtype=np.int32)
+    tok = np.zeros(1, np.int32)
+    u = np.zeros(1, np.float32)
+    _check(lib().llmrs_sample_logits(_ptr(lg), lg.size, _ptr(h) if h.size else None, h.size,
+                                     C.byref(sampling), int(position), _ptr(tok), _ptr(u)))
+    return int(tok[0]), float(u[0])
+
+
 W_Q, W_K, W_V, W_O, W_GATE, W_UP, W_DOWN, W_LM_HEAD = range(8)
 N_INPUT, N_POST, N_FINAL = range(3)
 
@@ -434,10 +473,25 @@ class HipModel:
         return lg, int(nxt[0]), tr
 
     def generate(self, prompt, n_steps: int) -> np.ndarray:
+        """The tokens produced; with sampling, those before a drawn
+        end-of-sequence id (fewer than n_steps)."""
         ids = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.empty(n_steps, np.int32)
         _check(lib().llmrs_model_generate(self._h, _ptr(ids), ids.size, n_steps, _ptr(out)))
-        return out
+        end = np.nonzero(out < 0)[0]
+        return out[: int(end[0])] if end.size else out
+
+    def set_sampling(self, sampling: Sampling | None) -> None:
+        """Sampling (main.rs:192-305) in place of the greedy argmax; None
+        restores greedy decoding."""
+        _check(lib().llmrs_model_set_sampling(self._h, C.byref(sampling) if sampling is not None else None))
+
+    def produced(self) -> tuple[int, bool]:
+        """(tokens produced since begin, whether an end-of-sequence id stopped the run)."""
+        n = C.c_size_t(0)
+        st = C.c_int32(0)
+        _check(lib().llmrs_model_produced(self._h, C.byref(n), C.byref(st)))
+        return int(n.value), bool(st.value)
 
     def begin(self, prompt, start_pos: int = 0) -> None:
         """Process the prompt at [start_pos, start_pos + n) (the cache below

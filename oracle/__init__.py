@@ -49,6 +49,8 @@ _SIGS = {
     "orc_f32_to_f16": (C.c_uint16, [C.c_float]),
     "orc_f16_to_f32": (C.c_float, [C.c_uint16]),
     "orc_argmax": (_I64, [_P, _I64, _P]),
+    "orc_sample": (C.c_int32, [_P, _I64, _P, _I64, C.c_float, C.c_float, C.c_float, _I64, C.c_float,
+                               C.c_int32, _P]),
     "orc_model_create": (_P, [_P]),
     "orc_model_free": (None, [_P]),
     "orc_model_set_embedding": (C.c_int, [_P, _P]),
@@ -275,6 +277,19 @@ def argmax(x):
     m = C.c_float()
     i = lib().orc_argmax(_p(x), x.size, C.byref(m))
     return int(i), float(m.value)
+
+
+def sample(logits, history, penalty, temperature, top_p, window, u, candidate=-1):
+    """The reference's sampling (main.rs:192-305) for the draw u: (id,
+    whether `candidate` is acceptable - equal, or within the rounding of the
+    reference's f32 running sums)."""
+    x = _f32(logits)
+    h = np.ascontiguousarray(history, np.int32)
+    acc = C.c_int32(0)
+    t = lib().orc_sample(_p(x), x.size, _p(h) if h.size else None, h.size, float(penalty),
+                         float(temperature), float(top_p), int(window), float(u), int(candidate),
+                         C.byref(acc))
+    return int(t), bool(acc.value)
 
 
 class OrcConfig(C.Structure):

@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cfloat>
 #include <cmath>
 #include <condition_variable>
 #include <cstring>
@@ -566,6 +567,162 @@ int64_t orc_argmax(const float* x, int64_t n, float* margin) {
     *margin = x[best] - second;
   }
   return best;
+}
+
+namespace {
+
+// Walk of the draw (main.rs:275-281 / 286-292): the first entry, in walk
+// order, at which r minus the running f32 sum reaches <= 0; `fallback` when
+// none does.
+int64_t walk_f32(const std::vector<std::pair<float, int64_t>>& c, size_t n, float r, int64_t fallback) {
+  for (size_t k = 0; k < n; ++k) {
+    r -= c[k].first;
+    if (r <= 0.0f) return c[k].second;
+  }
+  return fallback;
+}
+
+// Whether `token` is the entry at which the exact (double) running sum of
+// the first n walk entries crosses some r' within tol of r, or the fallback
+// when the exact total may fall short of r (within tol).
+bool walk_accepts(const std::vector<std::pair<float, int64_t>>& c, size_t n, double r, double tol,
+                  int64_t fallback, int64_t token) {
+  double acc = 0.0;
+  for (size_t k = 0; k < n; ++k) {
+    const double lo = acc;
+    acc += c[k].first;
+    if (c[k].second == token && lo <= r + tol && acc >= r - tol) return true;
+  }
+  return token == fallback && acc <= r + tol;
+}
+
+}  // namespace
+
+// The token loop's sampling (main.rs:192-305) for a given draw U: repetition
+// penalty over the distinct ids of the last `window` history entries (<= 0:
+// all; only when penalty > 1; a logit below 0 multiplied by the penalty,
+// else divided; main.rs:193-212), temperature (logits / t unless |t - 1| <=
+// 1e-6; main.rs:214-220), softmax (max folded from f32::MIN, exp(l - max),
+// f32 sum in index order, p /= sum; main.rs:237-246), then top-p
+// (main.rs:249-283: ids with p > 1e-5 - every id when none is - in
+// descending p, cut at the first prefix whose f32 sum exceeds top_p, r = U *
+// (f32 sum of the cut), walk) or, with top_p >= 1, the roulette walk over
+// every id in index order with r = U (main.rs:284-294).  sort_unstable_by
+// leaves equal probabilities in an unspecified order; this takes them in
+// index order, as the GPU sampler does.
+//
+// `candidate` (>= 0) is another implementation's draw, judged acceptable
+// (*accept = 1) when it equals this one or when the draw lies within the
+// rounding of the reference's f32 sums: the candidate's interval of the
+// exact running sum meets r +- tol.  tol = the largest gap between the f32
+// and the exact running sums, plus 1e-6 of the total, plus - where the
+// normalisation does not cancel (the roulette's r = U, the top-p cut, the
+// 1e-5 threshold) - the relative error of the f32 softmax sum (another
+// implementation normalises by its own sum).  Alternative top-p cuts whose
+// exact prefix lies within tol of top_p are tried too.
+int32_t orc_sample(const float* logits, int64_t vocab, const int32_t* hist, int64_t n_hist, float penalty,
+                   float temperature, float top_p, int64_t window, float u, int32_t candidate,
+                   int32_t* accept) {
+  std::vector<float> l(logits, logits + vocab);
+  if (penalty > 1.0f) {
+    const int64_t w0 = window > 0 && n_hist > window ? n_hist - window : 0;
+    std::vector<char> seen(vocab, 0);
+    for (int64_t j = w0; j < n_hist; ++j) {
+      const int64_t id = hist[j];
+      if (id < 0 || id >= vocab || seen[id]) continue;
+      seen[id] = 1;
+      l[id] = l[id] < 0.0f ? l[id] * penalty : l[id] / penalty;
+    }
+  }
+  if (std::fabs(temperature - 1.0f) > 1e-6f)
+    for (float& v : l) v /= temperature;
+  float mx = -FLT_MAX;
+  for (float v : l) mx = std::max(mx, v);  // f32::max ignores NaN like fmaxf
+  std::vector<float> p(vocab);
+  float sum = 0.0f;
+  for (int64_t i = 0; i < vocab; ++i) {
+    p[i] = expf(l[i] - mx);
+  }
+  double sum_exact = 0.0;
+  for (int64_t i = 0; i < vocab; ++i) {
+    sum += p[i];
+    sum_exact += p[i];
+  }
+  for (float& v : p) v /= sum;
+  // relative error of the f32 softmax sum, plus room for another order's
+  const double delta = std::fabs((double)sum - sum_exact) / sum_exact + 1e-6;
+
+  std::vector<std::pair<float, int64_t>> c;
+  int64_t token;
+  int ok = 0;
+  if (top_p < 1.0f) {
+    for (int64_t i = 0; i < vocab; ++i)
+      if (p[i] > 1e-5f) c.emplace_back(p[i], i);
+    int64_t near_threshold = 0;  // ids whose membership a rounding of p could change
+    for (int64_t i = 0; i < vocab; ++i)
+      if (std::fabs((double)p[i] - 1e-5) <= (delta + 1e-6) * 1e-5) ++near_threshold;
+    if (c.empty())
+      for (int64_t i = 0; i < vocab; ++i) c.emplace_back(p[i], i);
+    std::stable_sort(c.begin(), c.end(), [](const std::pair<float, int64_t>& a, const std::pair<float, int64_t>& b) {
+      return a.first > b.first;
+    });
+    size_t cut = c.size() - 1;
+    float cum = 0.0f;
+    double exact = 0.0, gap = 0.0;
+    std::vector<double> prefix(c.size());
+    for (size_t k = 0; k < c.size(); ++k) {
+      exact += c[k].first;
+      prefix[k] = exact;
+    }
+    for (size_t k = 0; k < c.size(); ++k) {
+      cum += c[k].first;
+      gap = std::max(gap, std::fabs((double)cum - prefix[k]));
+      if (cum > top_p) {
+        cut = k;
+        break;
+      }
+    }
+    float total = 0.0f;
+    for (size_t k = 0; k <= cut; ++k) total += c[k].first;
+    const float r = u * total;
+    token = walk_f32(c, cut + 1, r, c[0].second);
+    if (candidate >= 0) {
+      double g2 = 0.0, acc = 0.0;
+      float cum2 = 0.0f;
+      for (size_t k = 0; k < c.size(); ++k) {
+        cum2 += c[k].first;
+        acc += c[k].first;
+        g2 = std::max(g2, std::fabs((double)cum2 - acc));
+      }
+      const double tol = std::max(gap, g2) + 1e-6 * prefix.back() + near_threshold * 1.1e-5;
+      const double tol_cut = tol + delta * std::max(0.0f, top_p);
+      ok = candidate == token;
+      // every cut whose boundary the rounding could move: prefixes within
+      // tol_cut of top_p, plus the reference's own
+      for (size_t k = 0; k < c.size() && !ok; ++k) {
+        const bool cand_cut = k == cut || std::fabs(prefix[k] - (double)top_p) <= tol_cut ||
+                              (k > 0 && std::fabs(prefix[k - 1] - (double)top_p) <= tol_cut);
+        if (!cand_cut) continue;
+        const double tot = prefix[k];
+        ok = walk_accepts(c, k + 1, (double)u * tot, tol, c[0].second, candidate);
+      }
+    }
+  } else {
+    for (int64_t i = 0; i < vocab; ++i) c.emplace_back(p[i], i);
+    token = walk_f32(c, c.size(), u, 0);
+    if (candidate >= 0) {
+      double acc = 0.0, gap = 0.0;
+      float cum = 0.0f;
+      for (size_t k = 0; k < c.size(); ++k) {
+        cum += c[k].first;
+        acc += c[k].first;
+        gap = std::max(gap, std::fabs((double)cum - acc));
+      }
+      ok = candidate == token || walk_accepts(c, c.size(), u, gap + 1e-6 * acc + delta * u, 0, candidate);
+    }
+  }
+  if (accept) *accept = ok;
+  return (int32_t)token;
 }
 
 }  // extern "C"

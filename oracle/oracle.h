@@ -128,6 +128,12 @@ void orc_gemv_codes(const int8_t* xq, const float* xd, int64_t m, int64_t k, con
                     const float* scales, int64_t n, int q8w, float* out);
 int orc_model_attention(orc_model* m, int layer, const float* qkv, int64_t seq,
                         int64_t start_pos, float* ctx);
+/* The token loop's sampling (main.rs:192-305) for the draw u in [0, 1):
+ * returns the id; with candidate >= 0, *accept = 1 when the candidate id is
+ * this one or within the rounding of the reference's f32 running sums. */
+int32_t orc_sample(const float* logits, int64_t vocab, const int32_t* hist, int64_t n_hist,
+                   float penalty, float temperature, float top_p, int64_t window, float u,
+                   int32_t candidate, int32_t* accept);
 /* Greedy token loop (main.rs:128-327 with argmax).  out: n_steps ids;
  * margins: top1-top2 logit gap per step (may be NULL). */
 int orc_model_generate(orc_model* m, const int32_t* prompt, int64_t n_prompt,

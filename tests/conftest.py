@@ -69,3 +69,19 @@ def check_stream(gpu, ref, margins, min_steps=64):
         f"gpu {gpu[max(0, i - 2):i + 3]} oracle {ref[max(0, i - 2):i + 3]}")
     assert i >= min(min_steps, len(ref)) or margins[i] < NEAR_TIE
     return i
+
+
+_M64 = (1 << 64) - 1
+
+
+def splitmix64(seed: int, n: int) -> int:
+    """Output n (1-based) of the SplitMix64 stream seeded with `seed`."""
+    z = (seed + n * 0x9E3779B97F4A7C15) & _M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def sample_u(seed: int, pos: int) -> float:
+    """The draw after the token at position `pos`: 24 bits of output pos+1."""
+    return float(np.float32((splitmix64(seed, pos + 1) >> 40) / float(1 << 24)))
