@@ -138,3 +138,31 @@ def gguf_meta(spec) -> dict:
             "llama.feed_forward_length": spec.ffn,
             "llama.attention.layer_norm_rms_epsilon": float(spec.rms_eps),
             "llama.rope.freq_base": float(spec.rope_theta)}
+
+
+# ---- tokenizer ----------------------------------------------------------------
+
+_WORDS = ("the model reads every weight once per token and the cache grows by one row "
+          "a prompt goes in and text comes out while the device keeps its state resident "
+          "blocks of thirty two codes share one scale the matrix cores add the products "
+          "hello world sampling draws one id from the nucleus of the distribution").split()
+
+
+def write_tokenizer(path, vocab_size: int) -> None:
+    """A byte-level BPE tokenizer (as Llama 3's) with vocab_size ids, trained
+    on a fixed synthetic corpus; specials <|begin_of_text|> (added in front
+    of every encoding), <|end_of_text|>, <|eot_id|>."""
+    from tokenizers import Tokenizer, decoders, models, pre_tokenizers, processors, trainers
+    tok = Tokenizer(models.BPE())
+    tok.pre_tokenizer = pre_tokenizers.ByteLevel(add_prefix_space=False)
+    tok.decoder = decoders.ByteLevel()
+    specials = ["<|begin_of_text|>", "<|end_of_text|>", "<|eot_id|>"]
+    trainer = trainers.BpeTrainer(vocab_size=vocab_size, special_tokens=specials, show_progress=False,
+                                  initial_alphabet=pre_tokenizers.ByteLevel.alphabet())
+    rng = np.random.default_rng(1234)
+    corpus = [" ".join(rng.choice(_WORDS, 12)) + f" {i} {i * 37 % 1000}" for i in range(3000)]
+    tok.train_from_iterator(corpus, trainer)
+    bos = tok.token_to_id("<|begin_of_text|>")
+    tok.post_processor = processors.TemplateProcessing(single="<|begin_of_text|> $A",
+                                                       special_tokens=[("<|begin_of_text|>", bos)])
+    tok.save(str(path))
