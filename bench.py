@@ -266,6 +266,8 @@ def main() -> int:
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--prefill-steps", type=int, default=3,
                     help="timed 2048-token prefills in the decode run (0 = none)")
+    ap.add_argument("--batch-sizes", type=lambda v: [int(x) for x in v.split(",") if x], default=[4, 16, 64],
+                    help="batched-decode sizes measured after the single-sequence run (empty: none)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -402,6 +404,29 @@ def main() -> int:
                "temperature": 0.8, "top_p": 0.9, "repeat_penalty": 1.2, "penalty_window": 64}
     log(f"sampled decode: {sampled['tok_s']} tok/s, sampler {sampled['sampler_us']} us per token")
 
+    # Batched decode: B sequences with their own prompts and caches stepping
+    # together (greedy), on the same weights; aggregate tok/s per batch size.
+    batched = None
+    if args.batch_sizes:
+        batched = {"sizes": {}, "prompt": 64, "steps": 32,
+                   "note": "B sequences, each its own 64-token random prompt and K/V cache; "
+                           "aggregate tokens/s over 32 greedy steps (HIP-graph replay)"}
+        import numpy as np
+        rng = np.random.default_rng(7)
+        for B in args.batch_sizes:
+            bt = lh.HipBatch(model, B)
+            for sl in range(B):
+                bt.begin(sl, rng.integers(0, spec.vocab, 64).astype(np.int32))
+            bt.decode_steps(2)
+            lh.sync()
+            t0 = time.perf_counter()
+            bt.decode_steps(32)
+            lh.sync()
+            bdt = time.perf_counter() - t0
+            batched["sizes"][str(B)] = {"tok_s": round(32 * B / bdt, 1), "ms_per_step": round(bdt / 32 * 1e3, 3)}
+            bt.close()
+            log(f"batched decode B={B}: {32 * B / bdt:.1f} tok/s ({bdt / 32 * 1e3:.3f} ms/step)")
+
     prefill = None
     if pf_spec:
         t0 = time.perf_counter()
@@ -450,6 +475,7 @@ def main() -> int:
         "prompt_ms": round(prompt_s * 1e3, 1),
         "prefill": prefill,
         "sampled_decode": sampled,
+        "batched_decode": batched,
         "kernels": kernels,
     }
     print(json.dumps(line), flush=True)

@@ -317,6 +317,32 @@ int llmrs_model_time_linear(llmrs_model* m, int slot, int reps, double* us_per_l
 int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
                                 size_t start_pos, char* names, float* ms,
                                 double* work, int cap);
+/* ---- batched decode (no reference counterpart) ---------------------------
+ * B sequences of one model decoding together (greedy), each with its own K/V
+ * cache, position and history.  The reference decodes one sequence; its
+ * layer code takes any number of rows (layer.rs:175-333), and each row's
+ * values depend only on that row and its own cache.  Every linear layer runs
+ * the B rows as one exact int8 GEMM (the prefill path's, cpu.rs:90-110 per
+ * row); the decode attention runs one slice per sequence.  A batch shares the
+ * model's weights; it holds B caches of the model's max_seq positions. */
+typedef struct llmrs_batch llmrs_batch;
+int llmrs_batch_create(llmrs_model* m, int32_t batch, llmrs_batch** out);
+int llmrs_batch_free(llmrs_batch* b);
+/* Prefills slot `slot` with a prompt (the model's prefill kernels, into the
+ * slot's cache) and takes its first greedy token.  Uses the model's own
+ * sequence state as scratch (a later llmrs_model_decode_steps needs a new
+ * llmrs_model_begin).  The model's sampling must be cleared. */
+int llmrs_batch_begin(llmrs_batch* b, int32_t slot, const int32_t* prompt, size_t n_prompt);
+/* n greedy steps of every slot (each slot must have been begun), one HIP
+ * graph replay per step. */
+int llmrs_batch_decode_steps(llmrs_batch* b, size_t n);
+/* The ids of slot `slot` from position 0: its prompt, then what it produced. */
+int llmrs_batch_tokens(llmrs_batch* b, int32_t slot, int32_t* out, size_t count);
+/* The logits of the last step, f32 [B][vocab] (tests). */
+int llmrs_batch_logits(llmrs_batch* b, float* out);
+/* Per-launch timing of one eager batched step (as llmrs_model_profile_step). */
+int llmrs_batch_profile_step(llmrs_batch* b, char* names, float* ms, double* work, int cap);
+
 /* ---- test probes (no reference counterpart) ------------------------------
  * One layer's kernels run on inputs given by the host, with every
  * intermediate the kernels produce copied back, so each kernel can be held to

@@ -507,7 +507,7 @@ struct PrefillProbe {
 // 6 gate|up GEMM + SwiGLU + Q8, 7 down GEMM + residual.  The recorded figure
 // per launch is its FLOPs for the GEMMs and attention, bytes for the rest.
 void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, int M,
-                           const PrefillProbe* probe = nullptr) {
+                           const PrefillProbe* probe = nullptr, void* kc = nullptr, void* vc = nullptr) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
   const int qd = nq * hd, QR = m->qkv_rows;
@@ -528,8 +528,12 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
   // causal score and P.V products over the chunk
   const double attn_flops = 4.0 * nq * hd * ((double)M * start + (double)M * (M + 1) / 2.0);
   LayerBufs& Lb = m->layers[li];
+  if (!kc) {  // the model's own cache (a batch slot's otherwise)
+    kc = Lb.kc;
+    vc = Lb.vc;
+  }
   {  // RMSNorm + Q8_0 of each row (layer.rs:378; cpu.rs:90-93)
-    PrefillRowArgs r{m->pf_x, Lb.norm[0], m->pf_aq, m->pf_ad, M, H, c.rms_eps};
+    PrefillRowArgs r{m->pf_x, Lb.norm[0], m->pf_aq, m->pf_ad, M, H, c.rms_eps, llmrs::kActNatural};
     L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
   }
   after(0);
@@ -540,7 +544,7 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
   }
   after(1);
   {  // RoPE + K/V append
-    PrefillRopeArgs r{m->pf_qkv, m->pf_q, Lb.kc, Lb.vc, m->rope_cos, m->rope_sin, M, nq, nkv, hd,
+    PrefillRopeArgs r{m->pf_qkv, m->pf_q, kc, vc, m->rope_cos, m->rope_sin, M, nq, nkv, hd,
                       kv_rows(m), (int)start, QR, kv16 ? 1 : 0};
     const long total = (long)M * (nq + 2 * nkv) * (hd / 2);
     const unsigned grid = (unsigned)std::min<long>((total + 255) / 256, 8192);
@@ -548,7 +552,7 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
   }
   after(2);
   {  // causal attention
-    PrefillAttnArgs a{m->pf_q, Lb.kc, Lb.vc, probe ? probe->ctx : nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq,
+    PrefillAttnArgs a{m->pf_q, kc, vc, probe ? probe->ctx : nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq,
                       nkv, kv_rows(m), (int)start, scale};
     if (mfma_attn)
       L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nkv), dim3(512), 0, a);
@@ -563,7 +567,7 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
   }
   after(4);
   {  // post-attention RMSNorm + Q8_0
-    PrefillRowArgs r{m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, M, H, c.rms_eps};
+    PrefillRowArgs r{m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, M, H, c.rms_eps, llmrs::kActNatural};
     L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
   }
   after(5);
@@ -586,7 +590,7 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
 // at the device position.  trace_dev, when set, is
 // [M][n_layers+1][hidden].
 void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head, bool write_logits,
-                     float* trace_dev) {
+                     float* trace_dev, void* const* kcs = nullptr, void* const* vcs = nullptr) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden;
   auto trace = [&](int li) {
@@ -596,11 +600,11 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
                                  hipMemcpyDeviceToDevice, L.s));
   };
   EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab, nullptr, nullptr, nullptr,
-              nullptr, nullptr};
+              nullptr, nullptr, 0};
   L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), dim3(256), 0, e);
   for (int li = 0; li < c.n_layers; ++li) {
     trace(li);
-    enqueue_prefill_layer(m, L, li, start, M);
+    enqueue_prefill_layer(m, L, li, start, M, nullptr, kcs ? kcs[li] : nullptr, vcs ? vcs[li] : nullptr);
   }
   trace(c.n_layers);
   if (head) {
@@ -621,7 +625,8 @@ void set_state(llmrs_model* m, size_t pos, int n_prompt);
 // Runs rows [start, start+n) through the prefill kernels in chunks; the last
 // chunk ends with the lm_head and greedy step, leaving the device position
 // at start+n.  trace (host, may be null) is [n][n_layers+1][hidden].
-void run_prefill(llmrs_model* m, size_t start, size_t n, int n_prompt, bool write_logits, float* trace) {
+void run_prefill(llmrs_model* m, size_t start, size_t n, int n_prompt, bool write_logits, float* trace,
+                 void* const* kcs = nullptr, void* const* vcs = nullptr) {
   ensure_prefill(m);
   const llmrs_model_config& c = m->c;
   const size_t rowf = (size_t)(c.n_layers + 1) * c.hidden;
@@ -637,7 +642,7 @@ void run_prefill(llmrs_model* m, size_t start, size_t n, int n_prompt, bool writ
       LLMRS_HIP(hipMemcpyAsync(m->pf_start, &s0, sizeof(int), hipMemcpyHostToDevice, ctx().stream));
       set_state(m, start + done + M - 1, n_prompt);  // synchronises the stream
       Launcher L{ctx().stream};
-      enqueue_prefill(m, L, start + done, M, last, write_logits && last, tdev);
+      enqueue_prefill(m, L, start + done, M, last, write_logits && last, tdev, kcs, vcs);
       if (trace) {
         LLMRS_HIP(hipMemcpyAsync(trace + done * rowf, tdev, (size_t)M * rowf * sizeof(float),
                                  hipMemcpyDeviceToHost, ctx().stream));
@@ -1598,6 +1603,315 @@ int llmrs_model_probe_prefill_layer(llmrs_model* m, int layer, size_t start_pos,
     enqueue_prefill_layer(m, L, layer, start_pos, (int)M, &p);
     m->begun = false;
   });
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Batched decode: B sequences of one model stepping together, each with its
+// own K/V cache, position and token history.  The reference runs one
+// sequence; its layer code would take any number of rows (layer.rs:175-333,
+// the mask at :264), and a row's values depend only on that row and its own
+// cache.  Here the B rows go through every linear layer at once - the exact
+// int8 GEMM of the prefill path with M = B, which gives each row the
+// reference's per-output block loop (cpu.rs:90-110) - and the decode
+// attention runs one grid slice per sequence (grid.z), over that sequence's
+// cache at its position.  The head is the lm_head GEMM over the B rows and a
+// per-row greedy step.
+// ---------------------------------------------------------------------------
+struct llmrs_batch {
+  llmrs_model* m = nullptr;
+  int B = 0, cap = 0;
+  size_t kv_bytes = 0;  // one sequence's K (or V) cache of one layer
+  std::vector<void*> kc, vc;  // per layer: B caches back to back
+  float *x = nullptr, *h = nullptr, *qkv = nullptr, *ctxv = nullptr, *logits = nullptr;
+  float *ad = nullptr, *ctx_d = nullptr, *m_d = nullptr, *part_o = nullptr, *part_ml = nullptr;
+  int8_t *aq = nullptr, *ctx_q = nullptr, *m_q = nullptr;
+  int *pos = nullptr, *tokens = nullptr, *gen = nullptr, *counters = nullptr;
+  // linear layers on the skinny GEMM (sgemm.hip; token tiles of 16, the
+  // activation codes in its operand order) or, beyond 64 sequences or for
+  // widths not a multiple of 128, on the prefill GEMM
+  bool skinny = false;
+  int tiles = 1, layout = llmrs::kActNatural;
+  std::vector<size_t> host_pos;
+  std::vector<char> begun;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  bool graph_failed = false;
+  std::vector<void*> allocs;
+
+  template <class T>
+  T* dalloc(size_t count) {
+    void* p = nullptr;
+    const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+      (void)hipGetLastError();
+      fail(LLMRS_E_OOM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+    }
+    allocs.push_back(p);
+    LLMRS_HIP(hipMemsetAsync(p, 0, bytes, ctx().stream));
+    return (T*)p;
+  }
+  ~llmrs_batch() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    for (void* p : allocs) (void)hipFree(p);
+  }
+};
+
+namespace {
+
+// Kernel name of a batched linear layer (epi: store, resid, silu).
+std::string batch_linear_kernel(const llmrs_batch* b, const char* epi) {
+  if (!b->skinny) return gemm_kernel(b->m, epi);
+  return std::string("sgemm_") + wt_tag(b->m->wt) + "_" + epi + "_t" + std::to_string(b->tiles);
+}
+
+// One greedy step of every sequence of the batch.
+void enqueue_batch_step(llmrs_batch* b, Launcher& L) {
+  llmrs_model* m = b->m;
+  const llmrs_model_config& c = m->c;
+  const int B = b->B, H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
+  const dim3 blk(256);
+  const size_t glds = gemm_lds_bytes();
+  // One linear layer over the B rows: Y = X W^T (+ res), or the SwiGLU
+  // product's Q8_0 codes; work figure = the weight bytes.
+  auto linear = [&](const char* epi, const DevLinear& W, const int8_t* xq, const float* xd, float* y,
+                    const float* res, int8_t* yq, float* yd) {
+    const std::string name = batch_linear_kernel(b, epi);
+    const bool silu = std::string(epi) == "silu";
+    const double wb = linear_weight_bytes(m, W);
+    if (b->skinny) {
+      SgemmArgs g{xq, xd, W.codes, W.scales, y, res, yq, yd, B, W.n, W.k, W.n, b->layout};
+      L(name, wb, dim3(silu ? (unsigned)(W.n / 64) : (unsigned)((W.n + 15) / 16)), blk, 0, g);
+    } else {
+      PrefillGemmArgs g{xq, xd, W.codes, W.scales, y, res, yq, yd, B, W.n, W.k, silu ? W.n / 2 : W.n, gemm_group_m()};
+      L(name, wb, gemm_grid(B, W.n), blk, glds, g);
+    }
+  };
+  EmbedArgs e{m->embed, b->tokens, b->pos, b->x, m->err, H, c.vocab, nullptr, nullptr, nullptr, nullptr, nullptr,
+              b->cap};
+  L("embed_gather", 8.0 * H * B, dim3((unsigned)((H + 255) / 256), (unsigned)B), blk, 0, e);
+  for (int li = 0; li < c.n_layers; ++li) {
+    LayerBufs& Lb = m->layers[li];
+    {  // RMSNorm + Q8_0 of each sequence's row (layer.rs:377)
+      PrefillRowArgs r{b->x, Lb.norm[0], b->aq, b->ad, B, H, c.rms_eps, b->layout};
+      L("prefill_rows_q8", 5.0 * H * B, dim3((unsigned)B), blk, gemv_act_lds_host(H), r);
+    }
+    linear("store", Lb.qkv, b->aq, b->ad, b->qkv, nullptr, nullptr, nullptr);  // Q|K|V
+    {  // decode attention, one grid slice per sequence (RoPE and the K/V append inside)
+      AttnArgs a{};
+      a.qkv = b->qkv;
+      a.pos_ptr = b->pos;
+      a.kc = b->kc[li];
+      a.vc = b->vc[li];
+      a.rope_cos = m->rope_cos;
+      a.rope_sin = m->rope_sin;
+      a.part_o = b->part_o;
+      a.part_ml = b->part_ml;
+      a.counters = b->counters + (size_t)li * B * nkv * llmrs::kTicketStride;
+      a.ctx = b->ctxv;
+      a.ctx_q = b->ctx_q;
+      a.ctx_d = b->ctx_d;
+      a.max_seq = kv_rows(m);
+      a.nq = nq;
+      a.nkv = nkv;
+      a.nsplit = m->nsplit;
+      a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
+      a.kv_batch_bytes = b->kv_bytes;
+      a.ctx_layout = b->layout;
+      L(attn_kernel(m), 0.0, dim3((unsigned)m->nsplit, (unsigned)nkv, (unsigned)B), dim3(attn_threads(m)), 0, a);
+    }
+    linear("resid", Lb.o, b->ctx_q, b->ctx_d, b->h, b->x, nullptr, nullptr);  // O + residual (layer.rs:386)
+    {  // post-attention RMSNorm + Q8_0
+      PrefillRowArgs r{b->h, Lb.norm[1], b->aq, b->ad, B, H, c.rms_eps, b->layout};
+      L("prefill_rows_q8", 5.0 * H * B, dim3((unsigned)B), blk, gemv_act_lds_host(H), r);
+    }
+    linear("silu", Lb.gu, b->aq, b->ad, nullptr, nullptr, b->m_q, b->m_d);  // gate|up + SwiGLU + Q8_0 of m
+    linear("resid", Lb.down, b->m_q, b->m_d, b->x, b->h, nullptr, nullptr);  // down + residual (layer.rs:403)
+  }
+  {  // final RMSNorm (model.rs:39) + lm_head over the B rows, then each row's greedy step
+    PrefillRowArgs r{b->x, m->final_norm, b->aq, b->ad, B, H, c.rms_eps, b->layout};
+    L("prefill_rows_q8", 5.0 * H * B, dim3((unsigned)B), blk, gemv_act_lds_host(H), r);
+    linear("store", m->lm_head, b->aq, b->ad, b->logits, nullptr, nullptr, nullptr);
+    ArgmaxBatchArgs am{b->logits, c.vocab, b->pos, b->tokens, b->gen, b->cap};
+    L("argmax_batch", 4.0 * c.vocab * B, dim3((unsigned)B), dim3(1024), 0, am);
+  }
+}
+
+void replay_batch_step(llmrs_batch* b) {
+  hipStream_t s = ctx().stream;
+  if (!b->exec && !b->graph_failed && env_int("LLMRS_GRAPH", 1)) {
+    Launcher L{s};
+    bool ok = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess;
+    if (ok) {
+      try {
+        enqueue_batch_step(b, L);
+      } catch (const Error&) {
+        ok = false;
+      }
+      hipGraph_t g = nullptr;
+      const hipError_t e = hipStreamEndCapture(s, &g);
+      ok = ok && e == hipSuccess && g;
+      if (ok) {
+        b->graph = g;
+        ok = hipGraphInstantiate(&b->exec, g, nullptr, nullptr, 0) == hipSuccess;
+      } else if (g) {
+        (void)hipGraphDestroy(g);
+      }
+    }
+    if (!ok) {
+      (void)hipGetLastError();
+      b->graph_failed = true;
+      b->exec = nullptr;
+      std::fprintf(stderr, "llmrs_hip: HIP graph capture failed; using per-kernel launches\n");
+    }
+  }
+  if (b->exec) {
+    LLMRS_HIP(hipGraphLaunch(b->exec, s));
+  } else {
+    Launcher L{s};
+    enqueue_batch_step(b, L);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmrs_batch_create(llmrs_model* m, int32_t batch, llmrs_batch** out) {
+  return guard([&] {
+    check_ready(m);
+    LLMRS_REQUIRE(out && batch >= 1 && batch <= 256, LLMRS_E_INVALID, "batch must be in [1, 256]");
+    const llmrs_model_config& c = m->c;
+    std::unique_ptr<llmrs_batch> b(new llmrs_batch());
+    b->m = m;
+    b->B = batch;
+    b->cap = m->cap;
+    b->kv_bytes = align_up(kv_layer_elems(m) * kv_elem_bytes(m), 256);
+    const size_t B = (size_t)batch, H = c.hidden, F = c.ffn, qd = (size_t)c.n_heads * c.head_dim;
+    for (int li = 0; li < c.n_layers; ++li) {
+      b->kc.push_back(b->dalloc<uint8_t>(B * b->kv_bytes));
+      b->vc.push_back(b->dalloc<uint8_t>(B * b->kv_bytes));
+    }
+    b->x = b->dalloc<float>(B * H);
+    b->h = b->dalloc<float>(B * H);
+    b->qkv = b->dalloc<float>(B * m->qkv_rows);
+    b->ctxv = b->dalloc<float>(B * qd);
+    b->logits = b->dalloc<float>(B * c.vocab);
+    b->aq = b->dalloc<int8_t>(B * H);
+    b->ad = b->dalloc<float>(B * H / 32);
+    b->ctx_q = b->dalloc<int8_t>(B * qd);
+    b->ctx_d = b->dalloc<float>(B * qd / 32);
+    b->m_q = b->dalloc<int8_t>(B * F);
+    b->m_d = b->dalloc<float>(B * F / 32);
+    b->part_o = b->dalloc<float>(B * qd * m->nsplit);
+    b->part_ml = b->dalloc<float>(B * c.n_heads * llmrs::ml_stride(m->nsplit) * 2);
+    b->counters = b->dalloc<int>((size_t)c.n_layers * B * c.n_kv_heads * llmrs::kTicketStride);
+    b->pos = b->dalloc<int>(B);
+    b->tokens = b->dalloc<int>(B * b->cap);
+    b->gen = b->dalloc<int>(B * b->cap);
+    b->host_pos.assign(B, 0);
+    b->begun.assign(B, 0);
+    const int qdim = c.n_heads * c.head_dim;
+    const char* bg = std::getenv("LLMRS_BATCH_GEMM");
+    b->skinny = batch <= 64 && c.hidden % 128 == 0 && c.ffn % 128 == 0 && qdim % 128 == 0 &&
+                !(bg && std::string(bg) == "prefill");
+    b->tiles = batch <= 16 ? 1 : batch <= 32 ? 2 : 4;
+    b->layout = b->skinny ? llmrs::kActMfma : llmrs::kActNatural;
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    (void)kernel("argmax_batch", dim3(1024));
+    for (const char* epi : {"store", "resid", "silu"}) (void)kernel(batch_linear_kernel(b.get(), epi), dim3(256));
+    *out = b.release();
+  });
+}
+
+int llmrs_batch_free(llmrs_batch* b) {
+  return guard([&] {
+    if (!b) return;
+    (void)hipStreamSynchronize(ctx().stream);
+    delete b;
+  });
+}
+
+int llmrs_batch_begin(llmrs_batch* b, int32_t slot, const int32_t* prompt, size_t n_prompt) {
+  return guard([&] {
+    LLMRS_REQUIRE(b && prompt && n_prompt > 0, LLMRS_E_INVALID, "empty prompt");
+    LLMRS_REQUIRE(slot >= 0 && slot < b->B, LLMRS_E_RANGE, "slot out of range");
+    llmrs_model* m = b->m;
+    LLMRS_REQUIRE(!m->sampling, LLMRS_E_INVALID, "batched decoding is greedy: clear the model's sampling first");
+    LLMRS_REQUIRE(n_prompt < (size_t)m->c.max_seq, LLMRS_E_RANGE, "prompt beyond max_seq");
+    // the prompt through the prefill kernels into the slot's cache, then the
+    // lm_head and greedy step of its last row, on the model's own buffers
+    upload_tokens(m, 0, prompt, n_prompt);
+    set_state(m, 0, (int)n_prompt);
+    std::vector<void*> kcs(b->kc.size()), vcs(b->vc.size());
+    for (size_t li = 0; li < kcs.size(); ++li) {
+      kcs[li] = (uint8_t*)b->kc[li] + (size_t)slot * b->kv_bytes;
+      vcs[li] = (uint8_t*)b->vc[li] + (size_t)slot * b->kv_bytes;
+    }
+    run_prefill(m, 0, n_prompt, (int)n_prompt, false, nullptr, kcs.data(), vcs.data());
+    m->begun = false;  // the model's own sequence state was used as scratch
+    m->host_pos = n_prompt;
+    hipStream_t s = ctx().stream;
+    const int p = (int)n_prompt;
+    LLMRS_HIP(hipMemcpyAsync(b->tokens + (size_t)slot * b->cap, m->tokens, (n_prompt + 1) * sizeof(int32_t),
+                             hipMemcpyDeviceToDevice, s));
+    LLMRS_HIP(hipMemcpyAsync(b->gen + (size_t)slot * b->cap, m->gen, (n_prompt + 1) * sizeof(int32_t),
+                             hipMemcpyDeviceToDevice, s));
+    LLMRS_HIP(hipMemcpyAsync(b->pos + slot, &p, sizeof(int), hipMemcpyHostToDevice, s));
+    LLMRS_HIP(hipStreamSynchronize(s));
+    check_err(m);
+    b->host_pos[slot] = n_prompt;
+    b->begun[slot] = 1;
+  });
+}
+
+int llmrs_batch_decode_steps(llmrs_batch* b, size_t n) {
+  return guard([&] {
+    LLMRS_REQUIRE(b, LLMRS_E_INVALID, "null batch");
+    for (int s = 0; s < b->B; ++s) {
+      LLMRS_REQUIRE(b->begun[s], LLMRS_E_INVALID, "slot " + std::to_string(s) + " has not been begun");
+      LLMRS_REQUIRE(b->host_pos[s] + n < (size_t)b->m->c.max_seq, LLMRS_E_RANGE,
+                    "slot " + std::to_string(s) + " would decode beyond max_seq");
+    }
+    for (size_t i = 0; i < n; ++i) replay_batch_step(b);
+    for (auto& p : b->host_pos) p += n;
+  });
+}
+
+int llmrs_batch_tokens(llmrs_batch* b, int32_t slot, int32_t* out, size_t count) {
+  return guard([&] {
+    LLMRS_REQUIRE(b && out, LLMRS_E_INVALID, "null argument");
+    LLMRS_REQUIRE(slot >= 0 && slot < b->B, LLMRS_E_RANGE, "slot out of range");
+    LLMRS_REQUIRE(count <= b->host_pos[slot] + 1, LLMRS_E_RANGE, "more tokens requested than produced");
+    LLMRS_HIP(hipMemcpyAsync(out, b->tokens + (size_t)slot * b->cap, count * sizeof(int32_t),
+                             hipMemcpyDeviceToHost, ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    check_err(b->m);
+  });
+}
+
+int llmrs_batch_logits(llmrs_batch* b, float* out) {
+  return guard([&] {
+    LLMRS_REQUIRE(b && out, LLMRS_E_INVALID, "null argument");
+    LLMRS_HIP(hipMemcpyAsync(out, b->logits, (size_t)b->B * b->m->c.vocab * sizeof(float), hipMemcpyDeviceToHost,
+                             ctx().stream));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+  });
+}
+
+int llmrs_batch_profile_step(llmrs_batch* b, char* names, float* ms, double* work, int cap) {
+  int count = 0;
+  const int rc = guard([&] {
+    LLMRS_REQUIRE(b, LLMRS_E_INVALID, "null batch");
+    for (int s = 0; s < b->B; ++s)
+      LLMRS_REQUIRE(b->begun[s] && b->host_pos[s] + 1 < (size_t)b->m->c.max_seq, LLMRS_E_INVALID,
+                    "every slot must be begun, with room for one more step");
+    count = profile_launches([&](Launcher& L) { enqueue_batch_step(b, L); }, names, ms, work, cap);
+    for (auto& p : b->host_pos) p += 1;
+  });
+  return rc ? rc : count;
 }
 
 }  // extern "C"

@@ -201,7 +201,7 @@ int llmrs_matmul_transposed(const llmrs_tensor* a, const llmrs_tensor* b, llmrs_
       hipStream_t s = ctx().stream;
       int8_t* xq = (int8_t*)ctx().alloc.alloc(m * k);
       float* xd = (float*)ctx().alloc.alloc(m * (k / 32) * sizeof(float));
-      PrefillRowArgs r{(const float*)a->data, nullptr, xq, xd, (int)m, (int)k, 0.0f};
+      PrefillRowArgs r{(const float*)a->data, nullptr, xq, xd, (int)m, (int)k, 0.0f, llmrs::kActNatural};
       launch("prefill_rows_q8", dim3((unsigned)m), dim3(kBlock), gemv_act_lds_host((int)k), s, r);
       PrefillGemmArgs g{xq, xd, (const uint8_t*)b->data, b->scales, (float*)o->data, nullptr,
                         nullptr, nullptr, (int)m, (int)n, (int)k, (int)n, gemm_group_m()};

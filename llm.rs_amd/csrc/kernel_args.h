@@ -62,6 +62,48 @@ struct ArgmaxFinalArgs {
   int cap;
 };
 
+// Activation codes in the skinny GEMM's operand order (sgemm.hip).  Every
+// run of 4 blocks (128 elements) is stored as [4 lane groups][4 blocks][8
+// bytes]: lane group g's 8 bytes of a block are the elements its weight
+// dword multiplies - dword g of a device Q4 block holds elements 4g..4g+3 in
+// its low nibbles and 16+4g..16+4g+3 in its high ones (dwords g and g+4 of
+// a Q8 block the same elements) - so elements 4g..4g+3, then 16+4g..16+4g+3.
+// Aligned runs of 4 elements stay together.  Needs the row length a
+// multiple of 128.
+enum { kActNatural = 0, kActMfma = 1 };
+constexpr int act_offset(int k, int layout) {
+  return layout == kActNatural ? k
+                               : ((k >> 5) >> 2) * 128 + ((k >> 5) & 3) * 8 + ((k & 31) >> 2 & 3) * 32 +
+                                     ((k & 31) >> 4) * 4 + (k & 3);
+}
+
+// Skinny GEMM of batched decode (sgemm.hip): Y[t][n] = sum_b isum_b(t, n) *
+// (d_w[n,b] * d_a[t,b]) over M <= 64 rows of Q8_0 activation codes (in the
+// operand order of the weight type) and an [N, K] quantised weight.
+struct SgemmArgs {
+  const int8_t* xq;      // [M][K] activation codes, act_offset order
+  const float* xd;       // [M][K/32] activation scales
+  const uint8_t* wq;     // weight codes [N][nb][B]
+  const void* ws;        // weight scales [N][nb]
+  float* y;              // [M][ldy] (STORE, RESID)
+  const float* res;      // [M][N] residual (RESID; may alias y)
+  int8_t* yq;            // SILU: [M][N/2] codes of m, in the order `layout`
+  float* yd;             // SILU: [M][N/64] scales of m
+  int M, N, K, ldy, layout;
+};
+
+// Greedy step of a batch of sequences (gemv.hip: argmax_batch): row b of
+// the logits, next = argmax (lowest index on ties), then sequence b's
+// bookkeeping as argmax_final does for one sequence.
+struct ArgmaxBatchArgs {
+  const float* logits;   // [B][vocab]
+  int vocab;
+  int* pos;              // [B] device positions
+  int* tokens;           // [B][cap]
+  int* gen;              // [B][cap]
+  int cap;
+};
+
 // Sampling of the next token (sample.hip): a chain of launches over
 // workgroups of kSampleThreads threads, each owning kSampleSlice consecutive
 // ids.  Vocabularies up to kSampleMaxVocab ids.
@@ -139,6 +181,12 @@ struct AttnArgs {
   int max_seq, nq, nkv, nsplit;  // max_seq: cache rows per KV head (kv_rows)
   float scale;             // fl(1 / fl(sqrt(hd))), layer.rs:258
   unsigned long long* ts;  // profiling: 8 stage timestamps per item (null = off)
+  // Batched decode (grid.z = sequences): sequence z's qkv, position, partials,
+  // tickets and ctx rows follow sequence 0's at their natural strides, its
+  // K and V caches kv_batch_bytes after sequence 0's; ctx_q in the skinny
+  // GEMM's operand order ctx_layout (act_offset within the row).
+  size_t kv_batch_bytes;
+  int ctx_layout;
 };
 
 // Elementwise trait operators (ops.hip).
@@ -188,6 +236,9 @@ struct EmbedArgs {
   float* xd;
   float* xss;
   const float* x_in;
+  // Batched decode (> 0): row y is sequence y, token tokens[y * batch_stride
+  // + pos_ptr[y]]; 0: row y of a chunk, token tokens[*pos_ptr + y].
+  int batch_stride;
 };
 
 // Prefill GEMM (prefill.hip): Y[t][r] = sum_b isum_b(t, r) * (d_w[r,b] * d_a[t,b])
@@ -220,10 +271,11 @@ constexpr size_t gemm_lds_bytes() {
 struct PrefillRowArgs {
   const float* x;        // [M][dim] input rows
   const float* w;        // [dim] RMSNorm weight (null: plain Q8_0)
-  int8_t* xq;            // [M][dim] codes
+  int8_t* xq;            // [M][dim] codes (act_offset order `layout` within a row)
   float* xd;             // [M][dim/32] scales
   int M, dim;
   float eps;
+  int layout;
 };
 
 // RoPE of the projections and K/V append for positions start_pos + t.

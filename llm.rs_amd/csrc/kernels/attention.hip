@@ -10,15 +10,39 @@
 
 using namespace llmrs;
 
+// Sequence blockIdx.z of a batched decode launch (grid.z > 1): its buffers.
+template <int HD>
+__device__ __forceinline__ AttnArgs sequence_args(const AttnArgs& a0) {
+  AttnArgs a = a0;
+  const int z = blockIdx.z;
+  if (z) {
+    const size_t qd = (size_t)a.nq * HD;
+    a.qkv += (size_t)z * (a.nq + 2 * a.nkv) * HD;
+    a.pos_ptr += z;
+    a.kc = (uint8_t*)a.kc + z * a.kv_batch_bytes;
+    a.vc = (uint8_t*)a.vc + z * a.kv_batch_bytes;
+    a.part_o += (size_t)z * qd * a.nsplit;
+    a.part_ml += (size_t)z * a.nq * ml_stride(a.nsplit) * 2;
+    a.counters += (size_t)z * a.nkv * kTicketStride;
+    a.ctx += z * qd;
+    a.ctx_q += z * qd;
+    a.ctx_d += z * qd / 32;
+    a.ts = nullptr;
+  }
+  return a;
+}
+
 template <int HD, int S>
-__device__ __forceinline__ void attn_decode_impl(const AttnArgs& a) {
+__device__ __forceinline__ void attn_decode_impl(const AttnArgs& a0) {
   __shared__ __align__(16) uint8_t lds[AttnLds<HD, false, S>::BYTES];
+  const AttnArgs a = sequence_args<HD>(a0);
   attn_item<HD, false, false, S>(a, blockIdx.y, blockIdx.x, *a.pos_ptr, lds);
 }
 
 template <int HD, int TW>
-__device__ __forceinline__ void attn_decode_mfma_impl(const AttnArgs& a) {
+__device__ __forceinline__ void attn_decode_mfma_impl(const AttnArgs& a0) {
   __shared__ __align__(16) uint8_t lds[MfmaAttnLds<HD, TW>::BYTES];
+  const AttnArgs a = sequence_args<HD>(a0);
   attn_mfma_item<HD, TW>(a, *a.pos_ptr, lds);
 }
 

@@ -575,7 +575,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
       const int dd = DPL * lane + e;
       st_act<true>(a.ctx, (size_t)h * HD + dd, v[e]);
       const int8_t q = amax == 0.0f ? (int8_t)0 : (int8_t)q8_code(v[e], inv);
-      dev_st8(a.ctx_q, (int)((size_t)h * HD + dd), q);
+      dev_st8(a.ctx_q, act_offset((int)((size_t)h * HD + dd), a.ctx_layout), q);
     }
     if ((lane % LPB) == 0) st_act<true>(a.ctx_d, ((size_t)h * HD + DPL * lane) / 32, amax == 0.0f ? 0.0f : d);
   }

@@ -540,7 +540,7 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
       codes |= ((unsigned)q8 & 0xFFu) << (8 * i);
     }
     *(f32x4*)(a.ctx + e) = f32x4{v[0], v[1], v[2], v[3]};
-    *(unsigned*)(a.ctx_q + e) = codes;
+    *(unsigned*)(a.ctx_q + act_offset((int)e, a.ctx_layout)) = codes;  // aligned runs of 4 stay together
     if ((j & 7) == 0) a.ctx_d[e / 32] = bmax == 0.0f ? 0.0f : d;
   }
   if (tid == 0) dev_stu(a.counters, 4 * g * kTicketStride, 0u);

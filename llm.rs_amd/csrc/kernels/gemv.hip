@@ -92,3 +92,49 @@ extern "C" __global__ __launch_bounds__(256) void argmax_final(ArgmaxFinalArgs a
     *a.pos = pos + 1;
   }
 }
+
+// Greedy step of a batch: workgroup b takes the argmax of logits row b
+// (lowest index on ties; every logit NaN gives 0) and advances sequence b
+// as argmax_final advances one sequence (its prompt is consumed: the id is
+// both produced and the next input).
+extern "C" __global__ __launch_bounds__(1024) void argmax_batch(ArgmaxBatchArgs a) {
+  __shared__ float s_bv[16];
+  __shared__ int s_bi[16];
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id(), b = blockIdx.x;
+  const float* row = a.logits + (size_t)b * a.vocab;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < a.vocab; i += blockDim.x)
+    if (better(row[i], i, bv, bi)) {
+      bv = row[i];
+      bi = i;
+    }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    s_bv[wave] = bv;
+    s_bi[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < (int)(blockDim.x / LLMRS_WAVE); ++w)
+      if (better(s_bv[w], s_bi[w], bv, bi)) {
+        bv = s_bv[w];
+        bi = s_bi[w];
+      }
+    if (bi == 0x7fffffff) bi = 0;
+    const int pos = a.pos[b];
+    if (pos + 1 < a.cap) {
+      a.gen[(size_t)b * a.cap + pos + 1] = bi;
+      a.tokens[(size_t)b * a.cap + pos + 1] = bi;
+    }
+    a.pos[b] = pos + 1;
+  }
+}

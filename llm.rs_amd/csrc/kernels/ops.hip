@@ -137,8 +137,10 @@ extern "C" __global__ __launch_bounds__(256) void embed_gather(EmbedArgs e) {
   if (e.x_in) {
     row = e.x_in;
   } else {
-    // Row blockIdx.y of a chunk starting at *pos_ptr (one row when decoding).
-    int tok = e.tokens[*e.pos_ptr + blockIdx.y];
+    // Row blockIdx.y of a chunk starting at *pos_ptr (one row when decoding),
+    // or sequence blockIdx.y of a batch at its own position.
+    int tok = e.batch_stride ? e.tokens[(size_t)blockIdx.y * e.batch_stride + e.pos_ptr[blockIdx.y]]
+                             : e.tokens[*e.pos_ptr + blockIdx.y];
     if (tok < 0 || tok >= e.vocab) {
       if (threadIdx.x == 0 && blockIdx.x == 0) *e.err = 1;
       tok = 0;

@@ -349,9 +349,14 @@ extern "C" __global__ __launch_bounds__(kThreads) void prefill_rows_q8(PrefillRo
   if (r.w) load_activation<PRO_NORM, false, false>(g, row, s_q, s_d, s_off, s_red);
   else load_activation<PRO_QUANT, false, false>(g, row, s_q, s_d, s_off, s_red);
   __syncthreads();
-  const i32x4* src = (const i32x4*)s_q;
-  i32x4* dst = (i32x4*)(r.xq + (size_t)row * r.dim);
-  for (int i = threadIdx.x; i < r.dim / 16; i += kThreads) dst[i] = src[i];
+  if (r.layout == kActNatural) {
+    const i32x4* src = (const i32x4*)s_q;
+    i32x4* dst = (i32x4*)(r.xq + (size_t)row * r.dim);
+    for (int i = threadIdx.x; i < r.dim / 16; i += kThreads) dst[i] = src[i];
+  } else {
+    int8_t* dst = r.xq + (size_t)row * r.dim;
+    for (int i = threadIdx.x; i < r.dim; i += kThreads) dst[act_offset(i, r.layout)] = s_q[i];
+  }
   for (int b = threadIdx.x; b < nb; b += kThreads) r.xd[(size_t)row * nb + b] = s_d[b];
 }
 

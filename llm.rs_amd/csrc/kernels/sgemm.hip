@@ -1,0 +1,263 @@
+// sgemm.hip - skinny GEMM of batched decode for gfx950.
+//
+// Reference: the Q4/Q8 x Q8_0 block loop of CpuBackend::matmul_transposed
+// per activation row (cpu.rs:90-110; kernel_avx2 cpu.rs:888-941):
+// y[t][n] = sum over blocks b of fl(isum_b * fl(d_w[n,b] * d_a[t,b])), isum_b
+// the exact int32 dot of the block's weight and activation codes.
+//
+// MI355X design: M <= 64 activation rows (the sequences of a batch) against
+// a weight streamed once.  One v_mfma_i32_16x16x32_i8 per block gives the 16
+// rows x 16 tokens of exact block sums; the epilogue scales them in f32 as
+// the reference does (per output: the scale product, then the multiply, then
+// the add).  Lane (r, g) of a wave (r = lane % 16, g = lane / 16) loads 16
+// bytes: one Q4 block of weight row r (four blocks per lane group), so each
+// load instruction reads 64 contiguous bytes of each of 16 rows; a 4x4 dword
+// transpose across the lane groups (v_permlane32_swap, v_permlane16_swap)
+// then gives lane group g dword g of each of the four blocks - its MFMA
+// operand (the nibbles unpacked to q - 8 in four instructions; the device
+// Q4 layout is the same for both Q4 storages, only their scales differ).
+// The activation codes are stored in the matching operand order
+// (act_offset), so a lane reads its four blocks' operands as 32 contiguous
+// bytes.
+//
+// Workgroups of four waves.  STORE / RESID: 16 weight rows per workgroup,
+// the blocks split over the waves in contiguous quarters, partial sums added
+// in wave order.  SILU: 64 rows per workgroup - a run of 32 gate and 32 up
+// rows - one wave per 16 rows over all blocks; m = silu(gate) * up and its
+// Q8_0 codes (one 32-element block per run) in the operand order of the down
+// projection.  Each wave keeps PF groups of loads in flight (a ring of
+// register sets, the loop unrolled by PF so every set has a fixed place).
+#include "common.h"
+#include "gemv_core.h"
+#include "../kernel_args.h"
+
+using namespace llmrs;
+
+namespace {
+
+constexpr int kT = 256;
+
+// q - 8 for four nibbles held one per byte (0..15): (v + 0x78) ^ 0x80 per
+// byte, no carry between bytes.
+__device__ __forceinline__ unsigned nib_s8(unsigned v) { return (v + 0x78787878u) ^ 0x80808080u; }
+
+// In: lane group g holds the four dwords of its block g.  Out: x[j] = dword
+// g of block j.  v_permlane32_swap(a, b) exchanges the upper half of a with
+// the lower half of b; v_permlane16_swap the odd 16-lane rows of a with the
+// even rows of b.
+__device__ __forceinline__ void transpose4(unsigned x[4]) {
+  auto p = __builtin_amdgcn_permlane32_swap(x[0], x[2], false, false);
+  x[0] = p[0];
+  x[2] = p[1];
+  p = __builtin_amdgcn_permlane32_swap(x[1], x[3], false, false);
+  x[1] = p[0];
+  x[3] = p[1];
+  p = __builtin_amdgcn_permlane16_swap(x[0], x[1], false, false);
+  x[0] = p[0];
+  x[1] = p[1];
+  p = __builtin_amdgcn_permlane16_swap(x[2], x[3], false, false);
+  x[2] = p[0];
+  x[3] = p[1];
+}
+
+// What one 128-element group needs in registers.
+template <int WT, int TT>
+struct Group {
+  u32x4 w;             // Q4: this lane's block (transposed after arrival)
+  unsigned w8[4][2];   // Q8: dwords g and g + 4 of each block
+  unsigned dw[4][WT == WT_Q4F ? 4 : 2];  // scales of the 4 output rows of this lane x 4 blocks (bits)
+  u32x4 x[TT][2];      // activation operands of 4 blocks, per token tile
+  f32x4 da[TT];        // activation scales of 4 blocks, per token tile
+};
+
+template <int WT, int TT>
+__device__ __forceinline__ void load_group(Group<WT, TT>& G, const SgemmArgs& a, int q, int wrow, int orow0,
+                                           int tok, int nb, int g) {
+  if (WT == WT_Q8H) {
+    const unsigned* base = (const unsigned*)(a.wq + ((size_t)wrow * nb + 4 * q) * 32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      G.w8[j][0] = __builtin_nontemporal_load(base + 8 * j + g);
+      G.w8[j][1] = __builtin_nontemporal_load(base + 8 * j + g + 4);
+    }
+  } else {
+    G.w = __builtin_nontemporal_load((const u32x4*)(a.wq + ((size_t)wrow * nb + 4 * q + g) * 16));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const size_t s = (size_t)min(orow0 + i, a.N - 1) * nb + 4 * q;
+    if (WT == WT_Q4F) {
+      const u32x4 v = *(const u32x4*)((const float*)a.ws + s);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) G.dw[i][j] = v[j];
+    } else {
+      const uint2 v = *(const uint2*)((const uint16_t*)a.ws + s);
+      G.dw[i][0] = v.x;
+      G.dw[i][1] = v.y;
+    }
+  }
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    const int t = min(16 * tt + tok, a.M - 1);
+    const u32x4* xp = (const u32x4*)(a.xq + (size_t)t * a.K + (size_t)q * 128 + g * 32);
+    G.x[tt][0] = xp[0];
+    G.x[tt][1] = xp[1];
+    G.da[tt] = *(const f32x4*)(a.xd + (size_t)t * nb + 4 * q);
+  }
+}
+
+// Weight scale of output row i, block j of the group.
+template <int WT, int TT>
+__device__ __forceinline__ float scale_of(const Group<WT, TT>& G, int i, int j) {
+  if (WT == WT_Q4F) return __uint_as_float(G.dw[i][j]);
+  return h2f((uint16_t)(G.dw[i][j >> 1] >> (16 * (j & 1))));
+}
+
+// One group's MFMAs and epilogue into acc[tt][i] (output row orow0 + i,
+// token 16 tt + tok).
+template <int WT, int TT>
+__device__ __forceinline__ void compute_group(Group<WT, TT>& G, f32x4 (&acc)[TT]) {
+  unsigned wd[4];
+  if (WT != WT_Q8H) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wd[j] = G.w[j];
+    transpose4(wd);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    long op_a;
+    if (WT == WT_Q8H) {
+      op_a = (long)((unsigned long long)G.w8[j][0] | ((unsigned long long)G.w8[j][1] << 32));
+    } else {
+      const unsigned lo = nib_s8(wd[j] & 0x0F0F0F0Fu), hi = nib_s8((wd[j] >> 4) & 0x0F0F0F0Fu);
+      op_a = (long)((unsigned long long)lo | ((unsigned long long)hi << 32));
+    }
+    float dw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dw[i] = scale_of<WT, TT>(G, i, j);
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const unsigned b0 = G.x[tt][j >> 1][2 * (j & 1)], b1 = G.x[tt][j >> 1][2 * (j & 1) + 1];
+      const long op_b = (long)((unsigned long long)b0 | ((unsigned long long)b1 << 32));
+      const i32x4 isum = __builtin_amdgcn_mfma_i32_16x16x32_i8(op_a, op_b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+      const float da = G.da[tt][j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float s = dw[i] * da;                      // fl(d_w * d_a)
+        acc[tt][i] = acc[tt][i] + (float)isum[i] * s;    // cpu.rs:930-935
+      }
+    }
+  }
+}
+
+// Groups of loads in flight per wave (register sets of the ring).
+template <int WT, int TT>
+constexpr int prefetch_depth() {
+  return TT == 1 ? 4 : TT == 2 ? 3 : 2;
+}
+
+// The rows' partial sums over groups [q0, q1) in group order, PF groups of
+// loads ahead (addresses past the range clamped to its last group).
+template <int WT, int TT>
+__device__ __forceinline__ void run_groups(const SgemmArgs& a, int q0, int q1, int wrow, int orow0, int tok,
+                                           int nb, int g, f32x4 (&acc)[TT]) {
+  constexpr int PF = prefetch_depth<WT, TT>();
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) acc[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (q0 >= q1) return;
+  Group<WT, TT> ring[PF];
+#pragma unroll
+  for (int s = 0; s < PF; ++s) load_group<WT, TT>(ring[s], a, min(q0 + s, q1 - 1), wrow, orow0, tok, nb, g);
+  for (int q = q0; q < q1; q += PF) {
+#pragma unroll
+    for (int s = 0; s < PF; ++s) {
+      if (q + s < q1) compute_group<WT, TT>(ring[s], acc);
+      load_group<WT, TT>(ring[s], a, min(q + s + PF, q1 - 1), wrow, orow0, tok, nb, g);
+    }
+  }
+}
+
+template <int WT, int EPI, int TT>
+__device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
+  __shared__ f32x4 s_acc[4][TT][64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int nb = a.K >> 5, ngroups = nb >> 2;
+  f32x4 acc[TT];
+  if (EPI == EPI_SILU) {
+    // rows 64 blockIdx.x + 16 w + .. : waves 0, 1 the run's gate rows, 2, 3 its up rows
+    const int n0 = blockIdx.x * 64 + 16 * w;
+    run_groups<WT, TT>(a, 0, ngroups, min(n0 + r, a.N - 1), n0 + 4 * g, r, nb, g, acc);
+  } else {
+    const int n0 = blockIdx.x * 16;
+    run_groups<WT, TT>(a, w * ngroups / 4, (w + 1) * ngroups / 4, min(n0 + r, a.N - 1), n0 + 4 * g, r, nb, g,
+                       acc);
+  }
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) s_acc[w][tt][lane] = acc[tt];
+  __syncthreads();
+
+  if (EPI == EPI_SILU) {
+    // m = silu(gate) * up (layer.rs:72-79) for 8 tokens x 32 elements per
+    // pass; Q8_0 of the 32 elements of a token (one block of m)
+    const int run = blockIdx.x;
+    const int j = tid & 31;
+    const int wg = j >> 4, gg = (j & 15) >> 2, ii = j & 3;  // gate row j: wave wg, lane group gg, register ii
+    for (int t0 = tid >> 5; t0 < 16 * TT; t0 += kT / 32) {
+      const int tt = t0 >> 4, tok = t0 & 15;
+      const float gv = s_acc[wg][tt][16 * gg + tok][ii];
+      const float uv = s_acc[2 + wg][tt][16 * gg + tok][ii];
+      const float mv = (gv / (1.0f + expf(-gv))) * uv;
+      float amax = fabsf(mv);
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+      const float d = amax / 127.0f;
+      const float inv = amax == 0.0f ? 0.0f : 1.0f / d;
+      if (t0 < a.M) {
+        const int F = a.N / 2;
+        a.yq[(size_t)t0 * F + act_offset(32 * run + j, a.layout)] =
+            amax == 0.0f ? (int8_t)0 : (int8_t)q8_code(mv, inv);
+        if (j == 0) a.yd[(size_t)t0 * (F / 32) + run] = amax == 0.0f ? 0.0f : d;
+      }
+    }
+    return;
+  }
+  if (w != 0) return;
+  const int row0 = blockIdx.x * 16 + 4 * g;
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) {
+    const int t = 16 * tt + r;
+    f32x4 v = s_acc[0][tt][lane];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) v = v + s_acc[k][tt][lane];
+    if (t < a.M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = row0 + i;
+        if (row < a.N) {
+          float o = v[i];
+          if (EPI == EPI_RESID) o = o + a.res[(size_t)t * a.N + row];  // layer.rs:386,403
+          a.y[(size_t)t * a.ldy + row] = o;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+#define LLMRS_SGEMM(name, WT, EPI, TT) \
+  extern "C" __global__ __launch_bounds__(kT) void name(SgemmArgs a) { sgemm_impl<WT, EPI, TT>(a); }
+#define LLMRS_SGEMM_TILES(tag, WT, EPI)        \
+  LLMRS_SGEMM(sgemm_##tag##_t1, WT, EPI, 1)    \
+  LLMRS_SGEMM(sgemm_##tag##_t2, WT, EPI, 2)    \
+  LLMRS_SGEMM(sgemm_##tag##_t4, WT, EPI, 4)
+LLMRS_SGEMM_TILES(q4h_store, WT_Q4H, EPI_STORE)
+LLMRS_SGEMM_TILES(q4h_resid, WT_Q4H, EPI_RESID)
+LLMRS_SGEMM_TILES(q4h_silu, WT_Q4H, EPI_SILU)
+LLMRS_SGEMM_TILES(q4f_store, WT_Q4F, EPI_STORE)
+LLMRS_SGEMM_TILES(q4f_resid, WT_Q4F, EPI_RESID)
+LLMRS_SGEMM_TILES(q4f_silu, WT_Q4F, EPI_SILU)
+LLMRS_SGEMM_TILES(q8h_store, WT_Q8H, EPI_STORE)
+LLMRS_SGEMM_TILES(q8h_resid, WT_Q8H, EPI_RESID)
+LLMRS_SGEMM_TILES(q8h_silu, WT_Q8H, EPI_SILU)

@@ -98,6 +98,13 @@ _SIGS = {
     "llmrs_model_decode_steps": (C.c_int, [C.c_void_p, C.c_size_t]),
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "llmrs_model_set_sampling": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "llmrs_batch_create": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_void_p)]),
+    "llmrs_batch_free": (C.c_int, [C.c_void_p]),
+    "llmrs_batch_begin": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_size_t]),
+    "llmrs_batch_decode_steps": (C.c_int, [C.c_void_p, C.c_size_t]),
+    "llmrs_batch_tokens": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_size_t]),
+    "llmrs_batch_logits": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "llmrs_batch_profile_step": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_produced": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t), C.POINTER(C.c_int32)]),
     "llmrs_sample_logits": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_size_t, C.c_void_p, C.c_uint64,
                                       C.c_void_p, C.c_void_p]),
@@ -580,6 +587,54 @@ class HipModel:
 
 
 # -- seeded synthetic inputs (llmrs_synth_*) ------------------------------
+class HipBatch:
+    """B sequences of one model decoding together (llmrs_batch_*)."""
+
+    def __init__(self, model: HipModel, batch: int):
+        self.model = model
+        self.batch = batch
+        h = C.c_void_p()
+        _check(lib().llmrs_batch_create(model._h, int(batch), C.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().llmrs_batch_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def begin(self, slot: int, prompt) -> None:
+        ids = np.ascontiguousarray(prompt, dtype=np.int32)
+        _check(lib().llmrs_batch_begin(self._h, int(slot), _ptr(ids), ids.size))
+
+    def decode_steps(self, n: int) -> None:
+        _check(lib().llmrs_batch_decode_steps(self._h, int(n)))
+
+    def tokens(self, slot: int, count: int) -> np.ndarray:
+        out = np.empty(count, np.int32)
+        _check(lib().llmrs_batch_tokens(self._h, int(slot), _ptr(out), count))
+        return out
+
+    def logits(self) -> np.ndarray:
+        out = np.empty((self.batch, self.model.cfg.vocab), np.float32)
+        _check(lib().llmrs_batch_logits(self._h, _ptr(out)))
+        return out
+
+    def profile_step(self, cap: int = 8192) -> list[KernelTiming]:
+        names = C.create_string_buffer(32 * cap)
+        ms = np.zeros(cap, np.float32)
+        work = np.zeros(cap, np.float64)
+        n = _check(lib().llmrs_batch_profile_step(self._h, names, _ptr(ms), _ptr(work), cap))
+        raw = names.raw
+        return [KernelTiming(raw[32 * i:32 * i + 32].split(b"\0")[0].decode(), float(ms[i]), float(work[i]))
+                for i in range(n)]
+
+
 def synth_q4(seed: int, tid: int, n: int, k: int, lo: float, hi: float, threads: int = 0):
     qs = np.empty(n * k // 2, np.uint8)
     sc = np.empty(n * k // 32, np.float32)

@@ -1,0 +1,108 @@
+"""Batched decode (llmrs_batch_*): B sequences of one model decoding together.
+
+The reference decodes one sequence; a row's values in its layer code depend
+only on that row and its own cache (layer.rs:175-333).  Bars: each slot's
+logits within 1e-2 of the oracle's forward over that slot's sequence and its
+greedy stream identical to the oracle's (a divergence only at a near-tie,
+as for single-sequence decoding); a slot's logits bit-identical whichever
+other sequences share the batch; every slot at its own position."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import check_stream
+from llmrs_hip import DType, HipBatch, synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+SPECS = [
+    syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_heads=8, n_kv_heads=2, ffn=1024, seed=21),
+    syn.tiny(DType.Q8_0, DType.F32, head_dim=64, n_heads=4, n_kv_heads=2, ffn=512, seed=22),
+    syn.tiny(DType.Q4, DType.F16, head_dim=64, n_heads=8, n_kv_heads=1, ffn=512, seed=23),
+]
+
+
+def prompts(spec, B, seed=5):
+    rng = np.random.default_rng(seed)
+    return [rng.integers(0, spec.vocab, int(rng.integers(1, 20))).astype(np.int32) for _ in range(B)]
+
+
+@pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)
+def test_batch_streams_vs_oracle(hip, orc, spec):
+    w = syn.make_weights(spec)
+    gm = hip.HipModel(spec.config(128))
+    syn.load_model(gm, w)
+    om = orc.OracleModel.from_spec(spec, max_seq=128)
+    om.load(w)
+    B, steps = 5, 72
+    ps = prompts(spec, B)
+    bt = HipBatch(gm, B)
+    for s, p in enumerate(ps):
+        bt.begin(s, p)
+    bt.decode_steps(steps - 1)
+    lg = bt.logits()
+    for s, p in enumerate(ps):
+        toks = bt.tokens(s, p.size + steps)
+        assert np.array_equal(toks[:p.size], p)
+        gen = toks[p.size:]
+        ref, margins = om.generate(p, steps)
+        check_stream(gen, ref, margins)
+        # the last step's logits against the oracle's forward over the same sequence
+        olg, _ = om.forward(toks[:-1], 0)
+        assert np.max(np.abs(lg[s] - olg)) < 1e-2, f"slot {s}"
+    bt.close()
+    gm.close()
+
+
+def test_batch_rows_independent(hip, orc):
+    spec = SPECS[0]
+    w = syn.make_weights(spec)
+    gm = hip.HipModel(spec.config(96))
+    syn.load_model(gm, w)
+    ps = prompts(spec, 4, seed=9)
+    out = {}
+    for B in (4, 1):
+        bt = HipBatch(gm, B)
+        for s in range(B):
+            bt.begin(s, ps[s])
+        bt.decode_steps(20)
+        out[B] = (bt.logits(), [bt.tokens(s, ps[s].size + 21) for s in range(B)])
+        bt.close()
+    assert np.array_equal(out[4][0][0], out[1][0][0]), "slot 0's logits depend on the other slots"
+    assert np.array_equal(out[4][1][0], out[1][1][0])
+    # a slot restarted with another prompt keeps the others unchanged
+    bt = HipBatch(gm, 2)
+    bt.begin(0, ps[0])
+    bt.begin(1, ps[1])
+    bt.decode_steps(5)
+    a = bt.tokens(0, ps[0].size + 6)
+    bt.begin(1, ps[2])
+    bt.decode_steps(5)
+    b0 = bt.tokens(0, ps[0].size + 11)
+    assert np.array_equal(b0[:a.size], a)
+    assert np.array_equal(b0, out[4][1][0][:b0.size])
+    bt.close()
+    gm.close()
+
+
+def test_batch_errors(hip):
+    spec = SPECS[1]
+    gm = hip.HipModel(spec.config(32))
+    syn.load_model(gm, syn.make_weights(spec))
+    bt = HipBatch(gm, 2)
+    with pytest.raises(hip.LlmrsError):
+        bt.decode_steps(1)  # slots not begun
+    bt.begin(0, [1, 2, 3])
+    bt.begin(1, [4])
+    with pytest.raises(hip.LlmrsError):
+        bt.begin(2, [1])
+    with pytest.raises(hip.LlmrsError):
+        bt.decode_steps(40)  # beyond max_seq
+    bt.decode_steps(3)
+    with pytest.raises(hip.LlmrsError):
+        bt.tokens(0, 3 + 5)  # more than produced
+    bt.close()
+    with pytest.raises(hip.LlmrsError):
+        HipBatch(gm, 0)
+    gm.close()
