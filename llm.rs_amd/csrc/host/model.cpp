@@ -1633,6 +1633,9 @@ struct llmrs_batch {
   // widths not a multiple of 128, on the prefill GEMM
   bool skinny = false;
   int tiles = 1, layout = llmrs::kActNatural;
+  // attention splits per sequence: the model's (planned for one sequence)
+  // cut so that the B sequences' workgroups fill the GPU about twice
+  int nsplit = 1;
   std::vector<size_t> host_pos;
   std::vector<char> begun;
   hipGraph_t graph = nullptr;
@@ -1683,7 +1686,8 @@ void enqueue_batch_step(llmrs_batch* b, Launcher& L) {
     const double wb = linear_weight_bytes(m, W);
     if (b->skinny) {
       SgemmArgs g{xq, xd, W.codes, W.scales, y, res, yq, yd, B, W.n, W.k, W.n, b->layout};
-      L(name, wb, dim3(silu ? (unsigned)(W.n / 64) : (unsigned)((W.n + 15) / 16)), blk, 0, g);
+      const int rows = silu ? 64 : std::string(epi) == "resid" ? 16 : 32;  // rows per workgroup (sgemm.hip)
+      L(name, wb, dim3((unsigned)((W.n + rows - 1) / rows)), blk, 0, g);
     } else {
       PrefillGemmArgs g{xq, xd, W.codes, W.scales, y, res, yq, yd, B, W.n, W.k, silu ? W.n / 2 : W.n, gemm_group_m()};
       L(name, wb, gemm_grid(B, W.n), blk, glds, g);
@@ -1716,11 +1720,11 @@ void enqueue_batch_step(llmrs_batch* b, Launcher& L) {
       a.max_seq = kv_rows(m);
       a.nq = nq;
       a.nkv = nkv;
-      a.nsplit = m->nsplit;
+      a.nsplit = b->nsplit;
       a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
       a.kv_batch_bytes = b->kv_bytes;
       a.ctx_layout = b->layout;
-      L(attn_kernel(m), 0.0, dim3((unsigned)m->nsplit, (unsigned)nkv, (unsigned)B), dim3(attn_threads(m)), 0, a);
+      L(attn_kernel(m), 0.0, dim3((unsigned)b->nsplit, (unsigned)nkv, (unsigned)B), dim3(attn_threads(m)), 0, a);
     }
     linear("resid", Lb.o, b->ctx_q, b->ctx_d, b->h, b->x, nullptr, nullptr);  // O + residual (layer.rs:386)
     {  // post-attention RMSNorm + Q8_0
@@ -1819,6 +1823,8 @@ int llmrs_batch_create(llmrs_model* m, int32_t batch, llmrs_batch** out) {
                 !(bg && std::string(bg) == "prefill");
     b->tiles = batch <= 16 ? 1 : batch <= 32 ? 2 : 4;
     b->layout = b->skinny ? llmrs::kActMfma : llmrs::kActNatural;
+    b->nsplit = std::max(1, std::min(m->nsplit, (2 * ctx().num_cus + batch * c.n_kv_heads - 1) /
+                                                     (batch * c.n_kv_heads)));
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));
     (void)kernel("argmax_batch", dim3(1024));
     for (const char* epi : {"store", "resid", "silu"}) (void)kernel(batch_linear_kernel(b.get(), epi), dim3(256));

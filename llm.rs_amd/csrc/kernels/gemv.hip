@@ -96,7 +96,8 @@ extern "C" __global__ __launch_bounds__(256) void argmax_final(ArgmaxFinalArgs a
 // Greedy step of a batch: workgroup b takes the argmax of logits row b
 // (lowest index on ties; every logit NaN gives 0) and advances sequence b
 // as argmax_final advances one sequence (its prompt is consumed: the id is
-// both produced and the next input).
+// both produced and the next input).  16-byte loads, four per thread in
+// flight.
 extern "C" __global__ __launch_bounds__(1024) void argmax_batch(ArgmaxBatchArgs a) {
   __shared__ float s_bv[16];
   __shared__ int s_bi[16];
@@ -104,11 +105,31 @@ extern "C" __global__ __launch_bounds__(1024) void argmax_batch(ArgmaxBatchArgs 
   const float* row = a.logits + (size_t)b * a.vocab;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < a.vocab; i += blockDim.x)
-    if (better(row[i], i, bv, bi)) {
-      bv = row[i];
+  auto take = [&](float v, int i) {
+    if (better(v, i, bv, bi)) {
+      bv = v;
       bi = i;
     }
+  };
+  // rows start 16-byte aligned when vocab % 4 == 0; else scalar loads
+  const int nv = a.vocab % 4 == 0 ? a.vocab / 4 : 0;
+  const f32x4* row4 = (const f32x4*)row;
+  for (int v0 = tid; v0 < nv; v0 += 4 * (int)blockDim.x) {
+    f32x4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int v = v0 + u * (int)blockDim.x;
+      x[u] = v < nv ? row4[v] : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int v = v0 + u * (int)blockDim.x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (v < nv) take(x[u][e], 4 * v + e);
+    }
+  }
+  for (int i = 4 * nv + tid; i < a.vocab; i += blockDim.x) take(row[i], i);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o);

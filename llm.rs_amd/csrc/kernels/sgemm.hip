@@ -20,12 +20,15 @@
 // (act_offset), so a lane reads its four blocks' operands as 32 contiguous
 // bytes.
 //
-// Workgroups of four waves.  STORE / RESID: 16 weight rows per workgroup,
-// the blocks split over the waves in contiguous quarters, partial sums added
-// in wave order.  SILU: 64 rows per workgroup - a run of 32 gate and 32 up
-// rows - one wave per 16 rows over all blocks; m = silu(gate) * up and its
-// Q8_0 codes (one 32-element block per run) in the operand order of the down
-// projection.  Each wave keeps PF groups of loads in flight (a ring of
+// A wave takes RT 16-row tiles, which share its activation operands (the
+// activation bytes a group loads are twice its weight bytes per tile): two,
+// or one for the residual projections, whose few rows would leave too few
+// workgroups.  Workgroups of four waves.  STORE / RESID: 16 RT weight rows
+// per workgroup, the blocks split over the waves in contiguous quarters,
+// partial sums added in wave order.  SILU: 64 rows per workgroup - a run of 32 gate and 32 up
+// rows - two waves per 32 rows, each half of the blocks; m = silu(gate) * up
+// and its Q8_0 codes (one 32-element block per run) in the operand order of
+// the down projection.  Each wave keeps PF groups of loads in flight (a ring of
 // register sets, the loop unrolled by PF so every set has a fixed place).
 #include "common.h"
 #include "gemv_core.h"
@@ -61,39 +64,43 @@ __device__ __forceinline__ void transpose4(unsigned x[4]) {
 }
 
 // What one 128-element group needs in registers.
-template <int WT, int TT>
+template <int WT, int TT, int RT>
 struct Group {
-  u32x4 w;             // Q4: this lane's block (transposed after arrival)
-  unsigned w8[4][2];   // Q8: dwords g and g + 4 of each block
-  unsigned dw[4][WT == WT_Q4F ? 4 : 2];  // scales of the 4 output rows of this lane x 4 blocks (bits)
-  u32x4 x[TT][2];      // activation operands of 4 blocks, per token tile
-  f32x4 da[TT];        // activation scales of 4 blocks, per token tile
+  u32x4 w[RT];          // Q4: this lane's block of each row tile (transposed after arrival)
+  unsigned w8[RT][4][2];  // Q8: dwords g and g + 4 of each block
+  // scales of 4 blocks of output row (lane % 4) of this lane's four per row
+  // tile (fp16 pairs or f32 bits); the other rows' come from the quad (DPP)
+  unsigned dw[RT][WT == WT_Q4F ? 4 : 2];
+  u32x4 x[TT][2];       // activation operands of 4 blocks, per token tile
+  f32x4 da[TT];         // activation scales of 4 blocks, per token tile
 };
 
-template <int WT, int TT>
-__device__ __forceinline__ void load_group(Group<WT, TT>& G, const SgemmArgs& a, int q, int wrow, int orow0,
-                                           int tok, int nb, int g) {
-  if (WT == WT_Q8H) {
-    const unsigned* base = (const unsigned*)(a.wq + ((size_t)wrow * nb + 4 * q) * 32);
+// Loads of group q for the wave's rows n0 .. n0 + 16 RT - 1.
+template <int WT, int TT, int RT>
+__device__ __forceinline__ void load_group(Group<WT, TT, RT>& G, const SgemmArgs& a, int q, int n0, int tok, int nb,
+                                           int g) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      G.w8[j][0] = __builtin_nontemporal_load(base + 8 * j + g);
-      G.w8[j][1] = __builtin_nontemporal_load(base + 8 * j + g + 4);
+  for (int rt = 0; rt < RT; ++rt) {
+    const int wrow = min(n0 + 16 * rt + tok, a.N - 1);
+    if (WT == WT_Q8H) {
+      const unsigned* base = (const unsigned*)(a.wq + ((size_t)wrow * nb + 4 * q) * 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        G.w8[rt][j][0] = __builtin_nontemporal_load(base + 8 * j + g);
+        G.w8[rt][j][1] = __builtin_nontemporal_load(base + 8 * j + g + 4);
+      }
+    } else {
+      G.w[rt] = __builtin_nontemporal_load((const u32x4*)(a.wq + ((size_t)wrow * nb + 4 * q + g) * 16));
     }
-  } else {
-    G.w = __builtin_nontemporal_load((const u32x4*)(a.wq + ((size_t)wrow * nb + 4 * q + g) * 16));
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const size_t s = (size_t)min(orow0 + i, a.N - 1) * nb + 4 * q;
+    const size_t s = (size_t)min(n0 + 16 * rt + 4 * g + (tok & 3), a.N - 1) * nb + 4 * q;
     if (WT == WT_Q4F) {
       const u32x4 v = *(const u32x4*)((const float*)a.ws + s);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) G.dw[i][j] = v[j];
+      for (int j = 0; j < 4; ++j) G.dw[rt][j] = v[j];
     } else {
       const uint2 v = *(const uint2*)((const uint16_t*)a.ws + s);
-      G.dw[i][0] = v.x;
-      G.dw[i][1] = v.y;
+      G.dw[rt][0] = v.x;
+      G.dw[rt][1] = v.y;
     }
   }
 #pragma unroll
@@ -106,45 +113,64 @@ __device__ __forceinline__ void load_group(Group<WT, TT>& G, const SgemmArgs& a,
   }
 }
 
-// Weight scale of output row i, block j of the group.
-template <int WT, int TT>
-__device__ __forceinline__ float scale_of(const Group<WT, TT>& G, int i, int j) {
-  if (WT == WT_Q4F) return __uint_as_float(G.dw[i][j]);
-  return h2f((uint16_t)(G.dw[i][j >> 1] >> (16 * (j & 1))));
+// Lane i of the lane's quad (DPP quad_perm [i, i, i, i]).
+template <int I>
+__device__ __forceinline__ unsigned quad_bcast(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, I * 0x55, 0xF, 0xF, false);
 }
 
-// One group's MFMAs and epilogue into acc[tt][i] (output row orow0 + i,
-// token 16 tt + tok).
-template <int WT, int TT>
-__device__ __forceinline__ void compute_group(Group<WT, TT>& G, f32x4 (&acc)[TT]) {
-  unsigned wd[4];
-  if (WT != WT_Q8H) {
+// One group's MFMAs and epilogue into acc[rt][tt][i] (output row n0 + 16 rt
+// + 4 g + i, token 16 tt + tok).
+template <int WT, int TT, int RT>
+__device__ __forceinline__ void compute_group(Group<WT, TT, RT>& G, f32x4 (&acc)[RT][TT]) {
+  constexpr int ND = WT == WT_Q4F ? 4 : 2;
+  unsigned sc[RT][4][ND];
+  unsigned wd[RT][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) wd[j] = G.w[j];
-    transpose4(wd);
+  for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      sc[rt][0][d] = quad_bcast<0>(G.dw[rt][d]);
+      sc[rt][1][d] = quad_bcast<1>(G.dw[rt][d]);
+      sc[rt][2][d] = quad_bcast<2>(G.dw[rt][d]);
+      sc[rt][3][d] = quad_bcast<3>(G.dw[rt][d]);
+    }
+    if (WT != WT_Q8H) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wd[rt][j] = G.w[rt][j];
+      transpose4(wd[rt]);
+    }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    long op_a;
-    if (WT == WT_Q8H) {
-      op_a = (long)((unsigned long long)G.w8[j][0] | ((unsigned long long)G.w8[j][1] << 32));
-    } else {
-      const unsigned lo = nib_s8(wd[j] & 0x0F0F0F0Fu), hi = nib_s8((wd[j] >> 4) & 0x0F0F0F0Fu);
-      op_a = (long)((unsigned long long)lo | ((unsigned long long)hi << 32));
-    }
-    float dw[4];
+    long op_a[RT];
+    float dw[RT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dw[i] = scale_of<WT, TT>(G, i, j);
+    for (int rt = 0; rt < RT; ++rt) {
+      if (WT == WT_Q8H) {
+        op_a[rt] = (long)((unsigned long long)G.w8[rt][j][0] | ((unsigned long long)G.w8[rt][j][1] << 32));
+      } else {
+        const unsigned lo = nib_s8(wd[rt][j] & 0x0F0F0F0Fu), hi = nib_s8((wd[rt][j] >> 4) & 0x0F0F0F0Fu);
+        op_a[rt] = (long)((unsigned long long)lo | ((unsigned long long)hi << 32));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dw[rt][i] = WT == WT_Q4F ? __uint_as_float(sc[rt][i][j])
+                                 : h2f((uint16_t)(sc[rt][i][j >> 1] >> (16 * (j & 1))));
+    }
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       const unsigned b0 = G.x[tt][j >> 1][2 * (j & 1)], b1 = G.x[tt][j >> 1][2 * (j & 1) + 1];
       const long op_b = (long)((unsigned long long)b0 | ((unsigned long long)b1 << 32));
-      const i32x4 isum = __builtin_amdgcn_mfma_i32_16x16x32_i8(op_a, op_b, i32x4{0, 0, 0, 0}, 0, 0, 0);
       const float da = G.da[tt][j];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float s = dw[i] * da;                      // fl(d_w * d_a)
-        acc[tt][i] = acc[tt][i] + (float)isum[i] * s;    // cpu.rs:930-935
+      for (int rt = 0; rt < RT; ++rt) {
+        const i32x4 isum = __builtin_amdgcn_mfma_i32_16x16x32_i8(op_a[rt], op_b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float sc2 = dw[rt][i] * da;                         // fl(d_w * d_a)
+          acc[rt][tt][i] = acc[rt][tt][i] + (float)isum[i] * sc2;   // cpu.rs:930-935
+        }
       }
     }
   }
@@ -158,43 +184,49 @@ constexpr int prefetch_depth() {
 
 // The rows' partial sums over groups [q0, q1) in group order, PF groups of
 // loads ahead (addresses past the range clamped to its last group).
-template <int WT, int TT>
-__device__ __forceinline__ void run_groups(const SgemmArgs& a, int q0, int q1, int wrow, int orow0, int tok,
-                                           int nb, int g, f32x4 (&acc)[TT]) {
+template <int WT, int TT, int RT>
+__device__ __forceinline__ void run_groups(const SgemmArgs& a, int q0, int q1, int n0, int tok, int nb, int g,
+                                           f32x4 (&acc)[RT][TT]) {
   constexpr int PF = prefetch_depth<WT, TT>();
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt) acc[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  if (q0 >= q1) return;
-  Group<WT, TT> ring[PF];
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-  for (int s = 0; s < PF; ++s) load_group<WT, TT>(ring[s], a, min(q0 + s, q1 - 1), wrow, orow0, tok, nb, g);
+    for (int tt = 0; tt < TT; ++tt) acc[rt][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (q0 >= q1) return;
+  Group<WT, TT, RT> ring[PF];
+#pragma unroll
+  for (int s = 0; s < PF; ++s) load_group<WT, TT, RT>(ring[s], a, min(q0 + s, q1 - 1), n0, tok, nb, g);
   for (int q = q0; q < q1; q += PF) {
 #pragma unroll
     for (int s = 0; s < PF; ++s) {
-      if (q + s < q1) compute_group<WT, TT>(ring[s], acc);
-      load_group<WT, TT>(ring[s], a, min(q + s + PF, q1 - 1), wrow, orow0, tok, nb, g);
+      if (q + s < q1) compute_group<WT, TT, RT>(ring[s], acc);
+      load_group<WT, TT, RT>(ring[s], a, min(q + s + PF, q1 - 1), n0, tok, nb, g);
     }
   }
 }
 
 template <int WT, int EPI, int TT>
 __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
-  __shared__ f32x4 s_acc[4][TT][64];
+  // row tiles per wave: one for the residual projections (O, down: few
+  // rows, so the workgroups stay many), two otherwise
+  constexpr int RT = EPI == EPI_RESID ? 1 : 2;
+  __shared__ f32x4 s_acc[4][RT][TT][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int nb = a.K >> 5, ngroups = nb >> 2;
-  f32x4 acc[TT];
+  f32x4 acc[RT][TT];
   if (EPI == EPI_SILU) {
-    // rows 64 blockIdx.x + 16 w + .. : waves 0, 1 the run's gate rows, 2, 3 its up rows
-    const int n0 = blockIdx.x * 64 + 16 * w;
-    run_groups<WT, TT>(a, 0, ngroups, min(n0 + r, a.N - 1), n0 + 4 * g, r, nb, g, acc);
+    // waves 0, 1: the run's 32 gate rows, 2, 3: its 32 up rows; each pair
+    // splits the blocks in halves
+    const int n0 = blockIdx.x * 64 + 32 * (w >> 1), ks = w & 1;
+    run_groups<WT, TT, RT>(a, ks * ngroups / 2, (ks + 1) * ngroups / 2, n0, r, nb, g, acc);
   } else {
-    const int n0 = blockIdx.x * 16;
-    run_groups<WT, TT>(a, w * ngroups / 4, (w + 1) * ngroups / 4, min(n0 + r, a.N - 1), n0 + 4 * g, r, nb, g,
-                       acc);
+    run_groups<WT, TT, RT>(a, w * ngroups / 4, (w + 1) * ngroups / 4, blockIdx.x * 16 * RT, r, nb, g, acc);
   }
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt) s_acc[w][tt][lane] = acc[tt];
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) s_acc[w][rt][tt][lane] = acc[rt][tt];
   __syncthreads();
 
   if (EPI == EPI_SILU) {
@@ -202,11 +234,11 @@ __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
     // pass; Q8_0 of the 32 elements of a token (one block of m)
     const int run = blockIdx.x;
     const int j = tid & 31;
-    const int wg = j >> 4, gg = (j & 15) >> 2, ii = j & 3;  // gate row j: wave wg, lane group gg, register ii
+    const int rt = j >> 4, gg = (j & 15) >> 2, ii = j & 3;  // gate row j: row tile, lane group, register
     for (int t0 = tid >> 5; t0 < 16 * TT; t0 += kT / 32) {
-      const int tt = t0 >> 4, tok = t0 & 15;
-      const float gv = s_acc[wg][tt][16 * gg + tok][ii];
-      const float uv = s_acc[2 + wg][tt][16 * gg + tok][ii];
+      const int tt = t0 >> 4, l = 16 * gg + (t0 & 15);
+      const float gv = s_acc[0][rt][tt][l][ii] + s_acc[1][rt][tt][l][ii];
+      const float uv = s_acc[2][rt][tt][l][ii] + s_acc[3][rt][tt][l][ii];
       const float mv = (gv / (1.0f + expf(-gv))) * uv;
       float amax = fabsf(mv);
 #pragma unroll
@@ -223,21 +255,24 @@ __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
     return;
   }
   if (w != 0) return;
-  const int row0 = blockIdx.x * 16 + 4 * g;
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt) {
-    const int t = 16 * tt + r;
-    f32x4 v = s_acc[0][tt][lane];
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row0 = blockIdx.x * 16 * RT + 16 * rt + 4 * g;
 #pragma unroll
-    for (int k = 1; k < 4; ++k) v = v + s_acc[k][tt][lane];
-    if (t < a.M) {
+    for (int tt = 0; tt < TT; ++tt) {
+      const int t = 16 * tt + r;
+      f32x4 v = s_acc[0][rt][tt][lane];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = row0 + i;
-        if (row < a.N) {
-          float o = v[i];
-          if (EPI == EPI_RESID) o = o + a.res[(size_t)t * a.N + row];  // layer.rs:386,403
-          a.y[(size_t)t * a.ldy + row] = o;
+      for (int k = 1; k < 4; ++k) v = v + s_acc[k][rt][tt][lane];
+      if (t < a.M) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + i;
+          if (row < a.N) {
+            float o = v[i];
+            if (EPI == EPI_RESID) o = o + a.res[(size_t)t * a.N + row];  // layer.rs:386,403
+            a.y[(size_t)t * a.ldy + row] = o;
+          }
         }
       }
     }
