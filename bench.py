@@ -231,7 +231,8 @@ def traffic_probe(args, lh, syn) -> int:
     """Dispatches for HBM-traffic counters: the workload's prompt as one
     batched prefill (every prefill kernel once per layer at its real M),
     four eager decode steps right after it (every decode kernel at the
-    prompt's context length) and a scale_f32 pass over 64 Mi floats, whose
+    prompt's context length), two batched decode steps of 16 sequences
+    (after their 8-token prefills) and a scale_f32 pass over 64 Mi floats, whose
     FETCH_SIZE / WRITE_SIZE readings calibrate the counters (each ideally
     256 MiB)."""
     import numpy as np
@@ -246,6 +247,13 @@ def traffic_probe(args, lh, syn) -> int:
     for _ in range(2):
         model.profile_step()
     lh.sync()
+    # two batched decode steps of 16 sequences (8-token prompts): the skinny GEMMs
+    bt = lh.HipBatch(model, 16)
+    for sl in range(16):
+        bt.begin(sl, syn.prompt(spec)[:8])
+    bt.decode_steps(2)
+    lh.sync()
+    bt.close()
     n = 64 << 20
     x = lh.Tensor.from_numpy(np.ones((n // 4096, 4096), np.float32))
     lh.HipBackend().scale(x, 1.0)
