@@ -491,6 +491,34 @@ std::string gemm_kernel(const llmrs_model* m, const char* epi) {
   return std::string("gemm_") + wt_tag(m->wt) + "_" + epi;
 }
 
+// Whether M prefill rows run their linear layers on the skinny GEMM's exact
+// launches (sgemm.hip, up to 64 rows; the activation codes then in its
+// operand order) rather than the 128 x 128-tile GEMM, which a short prompt
+// leaves mostly idle; both are bit-identical to the reference's block loop.
+// LLMRS_PREFILL_SKINNY=0 keeps every prefill on the tile GEMM.
+bool prefill_skinny(const llmrs_model* m, int M) {
+  const llmrs_model_config& c = m->c;
+  return M <= 64 && c.hidden % 128 == 0 && c.ffn % 128 == 0 && (c.n_heads * c.head_dim) % 128 == 0 &&
+         env_int("LLMRS_PREFILL_SKINNY", 1) != 0;
+}
+
+// The skinny GEMM kernel of an epilogue for M rows (store, resid, silu);
+// exact: each output's blocks in one wave, in order (prompt prefill).
+std::string sgemm_kernel(const llmrs_model* m, const char* epi, int M, bool exact) {
+  return std::string("sgemm_") + wt_tag(m->wt) + "_" + epi + "_t" + (M <= 16 ? "1" : M <= 32 ? "2" : "4") +
+         (exact ? "_exact" : "");
+}
+
+// Launch shape of a skinny GEMM (sgemm.hip): SwiGLU 64 rows per 256-thread
+// workgroup; exact store / residual 16 rows per one-wave workgroup; else
+// residual 16 and store 32 rows per 256-thread workgroup.
+std::pair<dim3, dim3> sgemm_shape(const char* epi, int N, bool exact) {
+  const std::string e(epi);
+  const int rows = e == "silu" ? 64 : exact || e == "resid" ? 16 : 32;
+  const unsigned threads = exact && e != "silu" ? 64 : 256;
+  return {dim3((unsigned)((N + rows - 1) / rows)), dim3(threads)};
+}
+
 dim3 gemm_grid(int M, int N) { return dim3((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128)); }
 
 // Device buffers a test probe adds to one prefill layer: ctx and the SwiGLU
@@ -510,7 +538,7 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
                            const PrefillProbe* probe = nullptr, void* kc = nullptr, void* vc = nullptr) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
-  const int qd = nq * hd, QR = m->qkv_rows;
+  const int QR = m->qkv_rows;
   const bool kv16 = c.kv_dtype == LLMRS_F16;
   const dim3 blk(256);
   auto flops = [](double a, double b, double k) { return 2.0 * a * b * k; };
@@ -532,16 +560,27 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
     kc = Lb.kc;
     vc = Lb.vc;
   }
+  const bool skinny = prefill_skinny(m, M);
+  const int layout = skinny ? llmrs::kActMfma : llmrs::kActNatural;
+  // One linear layer over the M rows on the tile GEMM or the skinny GEMM.
+  auto linear = [&](const char* epi, const DevLinear& W, const int8_t* xq, const float* xd, float* y,
+                    const float* res, int8_t* yq, float* yd, int ldy) {
+    const double work = flops(M, W.n, W.k);
+    if (skinny) {
+      SgemmArgs g{xq, xd, W.codes, W.scales, y, res, yq, yd, M, W.n, W.k, ldy, layout};
+      const auto sh = sgemm_shape(epi, W.n, true);
+      L(sgemm_kernel(m, epi, M, true), work, sh.first, sh.second, 0, g);
+    } else {
+      PrefillGemmArgs g{xq, xd, W.codes, W.scales, y, res, yq, yd, M, W.n, W.k, ldy, gemm_group_m()};
+      L(gemm_kernel(m, epi), work, gemm_grid(M, W.n), blk, glds, g);
+    }
+  };
   {  // RMSNorm + Q8_0 of each row (layer.rs:378; cpu.rs:90-93)
-    PrefillRowArgs r{m->pf_x, Lb.norm[0], m->pf_aq, m->pf_ad, M, H, c.rms_eps, llmrs::kActNatural};
+    PrefillRowArgs r{m->pf_x, Lb.norm[0], m->pf_aq, m->pf_ad, M, H, c.rms_eps, layout};
     L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
   }
   after(0);
-  {  // Q|K|V
-    PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.qkv.codes, Lb.qkv.scales, m->pf_qkv, nullptr,
-                      nullptr, nullptr, M, QR, H, QR, gemm_group_m()};
-    L(gemm_kernel(m, "store"), flops(M, QR, H), gemm_grid(M, QR), blk, glds, g);
-  }
+  linear("store", Lb.qkv, m->pf_aq, m->pf_ad, m->pf_qkv, nullptr, nullptr, nullptr, QR);  // Q|K|V
   after(1);
   {  // RoPE + K/V append
     PrefillRopeArgs r{m->pf_qkv, m->pf_q, kc, vc, m->rope_cos, m->rope_sin, M, nq, nkv, hd,
@@ -553,35 +592,24 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
   after(2);
   {  // causal attention
     PrefillAttnArgs a{m->pf_q, kc, vc, probe ? probe->ctx : nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq,
-                      nkv, kv_rows(m), (int)start, scale};
+                      nkv, kv_rows(m), (int)start, scale, layout};
     if (mfma_attn)
       L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nkv), dim3(512), 0, a);
     else
       L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nq), blk, 0, a);
   }
   after(3);
-  {  // O projection + residual (layer.rs:386)
-    PrefillGemmArgs g{m->pf_ctx_q, m->pf_ctx_d, Lb.o.codes, Lb.o.scales, m->pf_h, m->pf_x,
-                      nullptr, nullptr, M, H, qd, H, gemm_group_m()};
-    L(gemm_kernel(m, "resid"), flops(M, H, qd), gemm_grid(M, H), blk, glds, g);
-  }
+  linear("resid", Lb.o, m->pf_ctx_q, m->pf_ctx_d, m->pf_h, m->pf_x, nullptr, nullptr, H);  // O + residual
   after(4);
   {  // post-attention RMSNorm + Q8_0
-    PrefillRowArgs r{m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, M, H, c.rms_eps, llmrs::kActNatural};
+    PrefillRowArgs r{m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, M, H, c.rms_eps, layout};
     L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
   }
   after(5);
-  {  // gate|up + SiLU + Q8_0 of m (layer.rs:40-89)
-    PrefillGemmArgs g{m->pf_aq, m->pf_ad, Lb.gu.codes, Lb.gu.scales, probe ? probe->mf : nullptr, nullptr,
-                      m->pf_m_q, m->pf_m_d, M, 2 * F, H, F, gemm_group_m()};
-    L(gemm_kernel(m, "silu"), flops(M, 2 * F, H), gemm_grid(M, 2 * F), blk, glds, g);
-  }
+  // gate|up + SiLU + Q8_0 of m (layer.rs:40-89)
+  linear("silu", Lb.gu, m->pf_aq, m->pf_ad, probe ? probe->mf : nullptr, nullptr, m->pf_m_q, m->pf_m_d, F);
   after(6);
-  {  // down projection + residual (layer.rs:403)
-    PrefillGemmArgs g{m->pf_m_q, m->pf_m_d, Lb.down.codes, Lb.down.scales, m->pf_x, m->pf_h,
-                      nullptr, nullptr, M, H, F, H, gemm_group_m()};
-    L(gemm_kernel(m, "resid"), flops(M, H, F), gemm_grid(M, H), blk, glds, g);
-  }
+  linear("resid", Lb.down, m->pf_m_q, m->pf_m_d, m->pf_x, m->pf_h, nullptr, nullptr, H);  // down + residual
   after(7);
 }
 
@@ -1601,6 +1629,21 @@ int llmrs_model_probe_prefill_layer(llmrs_model* m, int layer, size_t start_pos,
     };
     Launcher L{s};
     enqueue_prefill_layer(m, L, layer, start_pos, (int)M, &p);
+    if (prefill_skinny(m, (int)M)) {  // codes back into element order
+      auto natural = [&](int8_t* rows, size_t K) {
+        if (!rows) return;
+        std::vector<int8_t> tmp(K);
+        for (size_t t = 0; t < M; ++t) {
+          int8_t* r = rows + t * K;
+          for (size_t k = 0; k < K; ++k) tmp[k] = r[llmrs::act_offset((int)k, llmrs::kActMfma)];
+          std::memcpy(r, tmp.data(), K);
+        }
+      };
+      natural(out->xq, H);
+      natural(out->ctx_q, qd);
+      natural(out->hq, H);
+      natural(out->m_q, F);
+    }
     m->begun = false;
   });
 }
@@ -1632,7 +1675,7 @@ struct llmrs_batch {
   // activation codes in its operand order) or, beyond 64 sequences or for
   // widths not a multiple of 128, on the prefill GEMM
   bool skinny = false;
-  int tiles = 1, layout = llmrs::kActNatural;
+  int layout = llmrs::kActNatural;
   // attention splits per sequence: the model's (planned for one sequence)
   // cut so that the B sequences' workgroups fill the GPU about twice
   int nsplit = 1;
@@ -1666,8 +1709,7 @@ namespace {
 
 // Kernel name of a batched linear layer (epi: store, resid, silu).
 std::string batch_linear_kernel(const llmrs_batch* b, const char* epi) {
-  if (!b->skinny) return gemm_kernel(b->m, epi);
-  return std::string("sgemm_") + wt_tag(b->m->wt) + "_" + epi + "_t" + std::to_string(b->tiles);
+  return b->skinny ? sgemm_kernel(b->m, epi, b->B, false) : gemm_kernel(b->m, epi);
 }
 
 // One greedy step of every sequence of the batch.
@@ -1686,8 +1728,8 @@ void enqueue_batch_step(llmrs_batch* b, Launcher& L) {
     const double wb = linear_weight_bytes(m, W);
     if (b->skinny) {
       SgemmArgs g{xq, xd, W.codes, W.scales, y, res, yq, yd, B, W.n, W.k, W.n, b->layout};
-      const int rows = silu ? 64 : std::string(epi) == "resid" ? 16 : 32;  // rows per workgroup (sgemm.hip)
-      L(name, wb, dim3((unsigned)((W.n + rows - 1) / rows)), blk, 0, g);
+      const auto sh = sgemm_shape(epi, W.n, false);
+      L(name, wb, sh.first, sh.second, 0, g);
     } else {
       PrefillGemmArgs g{xq, xd, W.codes, W.scales, y, res, yq, yd, B, W.n, W.k, silu ? W.n / 2 : W.n, gemm_group_m()};
       L(name, wb, gemm_grid(B, W.n), blk, glds, g);
@@ -1821,7 +1863,6 @@ int llmrs_batch_create(llmrs_model* m, int32_t batch, llmrs_batch** out) {
     const char* bg = std::getenv("LLMRS_BATCH_GEMM");
     b->skinny = batch <= 64 && c.hidden % 128 == 0 && c.ffn % 128 == 0 && qdim % 128 == 0 &&
                 !(bg && std::string(bg) == "prefill");
-    b->tiles = batch <= 16 ? 1 : batch <= 32 ? 2 : 4;
     b->layout = b->skinny ? llmrs::kActMfma : llmrs::kActNatural;
     b->nsplit = std::max(1, std::min(m->nsplit, (2 * ctx().num_cus + batch * c.n_kv_heads - 1) /
                                                      (batch * c.n_kv_heads)));

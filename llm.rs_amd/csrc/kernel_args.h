@@ -300,6 +300,7 @@ struct PrefillAttnArgs {
   float* ctx_d;          // [M][nq*hd/32]
   int M, nq, nkv, max_seq, start_pos;
   float scale;           // fl(1 / fl(sqrt(hd)))
+  int ctx_layout;        // operand order of ctx_q within a row (act_offset)
 };
 
 // ints between the split tickets of two KV heads: each head's counter has a

@@ -547,7 +547,8 @@ __device__ __forceinline__ void attn_prefill_impl(const PrefillAttnArgs& a) {
 #pragma unroll
       for (int e = 0; e < DPT; ++e) {
         if (a.ctx) a.ctx[base + e] = v[e];
-        a.ctx_q[base + e] = amax == 0.0f ? (int8_t)0 : (int8_t)q8_code(v[e], inv);
+        a.ctx_q[(size_t)t * qdim + act_offset(h * HD + DPT * ki + e, a.ctx_layout)] =
+            amax == 0.0f ? (int8_t)0 : (int8_t)q8_code(v[e], inv);
       }
       if ((ki % TPB) == 0) a.ctx_d[base / 32] = amax == 0.0f ? 0.0f : d;
     }
@@ -781,7 +782,8 @@ __device__ __forceinline__ void attn_prefill_mfma_impl(const PrefillAttnArgs& a)
             const int q8 = amax == 0.0f ? 0 : q8_code(v[4 * gq + c], inv);
             w |= ((unsigned)q8 & 0xFFu) << (8 * c);
           }
-          *(unsigned*)(a.ctx_q + e) = w;
+          *(unsigned*)(a.ctx_q + (base - (size_t)h * HD) +
+                       act_offset(h * HD + 32 * d + 8 * gq + 4 * h2, a.ctx_layout)) = w;
           if (a.ctx) *(f32x4*)(a.ctx + e) = f32x4{v[4 * gq], v[4 * gq + 1], v[4 * gq + 2], v[4 * gq + 3]};
         }
         if (h2 == 0) a.ctx_d[base / 32 + d] = amax == 0.0f ? 0.0f : dq;

@@ -20,16 +20,23 @@
 // (act_offset), so a lane reads its four blocks' operands as 32 contiguous
 // bytes.
 //
-// A wave takes RT 16-row tiles, which share its activation operands (the
-// activation bytes a group loads are twice its weight bytes per tile): two,
-// or one for the residual projections, whose few rows would leave too few
-// workgroups.  Workgroups of four waves.  STORE / RESID: 16 RT weight rows
-// per workgroup, the blocks split over the waves in contiguous quarters,
-// partial sums added in wave order.  SILU: 64 rows per workgroup - a run of 32 gate and 32 up
-// rows - two waves per 32 rows, each half of the blocks; m = silu(gate) * up
-// and its Q8_0 codes (one 32-element block per run) in the operand order of
-// the down projection.  Each wave keeps PF groups of loads in flight (a ring of
-// register sets, the loop unrolled by PF so every set has a fixed place).
+// Batched decode: a wave takes RT 16-row tiles, which share its activation
+// operands (the activation bytes a group loads are twice its weight bytes
+// per tile): two, or one for the residual projections, whose few rows would
+// leave too few workgroups.  Workgroups of four waves.  STORE / RESID: 16 RT
+// weight rows per workgroup, the blocks split over the waves in contiguous
+// quarters, partial sums added in wave order.  SILU: 64 rows per workgroup -
+// a run of 32 gate and 32 up rows - two waves per 32 rows, each half of the
+// blocks; m = silu(gate) * up and its Q8_0 codes (one 32-element block per
+// run) in the operand order of the down projection.
+//
+// EXACT launches (prompt prefill) give each output row's blocks to one wave
+// in order, as the reference adds them, so the result is bit-identical to
+// the reference's for the same activation codes: STORE / RESID run one wave
+// (16 rows) per workgroup, SILU four (the run's 64 rows).
+//
+// Each wave keeps PF groups of loads in flight (a ring of register sets, the
+// loop unrolled by PF so every set has a fixed place).
 #include "common.h"
 #include "gemv_core.h"
 #include "../kernel_args.h"
@@ -205,23 +212,55 @@ __device__ __forceinline__ void run_groups(const SgemmArgs& a, int q0, int q1, i
   }
 }
 
-template <int WT, int EPI, int TT>
+// EXACT: every output's blocks in order in one wave, as the reference adds
+// them (bit-identical to it for the same activation codes; prompt prefill).
+// Otherwise the blocks are split over the waves of a workgroup and the
+// partial sums added in wave order (batched decode: more workgroups).
+template <int WT, int EPI, int TT, bool EXACT>
 __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
   // row tiles per wave: one for the residual projections (O, down: few
-  // rows, so the workgroups stay many), two otherwise
-  constexpr int RT = EPI == EPI_RESID ? 1 : 2;
+  // rows, so the workgroups stay many) and in EXACT mode, two otherwise
+  constexpr int RT = EXACT || EPI == EPI_RESID ? 1 : 2;
   __shared__ f32x4 s_acc[4][RT][TT][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int nb = a.K >> 5, ngroups = nb >> 2;
   f32x4 acc[RT][TT];
   if (EPI == EPI_SILU) {
-    // waves 0, 1: the run's 32 gate rows, 2, 3: its 32 up rows; each pair
-    // splits the blocks in halves
-    const int n0 = blockIdx.x * 64 + 32 * (w >> 1), ks = w & 1;
-    run_groups<WT, TT, RT>(a, ks * ngroups / 2, (ks + 1) * ngroups / 2, n0, r, nb, g, acc);
+    if (EXACT) {
+      // waves 0, 1: the run's gate rows 0-15, 16-31; 2, 3: its up rows
+      run_groups<WT, TT, RT>(a, 0, ngroups, blockIdx.x * 64 + 16 * w, r, nb, g, acc);
+    } else {
+      // waves 0, 1: the run's 32 gate rows, 2, 3: its 32 up rows; each pair
+      // splits the blocks in halves
+      const int n0 = blockIdx.x * 64 + 32 * (w >> 1), ks = w & 1;
+      run_groups<WT, TT, RT>(a, ks * ngroups / 2, (ks + 1) * ngroups / 2, n0, r, nb, g, acc);
+    }
+  } else if (EXACT) {
+    // one wave per workgroup (64 threads): 16 rows over all blocks
+    run_groups<WT, TT, RT>(a, 0, ngroups, blockIdx.x * 16, r, nb, g, acc);
   } else {
     run_groups<WT, TT, RT>(a, w * ngroups / 4, (w + 1) * ngroups / 4, blockIdx.x * 16 * RT, r, nb, g, acc);
+  }
+
+  if (EPI != EPI_SILU && EXACT) {
+    const int row0 = blockIdx.x * 16 + 4 * g;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const int t = 16 * tt + r;
+      if (t < a.M) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + i;
+          if (row < a.N) {
+            float o = acc[0][tt][i];
+            if (EPI == EPI_RESID) o = o + a.res[(size_t)t * a.N + row];  // layer.rs:386,403
+            a.y[(size_t)t * a.ldy + row] = o;
+          }
+        }
+      }
+    }
+    return;
   }
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
@@ -234,11 +273,18 @@ __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
     // pass; Q8_0 of the 32 elements of a token (one block of m)
     const int run = blockIdx.x;
     const int j = tid & 31;
-    const int rt = j >> 4, gg = (j & 15) >> 2, ii = j & 3;  // gate row j: row tile, lane group, register
+    // gate row j of the run: row tile (or, EXACT, wave), lane group, register
+    const int rt = j >> 4, gg = (j & 15) >> 2, ii = j & 3;
     for (int t0 = tid >> 5; t0 < 16 * TT; t0 += kT / 32) {
       const int tt = t0 >> 4, l = 16 * gg + (t0 & 15);
-      const float gv = s_acc[0][rt][tt][l][ii] + s_acc[1][rt][tt][l][ii];
-      const float uv = s_acc[2][rt][tt][l][ii] + s_acc[3][rt][tt][l][ii];
+      float gv, uv;
+      if (EXACT) {
+        gv = s_acc[rt][0][tt][l][ii];
+        uv = s_acc[2 + rt][0][tt][l][ii];
+      } else {
+        gv = s_acc[0][rt][tt][l][ii] + s_acc[1][rt][tt][l][ii];
+        uv = s_acc[2][rt][tt][l][ii] + s_acc[3][rt][tt][l][ii];
+      }
       const float mv = (gv / (1.0f + expf(-gv))) * uv;
       float amax = fabsf(mv);
 #pragma unroll
@@ -247,6 +293,7 @@ __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
       const float inv = amax == 0.0f ? 0.0f : 1.0f / d;
       if (t0 < a.M) {
         const int F = a.N / 2;
+        if (a.y) a.y[(size_t)t0 * a.ldy + 32 * run + j] = mv;  // the f32 product (test probes)
         a.yq[(size_t)t0 * F + act_offset(32 * run + j, a.layout)] =
             amax == 0.0f ? (int8_t)0 : (int8_t)q8_code(mv, inv);
         if (j == 0) a.yd[(size_t)t0 * (F / 32) + run] = amax == 0.0f ? 0.0f : d;
@@ -281,12 +328,15 @@ __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
 
 }  // namespace
 
-#define LLMRS_SGEMM(name, WT, EPI, TT) \
-  extern "C" __global__ __launch_bounds__(kT) void name(SgemmArgs a) { sgemm_impl<WT, EPI, TT>(a); }
-#define LLMRS_SGEMM_TILES(tag, WT, EPI)        \
-  LLMRS_SGEMM(sgemm_##tag##_t1, WT, EPI, 1)    \
-  LLMRS_SGEMM(sgemm_##tag##_t2, WT, EPI, 2)    \
-  LLMRS_SGEMM(sgemm_##tag##_t4, WT, EPI, 4)
+#define LLMRS_SGEMM(name, WT, EPI, TT, EXACT) \
+  extern "C" __global__ __launch_bounds__(kT) void name(SgemmArgs a) { sgemm_impl<WT, EPI, TT, EXACT>(a); }
+#define LLMRS_SGEMM_TILES(tag, WT, EPI)                \
+  LLMRS_SGEMM(sgemm_##tag##_t1, WT, EPI, 1, false)     \
+  LLMRS_SGEMM(sgemm_##tag##_t2, WT, EPI, 2, false)     \
+  LLMRS_SGEMM(sgemm_##tag##_t4, WT, EPI, 4, false)     \
+  LLMRS_SGEMM(sgemm_##tag##_t1_exact, WT, EPI, 1, true) \
+  LLMRS_SGEMM(sgemm_##tag##_t2_exact, WT, EPI, 2, true) \
+  LLMRS_SGEMM(sgemm_##tag##_t4_exact, WT, EPI, 4, true)
 LLMRS_SGEMM_TILES(q4h_store, WT_Q4H, EPI_STORE)
 LLMRS_SGEMM_TILES(q4h_resid, WT_Q4H, EPI_RESID)
 LLMRS_SGEMM_TILES(q4h_silu, WT_Q4H, EPI_SILU)

@@ -235,7 +235,10 @@ def test_decode_attention_layouts(hip, orc, kv, head_dim, nkv, streams, splits, 
 
 def check_prefill_layer(hip, orc, spec, start, M):
     """Every prefill kernel of one layer on M rows at positions start..:
-    GEMMs bit-exact on the GPU's own operands."""
+    GEMMs bit-exact on the GPU's own operands (the tile GEMM, or for up to
+    64 rows the skinny GEMM's exact launches)."""
+    def same(got, want, what):
+        assert np.array_equal(got, want), f"{what} not bit-exact"
     gm, om, w = layer_models(hip, orc, spec, start + M)
     if start:
         fill_cache(gm, om, spec, start)
@@ -247,7 +250,7 @@ def check_prefill_layer(hip, orc, spec, start, M):
     for i in range(M):
         flips += check_norm_codes(orc, pr["xq"][i], pr["xd"][i], x[i], w.norms[0][0], eps)
     qkv = np.concatenate([gemv(orc, spec, pr["xq"], pr["xd"], L[s]) for s in (W_Q, W_K, W_V)], axis=1)
-    assert np.array_equal(pr["qkv"], qkv), "Q|K|V GEMM not bit-exact"
+    same(pr["qkv"], qkv, "Q|K|V GEMM")
     ctx = om.attention(0, pr["qkv"], start)
     assert_close(pr["ctx"], ctx, "causal attention ctx")
     exact = exact_attention(om, orc, pr["qkv"], start).astype(np.float64)
@@ -260,7 +263,7 @@ def check_prefill_layer(hip, orc, spec, start, M):
         ok_, ov = om.kv_read(0, g, start, M)
         assert np.array_equal(gk, ok_) and np.array_equal(gv, ov), f"K/V rows of KV head {g}"
     h = (gemv(orc, spec, pr["ctx_q"], pr["ctx_d"], L[W_O]) + x).astype(F32)
-    assert np.array_equal(pr["h"], h), "O GEMM + residual not bit-exact"
+    same(pr["h"], h, "O GEMM + residual")
     for i in range(M):
         flips += check_norm_codes(orc, pr["hq"][i], pr["hd"][i], pr["h"][i], w.norms[0][1], eps)
     g = gemv(orc, spec, pr["hq"], pr["hd"], L[W_GATE])
@@ -270,7 +273,7 @@ def check_prefill_layer(hip, orc, spec, start, M):
     for i in range(M):
         check_own_codes(orc, pr["m_q"][i], pr["m_d"][i], pr["m"][i])
     out = (gemv(orc, spec, pr["m_q"], pr["m_d"], L[W_DOWN]) + pr["h"]).astype(F32)
-    assert np.array_equal(pr["out"], out), "down GEMM + residual not bit-exact"
+    same(pr["out"], out, "down GEMM + residual")
     return flips
 
 
@@ -292,3 +295,13 @@ def test_prefill_layer_kernels_ragged_after_cache(hip, orc):
     over pre-filled positions, the head_dim-64 matrix-core attention."""
     spec = syn.with_sizes(syn.WORKLOADS[1], n_layers=1, vocab=1024, prompt=700, decode=0)
     check_prefill_layer(hip, orc, spec, 300, 700)
+
+
+@pytest.mark.parametrize("index,start,M", [(3, 0, 24), (1, 300, 40), (2, 0, 5), (4, 0, 64)],
+                         ids=["8b-24", "1b_q8-40-after-cache", "8b-5", "70b-64"])
+def test_prefill_layer_kernels_short(hip, orc, index, start, M):
+    """Prompts of up to 64 rows: the linear layers on the skinny GEMM's
+    exact launches (one, two and four 16-token tiles), Q4_0 and Q8_0
+    weights, the 70B widths, after a filled cache."""
+    spec = syn.with_sizes(syn.WORKLOADS[index], n_layers=1, vocab=1024, prompt=M, decode=0, prefilled=0)
+    check_prefill_layer(hip, orc, spec, start, M)
