@@ -70,7 +70,10 @@ struct llmrs_model {
   // h (gate|up input)
   int8_t *x_q = nullptr, *h_q = nullptr;
   float *x_d = nullptr, *x_ss = nullptr, *h_d = nullptr, *h_ss = nullptr;
-  bool nq = true;  // false: RMSNorm + Q8_0 inside the consumers (LLMRS_NQ=0)
+  // producer-side norm operands: x's (down -> next Q|K|V and lm_head,
+  // embedding -> layer 0) and h's (O -> gate|up); false: RMSNorm + Q8_0
+  // inside the consumers
+  bool nq_x = true, nq_h = true;
   int *part_idx = nullptr, *counters = nullptr, *tokens = nullptr, *gen = nullptr;
   int *pos = nullptr, *n_prompt = nullptr, *err = nullptr;
   int nsplit = 1, lm_grid = 1, cap = 0;
@@ -228,14 +231,14 @@ void enqueue_embed(llmrs_model* m, Launcher& L, const float* x_in, const float* 
   e.err = m->err;
   e.hidden = H;
   e.vocab = m->c.vocab;
-  if (m->nq) {
+  if (m->nq_x) {
     e.norm_w = norm_w;
     e.xq = m->x_q;
     e.xd = m->x_d;
     e.xss = m->x_ss;
   }
   e.x_in = x_in;
-  L("embed_gather", (m->nq ? 9.25 : 8.0) * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
+  L("embed_gather", (m->nq_x ? 9.25 : 8.0) * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
 }
 
 // The decode GEMV of one linear slot of layer li (LLMRS_W_Q = the stacked
@@ -260,7 +263,7 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot, int8_t* probe
       g.k = H;
       g.eps = c.rms_eps;
       g.y = m->qkv;
-      if (m->nq) {
+      if (m->nq_x) {
         g.xq = m->x_q;
         g.xd = m->x_d;
         g.xss = m->x_ss;
@@ -284,7 +287,7 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot, int8_t* probe
       g.res = m->x;
       kind = "q8_resid";
       bytes = linear_weight_bytes(m, Lb.o) + 1.125 * g.k + 8.0 * H;
-      if (m->nq) {  // and the post-attention RMSNorm's operand (layer.rs:393)
+      if (m->nq_h) {  // and the post-attention RMSNorm's operand (layer.rs:393)
         g.norm_next = Lb.norm[1];
         g.yq = m->h_q;
         g.yd = m->h_d;
@@ -302,7 +305,7 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot, int8_t* probe
       g.y = m->mf;
       g.yq = m->m_q;
       g.yd = m->m_d;
-      if (m->nq) {
+      if (m->nq_h) {
         g.xq = m->h_q;
         g.xd = m->h_d;
         g.xss = m->h_ss;
@@ -326,7 +329,7 @@ void enqueue_linear(llmrs_model* m, Launcher& L, int li, int slot, int8_t* probe
       g.res = m->h;
       kind = "q8_resid";
       bytes = linear_weight_bytes(m, Lb.down) + 1.125 * F + 8.0 * H;
-      if (m->nq) {  // and the next RMSNorm's operand: next layer's input norm or the final norm
+      if (m->nq_x) {  // and the next RMSNorm's operand: next layer's input norm or the final norm
         g.norm_next = li + 1 < c.n_layers ? m->layers[li + 1].norm[0] : m->final_norm;
         g.yq = m->x_q;
         g.yd = m->x_d;
@@ -350,10 +353,10 @@ unsigned linear_grid(llmrs_model* m, int slot) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden, F = c.ffn, qd = c.n_heads * c.head_dim, cus = ctx().num_cus;
   switch (slot) {
-    case LLMRS_W_Q: return gemv_plan(m->wt, m->nq ? "nq_store" : "norm_store", m->qkv_rows, H, cus).grid;
-    case LLMRS_W_O: return gemv_plan(m->wt, m->nq ? "q8_nq" : "q8_resid", H, qd, cus).grid;
-    case LLMRS_W_GATE: return gemv_plan(m->wt, m->nq ? "nq_silu" : "norm_silu", 2 * F, H, cus).grid;
-    case LLMRS_W_DOWN: return gemv_plan(m->wt, m->nq ? "q8_nq" : "q8_resid", H, F, cus).grid;
+    case LLMRS_W_Q: return gemv_plan(m->wt, m->nq_x ? "nq_store" : "norm_store", m->qkv_rows, H, cus).grid;
+    case LLMRS_W_O: return gemv_plan(m->wt, m->nq_h ? "q8_nq" : "q8_resid", H, qd, cus).grid;
+    case LLMRS_W_GATE: return gemv_plan(m->wt, m->nq_h ? "nq_silu" : "norm_silu", 2 * F, H, cus).grid;
+    case LLMRS_W_DOWN: return gemv_plan(m->wt, m->nq_x ? "q8_nq" : "q8_resid", H, F, cus).grid;
   }
   fail(LLMRS_E_INVALID, "slot must be Q, O, GATE or DOWN");
 }
@@ -422,7 +425,7 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
     g.n = c.vocab;
     g.k = H;
     g.eps = c.rms_eps;
-    if (m->nq) {
+    if (m->nq_x) {
       g.xq = m->x_q;
       g.xd = m->x_d;
       g.xss = m->x_ss;
@@ -435,9 +438,9 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
     g.part_idx = m->part_idx;
     g.probe_xq = probe_xq;
     g.probe_xd = probe_xd;
-    const GemvPlan p = gemv_plan(m->wt, m->nq ? "nq_argmax" : "norm_argmax", g.n, g.k, cus);
+    const GemvPlan p = gemv_plan(m->wt, m->nq_x ? "nq_argmax" : "norm_argmax", g.n, g.k, cus);
     LLMRS_REQUIRE((int)p.grid == m->lm_grid, LLMRS_E_INVALID, "lm_head grid changed since model creation");
-    L(p.name, linear_weight_bytes(m, m->lm_head) + (m->nq ? 1.125 : 8.0) * H, dim3(p.grid), dim3(256), p.lds, g);
+    L(p.name, linear_weight_bytes(m, m->lm_head) + (m->nq_x ? 1.125 : 8.0) * H, dim3(p.grid), dim3(256), p.lds, g);
   }
   if (m->sampling) {
     SampleArgs a = sample_args(m->samp, c.vocab);
@@ -636,7 +639,7 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
   }
   trace(c.n_layers);
   if (head) {
-    if (m->nq) {
+    if (m->nq_x) {
       enqueue_embed(m, L, m->pf_x + (size_t)(M - 1) * H, m->final_norm);
     } else {
       LLMRS_HIP(hipMemcpyAsync(m->x, m->pf_x + (size_t)(M - 1) * H, H * sizeof(float),
@@ -852,9 +855,12 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     // Producer-side RMSNorm operands when the producers' 32-row tiles fill
     // the GPU (measured on 256 CUs: hidden 8192, 70B shape, 103.9 -> 110.2
     // tok/s; hidden 4096, 8B shape, the 128-tile O and down GEMVs lose more
-    // than the consumers' prologues gain, 724 -> 707); LLMRS_NQ=0/1 forces.
+    // than the consumers' prologues gain, 724 -> 707).  LLMRS_NQ forces:
+    // 0 neither, 1 both, 2 x's only (down's epilogue), 3 h's only (O's).
     const int nqe = env_int("LLMRS_NQ", -1);
-    m->nq = H / 32 <= 256 && (nqe >= 0 ? nqe != 0 : H / 32 >= cx.num_cus);
+    const bool nq_fit = H / 32 <= 256, nq_auto = H / 32 >= cx.num_cus;
+    m->nq_x = nq_fit && (nqe >= 0 ? (nqe == 1 || nqe == 2) : nq_auto);
+    m->nq_h = nq_fit && (nqe >= 0 ? (nqe == 1 || nqe == 3) : nq_auto);
     m->x_q = m->dalloc<int8_t>(H);
     m->h_q = m->dalloc<int8_t>(H);
     m->x_d = m->dalloc<float>(H / 32);
@@ -889,12 +895,12 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     }
     LLMRS_HIP(hipStreamSynchronize(cx.stream));
     // Resolve every kernel of the step now, so graph capture never has to.
-    const bool nqk = m->nq;
-    (void)kernel(gemv_plan(m->wt, nqk ? "nq_store" : "norm_store", m->qkv_rows, H, cx.num_cus).name);
-    (void)kernel(gemv_plan(m->wt, nqk ? "q8_nq" : "q8_resid", H, nq * hd, cx.num_cus).name);
-    (void)kernel(gemv_plan(m->wt, nqk ? "nq_silu" : "norm_silu", 2 * F, H, cx.num_cus).name);
-    (void)kernel(gemv_plan(m->wt, nqk ? "q8_nq" : "q8_resid", H, F, cx.num_cus).name);
-    (void)kernel(gemv_plan(m->wt, nqk ? "nq_argmax" : "norm_argmax", c.vocab, H, cx.num_cus).name);
+    const bool nx = m->nq_x, nh = m->nq_h;
+    (void)kernel(gemv_plan(m->wt, nx ? "nq_store" : "norm_store", m->qkv_rows, H, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, nh ? "q8_nq" : "q8_resid", H, nq * hd, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, nh ? "nq_silu" : "norm_silu", 2 * F, H, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, nx ? "q8_nq" : "q8_resid", H, F, cx.num_cus).name);
+    (void)kernel(gemv_plan(m->wt, nx ? "nq_argmax" : "norm_argmax", c.vocab, H, cx.num_cus).name);
     (void)kernel("embed_gather");
     (void)kernel("argmax_final");
     for (const char* k : {"sample_prep", "sample_probs", "sample_refine", "sample_pick"})
