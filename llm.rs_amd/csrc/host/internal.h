@@ -87,6 +87,9 @@ std::recursive_mutex& api_mutex();
 // The kernel `name`; fails (LLMRS_E_INVALID) when `block` exceeds the
 // threads per workgroup it was compiled for (its launch bounds).
 hipFunction_t kernel(const std::string& name, dim3 block = dim3(1));
+// Whether the workgroups of a (gx, gy) launch whose linear indices agree mod 8
+// run on one XCD (measured with one launch of xcc_ids).
+bool xcd_dealt_mod8(unsigned gx, unsigned gy);
 
 template <class Args>
 void launch(const std::string& name, dim3 grid, dim3 block, size_t shmem, hipStream_t stream,

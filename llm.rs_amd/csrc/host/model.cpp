@@ -81,6 +81,9 @@ struct llmrs_model {
   // (f32 caches, 256 threads each), tile waves per 256-thread workgroup of
   // the matrix-core kernel (f16 caches)
   int attn_streams = 1, attn_waves = 1;
+  // matrix-core attention: the splits of a KV head on one XCD, exchanging
+  // partials through its L2 (AttnArgs::xcd_local)
+  bool attn_local = false;
   size_t host_pos = 0;
   bool begun = false;
   hipGraph_t graph = nullptr;
@@ -386,6 +389,7 @@ void enqueue_attention(llmrs_model* m, Launcher& L, int li, unsigned long long* 
   a.nsplit = m->nsplit;
   a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
   a.ts = stamps;
+  a.xcd_local = m->attn_local ? 1 : 0;
   const double kvb = 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
   L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(attn_threads(m)), 0, a);
 }
@@ -818,6 +822,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
       if (ew != 1 && ew != 4 && ew != 8)
         ew = tiles <= std::min(llmrs::kMfmaAttnMaxSplits, 2 * cx.num_cus / nkv) ? 1 : 8;
       m->attn_waves = ew;
+      m->attn_local = nkv % 8 == 0 && env_int("LLMRS_ATTN_LOCAL", 1) == 1;
       splits = ew == 1 ? tiles : std::min((tiles + ew - 1) / ew, std::max(1, cx.num_cus / nkv));
       splits = std::min(env_int("LLMRS_ATTN_SPLITS", splits), llmrs::kMfmaAttnMaxSplits);
     } else {
@@ -830,6 +835,8 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
       splits = env_int("LLMRS_ATTN_SPLITS", splits);
     }
     m->nsplit = std::max(1, splits);
+    // the XCD-local split exchange needs a head's workgroups on one XCD
+    if (m->attn_local) m->attn_local = xcd_dealt_mod8((unsigned)m->nsplit, (unsigned)nkv);
     m->lm_grid = (int)gemv_plan(m->wt, "nq_argmax", c.vocab, H, cx.num_cus).grid;
     m->layers.resize(c.n_layers);
     for (auto& L : m->layers) {
@@ -1772,6 +1779,7 @@ void enqueue_batch_step(llmrs_batch* b, Launcher& L) {
       a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
       a.kv_batch_bytes = b->kv_bytes;
       a.ctx_layout = b->layout;
+      a.xcd_local = m->attn_local ? 1 : 0;
       L(attn_kernel(m), 0.0, dim3((unsigned)b->nsplit, (unsigned)nkv, (unsigned)B), dim3(attn_threads(m)), 0, a);
     }
     linear("resid", Lb.o, b->ctx_q, b->ctx_d, b->h, b->x, nullptr, nullptr);  // O + residual (layer.rs:386)

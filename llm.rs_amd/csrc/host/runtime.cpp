@@ -64,6 +64,23 @@ hipFunction_t kernel(const std::string& name, dim3 block) {
   return it->second.f;
 }
 
+bool xcd_dealt_mod8(unsigned gx, unsigned gy) {
+  const size_t n = (size_t)gx * gy;
+  int* d = nullptr;
+  LLMRS_HIP(hipMalloc(&d, n * sizeof(int)));
+  std::vector<int> h(n);
+  hipError_t e = hipSuccess;
+  void* args[] = {&d};
+  e = hipModuleLaunchKernel(kernel("xcc_ids", dim3(64)), gx, gy, 1, 64, 1, 1, 0, ctx().stream, args, nullptr);
+  if (e == hipSuccess) e = hipMemcpyAsync(h.data(), d, n * sizeof(int), hipMemcpyDeviceToHost, ctx().stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx().stream);
+  (void)hipFree(d);
+  LLMRS_HIP(e);
+  for (size_t i = 8; i < n; ++i)
+    if (h[i] != h[i % 8]) return false;
+  return true;
+}
+
 int gemm_group_m() {
   // 4 token tiles per group: on the 8B shapes at M = 2048 this cuts the
   // gate|up GEMM's L2 fetches 2.7x against row-major (8 is close, 2 and 16

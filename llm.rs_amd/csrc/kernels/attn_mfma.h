@@ -85,7 +85,11 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   static_assert(TW == 1 || TW == 4 || TW == 8, "one, four or eight tile waves");
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int c = lane & 15, r = lane >> 4;  // MFMA column (query head of the group), lane group
-  const int g = blockIdx.y, split = blockIdx.x;
+  // xcd_local: KV head = linear workgroup index % nkv, so with nkv = 8 all
+  // splits of a head run on one XCD and exchange partials through its L2.
+  const bool loc = a.xcd_local != 0;
+  const int lin = blockIdx.x + blockIdx.y * gridDim.x;
+  const int g = loc ? lin % a.nkv : blockIdx.y, split = loc ? lin / a.nkv : blockIdx.x;
   const int n_rep = a.nq / a.nkv;
   const size_t hrow = (size_t)g * a.max_seq * HD;  // first element of this KV head
   const uint16_t* kc = (const uint16_t*)a.kc + hrow;
@@ -411,6 +415,19 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
 
   // The split's partials: with one tile wave its own (max, sum, O); with
   // more, merged through LDS, wave w writing O blocks w, w + TW, ...
+  auto pst16 = [&](float* base, int off, dev_u32x4 v) {
+    if (loc) xcd_st16(base, off, v);
+    else dev_st16(base, off, v);
+  };
+  auto pstml = [&](size_t mi, float mv, float lv) {
+    if (loc) {
+      __builtin_amdgcn_raw_buffer_store_b64(dev_u32x2{__float_as_uint(mv), __float_as_uint(lv)},
+                                            dev_rsrc(a.part_ml), (int)(8 * mi), 0, 0);
+    } else {
+      dev_stf(a.part_ml, (int)(8 * mi), mv);
+      dev_stf(a.part_ml, (int)(8 * mi + 4), lv);
+    }
+  };
   const size_t pidx = (size_t)(g * n_rep + c) * a.nsplit + split;
   const size_t midx = (size_t)(g * n_rep + c) * ml_stride(a.nsplit) + split;
   if constexpr (TW == 1) {
@@ -418,11 +435,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
 #pragma unroll
       for (int b = 0; b < NB; ++b)
         if (col_on)
-          dev_st16(a.part_o, (int)((pidx * HD + 16 * b + 4 * r) * 4),
-                   __builtin_bit_cast(dev_u32x4, o[b] * (1.0f / kP)));
+          pst16(a.part_o, (int)((pidx * HD + 16 * b + 4 * r) * 4),
+                __builtin_bit_cast(dev_u32x4, o[b] * (1.0f / kP)));
       if (r == 0 && col_on) {
-        dev_stf(a.part_ml, (int)(8 * midx), m);
-        dev_stf(a.part_ml, (int)(8 * midx + 4), l);
+        pstml(midx, m, l);
       }
     }
   } else {
@@ -455,11 +471,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = acc[i] + cw[w] * so[((w * NB + b) * 4 + i) * 64 + lane];
       acc = acc * (1.0f / kP);
-      if (col_on) dev_st16(a.part_o, (int)((pidx * HD + 16 * b + 4 * r) * 4), __builtin_bit_cast(dev_u32x4, acc));
+      if (col_on) pst16(a.part_o, (int)((pidx * HD + 16 * b + 4 * r) * 4), __builtin_bit_cast(dev_u32x4, acc));
     }
     if (wave == 0 && r == 0 && col_on) {
-      dev_stf(a.part_ml, (int)(8 * midx), M);
-      dev_stf(a.part_ml, (int)(8 * midx + 4), L);
+      pstml(midx, M, L);
     }
   }
   // Publish the partials (device scope: they bypass the per-XCD L2), then
@@ -468,7 +483,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   __syncthreads();
   stamp(4);
   int* s_ticket = (int*)(lds + LY::TICKET);
-  if (tid == 0) *s_ticket = atomicAdd(&a.counters[g * kTicketStride], 1);
+  if (tid == 0)
+    *s_ticket = loc ? __hip_atomic_fetch_add(&a.counters[g * kTicketStride], 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_WORKGROUP)
+                    : atomicAdd(&a.counters[g * kTicketStride], 1);
   __syncthreads();
   stamp(5);
   if (*s_ticket != a.nsplit - 1) {
@@ -487,6 +505,7 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   const bool cthr = tid < nthr;
   const int ct = min(tid, nthr - 1), hr = ct / G, j = ct % G;
   const size_t obase = (size_t)(g * n_rep + hr) * ns, mbase = (size_t)(g * n_rep + hr) * ns2;
+  auto pld16 = [&](const float* base, int off) { return loc ? xcd_ld16(base, off) : dev_ld16(base, off); };
   float Mx = -INFINITY, Lx = 0.0f;  // split 0 holds position 0: Mx ends finite
   f32x4 Ox = {0.0f, 0.0f, 0.0f, 0.0f};
   if (cthr) {
@@ -494,10 +513,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
       dev_u32x4 mq[CH / 2], po[CH];
 #pragma unroll
       for (int v2 = 0; v2 < CH / 2; ++v2)  // clamped: splits past nsplit get weight 0
-        mq[v2] = dev_ld16(a.part_ml, (int)(8 * (mbase + min(s0 + 2 * v2, ns2 - 2))));
+        mq[v2] = pld16(a.part_ml, (int)(8 * (mbase + min(s0 + 2 * v2, ns2 - 2))));
 #pragma unroll
       for (int u = 0; u < CH; ++u)
-        po[u] = dev_ld16(a.part_o, (int)(((obase + min(s0 + u, ns - 1)) * HD + 4 * j) * 4));
+        po[u] = pld16(a.part_o, (int)(((obase + min(s0 + u, ns - 1)) * HD + 4 * j) * 4));
       float ms[CH], mc = -INFINITY;
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
@@ -543,7 +562,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
     *(unsigned*)(a.ctx_q + act_offset((int)e, a.ctx_layout)) = codes;  // aligned runs of 4 stay together
     if ((j & 7) == 0) a.ctx_d[e / 32] = bmax == 0.0f ? 0.0f : d;
   }
-  if (tid == 0) dev_stu(a.counters, 4 * g * kTicketStride, 0u);
+  if (tid == 0) {
+    if (loc) xcd_stu(a.counters, 4 * g * kTicketStride, 0u);
+    else dev_stu(a.counters, 4 * g * kTicketStride, 0u);
+  }
   stamp(6);
   flush_stamps();
 }

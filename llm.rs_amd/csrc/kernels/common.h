@@ -159,6 +159,18 @@ __device__ __forceinline__ void dev_stu(void* base, int byte_off, unsigned v) {
 __device__ __forceinline__ void dev_st16(void* base, int byte_off, dev_u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, dev_rsrc(base), byte_off, 0, kSc1);
 }
+// XCD-local exchange between workgroups on one XCD: stores land in its L2
+// (the vector L1 writes through), loads skip the L1 (sc0) and read the L2.
+constexpr int kSc0 = 1;
+__device__ __forceinline__ void xcd_st16(void* base, int byte_off, dev_u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, dev_rsrc(base), byte_off, 0, 0);
+}
+__device__ __forceinline__ void xcd_stu(void* base, int byte_off, unsigned v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, dev_rsrc(base), byte_off, 0, 0);
+}
+__device__ __forceinline__ dev_u32x4 xcd_ld16(const void* base, int byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(dev_rsrc(base), byte_off, 0, kSc0);
+}
 __device__ __forceinline__ void dev_st8(void* base, int byte_off, int8_t v) {
   __builtin_amdgcn_raw_buffer_store_b8((unsigned char)v, dev_rsrc(base), byte_off, 0, kSc1);
 }

@@ -168,3 +168,9 @@ extern "C" __global__ __launch_bounds__(256) void embed_gather(EmbedArgs e) {
     }
   }
 }
+
+// XCD (XCC id) each workgroup of a (gx, gy) grid runs on, at its linear index:
+// lets the host check how workgroups are dealt to the XCDs.
+extern "C" __global__ __launch_bounds__(64) void xcc_ids(int* out) {
+  if (threadIdx.x == 0) out[blockIdx.x + blockIdx.y * gridDim.x] = __builtin_amdgcn_s_getreg((15 << 11) | 20);
+}

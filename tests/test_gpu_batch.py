@@ -86,6 +86,28 @@ def test_batch_rows_independent(hip, orc):
     gm.close()
 
 
+def test_batch_xcd_local(hip, monkeypatch):
+    """LLMRS_ATTN_LOCAL=1 gives the batch bit-identical logits and streams."""
+    spec = syn.tiny(DType.Q4_0, DType.F16, head_dim=64, n_heads=16, n_kv_heads=8, ffn=512, seed=24)
+    w = syn.make_weights(spec)
+    ps = prompts(spec, 3, seed=11)
+    out = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("LLMRS_ATTN_LOCAL", mode)
+        gm = hip.HipModel(spec.config(128))
+        syn.load_model(gm, w)
+        bt = HipBatch(gm, 3)
+        for s, p in enumerate(ps):
+            bt.begin(s, p)
+        bt.decode_steps(40)
+        out[mode] = (bt.logits(), [bt.tokens(s, p.size + 41) for s, p in enumerate(ps)])
+        bt.close()
+        gm.close()
+    assert np.array_equal(out["0"][0], out["1"][0])
+    for a, b in zip(out["0"][1], out["1"][1]):
+        assert np.array_equal(a, b)
+
+
 def test_batch_errors(hip):
     spec = SPECS[1]
     gm = hip.HipModel(spec.config(32))

@@ -233,6 +233,34 @@ def test_decode_attention_layouts(hip, orc, kv, head_dim, nkv, streams, splits, 
     assert np.array_equal(again["ctx"], pr2["ctx"]), "attention is not deterministic"
 
 
+@pytest.mark.parametrize("head_dim", [128, 64])
+@pytest.mark.parametrize("waves,splits", [(1, 1), (4, 2), (8, 7), (1, 64), (8, 32)], ids=lambda v: str(v))
+def test_decode_attention_xcd_local(hip, orc, head_dim, waves, splits, monkeypatch):
+    """LLMRS_ATTN_LOCAL=1 (8 KV heads: a head's splits on one XCD, partials
+    and tickets through its L2) gives ctx and codes bit-identical to the
+    device-scope exchange, within the oracle's bar."""
+    monkeypatch.setenv("LLMRS_ATTN_WAVES", str(waves))
+    monkeypatch.setenv("LLMRS_ATTN_SPLITS", str(splits))
+    pos = 700
+    spec = syn.tiny(DType.Q4_0, DType.F16, head_dim=head_dim, n_layers=1, n_heads=32, n_kv_heads=8, ffn=512,
+                    seed=41 + head_dim)
+    x = synth_normal(spec.seed, 98, spec.hidden, 0.0, 1.0)
+    got = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("LLMRS_ATTN_LOCAL", mode)
+        gm, om, _ = layer_models(hip, orc, spec, pos + 3)
+        fill_cache(gm, om, spec, pos)
+        got[mode] = []
+        for p in (pos, pos + 1):
+            got[mode].append(gm.probe_decode_layer(0, p, x))
+            if mode == "1":
+                check_decode_attention(gm, om, orc, spec, got[mode][-1], p)
+        gm.close()
+    for a, b in zip(got["0"], got["1"]):
+        for key in ("ctx", "ctx_q", "ctx_d"):
+            assert np.array_equal(a[key], b[key]), f"{key} differs with the XCD-local exchange"
+
+
 def check_prefill_layer(hip, orc, spec, start, M):
     """Every prefill kernel of one layer on M rows at positions start..:
     GEMMs bit-exact on the GPU's own operands (the tile GEMM, or for up to
