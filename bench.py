@@ -390,6 +390,11 @@ def main() -> int:
         f"back; HBM traffic per launch {traffic if traffic is None else round(traffic / 1e6, 2)} MB")
     wbytes = model.weight_bytes()
     roof_tok_s = HBM_PEAK_GBS * 1e9 / wbytes
+    # The weights + K/V variant: every layer also reads its cache rows
+    # 0..pos, 2 * nkv * hd * (pos + 1) elements, at the mean timed position.
+    kv_elem = 2 if spec.kv == lh.DType.F16 else 4
+    kv_bytes = 2 * spec.n_layers * spec.n_kv_heads * spec.head_dim * (first + (args.steps - 1) / 2 + 1) * kv_elem
+    roof_kv_tok_s = HBM_PEAK_GBS * 1e9 / (wbytes + kv_bytes)
 
     # Sampled decoding (the reference token loop's defaults: penalty 1.2 over
     # 64 ids, temperature 0.8, top_p 0.9; no end-of-sequence stop) from the
@@ -479,6 +484,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode_roofline_tok_s": round(roof_tok_s, 1),
         "frac_of_decode_roofline": round(value / roof_tok_s, 4),
+        "decode_roofline_weights_kv_tok_s": round(roof_kv_tok_s, 1),
+        "frac_of_weights_kv_roofline": round(value / roof_kv_tok_s, 4),
         "weight_gb_per_token": round(wbytes / 1e9, 4),
         "prompt_ms": round(prompt_s * 1e3, 1),
         "prefill": prefill,
