@@ -81,7 +81,7 @@ struct llmrs_model {
   // (f32 caches, 256 threads each), tile waves per 256-thread workgroup of
   // the matrix-core kernel (f16 caches)
   int attn_streams = 1, attn_waves = 1;
-  // matrix-core attention: the splits of a KV head on one XCD, exchanging
+  // decode attention: the splits of a KV head on one XCD, exchanging
   // partials through its L2 (AttnArgs::xcd_local)
   bool attn_local = false;
   size_t host_pos = 0;
@@ -822,7 +822,6 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
       if (ew != 1 && ew != 4 && ew != 8)
         ew = tiles <= std::min(llmrs::kMfmaAttnMaxSplits, 2 * cx.num_cus / nkv) ? 1 : 8;
       m->attn_waves = ew;
-      m->attn_local = nkv % 8 == 0 && env_int("LLMRS_ATTN_LOCAL", 1) == 1;
       splits = ew == 1 ? tiles : std::min((tiles + ew - 1) / ew, std::max(1, cx.num_cus / nkv));
       splits = std::min(env_int("LLMRS_ATTN_SPLITS", splits), llmrs::kMfmaAttnMaxSplits);
     } else {
@@ -836,7 +835,8 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     }
     m->nsplit = std::max(1, splits);
     // the XCD-local split exchange needs a head's workgroups on one XCD
-    if (m->attn_local) m->attn_local = xcd_dealt_mod8((unsigned)m->nsplit, (unsigned)nkv);
+    m->attn_local = nkv % 8 == 0 && env_int("LLMRS_ATTN_LOCAL", 1) == 1 &&
+                    xcd_dealt_mod8((unsigned)m->nsplit, (unsigned)nkv);
     m->lm_grid = (int)gemv_plan(m->wt, "nq_argmax", c.vocab, H, cx.num_cus).grid;
     m->layers.resize(c.n_layers);
     for (auto& L : m->layers) {

@@ -36,7 +36,10 @@ template <int HD, int S>
 __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a0) {
   __shared__ __align__(16) uint8_t lds[AttnLds<HD, false, S>::BYTES];
   const AttnArgs a = sequence_args<HD>(a0);
-  attn_item<HD, false, false, S>(a, blockIdx.y, blockIdx.x, *a.pos_ptr, lds);
+  // xcd_local: KV head = linear workgroup index % nkv (one XCD per head)
+  const int lin = blockIdx.x + blockIdx.y * gridDim.x;
+  const int g = a.xcd_local ? lin % a.nkv : blockIdx.y, split = a.xcd_local ? lin / a.nkv : blockIdx.x;
+  attn_item<HD, false, false, S>(a, g, split, *a.pos_ptr, lds);
 }
 
 template <int HD, int TW>

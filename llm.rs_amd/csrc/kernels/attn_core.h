@@ -142,6 +142,10 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
 
   const int tid = threadIdx.x, lane = lane_id();
   const int stm = wave_id() / 4, wave = wave_id() % 4;  // stream, wave within the stream
+  // xcd_local: all splits of KV head g run on one XCD (the caller's mapping)
+  // and exchange partials through its L2; otherwise with device-scope
+  // operations that bypass the per-XCD L2 copies.
+  const bool loc = a.xcd_local != 0;
   const int ltid = tid % 256;                           // thread within the stream
   float (*s_q)[HD] = (float (*)[HD])(lds + LY::Q);
   kv_t* s_k = (kv_t*)(lds + LY::K(stm));
@@ -464,23 +468,34 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     if (stm == 0 && hr < n_rep) {
       const int h = g * n_rep + hr;
       const size_t idx = (size_t)h * a.nsplit + split;
-      if (lane == 0) {
-        st_act<true>(a.part_ml, 2 * idx, m[j]);
-        st_act<true>(a.part_ml, 2 * idx + 1, l[j]);
-      }
+      if (loc) {
+        if (lane == 0) {
+          a.part_ml[2 * idx] = m[j];
+          a.part_ml[2 * idx + 1] = l[j];
+        }
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) st_act<true>(a.part_o, idx * HD + DPL * lane + e, acc[j][e]);
+        for (int e = 0; e < DPL; ++e) a.part_o[idx * HD + DPL * lane + e] = acc[j][e];
+      } else {
+        if (lane == 0) {
+          st_act<true>(a.part_ml, 2 * idx, m[j]);
+          st_act<true>(a.part_ml, 2 * idx + 1, l[j]);
+        }
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) st_act<true>(a.part_o, idx * HD + DPL * lane + e, acc[j][e]);
+      }
     }
   }
   // Publish the partials, then take a ticket; the last workgroup combines.
-  // Partials always move with device-scope stores and loads, which bypass
-  // the per-XCD L2 copies: the stores only need to have completed before the
-  // ticket, and no agent-scope fence (a write-back and invalidate of the
-  // whole L2, microseconds under contention) is needed.
+  // The stores only need to have completed before the ticket: no agent-scope
+  // fence (a write-back and invalidate of the whole L2, microseconds under
+  // contention) is needed.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   stamp(4);
-  if (tid == 0) s_ticket = atomicAdd(&a.counters[g * kTicketStride], 1);
+  if (tid == 0)
+    s_ticket = loc ? __hip_atomic_fetch_add(&a.counters[g * kTicketStride], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_WORKGROUP)
+                   : atomicAdd(&a.counters[g * kTicketStride], 1);
   __syncthreads();
   stamp(5);
   if (s_ticket != a.nsplit - 1) {
@@ -509,26 +524,30 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
         const int uu = min(c0 + u, a.nsplit - 1);  // clamped; weighted by 0 past nsplit
         const int off = (int)(((base + uu) * HD + DPL * lane) * 4);
         if constexpr (DPL == 2) {
-          const dev_u32x2 t = dev_ld8(a.part_o, off);
+          const dev_u32x2 t = loc ? xcd_ld8(a.part_o, off) : dev_ld8(a.part_o, off);
           opf[u][0] = __uint_as_float(t.x);
           opf[u][1] = __uint_as_float(t.y);
         } else {
-          opf[u][0] = dev_ldf(a.part_o, off);
+          opf[u][0] = loc ? xcd_ldf(a.part_o, off) : dev_ldf(a.part_o, off);
         }
       }
+    };
+    auto ld_ml = [&](int sp) {
+      const int off = (int)(2 * (base + sp) * 4);
+      return loc ? xcd_ld8(a.part_ml, off) : dev_ld8(a.part_ml, off);
     };
     load_chunk(0);
     float ms, ls;
     {
       const int sp = min(lane, a.nsplit - 1);
-      const dev_u32x2 t = dev_ld8(a.part_ml, (int)(2 * (base + sp) * 4));
+      const dev_u32x2 t = ld_ml(sp);
       ms = lane < a.nsplit ? __uint_as_float(t.x) : -INFINITY;
       ls = lane < a.nsplit ? __uint_as_float(t.y) : 0.0f;
     }
     float M = wave_max(ms);
     for (int s0 = LLMRS_WAVE; s0 < a.nsplit; s0 += LLMRS_WAVE) {
       const int sp = min(s0 + lane, a.nsplit - 1);
-      const dev_u32x2 t = dev_ld8(a.part_ml, (int)(2 * (base + sp) * 4));
+      const dev_u32x2 t = ld_ml(sp);
       M = fmaxf(M, wave_max(s0 + lane < a.nsplit ? __uint_as_float(t.x) : -INFINITY));
     }
     float L = 0.0f, o[DPL];
@@ -537,7 +556,7 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     for (int s0 = 0; s0 < a.nsplit; s0 += LLMRS_WAVE) {
       if (s0 > 0) {
         const int sp = min(s0 + lane, a.nsplit - 1);
-        const dev_u32x2 t = dev_ld8(a.part_ml, (int)(2 * (base + sp) * 4));
+        const dev_u32x2 t = ld_ml(sp);
         ms = s0 + lane < a.nsplit ? __uint_as_float(t.x) : -INFINITY;
         ls = s0 + lane < a.nsplit ? __uint_as_float(t.y) : 0.0f;
       }
@@ -579,7 +598,10 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
     }
     if ((lane % LPB) == 0) st_act<true>(a.ctx_d, ((size_t)h * HD + DPL * lane) / 32, amax == 0.0f ? 0.0f : d);
   }
-  if (tid == 0) dev_stu(a.counters, 4 * g * kTicketStride, 0u);
+  if (tid == 0) {
+    if (loc) xcd_stu(a.counters, 4 * g * kTicketStride, 0u);
+    else dev_stu(a.counters, 4 * g * kTicketStride, 0u);
+  }
   stamp(6);
   flush_stamps();
   return true;

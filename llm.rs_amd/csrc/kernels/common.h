@@ -171,6 +171,12 @@ __device__ __forceinline__ void xcd_stu(void* base, int byte_off, unsigned v) {
 __device__ __forceinline__ dev_u32x4 xcd_ld16(const void* base, int byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(dev_rsrc(base), byte_off, 0, kSc0);
 }
+__device__ __forceinline__ dev_u32x2 xcd_ld8(const void* base, int byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(dev_rsrc(base), byte_off, 0, kSc0);
+}
+__device__ __forceinline__ float xcd_ldf(const void* base, int byte_off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(dev_rsrc(base), byte_off, 0, kSc0));
+}
 __device__ __forceinline__ void dev_st8(void* base, int byte_off, int8_t v) {
   __builtin_amdgcn_raw_buffer_store_b8((unsigned char)v, dev_rsrc(base), byte_off, 0, kSc1);
 }

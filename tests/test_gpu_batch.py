@@ -86,9 +86,10 @@ def test_batch_rows_independent(hip, orc):
     gm.close()
 
 
-def test_batch_xcd_local(hip, monkeypatch):
+@pytest.mark.parametrize("kv", [DType.F16, DType.F32], ids=["f16", "f32"])
+def test_batch_xcd_local(hip, kv, monkeypatch):
     """LLMRS_ATTN_LOCAL=1 gives the batch bit-identical logits and streams."""
-    spec = syn.tiny(DType.Q4_0, DType.F16, head_dim=64, n_heads=16, n_kv_heads=8, ffn=512, seed=24)
+    spec = syn.tiny(DType.Q4_0, kv, head_dim=64, n_heads=16, n_kv_heads=8, ffn=512, seed=24)
     w = syn.make_weights(spec)
     ps = prompts(spec, 3, seed=11)
     out = {}
