@@ -82,7 +82,7 @@ struct llmrs_model {
   // the matrix-core kernel (f16 caches)
   int attn_streams = 1, attn_waves = 1;
   // decode attention: the splits of a KV head on one XCD, exchanging
-  // partials through its L2 (AttnArgs::xcd_local)
+  // partials through its L2 (the attention kernels' _l variants)
   bool attn_local = false;
   size_t host_pos = 0;
   bool begun = false;
@@ -174,9 +174,10 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
 
 // The decode-attention kernel of this model (attention.hip).
 std::string attn_kernel(const llmrs_model* m) {
+  const char* local = m->attn_local ? "_l" : "";
   if (m->c.kv_dtype == LLMRS_F16)
-    return "attn_decode_mfma_hd" + std::to_string(m->c.head_dim) + "_w" + std::to_string(m->attn_waves);
-  return "attn_decode_hd" + std::to_string(m->c.head_dim) + "_f32" + (m->attn_streams > 1 ? "_s4" : "");
+    return "attn_decode_mfma_hd" + std::to_string(m->c.head_dim) + "_w" + std::to_string(m->attn_waves) + local;
+  return "attn_decode_hd" + std::to_string(m->c.head_dim) + "_f32" + (m->attn_streams > 1 ? "_s4" : "") + local;
 }
 // Its threads per workgroup.
 unsigned attn_threads(const llmrs_model* m) {
@@ -389,7 +390,6 @@ void enqueue_attention(llmrs_model* m, Launcher& L, int li, unsigned long long* 
   a.nsplit = m->nsplit;
   a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
   a.ts = stamps;
-  a.xcd_local = m->attn_local ? 1 : 0;
   const double kvb = 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
   L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(attn_threads(m)), 0, a);
 }
@@ -1779,7 +1779,6 @@ void enqueue_batch_step(llmrs_batch* b, Launcher& L) {
       a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
       a.kv_batch_bytes = b->kv_bytes;
       a.ctx_layout = b->layout;
-      a.xcd_local = m->attn_local ? 1 : 0;
       L(attn_kernel(m), 0.0, dim3((unsigned)b->nsplit, (unsigned)nkv, (unsigned)B), dim3(attn_threads(m)), 0, a);
     }
     linear("resid", Lb.o, b->ctx_q, b->ctx_d, b->h, b->x, nullptr, nullptr);  // O + residual (layer.rs:386)

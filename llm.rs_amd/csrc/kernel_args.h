@@ -187,10 +187,6 @@ struct AttnArgs {
   // GEMM's operand order ctx_layout (act_offset within the row).
   size_t kv_batch_bytes;
   int ctx_layout;
-  // KV head = linear workgroup index % nkv and split = / nkv, the
-  // partials and tickets exchanged through the L2 of the XCD (nkv % 8 == 0:
-  // workgroups are dealt to the 8 XCDs round-robin)
-  int xcd_local;
 };
 
 // Elementwise trait operators (ops.hip).

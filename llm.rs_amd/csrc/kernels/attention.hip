@@ -32,41 +32,52 @@ __device__ __forceinline__ AttnArgs sequence_args(const AttnArgs& a0) {
   return a;
 }
 
-template <int HD, int S>
+template <int HD, int S, bool LOCAL>
 __device__ __forceinline__ void attn_decode_impl(const AttnArgs& a0) {
   __shared__ __align__(16) uint8_t lds[AttnLds<HD, false, S>::BYTES];
   const AttnArgs a = sequence_args<HD>(a0);
-  // xcd_local: KV head = linear workgroup index % nkv (one XCD per head)
+  // LOCAL: KV head = linear workgroup index % nkv (one XCD per head)
   const int lin = blockIdx.x + blockIdx.y * gridDim.x;
-  const int g = a.xcd_local ? lin % a.nkv : blockIdx.y, split = a.xcd_local ? lin / a.nkv : blockIdx.x;
-  attn_item<HD, false, false, S>(a, g, split, *a.pos_ptr, lds);
+  const int g = LOCAL ? lin % a.nkv : blockIdx.y, split = LOCAL ? lin / a.nkv : blockIdx.x;
+  attn_item<HD, false, false, S, LOCAL>(a, g, split, *a.pos_ptr, lds);
 }
 
-template <int HD, int TW>
+template <int HD, int TW, bool LOCAL>
 __device__ __forceinline__ void attn_decode_mfma_impl(const AttnArgs& a0) {
   __shared__ __align__(16) uint8_t lds[MfmaAttnLds<HD, TW>::BYTES];
   const AttnArgs a = sequence_args<HD>(a0);
-  attn_mfma_item<HD, TW>(a, *a.pos_ptr, lds);
+  attn_mfma_item<HD, TW, LOCAL>(a, *a.pos_ptr, lds);
 }
 
-// Variant names: attn_decode_hd<HD>_f32[_s<streams>].
-#define LLMRS_ATTN(name, HD, S)                                                    \
+// Variant names: attn_decode_hd<HD>_f32[_s<streams>][_l], where _l is the
+// XCD-local split exchange (a KV head's workgroups on one XCD).
+#define LLMRS_ATTN(name, HD, S, LOCAL)                                             \
   extern "C" __global__ __launch_bounds__(256 * S) void name(AttnArgs a) {        \
-    attn_decode_impl<HD, S>(a);                                                   \
+    attn_decode_impl<HD, S, LOCAL>(a);                                            \
   }
-LLMRS_ATTN(attn_decode_hd64_f32, 64, 1)
-LLMRS_ATTN(attn_decode_hd128_f32, 128, 1)
-LLMRS_ATTN(attn_decode_hd64_f32_s4, 64, 4)
-LLMRS_ATTN(attn_decode_hd128_f32_s4, 128, 4)
+LLMRS_ATTN(attn_decode_hd64_f32, 64, 1, false)
+LLMRS_ATTN(attn_decode_hd128_f32, 128, 1, false)
+LLMRS_ATTN(attn_decode_hd64_f32_s4, 64, 4, false)
+LLMRS_ATTN(attn_decode_hd128_f32_s4, 128, 4, false)
+LLMRS_ATTN(attn_decode_hd64_f32_l, 64, 1, true)
+LLMRS_ATTN(attn_decode_hd128_f32_l, 128, 1, true)
+LLMRS_ATTN(attn_decode_hd64_f32_s4_l, 64, 4, true)
+LLMRS_ATTN(attn_decode_hd128_f32_s4_l, 128, 4, true)
 
-// attn_decode_mfma_hd<HD>_w<tile waves>: max(4, tile waves) waves
-#define LLMRS_ATTN_MFMA(name, HD, TW)                                                   \
+// attn_decode_mfma_hd<HD>_w<tile waves>[_l]: max(4, tile waves) waves
+#define LLMRS_ATTN_MFMA(name, HD, TW, LOCAL)                                            \
   extern "C" __global__ __launch_bounds__(64 * (TW > 4 ? TW : 4)) void name(AttnArgs a) { \
-    attn_decode_mfma_impl<HD, TW>(a);                                                  \
+    attn_decode_mfma_impl<HD, TW, LOCAL>(a);                                           \
   }
-LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w1, 64, 1)
-LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w4, 64, 4)
-LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w8, 64, 8)
-LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w1, 128, 1)
-LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w4, 128, 4)
-LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w8, 128, 8)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w1, 64, 1, false)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w4, 64, 4, false)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w8, 64, 8, false)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w1, 128, 1, false)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w4, 128, 4, false)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w8, 128, 8, false)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w1_l, 64, 1, true)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w4_l, 64, 4, true)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd64_w8_l, 64, 8, true)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w1_l, 128, 1, true)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w4_l, 128, 4, true)
+LLMRS_ATTN_MFMA(attn_decode_mfma_hd128_w8_l, 128, 8, true)

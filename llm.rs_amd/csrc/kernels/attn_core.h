@@ -131,7 +131,7 @@ struct NoWait {
 // the streams merge through LDS before the partials are written, so a long
 // context needs S times fewer splits for the same parallelism (and the
 // combine reads S times fewer partials).
-template <int HD, bool KV16, bool DEV, int S = 1, class Wait = NoWait>
+template <int HD, bool KV16, bool DEV, int S = 1, bool LOCAL = false, class Wait = NoWait>
 __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, int pos, uint8_t* lds,
                                           const Wait& wait = Wait()) {
   typedef AttnCfg<HD, KV16> C;
@@ -142,10 +142,10 @@ __device__ __forceinline__ bool attn_item(const AttnArgs& a, int g, int split, i
 
   const int tid = threadIdx.x, lane = lane_id();
   const int stm = wave_id() / 4, wave = wave_id() % 4;  // stream, wave within the stream
-  // xcd_local: all splits of KV head g run on one XCD (the caller's mapping)
+  // LOCAL: all splits of KV head g run on one XCD (the caller's mapping)
   // and exchange partials through its L2; otherwise with device-scope
   // operations that bypass the per-XCD L2 copies.
-  const bool loc = a.xcd_local != 0;
+  constexpr bool loc = LOCAL;
   const int ltid = tid % 256;                           // thread within the stream
   float (*s_q)[HD] = (float (*)[HD])(lds + LY::Q);
   kv_t* s_k = (kv_t*)(lds + LY::K(stm));

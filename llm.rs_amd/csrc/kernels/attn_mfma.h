@@ -75,7 +75,7 @@ struct MfmaAttnLds {
 // `pos` (the new token's position) is read by the caller at kernel entry, so
 // it arrives through the scalar cache while the vector loads below are in
 // flight.
-template <int HD, int TW>
+template <int HD, int TW, bool LOCAL>
 __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8_t* lds) {
   constexpr int NS = HD / 32, NB = HD / 16, MID = HD / 2, TILE = kAttnTile;
   constexpr float kLog2e = 1.4426950408889634f;
@@ -85,9 +85,9 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   static_assert(TW == 1 || TW == 4 || TW == 8, "one, four or eight tile waves");
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int c = lane & 15, r = lane >> 4;  // MFMA column (query head of the group), lane group
-  // xcd_local: KV head = linear workgroup index % nkv, so with nkv = 8 all
+  // LOCAL: KV head = linear workgroup index % nkv, so with nkv = 8 all
   // splits of a head run on one XCD and exchange partials through its L2.
-  const bool loc = a.xcd_local != 0;
+  constexpr bool loc = LOCAL;
   const int lin = blockIdx.x + blockIdx.y * gridDim.x;
   const int g = loc ? lin % a.nkv : blockIdx.y, split = loc ? lin / a.nkv : blockIdx.x;
   const int n_rep = a.nq / a.nkv;
@@ -505,18 +505,17 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   const bool cthr = tid < nthr;
   const int ct = min(tid, nthr - 1), hr = ct / G, j = ct % G;
   const size_t obase = (size_t)(g * n_rep + hr) * ns, mbase = (size_t)(g * n_rep + hr) * ns2;
-  auto pld16 = [&](const float* base, int off) { return loc ? xcd_ld16(base, off) : dev_ld16(base, off); };
   float Mx = -INFINITY, Lx = 0.0f;  // split 0 holds position 0: Mx ends finite
   f32x4 Ox = {0.0f, 0.0f, 0.0f, 0.0f};
   if (cthr) {
     for (int s0 = 0; s0 < ns; s0 += CH) {
       dev_u32x4 mq[CH / 2], po[CH];
 #pragma unroll
-      for (int v2 = 0; v2 < CH / 2; ++v2)  // clamped: splits past nsplit get weight 0
-        mq[v2] = pld16(a.part_ml, (int)(8 * (mbase + min(s0 + 2 * v2, ns2 - 2))));
+      for (int v2 = 0; v2 < CH / 2; ++v2)  // past nsplit: zeros, weight 0
+        mq[v2] = part_ld16(a.part_ml, s0 + 2 * v2 < ns ? (int)(8 * (mbase + s0 + 2 * v2)) : kOobOff, loc);
 #pragma unroll
       for (int u = 0; u < CH; ++u)
-        po[u] = pld16(a.part_o, (int)(((obase + min(s0 + u, ns - 1)) * HD + 4 * j) * 4));
+        po[u] = part_ld16(a.part_o, s0 + u < ns ? (int)(((obase + s0 + u) * HD + 4 * j) * 4) : kOobOff, loc);
       float ms[CH], mc = -INFINITY;
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
