@@ -104,7 +104,9 @@ const char* wt_tag(int wt) {
 // Rows per wave-unit R and 64-block chunks per unit U follow the shape: U = 2
 // when the row splits into whole 128-block chunks, R = 2 for the narrow
 // (n <= 8192) projections so that more waves share them.  The SwiGLU tile is
-// 64 rows per workgroup; other kinds deal R-row groups to waves, capped at
+// 64 rows per workgroup (8-wave workgroups looping over the tiles, one per
+// CU, when the tiles outnumber the CUs); other kinds deal R-row groups to
+// waves, capped at
 // LLMRS_GEMV_WG_PER_CU (default 2, the best of 1/2/4/8 measured on the 8B
 // decode) workgroups per CU, beyond which waves loop.
 GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
@@ -123,6 +125,11 @@ GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
     R = 2;
     waves = 8;
   }
+  // SwiGLU with the RMSNorm prologue, more 64-row tiles than CUs: 8-wave
+  // workgroups, one per CU (LLMRS_GEMV_SILU_W8=0/1 forces either)
+  const char* es = std::getenv("LLMRS_GEMV_SILU_W8");
+  const bool silu_w8 = kind == "norm_silu" && (es && *es ? std::atoi(es) == 1 : n / 64 > num_cus);
+  if (silu_w8) waves = 8;
   // Workgroups per CU (measured on MI355X): 1 for the RMSNorm-prologue
   // store GEMV (Q|K|V: 8B 14 MB, 70B 47 MB) and for matrices under 24 MB -
   // fewer, longer-lived workgroups keep the activation loads from queueing
@@ -130,7 +137,7 @@ GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
   const double wbytes = (double)n * k * (wt == WT_Q8H ? 34.0 : wt == WT_Q4F ? 20.0 : 18.0) / 32.0;
   const char* ew = std::getenv("LLMRS_GEMV_WG_PER_CU");
   const bool store = kind == "norm_store" || kind == "nq_store";
-  const int per_cu = ew && *ew ? std::max(1, std::atoi(ew)) : (store || wbytes < 24e6 ? 1 : 2);
+  const int per_cu = ew && *ew ? std::max(1, std::atoi(ew)) : (store || silu_w8 || wbytes < 24e6 ? 1 : 2);
   const long cap = (long)std::max(1, num_cus) * per_cu;
   GemvPlan p;
   p.name = std::string("gemv_") + wt_tag(wt) + "_" + kind + "_r" + std::to_string(R) + "u" +
