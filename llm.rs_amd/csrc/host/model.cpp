@@ -48,6 +48,16 @@ int env_int(const char* name, int def) {
   const char* v = std::getenv(name);
   return (v && *v) ? std::atoi(v) : def;
 }
+std::string env_str(const char* name) {
+  const char* v = std::getenv(name);
+  return v ? std::string(v) : std::string();
+}
+
+// Batched decode runs its linear layers on the row-batched decode GEMV up to
+// this many sequences (8B shape, ms per step GEMV / skinny GEMM: B = 1 1.63 /
+// 2.73, 2 1.94 / 2.84, 4 2.66 / 3.04, 8 4.00 / 3.26); LLMRS_BATCH_GEMM=gemv,
+// skinny or prefill forces one path.
+constexpr int kBatchGemvMax = 4;
 
 }  // namespace
 
@@ -1684,9 +1694,14 @@ struct llmrs_batch {
   float *ad = nullptr, *ctx_d = nullptr, *m_d = nullptr, *part_o = nullptr, *part_ml = nullptr;
   int8_t *aq = nullptr, *ctx_q = nullptr, *m_q = nullptr;
   int *pos = nullptr, *tokens = nullptr, *gen = nullptr, *counters = nullptr;
-  // linear layers on the skinny GEMM (sgemm.hip; token tiles of 16, the
-  // activation codes in its operand order) or, beyond 64 sequences or for
-  // widths not a multiple of 128, on the prefill GEMM
+  // linear layers on the decode GEMV over all rows (gemv_*_q8b_*: one
+  // workgroup per row and weight slice, the rows' workgroups of a slice on
+  // one XCD so that the weights stream from HBM about once and the other rows
+  // read them from its L2; up to kBatchGemvMax sequences), on the skinny GEMM
+  // (sgemm.hip; token tiles of 16, the activation codes in its operand order)
+  // or, beyond 64 sequences or for widths not a multiple of 128, on the
+  // prefill GEMM
+  bool gemv = false;
   bool skinny = false;
   int layout = llmrs::kActNatural;
   // attention splits per sequence: the model's (planned for one sequence)
@@ -1721,7 +1736,12 @@ struct llmrs_batch {
 namespace {
 
 // Kernel name of a batched linear layer (epi: store, resid, silu).
-std::string batch_linear_kernel(const llmrs_batch* b, const char* epi) {
+GemvPlan batch_gemv_plan(const llmrs_batch* b, const char* epi, const DevLinear& W) {
+  return gemv_plan(b->m->wt, std::string("q8b_") + epi, W.n, W.k, ctx().num_cus);
+}
+
+std::string batch_linear_kernel(const llmrs_batch* b, const char* epi, const DevLinear& W) {
+  if (b->gemv) return batch_gemv_plan(b, epi, W).name;
   return b->skinny ? sgemm_kernel(b->m, epi, b->B, false) : gemm_kernel(b->m, epi);
 }
 
@@ -1736,10 +1756,26 @@ void enqueue_batch_step(llmrs_batch* b, Launcher& L) {
   // product's Q8_0 codes; work figure = the weight bytes.
   auto linear = [&](const char* epi, const DevLinear& W, const int8_t* xq, const float* xd, float* y,
                     const float* res, int8_t* yq, float* yd) {
-    const std::string name = batch_linear_kernel(b, epi);
+    const std::string name = batch_linear_kernel(b, epi, W);
     const bool silu = std::string(epi) == "silu";
     const double wb = linear_weight_bytes(m, W);
-    if (b->skinny) {
+    if (b->gemv) {
+      const GemvPlan p = batch_gemv_plan(b, epi, W);
+      GemvArgs g{};
+      g.wq = W.codes;
+      g.ws = W.scales;
+      g.n = W.n;
+      g.k = W.k;
+      g.xq = xq;
+      g.xd = xd;
+      g.y = y;
+      g.res = res;
+      g.yq = yq;
+      g.yd = yd;
+      g.batch_rows = B;
+      g.batch_nwg = (int)p.grid;
+      L(name, wb, dim3(8u * (unsigned)B * ((p.grid + 7) / 8)), dim3(p.threads), p.lds, g);
+    } else if (b->skinny) {
       SgemmArgs g{xq, xd, W.codes, W.scales, y, res, yq, yd, B, W.n, W.k, W.n, b->layout};
       const auto sh = sgemm_shape(epi, W.n, false);
       L(name, wb, sh.first, sh.second, 0, g);
@@ -1873,15 +1909,20 @@ int llmrs_batch_create(llmrs_model* m, int32_t batch, llmrs_batch** out) {
     b->host_pos.assign(B, 0);
     b->begun.assign(B, 0);
     const int qdim = c.n_heads * c.head_dim;
-    const char* bg = std::getenv("LLMRS_BATCH_GEMM");
-    b->skinny = batch <= 64 && c.hidden % 128 == 0 && c.ffn % 128 == 0 && qdim % 128 == 0 &&
-                !(bg && std::string(bg) == "prefill");
+    const std::string bg = env_str("LLMRS_BATCH_GEMM");  // gemv, skinny or prefill forces one
+    b->gemv = bg == "gemv" || (bg.empty() && batch <= kBatchGemvMax);
+    b->skinny = !b->gemv && batch <= 64 && c.hidden % 128 == 0 && c.ffn % 128 == 0 && qdim % 128 == 0 &&
+                bg != "prefill";
     b->layout = b->skinny ? llmrs::kActMfma : llmrs::kActNatural;
     b->nsplit = std::max(1, std::min(m->nsplit, (2 * ctx().num_cus + batch * c.n_kv_heads - 1) /
                                                      (batch * c.n_kv_heads)));
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));
     (void)kernel("argmax_batch", dim3(1024));
-    for (const char* epi : {"store", "resid", "silu"}) (void)kernel(batch_linear_kernel(b.get(), epi), dim3(256));
+    for (const char* epi : {"store", "resid", "silu"}) {
+      const DevLinear& W = std::string(epi) == "store" ? m->lm_head : std::string(epi) == "resid" ? m->layers[0].down
+                                                                                             : m->layers[0].gu;
+      (void)kernel(batch_linear_kernel(b.get(), epi, W), dim3(256));
+    }
     *out = b.release();
   });
 }

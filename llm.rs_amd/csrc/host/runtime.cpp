@@ -115,7 +115,8 @@ GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
   const char* eu = std::getenv("LLMRS_GEMV_U");
   if (eu && (std::atoi(eu) == 1 || std::atoi(eu) == 2)) U = std::atoi(eu);
   int R = 4;
-  if (kind == "norm_store" || kind == "q8_resid" || kind == "nq_store") {
+  if (kind == "norm_store" || kind == "q8_resid" || kind == "nq_store" || kind == "q8b_store" ||
+      kind == "q8b_resid") {
     R = 2;
     const char* er = std::getenv("LLMRS_GEMV_R");
     if (er && (std::atoi(er) == 2 || std::atoi(er) == 4)) R = std::atoi(er);
@@ -144,7 +145,7 @@ GemvPlan gemv_plan(int wt, const std::string& kind, int n, int k, int num_cus) {
            std::to_string(U) + (waves == 8 ? "_w8" : "");
   p.threads = 64 * waves;
   // tiled epilogues: whole 64-row SwiGLU tiles or 32-row next-norm tiles
-  const int tile = (kind == "norm_silu" || kind == "nq_silu") ? 64 : kind == "q8_nq" ? 32 : 0;
+  const int tile = (kind == "norm_silu" || kind == "nq_silu" || kind == "q8b_silu") ? 64 : kind == "q8_nq" ? 32 : 0;
   long wgs;
   if (tile) {
     wgs = (n + tile - 1) / tile;

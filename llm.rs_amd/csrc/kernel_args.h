@@ -33,6 +33,10 @@ struct GemvArgs {
   unsigned long long* ts;  // profiling: 4 stamps per workgroup (null = off)
   int8_t* probe_xq;      // [k] when set: workgroup 0 copies the Q8_0 activation codes of
   float* probe_xd;       // its prologue and [k/32] their scales here (test probes)
+  // Row-batched launches (gemv_*_b): batch_rows activation rows (PRO_Q8 codes
+  // [rows][k], scales [rows][k/32]; outputs at the row's stride) over
+  // batch_nwg workgroups per row.
+  int batch_rows, batch_nwg;
 };
 
 // Dynamic LDS of a decode GEMV (gemv_core.h): the quantised activation row

@@ -24,12 +24,35 @@ __device__ __forceinline__ void gemv_impl(const GemvArgs& a) {
                                                                false, smem, sh);
 }
 
+// Row-batched launch (batched decode): batch_rows rows of Q8_0 activation
+// codes over batch_nwg workgroups per row.  Workgroups are dealt to the 8 XCDs
+// by linear index mod 8, so the linear index is split as xcd + 8 * (row + rows
+// * (wg / 8)) with xcd = wg % 8: the rows' workgroups for one slice of the
+// weights run on one XCD, close together in dispatch order, and the weights
+// stream from HBM about once, the other rows reading them from that L2.
+template <int WT, int EPI, int R, int U>
+__device__ __forceinline__ void gemv_batch_impl(const GemvArgs& a) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ GemvShared sh;
+  const int L = blockIdx.x, xcd = L & 7, rest = L >> 3;
+  const int mrow = rest % a.batch_rows, wg = xcd + 8 * (rest / a.batch_rows);
+  if (wg >= a.batch_nwg) return;  // padding to whole groups of 8
+  UnitRegs<WT, R, U> ua, ub;
+  gemv_body<WT, PRO_Q8, EPI, R, U, false, 2>(a, mrow, wg, a.batch_nwg, ua, ub, false, smem, sh);
+}
+
+#define LLMRS_GEMV_B(name, WT, EPI, R, U)                                          \
+  extern "C" __global__ __launch_bounds__(kThreads) void name(GemvArgs a) {        \
+    gemv_batch_impl<WT, EPI, R, U>(a);                                             \
+  }
+
 #define LLMRS_GEMV(name, WT, PRO, EPI, R, U)                                       \
   extern "C" __global__ __launch_bounds__(kThreads) void name(GemvArgs a) {        \
     gemv_impl<WT, PRO, EPI, R, U>(a);                                              \
   }
 
-// Variant names: gemv_<weights>_<prologue>_<epilogue>_r<R>u<U>.
+// Variant names: gemv_<weights>_<prologue>_<epilogue>_r<R>u<U>; row-batched
+// gemv_<weights>_q8b_<epilogue>_r<R>u<U>.
 #define LLMRS_GEMV_FAMILY(tag, WT, U)                                                     \
   LLMRS_GEMV(gemv_##tag##_quant_store_r4u##U, WT, PRO_QUANT, EPI_STORE, 4, U)             \
   LLMRS_GEMV(gemv_##tag##_norm_store_r2u##U, WT, PRO_NORM, EPI_STORE, 2, U)               \
@@ -40,7 +63,10 @@ __device__ __forceinline__ void gemv_impl(const GemvArgs& a) {
   LLMRS_GEMV(gemv_##tag##_norm_argmax_r4u##U, WT, PRO_NORM, EPI_ARGMAX, 4, U)               \
   LLMRS_GEMV(gemv_##tag##_nq_store_r2u##U, WT, PRO_NQ, EPI_STORE, 2, U)                   \
   LLMRS_GEMV(gemv_##tag##_nq_silu_r4u##U, WT, PRO_NQ, EPI_SILU, 4, U)                     \
-  LLMRS_GEMV(gemv_##tag##_nq_argmax_r4u##U, WT, PRO_NQ, EPI_ARGMAX, 4, U)
+  LLMRS_GEMV(gemv_##tag##_nq_argmax_r4u##U, WT, PRO_NQ, EPI_ARGMAX, 4, U)                 \
+  LLMRS_GEMV_B(gemv_##tag##_q8b_store_r2u##U, WT, EPI_STORE, 2, U)                        \
+  LLMRS_GEMV_B(gemv_##tag##_q8b_resid_r2u##U, WT, EPI_RESID, 2, U)                        \
+  LLMRS_GEMV_B(gemv_##tag##_q8b_silu_r4u##U, WT, EPI_SILU, 4, U)
 
 LLMRS_GEMV_FAMILY(q4h, WT_Q4H, 1)
 LLMRS_GEMV_FAMILY(q4h, WT_Q4H, 2)

@@ -198,10 +198,11 @@ __device__ __forceinline__ void load_activation(const GemvArgs& a, int mrow, int
                                                 float* s_d, int* s_off, float* s_red) {
   const int k = a.k, nb = k >> 5, tid = threadIdx.x;
   if (PRO == PRO_Q8 || PRO == PRO_NQ) {
+    const int rb = mrow * nb;  // the row's first block (row-batched launches)
     float scale = 1.0f;
     if (PRO == PRO_NQ) {  // s from the per-block sums of squares
       float ss = 0.0f;
-      for (int b = tid; b < nb; b += kThreads) ss = ss + ld_act<DEV>(a.xss, b);
+      for (int b = tid; b < nb; b += kThreads) ss = ss + ld_act<DEV>(a.xss, rb + b);
       ss = wave_sum(ss);
       if (lane_id() == 0) s_red[wave_id()] = ss;
       __syncthreads();
@@ -213,18 +214,18 @@ __device__ __forceinline__ void load_activation(const GemvArgs& a, int mrow, int
     for (int b = tid; b < nb; b += kThreads) {
       i32x4 c0, c1;
       if (DEV) {
-        const dev_u32x4 u0 = dev_ld16(a.xq, 32 * b), u1 = dev_ld16(a.xq, 32 * b + 16);
+        const dev_u32x4 u0 = dev_ld16(a.xq, 32 * (rb + b)), u1 = dev_ld16(a.xq, 32 * (rb + b) + 16);
         c0 = i32x4{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w};
         c1 = i32x4{(int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
       } else {
-        const i32x4* src = (const i32x4*)(a.xq + 32 * b);
+        const i32x4* src = (const i32x4*)(a.xq + 32 * ((size_t)rb + b));
         c0 = src[0];
         c1 = src[1];
       }
       i32x4* dst = (i32x4*)(s_q + 32 * b);
       dst[0] = c0;
       dst[1] = c1;
-      s_d[b] = PRO == PRO_NQ ? ld_act<DEV>(a.xd, b) * scale : ld_act<DEV>(a.xd, b);
+      s_d[b] = PRO == PRO_NQ ? ld_act<DEV>(a.xd, rb + b) * scale : ld_act<DEV>(a.xd, rb + b);
       if (Q4) {
         int s = 0;
         s = dot4(c0.x, 0x01010101, s);
@@ -370,21 +371,22 @@ __device__ __forceinline__ void issue_activation(const GemvArgs& a, int mrow, Ac
   const int k = a.k, nb = k >> 5, tid = threadIdx.x;
   if (!act_in_regs<PRO>(k)) return;
   if (PRO == PRO_Q8 || PRO == PRO_NQ) {
-    if (PRO == PRO_NQ) r.ss = ld_act<DEV>(a.xss, min(tid, nb - 1));  // clamped; masked at use
+    const int rb = mrow * nb;  // the row's first block (row-batched launches)
+    if (PRO == PRO_NQ) r.ss = ld_act<DEV>(a.xss, rb + min(tid, nb - 1));  // clamped; masked at use
 #pragma unroll
     for (int i = 0; i < (PRO == PRO_NQ ? 1 : kQ8Blocks); ++i) {
       const int b = min(tid + kThreads * i, nb - 1);  // clamped; extra ones unused
       if (kThreads * i < nb) {
         if (DEV) {
-          const dev_u32x4 u0 = dev_ld16(a.xq, 32 * b), u1 = dev_ld16(a.xq, 32 * b + 16);
+          const dev_u32x4 u0 = dev_ld16(a.xq, 32 * (rb + b)), u1 = dev_ld16(a.xq, 32 * (rb + b) + 16);
           r.c0[i] = i32x4{(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w};
           r.c1[i] = i32x4{(int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
         } else {
-          const i32x4* src = (const i32x4*)(a.xq + 32 * b);
+          const i32x4* src = (const i32x4*)(a.xq + 32 * ((size_t)rb + b));
           r.c0[i] = src[0];
           r.c1[i] = src[1];
         }
-        r.d[i] = ld_act<DEV>(a.xd, b);
+        r.d[i] = ld_act<DEV>(a.xd, rb + b);
       }
     }
     return;
@@ -821,13 +823,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
         const int tile = wg + q * nwg;
         const float gv = s_out[q * kSiluTile + e], uv = s_out[q * kSiluTile + 32 + e];
         const float mv = (gv / (1.0f + expf(-gv))) * uv;
-        const int idx = tile * 32 + e;
+        const int idx = mrow * (a.n / 2) + tile * 32 + e;  // m row mrow (row-batched launches)
         if (a.y) st_act<DEV>(a.y, idx, mv);
         float d;
         const int qc = q8_group32(mv, &d);
         if (DEV) dev_st8(a.yq, idx, (int8_t)qc);
         else a.yq[idx] = (int8_t)qc;
-        if (e == 0) st_act<DEV>(a.yd, tile, d);
+        if (e == 0) st_act<DEV>(a.yd, mrow * (a.n / 64) + tile, d);
       }
     }
   } else if (EPI == EPI_NQ) {

@@ -199,6 +199,12 @@ __device__ __forceinline__ void run_groups(const SgemmArgs& a, int q0, int q1, i
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) acc[rt][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // Wave-uniform bounds (they derive from the wave index): the loop and its
+  // tail test become scalar branches, which the memory counter is tracked
+  // through; a per-lane (exec-mask) loop would make every iteration wait for
+  // all outstanding loads, ring included.
+  q0 = __builtin_amdgcn_readfirstlane(q0);
+  q1 = __builtin_amdgcn_readfirstlane(q1);
   if (q0 >= q1) return;
   Group<WT, TT, RT> ring[PF];
 #pragma unroll

@@ -28,8 +28,13 @@ def prompts(spec, B, seed=5):
     return [rng.integers(0, spec.vocab, int(rng.integers(1, 20))).astype(np.int32) for _ in range(B)]
 
 
+@pytest.mark.parametrize("mode", ["gemv", "skinny", "prefill"])
 @pytest.mark.parametrize("spec", SPECS, ids=lambda s: s.name)
-def test_batch_streams_vs_oracle(hip, orc, spec):
+def test_batch_streams_vs_oracle(hip, orc, spec, mode, monkeypatch):
+    """The three linear-layer paths: the row-batched decode GEMV (the
+    default up to 4 sequences), the skinny GEMM (up to 64) and the prefill
+    GEMM."""
+    monkeypatch.setenv("LLMRS_BATCH_GEMM", mode)
     w = syn.make_weights(spec)
     gm = hip.HipModel(spec.config(128))
     syn.load_model(gm, w)
