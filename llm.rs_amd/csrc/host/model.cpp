@@ -74,6 +74,7 @@ struct llmrs_model {
   float *x = nullptr, *h = nullptr, *qkv = nullptr, *ctxv = nullptr, *mf = nullptr;
   float *logits = nullptr, *ctx_d = nullptr, *m_d = nullptr, *part_o = nullptr, *part_ml = nullptr;
   float *part_val = nullptr, *rope_cos = nullptr, *rope_sin = nullptr, *trace = nullptr;
+  float* rope_now = nullptr;  // [hd]: the step position's RoPE row (embed_gather -> attention)
   int8_t *ctx_q = nullptr, *m_q = nullptr;
   // RMSNorm operands from the producers (gemv_core.h PRO_NQ): codes of x*w,
   // d' and sums of squares per block, of x (Q|K|V and lm_head input) and of
@@ -252,6 +253,11 @@ void enqueue_embed(llmrs_model* m, Launcher& L, const float* x_in, const float* 
     e.xss = m->x_ss;
   }
   e.x_in = x_in;
+  e.rope_cos = m->rope_cos;
+  e.rope_sin = m->rope_sin;
+  e.rope_now = m->rope_now;
+  e.rope_mid = m->c.head_dim / 2;
+  e.rope_rows = m->c.max_seq;  // rows of the RoPE tables
   L("embed_gather", (m->nq_x ? 9.25 : 8.0) * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
 }
 
@@ -388,6 +394,7 @@ void enqueue_attention(llmrs_model* m, Launcher& L, int li, unsigned long long* 
   a.vc = (uint8_t*)Lb.vc;
   a.rope_cos = m->rope_cos;
   a.rope_sin = m->rope_sin;
+  a.rope_now = m->rope_now;
   a.part_o = m->part_o;
   a.part_ml = m->part_ml;
   a.counters = m->counters + (size_t)li * nkv * llmrs::kTicketStride;
@@ -907,6 +914,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
       rope_table(0, c.max_seq, hd, c.rope_theta, cs.data(), sn.data());
       m->rope_cos = m->dalloc<float>(cs.size());
       m->rope_sin = m->dalloc<float>(sn.size());
+      m->rope_now = m->dalloc<float>(hd);
       LLMRS_HIP(hipMemcpyAsync(m->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, cx.stream));
       LLMRS_HIP(hipMemcpyAsync(m->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice, cx.stream));
     }
@@ -1692,6 +1700,7 @@ struct llmrs_batch {
   std::vector<void*> kc, vc;  // per layer: B caches back to back
   float *x = nullptr, *h = nullptr, *qkv = nullptr, *ctxv = nullptr, *logits = nullptr;
   float *ad = nullptr, *ctx_d = nullptr, *m_d = nullptr, *part_o = nullptr, *part_ml = nullptr;
+  float* rope_now = nullptr;  // [B][hd]: each sequence's RoPE row of the step
   int8_t *aq = nullptr, *ctx_q = nullptr, *m_q = nullptr;
   int *pos = nullptr, *tokens = nullptr, *gen = nullptr, *counters = nullptr;
   // linear layers on the decode GEMV over all rows (gemv_*_q8b_*: one
@@ -1785,7 +1794,7 @@ void enqueue_batch_step(llmrs_batch* b, Launcher& L) {
     }
   };
   EmbedArgs e{m->embed, b->tokens, b->pos, b->x, m->err, H, c.vocab, nullptr, nullptr, nullptr, nullptr, nullptr,
-              b->cap};
+              b->cap, m->rope_cos, m->rope_sin, b->rope_now, hd / 2, c.max_seq};
   L("embed_gather", 8.0 * H * B, dim3((unsigned)((H + 255) / 256), (unsigned)B), blk, 0, e);
   for (int li = 0; li < c.n_layers; ++li) {
     LayerBufs& Lb = m->layers[li];
@@ -1802,6 +1811,7 @@ void enqueue_batch_step(llmrs_batch* b, Launcher& L) {
       a.vc = b->vc[li];
       a.rope_cos = m->rope_cos;
       a.rope_sin = m->rope_sin;
+      a.rope_now = b->rope_now;
       a.part_o = b->part_o;
       a.part_ml = b->part_ml;
       a.counters = b->counters + (size_t)li * B * nkv * llmrs::kTicketStride;
@@ -1904,6 +1914,7 @@ int llmrs_batch_create(llmrs_model* m, int32_t batch, llmrs_batch** out) {
     b->part_ml = b->dalloc<float>(B * c.n_heads * llmrs::ml_stride(m->nsplit) * 2);
     b->counters = b->dalloc<int>((size_t)c.n_layers * B * c.n_kv_heads * llmrs::kTicketStride);
     b->pos = b->dalloc<int>(B);
+    b->rope_now = b->dalloc<float>((size_t)B * c.head_dim);
     b->tokens = b->dalloc<int>(B * b->cap);
     b->gen = b->dalloc<int>(B * b->cap);
     b->host_pos.assign(B, 0);

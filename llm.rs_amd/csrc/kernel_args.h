@@ -184,6 +184,9 @@ struct AttnArgs {
   float* ctx_d;            // [nq*hd/32]
   int max_seq, nq, nkv, nsplit;  // max_seq: cache rows per KV head (kv_rows)
   float scale;             // fl(1 / fl(sqrt(hd))), layer.rs:258
+  // [hd/2] cos then [hd/2] sin at the step's position, copied from the tables
+  // by embed_gather (matrix-core kernel; per sequence: + z * hd)
+  const float* rope_now;
   unsigned long long* ts;  // profiling: 8 stage timestamps per item (null = off)
   // Batched decode (grid.z = sequences): sequence z's qkv, position, partials,
   // tickets and ctx rows follow sequence 0's at their natural strides, its
@@ -243,6 +246,13 @@ struct EmbedArgs {
   // Batched decode (> 0): row y is sequence y, token tokens[y * batch_stride
   // + pos_ptr[y]]; 0: row y of a chunk, token tokens[*pos_ptr + y].
   int batch_stride;
+  // Decode steps: the RoPE row of the position (of sequence y: at y * 2 * rope_mid)
+  // copied to rope_now, so that the attention reads it without waiting for
+  // the position; null: none.
+  const float* rope_cos;
+  const float* rope_sin;
+  float* rope_now;
+  int rope_mid, rope_rows;
 };
 
 // Prefill GEMM (prefill.hip): Y[t][r] = sum_b isum_b(t, r) * (d_w[r,b] * d_a[t,b])

@@ -27,6 +27,7 @@ __device__ __forceinline__ AttnArgs sequence_args(const AttnArgs& a0) {
     a.ctx += z * qd;
     a.ctx_q += z * qd;
     a.ctx_d += z * qd / 32;
+    if (a.rope_now) a.rope_now += (size_t)z * HD;
     a.ts = nullptr;
   }
   return a;

@@ -143,15 +143,17 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   const bool col_on = c < n_rep;  // columns past the group stay zero
 
   // Operands of the query heads (B of S^T = K Q^T) and the score scale: q of
-  // query head g * n_rep + c, dims 32s + 8r + e (no position needed:
-  // requested first; `prefetch` runs next), then the RoPE tables at pos.
+  // query head g * n_rep + c, dims 32s + 8r + e, and the RoPE row of pos
+  // (neither needs the position: requested first; `prefetch` runs next).
   // The partner of dim d < hd/2 is d + hd/2, held by the same lane in step
   // s + NS/2.
   h16x8 qh[NS], ql[NS];
   float sl2;
+  // The RoPE row of pos (rope_now: copied by the step's embedding launch, so
+  // its loads need no position).
   auto load_rope = [&](float (&cs)[NS / 2][8], float (&sn)[NS / 2][8]) {
-    const float* rc = a.rope_cos + (size_t)pos * MID + 8 * r;
-    const float* rs = a.rope_sin + (size_t)pos * MID + 8 * r;
+    const float* rc = a.rope_now + 8 * r;
+    const float* rs = a.rope_now + MID + 8 * r;
 #pragma unroll
     for (int s = 0; s < NS / 2; ++s) {
       const f32x4 c0 = *(const f32x4*)(rc + 32 * s), c1 = *(const f32x4*)(rc + 32 * s + 4);
@@ -185,10 +187,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   auto q_prologue = [&](auto&& prefetch) {
     float qv[NS][8], cs[NS / 2][8], sn[NS / 2][8];
     load_row(qv, a.qkv + (size_t)(g * n_rep + min(c, n_rep - 1)) * HD + 8 * r);
+    load_rope(cs, sn);
     __builtin_amdgcn_sched_barrier(0);
     prefetch();
     __builtin_amdgcn_sched_barrier(0);
-    load_rope(cs, sn);
     rotate(qv, cs, sn);
     // Per-head power-of-two scale 2^ex: max |q| * 2^ex in [2^14, 2^15).
     float amax = 0.0f;
@@ -215,7 +217,8 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   };
   // The new row as operands: k rotated and in f16, per lane dims 32s + 8r +
   // e (for the K row of pos); v in f16, per lane dims 16b + c.  Its loads
-  // need no position; `owner` is only needed once they are back.
+  // (RoPE row included) need no position; `owner` is only needed once they
+  // are back.
   u32x4 knew[NS];
   uint16_t vnew[NB];
   auto row_prologue = [&](auto&& is_owner) {
@@ -224,8 +227,8 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
     const float* vr = a.qkv + (size_t)(a.nq + a.nkv) * HD + (size_t)g * HD + c;
 #pragma unroll
     for (int b = 0; b < NB; ++b) vraw[b] = vr[16 * b];
-    if (!is_owner()) return;
     load_rope(cs, sn);
+    if (!is_owner()) return;
 #pragma unroll
     for (int b = 0; b < NB; ++b) vnew[b] = f2h(vraw[b]);
     rotate(kv, cs, sn);

@@ -133,6 +133,14 @@ extern "C" __global__ __launch_bounds__(256) void matmul_t_f32(MatArgs g) {
 // 32-element block (one half-wave), Q8_0 codes of x*w with d' = amax/127
 // (cpu.rs:724-743) and the block's sum of x^2 (cpu.rs:381, summed per block).
 extern "C" __global__ __launch_bounds__(256) void embed_gather(EmbedArgs e) {
+  if (e.rope_now && blockIdx.x == 0 && (e.batch_stride || blockIdx.y == 0)) {
+    const int p = min(e.batch_stride ? e.pos_ptr[blockIdx.y] : *e.pos_ptr, e.rope_rows - 1);
+    float* dst = e.rope_now + (size_t)blockIdx.y * 2 * e.rope_mid;
+    for (int t = threadIdx.x; t < e.rope_mid; t += blockDim.x) {
+      dst[t] = e.rope_cos[(size_t)p * e.rope_mid + t];
+      dst[e.rope_mid + t] = e.rope_sin[(size_t)p * e.rope_mid + t];
+    }
+  }
   const float* row;
   if (e.x_in) {
     row = e.x_in;
