@@ -387,12 +387,21 @@ int llmrs_model_probe_prefill_layer(llmrs_model* m, int layer, size_t start_pos,
  * ready, unit loop done, end, input arrived, norm factor known, operand
  * quantised; attention, items (KV head, split) in head-major order:
  * start, projections loaded, first tile staged, tiles done, partials
- * written, ticket taken, splits combined), the XCC id and HW_ID.
- * Returns the count written. */
+ * written, ticket taken, splits combined), the XCC id and HW_ID.  Slot -3:
+ * the fused Q|K|V + attention launch (models that run it), 11 values per
+ * workgroup: the attention's with its rows stored and the KV head's rows
+ * all arrived after the start.  Returns the count written. */
 int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
                                int cap);
 /* Algorithmic weight bytes streamed per decode token (all linear weights). */
 double llmrs_model_weight_bytes(const llmrs_model* m);
+/* How a single-sequence decode step runs its attention (no reference
+ * counterpart; tests and the benchmark report it): out[0] splits per KV head
+ * of the standalone attention launch, out[1] its tile waves (f16 caches) or
+ * tile streams (f32), out[2] 1 when a KV head's splits exchange partials
+ * through one XCD's L2, out[3] 1 when the Q|K|V GEMV and the attention run
+ * as one launch, out[4] that launch's splits per KV head. */
+int llmrs_model_decode_plan(const llmrs_model* m, int32_t out[5]);
 
 /* ---- seeded synthetic inputs (benchmark and test data) ------------------ */
 /* Counter-based SplitMix64 generator keyed by (seed, tensor_id, index).

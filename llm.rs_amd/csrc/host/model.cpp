@@ -95,6 +95,11 @@ struct llmrs_model {
   // decode attention: the splits of a KV head on one XCD, exchanging
   // partials through its L2 (the attention kernels' _l variants)
   bool attn_local = false;
+  // decode: the Q|K|V GEMV and the attention as one launch (qkv_attn.hip)
+  // of fused_nsplit workgroups per KV head; attention partials are sized for
+  // max(nsplit, fused_nsplit) splits
+  bool fused_qkv = false;
+  int fused_nsplit = 0;
   size_t host_pos = 0;
   bool begun = false;
   hipGraph_t graph = nullptr;
@@ -411,6 +416,68 @@ void enqueue_attention(llmrs_model* m, Launcher& L, int li, unsigned long long* 
   L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(attn_threads(m)), 0, a);
 }
 
+// The Q|K|V GEMV and decode attention of layer li in one launch
+// (qkv_attn.hip): grid (fused_nsplit, nkv), KV head = linear index % nkv.
+// `probe_xq` / `probe_xd` (may be null) receive the GEMV prologue's operand.
+void enqueue_qkv_attention(llmrs_model* m, Launcher& L, int li, int8_t* probe_xq = nullptr,
+                           float* probe_xd = nullptr, unsigned long long* stamps = nullptr,
+                           unsigned long long* stamps_mid = nullptr) {
+  const llmrs_model_config& c = m->c;
+  const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
+  const int rows = (nq / nkv + 2) * hd;  // one KV head's q, k and v rows
+  LayerBufs& Lb = m->layers[li];
+  QkvAttnArgs f{};
+  GemvArgs& g = f.gemv;
+  g.wq = Lb.qkv.codes;
+  g.ws = Lb.qkv.scales;
+  g.n = rows;
+  g.k = H;
+  g.eps = c.rms_eps;
+  g.y = m->qkv;
+  g.probe_xq = probe_xq;
+  g.probe_xd = probe_xd;
+  double bytes = linear_weight_bytes(m, Lb.qkv) + 4.0 * m->qkv_rows;
+  if (m->nq_x) {
+    g.xq = m->x_q;
+    g.xd = m->x_d;
+    g.xss = m->x_ss;
+    bytes += 1.125 * H;
+  } else {
+    g.x = m->x;
+    g.norm_w = Lb.norm[0];
+    bytes += 8.0 * H;
+  }
+  AttnArgs& a = f.attn;
+  a.qkv = m->qkv;
+  a.pos_ptr = m->pos;
+  a.kc = (uint8_t*)Lb.kc;
+  a.vc = (uint8_t*)Lb.vc;
+  a.rope_cos = m->rope_cos;
+  a.rope_sin = m->rope_sin;
+  a.rope_now = m->rope_now;
+  a.part_o = m->part_o;
+  a.part_ml = m->part_ml;
+  a.counters = m->counters + (size_t)li * nkv * llmrs::kTicketStride;
+  a.ctx = m->ctxv;
+  a.ctx_q = m->ctx_q;
+  a.ctx_d = m->ctx_d;
+  a.max_seq = kv_rows(m);
+  a.nq = nq;
+  a.nkv = nkv;
+  a.nsplit = m->fused_nsplit;
+  a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
+  a.ts = stamps;
+  f.ts_mid = stamps_mid;
+  f.err = m->err;
+  f.spin_limit = 1 << 16;  // polls, each an L2 round trip: tens of ms at most
+  bytes += 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
+  const int U = (H / 32) % 128 == 0 ? 2 : 1;
+  const std::string name = std::string("qkv_attn_") + wt_tag(m->wt) + (m->nq_x ? "_nq" : "_norm") + "_hd" +
+                           std::to_string(hd) + "_u" + std::to_string(U);
+  const size_t lds = llmrs::gemv_lds_bytes(0, rows, H, 2, m->fused_nsplit, 4);
+  L(name, bytes, dim3((unsigned)m->fused_nsplit, (unsigned)nkv), dim3(256), lds, f);
+}
+
 void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden;
@@ -421,8 +488,12 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
     if (trace_dev)
       LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)li * H, m->x, H * sizeof(float),
                                hipMemcpyDeviceToDevice, L.s));
-    enqueue_linear(m, L, li, LLMRS_W_Q);
-    enqueue_attention(m, L, li);
+    if (m->fused_qkv) {
+      enqueue_qkv_attention(m, L, li);
+    } else {
+      enqueue_linear(m, L, li, LLMRS_W_Q);
+      enqueue_attention(m, L, li);
+    }
     enqueue_linear(m, L, li, LLMRS_W_O);
     enqueue_linear(m, L, li, LLMRS_W_GATE);
     enqueue_linear(m, L, li, LLMRS_W_DOWN);
@@ -729,6 +800,8 @@ void check_err(llmrs_model* m) {
     int zero = 0;
     LLMRS_HIP(hipMemcpyAsync(m->err, &zero, sizeof(int), hipMemcpyHostToDevice, ctx().stream));
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    if (e == 2)  // qkv_attn.hip: a workgroup stopped waiting for its KV head's projection rows
+      fail(LLMRS_E_HIP, "fused Q|K|V + attention launch: the wait for a KV head's rows timed out");
     fail(LLMRS_E_RANGE, "token id out of range [0, vocab)");
   }
 }
@@ -854,6 +927,31 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     // the XCD-local split exchange needs a head's workgroups on one XCD
     m->attn_local = nkv % 8 == 0 && env_int("LLMRS_ATTN_LOCAL", 1) == 1 &&
                     xcd_dealt_mod8((unsigned)m->nsplit, (unsigned)nkv);
+    // The fused Q|K|V + attention launch (qkv_attn.hip): f16 caches with the
+    // one-tile-wave attention and its XCD-local split exchange, 8 KV heads
+    // (one per XCD), one workgroup per CU that all fit at once, and the XCD
+    // dealing checked on its grid.  LLMRS_FUSED_QKV=0, or a split count set
+    // with LLMRS_ATTN_SPLITS, keeps the two launches.
+    {
+      const int fs = cx.num_cus / std::max(1, nkv);
+      const char* es = std::getenv("LLMRS_ATTN_SPLITS");
+      bool ok = env_int("LLMRS_FUSED_QKV", 1) == 1 && !(es && *es) && m->attn_local &&
+                c.kv_dtype == LLMRS_F16 && m->attn_waves == 1 &&
+                nkv == 8 && nq % nkv == 0 && nq / nkv <= 16 && (hd == 64 || hd == 128) && fs >= 1 &&
+                fs <= llmrs::kMfmaAttnMaxSplits && H % 32 == 0;
+      if (ok) {
+        const int U = (H / 32) % 128 == 0 ? 2 : 1;
+        const std::string name = std::string("qkv_attn_") + wt_tag(m->wt) + "_norm_hd" + std::to_string(hd) +
+                                 "_u" + std::to_string(U);
+        const size_t lds = llmrs::gemv_lds_bytes(0, (nq / nkv + 2) * hd, H, 2, fs, 4);
+        int per_cu = 0;
+        LLMRS_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel(name, dim3(256)), 256, lds));
+        ok = per_cu >= 1 && (long)per_cu * cx.num_cus >= (long)fs * nkv && xcd_dealt_mod8((unsigned)fs, (unsigned)nkv);
+      }
+      m->fused_qkv = ok;
+      m->fused_nsplit = ok ? fs : 0;
+    }
+    const int psplit = std::max(m->nsplit, m->fused_nsplit);  // attention partials per query head
     m->lm_grid = (int)gemv_plan(m->wt, "nq_argmax", c.vocab, H, cx.num_cus).grid;
     m->layers.resize(c.n_layers);
     for (auto& L : m->layers) {
@@ -894,8 +992,8 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     m->m_q = m->dalloc<int8_t>(F);
     m->m_d = m->dalloc<float>(F / 32);
     m->logits = m->dalloc<float>(c.vocab);
-    m->part_o = m->dalloc<float>((size_t)nq * m->nsplit * hd);
-    m->part_ml = m->dalloc<float>((size_t)nq * llmrs::ml_stride(m->nsplit) * 2);
+    m->part_o = m->dalloc<float>((size_t)nq * psplit * hd);
+    m->part_ml = m->dalloc<float>((size_t)nq * llmrs::ml_stride(psplit) * 2);
     const size_t nparts = (size_t)m->lm_grid;
     m->part_val = m->dalloc<float>(nparts);
     m->part_idx = m->dalloc<int>(nparts);
@@ -1447,19 +1545,29 @@ int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
     LLMRS_REQUIRE(m && m->begun && out, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
     LLMRS_REQUIRE(layer >= 0 && layer < m->c.n_layers, LLMRS_E_RANGE, "layer out of range");
     LLMRS_REQUIRE(m->host_pos + 1 <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
-    const unsigned nwg = slot == -2 ? (unsigned)(m->nsplit * m->c.n_kv_heads) : linear_grid(m, slot);
+    const bool fused = slot == -3;
+    LLMRS_REQUIRE(!fused || m->fused_qkv, LLMRS_E_INVALID, "slot -3: this model runs Q|K|V and attention apart");
+    const unsigned nwg = slot == -2   ? (unsigned)(m->nsplit * m->c.n_kv_heads)
+                         : fused      ? (unsigned)(m->fused_nsplit * m->c.n_kv_heads)
+                                      : linear_grid(m, slot);
+    const int per = fused ? 10 : 8;  // stamps per workgroup (the fused launch: 8 + rows stored, rows arrived)
     unsigned long long* ts = nullptr;
-    LLMRS_HIP(hipMalloc(&ts, (size_t)nwg * 8 * sizeof(unsigned long long)));
+    LLMRS_HIP(hipMalloc(&ts, (size_t)nwg * per * sizeof(unsigned long long)));
     hipStream_t s = ctx().stream;
-    std::vector<unsigned long long> h((size_t)nwg * 8);
+    std::vector<unsigned long long> h((size_t)nwg * per);
     try {
       LLMRS_HIP(hipMemsetAsync(ts, 0, h.size() * sizeof(unsigned long long), s));
       const llmrs_model_config& c = m->c;
       Launcher L{s};
       enqueue_embed(m, L, nullptr, m->layers[0].norm[0]);
       for (int li = 0; li < c.n_layers; ++li) {
-        enqueue_linear(m, L, li, LLMRS_W_Q, nullptr, nullptr, li == layer && slot == LLMRS_W_Q ? ts : nullptr);
-        enqueue_attention(m, L, li, li == layer && slot == -2 ? ts : nullptr);
+        if (m->fused_qkv && (fused || slot == LLMRS_W_O || slot == LLMRS_W_GATE || slot == LLMRS_W_DOWN)) {
+          const bool on = li == layer && fused;
+          enqueue_qkv_attention(m, L, li, nullptr, nullptr, on ? ts : nullptr, on ? ts + (size_t)nwg * 8 : nullptr);
+        } else {
+          enqueue_linear(m, L, li, LLMRS_W_Q, nullptr, nullptr, li == layer && slot == LLMRS_W_Q ? ts : nullptr);
+          enqueue_attention(m, L, li, li == layer && slot == -2 ? ts : nullptr);
+        }
         enqueue_linear(m, L, li, LLMRS_W_O, nullptr, nullptr, li == layer && slot == LLMRS_W_O ? ts : nullptr);
         enqueue_linear(m, L, li, LLMRS_W_GATE, nullptr, nullptr,
                        li == layer && slot == LLMRS_W_GATE ? ts : nullptr);
@@ -1477,12 +1585,19 @@ int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
     (void)hipFree(ts);
     m->host_pos += 1;
     // per workgroup: stamps 0-6 in us from the launch's earliest start (-1 =
-    // not recorded), then the XCC id and the HW_ID word
+    // not recorded), then the XCC id and the HW_ID word; the fused launch
+    // puts its rows-stored and rows-arrived stamps after stamp 0
     unsigned long long t0 = ~0ull;
     for (unsigned w = 0; w < nwg; ++w)
       if (h[8 * w]) t0 = std::min(t0, h[8 * w]);
-    for (unsigned w = 0; w < nwg && count + 9 <= cap; ++w) {
-      for (int i = 0; i < 7; ++i) out[count++] = h[8 * w + i] ? (double)(h[8 * w + i] - t0) / 100.0 : -1.0;
+    auto us = [&](unsigned long long v) { return v ? (double)(v - t0) / 100.0 : -1.0; };
+    for (unsigned w = 0; w < nwg && count + (fused ? 11 : 9) <= cap; ++w) {
+      out[count++] = us(h[8 * w]);
+      if (fused) {
+        out[count++] = us(h[(size_t)nwg * 8 + 2 * w]);
+        out[count++] = us(h[(size_t)nwg * 8 + 2 * w + 1]);
+      }
+      for (int i = 1; i < 7; ++i) out[count++] = us(h[8 * w + i]);
       out[count++] = (double)(h[8 * w + 7] >> 32);
       out[count++] = (double)(h[8 * w + 7] & 0xFFFFFFFFull);
     }
@@ -1494,6 +1609,17 @@ int llmrs_model_get_config(const llmrs_model* m, llmrs_model_config* out) {
   return guard([&] {
     LLMRS_REQUIRE(m && out, LLMRS_E_INVALID, "null argument");
     *out = m->c;
+  });
+}
+
+int llmrs_model_decode_plan(const llmrs_model* m, int32_t out[5]) {
+  return guard([&] {
+    LLMRS_REQUIRE(m && out, LLMRS_E_INVALID, "null argument");
+    out[0] = m->nsplit;
+    out[1] = m->c.kv_dtype == LLMRS_F16 ? m->attn_waves : m->attn_streams;
+    out[2] = m->attn_local ? 1 : 0;
+    out[3] = m->fused_qkv ? 1 : 0;
+    out[4] = m->fused_nsplit;
   });
 }
 
@@ -1564,12 +1690,19 @@ int llmrs_model_probe_decode_layer(llmrs_model* m, int layer, size_t pos, const 
     Launcher L{s};
     auto sync = [&] { LLMRS_HIP(hipStreamSynchronize(s)); };
     enqueue_embed(m, L, xin, m->layers[layer].norm[0]);
-    enqueue_linear(m, L, layer, LLMRS_W_Q, xq, xd);
-    probe_copy(out->qkv, m->qkv, m->qkv_rows * sizeof(float));
-    probe_copy(out->xq, xq, H);
-    probe_copy(out->xd, xd, H / 32 * sizeof(float));
-    sync();
-    enqueue_attention(m, L, layer);
+    if (m->fused_qkv) {  // one launch: projection rows and attention
+      enqueue_qkv_attention(m, L, layer, xq, xd);
+      probe_copy(out->qkv, m->qkv, m->qkv_rows * sizeof(float));
+      probe_copy(out->xq, xq, H);
+      probe_copy(out->xd, xd, H / 32 * sizeof(float));
+    } else {
+      enqueue_linear(m, L, layer, LLMRS_W_Q, xq, xd);
+      probe_copy(out->qkv, m->qkv, m->qkv_rows * sizeof(float));
+      probe_copy(out->xq, xq, H);
+      probe_copy(out->xd, xd, H / 32 * sizeof(float));
+      sync();
+      enqueue_attention(m, L, layer);
+    }
     probe_copy(out->ctx, m->ctxv, qd * sizeof(float));
     probe_copy(out->ctx_q, m->ctx_q, qd);
     probe_copy(out->ctx_d, m->ctx_d, qd / 32 * sizeof(float));
@@ -1587,6 +1720,7 @@ int llmrs_model_probe_decode_layer(llmrs_model* m, int layer, size_t pos, const 
     enqueue_linear(m, L, layer, LLMRS_W_DOWN);
     probe_copy(out->out, m->x, H * sizeof(float));
     sync();
+    check_err(m);
     m->begun = false;
   });
 }

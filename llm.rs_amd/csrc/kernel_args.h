@@ -37,6 +37,11 @@ struct GemvArgs {
   // [rows][k], scales [rows][k/32]; outputs at the row's stride) over
   // batch_nwg workgroups per row.
   int batch_rows, batch_nwg;
+  // Mapped rows (the fused Q|K|V + attention launch): logical row r < n
+  // stands for physical row map_b0 + r (r < map_n1), map_b1 + r - map_n1
+  // (r < map_n1 + map_n2) or map_b2 + r - map_n1 - map_n2, in the weights
+  // and in y: one KV head's query, key and value rows as one range.
+  int map_n1, map_n2, map_b0, map_b1, map_b2;
 };
 
 // Dynamic LDS of a decode GEMV (gemv_core.h): the quantised activation row
@@ -320,6 +325,25 @@ struct PrefillAttnArgs {
 // ints between the split tickets of two KV heads: each head's counter has a
 // 256-byte line of its own, so the heads' atomics do not queue on one line.
 constexpr int kTicketStride = 64;
+// Word of a KV head's counter line that counts the workgroups of the fused
+// Q|K|V + attention launch whose projection rows are stored (qkv_attn.hip);
+// reset with the ticket by the workgroup that combines the splits.
+constexpr int kArrivalWord = 32;
+
+// Fused Q|K|V GEMV + decode attention (qkv_attn.hip): nkv * nsplit
+// workgroups of 256 threads, one per CU, KV head = linear index % nkv so a
+// head's workgroups share one XCD; each first computes its share of the
+// head's query, key and value rows (gemv, mapped rows), then its attention
+// split.  err: set to 2 when a wait for the head's rows exceeds its spin limit.
+struct QkvAttnArgs {
+  GemvArgs gemv;         // wq/ws/k/x/norm_w/eps or xq/xd/xss, y = attn.qkv
+  AttnArgs attn;
+  int* err;
+  int spin_limit;        // polls of the arrival count before giving up
+  // profiling (with attn.ts): per item, the rows stored and the head's rows
+  // all arrived (null = off)
+  unsigned long long* ts_mid;
+};
 
 // Positions per decode-attention tile (attn_core.h, attn_mfma.h).
 constexpr int kAttnTile = 32;

@@ -74,9 +74,11 @@ struct MfmaAttnLds {
 
 // `pos` (the new token's position) is read by the caller at kernel entry, so
 // it arrives through the scalar cache while the vector loads below are in
-// flight.
-template <int HD, int TW, bool LOCAL>
-__device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8_t* lds) {
+// flight.  `mid()` runs on every wave after the first tile's loads are
+// requested and before q, k and v are read: the fused Q|K|V launch computes
+// them there (qkv_attn.hip); the standalone kernels pass a no-op.
+template <int HD, int TW, bool LOCAL, class Mid>
+__device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8_t* lds, Mid&& mid) {
   constexpr int NS = HD / 32, NB = HD / 16, MID = HD / 2, TILE = kAttnTile;
   constexpr float kLog2e = 1.4426950408889634f;
   constexpr float kP = 16384.0f;  // p is scaled by 2^14 before its hi/lo split
@@ -184,10 +186,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
         x[s + NS / 2][e] = re * sn[s][e] + im * cs[s][e];
       }
   };
-  auto q_prologue = [&](auto&& prefetch) {
-    float qv[NS][8], cs[NS / 2][8], sn[NS / 2][8];
+  // cs, sn: the RoPE row, requested by the caller (before mid()).
+  auto q_prologue = [&](auto&& prefetch, const float (&cs)[NS / 2][8], const float (&sn)[NS / 2][8]) {
+    float qv[NS][8];
     load_row(qv, a.qkv + (size_t)(g * n_rep + min(c, n_rep - 1)) * HD + 8 * r);
-    load_rope(cs, sn);
     __builtin_amdgcn_sched_barrier(0);
     prefetch();
     __builtin_amdgcn_sched_barrier(0);
@@ -221,13 +223,12 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   // are back.
   u32x4 knew[NS];
   uint16_t vnew[NB];
-  auto row_prologue = [&](auto&& is_owner) {
-    float kv[NS][8], vraw[NB], cs[NS / 2][8], sn[NS / 2][8];
+  auto row_prologue = [&](auto&& is_owner, const float (&cs)[NS / 2][8], const float (&sn)[NS / 2][8]) {
+    float kv[NS][8], vraw[NB];
     load_row(kv, a.qkv + (size_t)a.nq * HD + (size_t)g * HD + 8 * r);
     const float* vr = a.qkv + (size_t)(a.nq + a.nkv) * HD + (size_t)g * HD + c;
 #pragma unroll
     for (int b = 0; b < NB; ++b) vraw[b] = vr[16 * b];
-    load_rope(cs, sn);
     if (!is_owner()) return;
 #pragma unroll
     for (int b = 0; b < NB; ++b) vnew[b] = f2h(vraw[b]);
@@ -262,10 +263,12 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
     // Waves 1 (q) and 2 (new row) prepare the operands while wave 0 waits
     // for its tile.
     uint8_t* qop = lds + LY::QOP;
-    if (wave == 0) {
-      prefetch_first();
-    } else if (wave == 1) {
-      q_prologue([] {});
+    float cs[NS / 2][8], sn[NS / 2][8];  // the RoPE row (waves 1 and 2)
+    if (wave == 0) prefetch_first();
+    else if (wave <= 2) load_rope(cs, sn);
+    mid();
+    if (wave == 1) {
+      q_prologue([] {}, cs, sn);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         *(h16x8*)(qop + ((s * 2) * 64 + lane) * 16) = qh[s];
@@ -273,7 +276,7 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
       }
       if (r == 0) ((float*)(lds + LY::SL2))[c] = sl2;
     } else if (wave == 2) {
-      row_prologue([&] { return own_split; });
+      row_prologue([&] { return own_split; }, cs, sn);
       if (own_split) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) *(u32x4*)(lds + LY::KNEW + (s * 64 + lane) * 16) = knew[s];
@@ -301,9 +304,12 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
       append();  // after the handoff: the barrier does not wait for these stores
     }
   } else {
-    q_prologue(prefetch_first);
+    mid();
+    float cs[NS / 2][8], sn[NS / 2][8];
+    load_rope(cs, sn);
+    q_prologue(prefetch_first, cs, sn);
     if (owner) {
-      row_prologue([] { return true; });
+      row_prologue([] { return true; }, cs, sn);
       append();
     }
   }
@@ -505,25 +511,28 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   // been summed to the new max.  Only these threads issue loads.
   constexpr int G = HD / 4, CH = 32;
   const int nthr = n_rep * G, ns = a.nsplit, ns2 = ml_stride(ns);
+  // Splits past the context hold no tile (split s starts at tile s): their
+  // partials (max -inf, sum 0) would add exact zeros, so they are not read.
+  const int nlive = min(ns, (T + TILE - 1) / TILE);
   const bool cthr = tid < nthr;
   const int ct = min(tid, nthr - 1), hr = ct / G, j = ct % G;
   const size_t obase = (size_t)(g * n_rep + hr) * ns, mbase = (size_t)(g * n_rep + hr) * ns2;
   float Mx = -INFINITY, Lx = 0.0f;  // split 0 holds position 0: Mx ends finite
   f32x4 Ox = {0.0f, 0.0f, 0.0f, 0.0f};
   if (cthr) {
-    for (int s0 = 0; s0 < ns; s0 += CH) {
+    for (int s0 = 0; s0 < nlive; s0 += CH) {
       dev_u32x4 mq[CH / 2], po[CH];
 #pragma unroll
-      for (int v2 = 0; v2 < CH / 2; ++v2)  // past nsplit: zeros, weight 0
-        mq[v2] = part_ld16(a.part_ml, s0 + 2 * v2 < ns ? (int)(8 * (mbase + s0 + 2 * v2)) : kOobOff, loc);
+      for (int v2 = 0; v2 < CH / 2; ++v2)  // past the live splits: zeros, weight 0
+        mq[v2] = part_ld16(a.part_ml, s0 + 2 * v2 < nlive ? (int)(8 * (mbase + s0 + 2 * v2)) : kOobOff, loc);
 #pragma unroll
       for (int u = 0; u < CH; ++u)
-        po[u] = part_ld16(a.part_o, s0 + u < ns ? (int)(((obase + s0 + u) * HD + 4 * j) * 4) : kOobOff, loc);
+        po[u] = part_ld16(a.part_o, s0 + u < nlive ? (int)(((obase + s0 + u) * HD + 4 * j) * 4) : kOobOff, loc);
       float ms[CH], mc = -INFINITY;
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
         const unsigned mbits = u & 1 ? mq[u / 2].z : mq[u / 2].x;
-        ms[u] = s0 + u < ns ? __uint_as_float(mbits) : -INFINITY;
+        ms[u] = s0 + u < nlive ? __uint_as_float(mbits) : -INFINITY;
         mc = fmaxf(mc, ms[u]);
       }
       const float mn = fmaxf(Mx, mc);
@@ -564,9 +573,14 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
     *(unsigned*)(a.ctx_q + act_offset((int)e, a.ctx_layout)) = codes;  // aligned runs of 4 stay together
     if ((j & 7) == 0) a.ctx_d[e / 32] = bmax == 0.0f ? 0.0f : d;
   }
-  if (tid == 0) {
-    if (loc) xcd_stu(a.counters, 4 * g * kTicketStride, 0u);
-    else dev_stu(a.counters, 4 * g * kTicketStride, 0u);
+  if (tid == 0) {  // every split has taken its ticket: the ticket and the arrival count restart
+    if (loc) {
+      xcd_stu(a.counters, 4 * g * kTicketStride, 0u);
+      xcd_stu(a.counters, 4 * (g * kTicketStride + kArrivalWord), 0u);
+    } else {
+      dev_stu(a.counters, 4 * g * kTicketStride, 0u);
+      dev_stu(a.counters, 4 * (g * kTicketStride + kArrivalWord), 0u);
+    }
   }
   stamp(6);
   flush_stamps();

@@ -113,6 +113,7 @@ _SIGS = {
     "llmrs_model_profile_prefill": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_char_p,
                                                C.c_void_p, C.c_void_p, C.c_int]),
     "llmrs_model_weight_bytes": (C.c_double, [C.c_void_p]),
+    "llmrs_model_decode_plan": (C.c_int, [C.c_void_p, C.c_void_p]),
     "llmrs_model_profile_stamps": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int]),
     "llmrs_model_probe_decode_layer": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t, C.c_void_p, C.c_void_p]),
     "llmrs_model_probe_head": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -580,10 +581,17 @@ class HipModel:
         quantised [us], XCC id, HW_ID)."""
         out = np.zeros(cap, np.float64)
         n = _check(lib().llmrs_model_profile_stamps(self._h, layer, slot, _ptr(out), cap))
-        return out[:n].reshape(-1, 9)
+        return out[:n].reshape(-1, 11 if slot == -3 else 9)
 
     def weight_bytes(self) -> float:
         return float(lib().llmrs_model_weight_bytes(self._h))
+
+    def decode_plan(self) -> dict:
+        """How a decode step runs its attention (llmrs_model_decode_plan)."""
+        out = np.zeros(5, np.int32)
+        _check(lib().llmrs_model_decode_plan(self._h, _ptr(out)))
+        return {"nsplit": int(out[0]), "tile_waves": int(out[1]), "xcd_local": bool(out[2]),
+                "fused_qkv": bool(out[3]), "fused_nsplit": int(out[4])}
 
 
 # -- seeded synthetic inputs (llmrs_synth_*) ------------------------------
