@@ -349,7 +349,7 @@ struct QkvAttnArgs {
 constexpr int kAttnTile = 32;
 constexpr int attn_tile(bool) { return kAttnTile; }
 // Splits of one matrix-core decode-attention launch at most (its combine
-// stages every split's (max, sum) of the group in LDS).
+// holds split s's (max, sum) in lane s of a wave).
 constexpr int kMfmaAttnMaxSplits = 64;
 // (max, sum) pairs per query head in the decode-attention partials: the
 // split count rounded up to even, so the matrix-core combine reads them two

@@ -503,75 +503,84 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
     return;
   }
 
-  // Combine: thread t < n_rep * G (G = hd/4 consecutive lanes per head) owns
-  // head g * n_rep + t / G, dims 4 (t % G) .. +3.  32 splits per round, in
-  // one batch of loads: the (max, sum) of the head's splits, two per 16-byte
-  // load (the same addresses across the head's lanes), then the thread's
-  // slice of each split's partial O; rounds after the first rescale what has
-  // been summed to the new max.  Only these threads issue loads.
-  constexpr int G = HD / 4, CH = 32;
-  const int nthr = n_rep * G, ns = a.nsplit, ns2 = ml_stride(ns);
-  // Splits past the context hold no tile (split s starts at tile s): their
-  // partials (max -inf, sum 0) would add exact zeros, so they are not read.
+  // Combine: wave w takes query heads w, w + nw, ... of the group.  Lane s
+  // loads split s's (max, sum) (one 8-byte load), so the maximum M is one
+  // wave reduction and lane s forms the split's weight 2^(m_s - M); the
+  // weights and sums reach every lane by readlane.  Lane l owns dims
+  // DPL*l .. DPL*l + DPL-1 and adds the live splits' partial O in split
+  // order, loaded in batches of 8, 16 or 32 (the live split count rounded
+  // up; loads past it read zero with no memory access).  Splits past the
+  // context hold no tile (split s starts at tile s): their partials (max
+  // -inf, sum 0) would add exact zeros, so they are not read.
+  constexpr int DPL = HD / 64;  // dims per lane
+  const int nw = (int)(blockDim.x / LLMRS_WAVE), ns = a.nsplit, ns2 = ml_stride(ns);
   const int nlive = min(ns, (T + TILE - 1) / TILE);
-  const bool cthr = tid < nthr;
-  const int ct = min(tid, nthr - 1), hr = ct / G, j = ct % G;
-  const size_t obase = (size_t)(g * n_rep + hr) * ns, mbase = (size_t)(g * n_rep + hr) * ns2;
-  float Mx = -INFINITY, Lx = 0.0f;  // split 0 holds position 0: Mx ends finite
-  f32x4 Ox = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (cthr) {
-    for (int s0 = 0; s0 < nlive; s0 += CH) {
-      dev_u32x4 mq[CH / 2], po[CH];
+  for (int hr = wave; hr < n_rep; hr += nw) {
+    const size_t obase = (size_t)(g * n_rep + hr) * ns, mbase = (size_t)(g * n_rep + hr) * ns2;
+    const dev_u32x2 mlv = part_ld8(a.part_ml, lane < nlive ? (int)(8 * (mbase + lane)) : kOobOff, loc);
+    const float ms = lane < nlive ? __uint_as_float(mlv.x) : -INFINITY;  // split 0 holds position 0
+    const float ls = lane < nlive ? __uint_as_float(mlv.y) : 0.0f;
+    const float M = wave_max(ms);
+    const float wl = __builtin_amdgcn_exp2f(ms - M);  // 0 past the live splits
+    float Lx = 0.0f, Ox[DPL];
 #pragma unroll
-      for (int v2 = 0; v2 < CH / 2; ++v2)  // past the live splits: zeros, weight 0
-        mq[v2] = part_ld16(a.part_ml, s0 + 2 * v2 < nlive ? (int)(8 * (mbase + s0 + 2 * v2)) : kOobOff, loc);
+    for (int i = 0; i < DPL; ++i) Ox[i] = 0.0f;
+    auto batch = [&](auto nl_tag, int s0) {
+      constexpr int NL = decltype(nl_tag)::value;
+      float po[NL][DPL];
 #pragma unroll
-      for (int u = 0; u < CH; ++u)
-        po[u] = part_ld16(a.part_o, s0 + u < nlive ? (int)(((obase + s0 + u) * HD + 4 * j) * 4) : kOobOff, loc);
-      float ms[CH], mc = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const unsigned mbits = u & 1 ? mq[u / 2].z : mq[u / 2].x;
-        ms[u] = s0 + u < nlive ? __uint_as_float(mbits) : -INFINITY;
-        mc = fmaxf(mc, ms[u]);
+      for (int u = 0; u < NL; ++u) {
+        const int off = s0 + u < nlive ? (int)(((obase + s0 + u) * HD + DPL * lane) * 4) : kOobOff;
+        if constexpr (DPL == 2) {
+          const dev_u32x2 v = part_ld8(a.part_o, off, loc);
+          po[u][0] = __uint_as_float(v.x);
+          po[u][1] = __uint_as_float(v.y);
+        } else {
+          po[u][0] = __uint_as_float(part_ld4(a.part_o, off, loc));
+        }
       }
-      const float mn = fmaxf(Mx, mc);
-      const float corr = Mx == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(Mx - mn);
-      Lx = Lx * corr;
-      Ox = Ox * corr;
 #pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const float w = __builtin_amdgcn_exp2f(ms[u] - mn);  // masked and empty splits: exp2(-inf) = 0
-        Lx = Lx + w * __uint_as_float(u & 1 ? mq[u / 2].w : mq[u / 2].y);
-        Ox = Ox + __builtin_bit_cast(f32x4, po[u]) * w;
+      for (int u = 0; u < NL; ++u) {  // cpu.rs:395-423 order: sum, then weighted values
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), s0 + u));
+        const float l = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ls), s0 + u));
+        Lx = Lx + w * l;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) Ox[i] = Ox[i] + po[u][i] * w;
       }
-      Mx = mn;
+    };
+    for (int s0 = 0; s0 < nlive; s0 += 32) {
+      const int left = nlive - s0;
+      if (left <= 8) batch(std::integral_constant<int, 8>{}, s0);
+      else if (left <= 16) batch(std::integral_constant<int, 16>{}, s0);
+      else batch(std::integral_constant<int, 32>{}, s0);
     }
-  }
-  // ctx as f32 and as Q8_0: a 32-dim block is 8 consecutive threads.
-  float v[4];
-  float bmax = 0.0f;
+    // ctx as f32 and as Q8_0: a 32-dim block is 32 / DPL lanes.
+    float v[DPL], bmax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[i] = Ox[i] / Lx;
-    bmax = fmaxf(bmax, fabsf(v[i]));
-  }
-  bmax = fmaxf(bmax, dpp_c<0xB1>(bmax));   // quad_perm [1,0,3,2]
-  bmax = fmaxf(bmax, dpp_c<0x4E>(bmax));   // quad_perm [2,3,0,1]
-  bmax = fmaxf(bmax, dpp_c<0x141>(bmax));  // row_half_mirror: the 8-lane group
-  const float d = bmax / 127.0f;
-  const float inv = bmax == 0.0f ? 0.0f : 1.0f / d;
-  if (cthr) {
-    const size_t e = (size_t)(g * n_rep + hr) * HD + 4 * j;
+    for (int i = 0; i < DPL; ++i) {
+      v[i] = Ox[i] / Lx;
+      bmax = fmaxf(bmax, fabsf(v[i]));
+    }
+    bmax = max16(bmax);
+    if (DPL == 1) bmax = fmaxf(bmax, xor16(bmax));
+    const float d = bmax / 127.0f;
+    const float inv = bmax == 0.0f ? 0.0f : 1.0f / d;
+    const size_t e = (size_t)(g * n_rep + hr) * HD + DPL * lane;
     unsigned codes = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < DPL; ++i) {
       const int q8 = bmax == 0.0f ? 0 : q8_code(v[i], inv);
       codes |= ((unsigned)q8 & 0xFFu) << (8 * i);
     }
-    *(f32x4*)(a.ctx + e) = f32x4{v[0], v[1], v[2], v[3]};
-    *(unsigned*)(a.ctx_q + act_offset((int)e, a.ctx_layout)) = codes;  // aligned runs of 4 stay together
-    if ((j & 7) == 0) a.ctx_d[e / 32] = bmax == 0.0f ? 0.0f : d;
+    const int qo = act_offset((int)e, a.ctx_layout);  // aligned runs of 4 stay together
+    if constexpr (DPL == 2) {
+      *(float2*)(a.ctx + e) = make_float2(v[0], v[1]);
+      *(uint16_t*)(a.ctx_q + qo) = (uint16_t)codes;
+    } else {
+      a.ctx[e] = v[0];
+      a.ctx_q[qo] = (int8_t)codes;
+    }
+    if (lane % (32 / DPL) == 0) a.ctx_d[e / 32] = bmax == 0.0f ? 0.0f : d;
   }
   if (tid == 0) {  // every split has taken its ticket: the ticket and the arrival count restart
     if (loc) {

@@ -182,6 +182,14 @@ __device__ __forceinline__ dev_u32x4 part_ld16(const void* base, int byte_off, b
   return local ? __builtin_amdgcn_raw_buffer_load_b128(oob_rsrc(base), byte_off, 0, kSc0)
                : __builtin_amdgcn_raw_buffer_load_b128(oob_rsrc(base), byte_off, 0, kSc1);
 }
+__device__ __forceinline__ dev_u32x2 part_ld8(const void* base, int byte_off, bool local) {
+  return local ? __builtin_amdgcn_raw_buffer_load_b64(oob_rsrc(base), byte_off, 0, kSc0)
+               : __builtin_amdgcn_raw_buffer_load_b64(oob_rsrc(base), byte_off, 0, kSc1);
+}
+__device__ __forceinline__ unsigned part_ld4(const void* base, int byte_off, bool local) {
+  return local ? __builtin_amdgcn_raw_buffer_load_b32(oob_rsrc(base), byte_off, 0, kSc0)
+               : __builtin_amdgcn_raw_buffer_load_b32(oob_rsrc(base), byte_off, 0, kSc1);
+}
 __device__ __forceinline__ dev_u32x2 xcd_ld8(const void* base, int byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b64(dev_rsrc(base), byte_off, 0, kSc0);
 }
