@@ -517,16 +517,17 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   const int nlive = min(ns, (T + TILE - 1) / TILE);
   for (int hr = wave; hr < n_rep; hr += nw) {
     const size_t obase = (size_t)(g * n_rep + hr) * ns, mbase = (size_t)(g * n_rep + hr) * ns2;
-    const dev_u32x2 mlv = part_ld8(a.part_ml, lane < nlive ? (int)(8 * (mbase + lane)) : kOobOff, loc);
-    const float ms = lane < nlive ? __uint_as_float(mlv.x) : -INFINITY;  // split 0 holds position 0
-    const float ls = lane < nlive ? __uint_as_float(mlv.y) : 0.0f;
-    const float M = wave_max(ms);
-    const float wl = __builtin_amdgcn_exp2f(ms - M);  // 0 past the live splits
     float Lx = 0.0f, Ox[DPL];
 #pragma unroll
     for (int i = 0; i < DPL; ++i) Ox[i] = 0.0f;
-    auto batch = [&](auto nl_tag, int s0) {
+    float ls = 0.0f, wl = 0.0f;
+    // NL partial-O loads from split s0 (zeros past the live splits), issued
+    // together; `ml` also requests the (max, sum) loads with the first batch
+    // and forms the weights, so nothing waits between the two requests.
+    auto batch = [&](auto nl_tag, int s0, bool ml) {
       constexpr int NL = decltype(nl_tag)::value;
+      dev_u32x2 mlv = {0u, 0u};
+      if (ml) mlv = part_ld8(a.part_ml, lane < nlive ? (int)(8 * (mbase + lane)) : kOobOff, loc);
       float po[NL][DPL];
 #pragma unroll
       for (int u = 0; u < NL; ++u) {
@@ -539,6 +540,12 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
           po[u][0] = __uint_as_float(part_ld4(a.part_o, off, loc));
         }
       }
+      if (ml) {
+        const float ms = lane < nlive ? __uint_as_float(mlv.x) : -INFINITY;  // split 0 holds position 0
+        ls = lane < nlive ? __uint_as_float(mlv.y) : 0.0f;
+        const float M = wave_max(ms);
+        wl = __builtin_amdgcn_exp2f(ms - M);  // 0 past the live splits
+      }
 #pragma unroll
       for (int u = 0; u < NL; ++u) {  // cpu.rs:395-423 order: sum, then weighted values
         const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), s0 + u));
@@ -548,12 +555,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
         for (int i = 0; i < DPL; ++i) Ox[i] = Ox[i] + po[u][i] * w;
       }
     };
-    for (int s0 = 0; s0 < nlive; s0 += 32) {
-      const int left = nlive - s0;
-      if (left <= 8) batch(std::integral_constant<int, 8>{}, s0);
-      else if (left <= 16) batch(std::integral_constant<int, 16>{}, s0);
-      else batch(std::integral_constant<int, 32>{}, s0);
-    }
+    if (nlive <= 8) batch(std::integral_constant<int, 8>{}, 0, true);
+    else if (nlive <= 16) batch(std::integral_constant<int, 16>{}, 0, true);
+    else batch(std::integral_constant<int, 32>{}, 0, true);
+    for (int s0 = 32; s0 < nlive; s0 += 32) batch(std::integral_constant<int, 32>{}, s0, false);
     // ctx as f32 and as Q8_0: a 32-dim block is 32 / DPL lanes.
     float v[DPL], bmax = 0.0f;
 #pragma unroll
