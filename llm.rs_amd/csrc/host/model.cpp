@@ -927,15 +927,17 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     // the XCD-local split exchange needs a head's workgroups on one XCD
     m->attn_local = nkv % 8 == 0 && env_int("LLMRS_ATTN_LOCAL", 1) == 1 &&
                     xcd_dealt_mod8((unsigned)m->nsplit, (unsigned)nkv);
-    // The fused Q|K|V + attention launch (qkv_attn.hip): f16 caches with the
-    // one-tile-wave attention and its XCD-local split exchange, 8 KV heads
-    // (one per XCD), one workgroup per CU that all fit at once, and the XCD
-    // dealing checked on its grid.  LLMRS_FUSED_QKV=0, or a split count set
-    // with LLMRS_ATTN_SPLITS, keeps the two launches.
+    // The fused Q|K|V + attention launch (qkv_attn.hip), with
+    // LLMRS_FUSED_QKV=1: f16 caches with the one-tile-wave attention and its
+    // XCD-local split exchange, 8 KV heads (one per XCD), one workgroup per
+    // CU that all fit at once, and the XCD dealing checked on its grid; a
+    // split count set with LLMRS_ATTN_SPLITS keeps the two launches.  Off by
+    // default: measured on one MI355X it runs as fast as the two launches
+    // (8B 725.4 vs 726.1, 1B Q8_0 1904.8 vs 1898.7 tok/s).
     {
       const int fs = cx.num_cus / std::max(1, nkv);
       const char* es = std::getenv("LLMRS_ATTN_SPLITS");
-      bool ok = env_int("LLMRS_FUSED_QKV", 1) == 1 && !(es && *es) && m->attn_local &&
+      bool ok = env_int("LLMRS_FUSED_QKV", 0) == 1 && !(es && *es) && m->attn_local &&
                 c.kv_dtype == LLMRS_F16 && m->attn_waves == 1 &&
                 nkv == 8 && nq % nkv == 0 && nq / nkv <= 16 && (hd == 64 || hd == 128) && fs >= 1 &&
                 fs <= llmrs::kMfmaAttnMaxSplits && H % 32 == 0;

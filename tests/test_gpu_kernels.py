@@ -282,8 +282,8 @@ def test_fused_qkv_attention(hip, orc, weight, head_dim, n_heads, pos, monkeypat
                     seed=51 + head_dim + n_heads)
     got = {}
     for mode in ("fused", "split"):
+        monkeypatch.setenv("LLMRS_FUSED_QKV", "1" if mode == "fused" else "0")
         if mode == "split":
-            monkeypatch.setenv("LLMRS_FUSED_QKV", "0")
             monkeypatch.setenv("LLMRS_ATTN_SPLITS", str(fs))
         gm, om, w = layer_models(hip, orc, spec, pos + 6)
         plan = gm.decode_plan()
