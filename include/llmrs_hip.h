@@ -135,7 +135,7 @@ int llmrs_copy_from(const llmrs_tensor* t, llmrs_tensor** out);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc): Backend::matmul_transposed (backend.rs:24) into `out`,
+ * forbid hipMalloc): the product of llmrs_matmul_transposed written into `out`,
  * an f32 tensor of shape [m, n] the caller allocated beforehand, with no
  * device allocation.  Quantised b with m > 1 stages each row's Q8_0 codes in
  * a fixed per-device scratch of 16 MiB: m*k + 4*m*k/32 bytes must fit
@@ -143,6 +143,11 @@ int llmrs_copy_from(const llmrs_tensor* t, llmrs_tensor** out);
  * scratch.  Results equal llmrs_matmul_transposed's. */
 int llmrs_matmul_transposed_noalloc(const llmrs_tensor* a, const llmrs_tensor* b,
                                     llmrs_tensor* out);
+
+/* Test probe (no reference counterpart): the device exponential used by
+ * SiLU and softmax on n host values, out[i] = expf(x[i]) as the reference's
+ * host libm (glibc) computes it, bit for bit. */
+int llmrs_probe_expf(const float* x, size_t n, float* out);
 
 /* ---- resident decode model (no trait counterpart) ----------------------- */
 /* Mirrors LlamaConfig (src/core/config.rs:3-17) plus what the reference
@@ -273,6 +278,18 @@ typedef struct {
  * llmrs_model_generate then fills the rest of out_tokens with -1.
  * Vocabularies up to 262144 ids. */
 int llmrs_model_set_sampling(llmrs_model* m, const llmrs_sampling* s);
+/* Reference-order decode (on != 0; no trait counterpart; environment
+ * LLMRS_EXACT=1 sets it at llmrs_model_create).  Single-sequence steps then
+ * run kernels that add every f32 sum in the reference CPU path's order
+ * (x86-64 build): the RMSNorm sum of squares (cpu.rs:381-389), each GEMV
+ * output's block loop (kernel_avx2, cpu.rs:903-938), the attention's dots,
+ * softmax sum and P.V (layer.rs:257-299, cpu.rs:395-423), and glibc's expf
+ * for SiLU and softmax (layer.rs:75-79).  For the same weights and tokens,
+ * logits and greedy tokens then equal the reference's bit for bit.  Prompts
+ * run one position per step (the reference's batched prompt gives the same
+ * values row by row).  Costs about 2x the fast step per token; needs max_seq
+ * <= 16384.  Batches (llmrs_batch_*) always use the fast kernels. */
+int llmrs_model_set_exact(llmrs_model* m, int on);
 /* Tokens produced since llmrs_model_begin (the first comes from the prompt's
  * last position) and whether an end-of-sequence id stopped the run. */
 int llmrs_model_produced(llmrs_model* m, size_t* n, int32_t* stopped);
@@ -387,10 +404,8 @@ int llmrs_model_probe_prefill_layer(llmrs_model* m, int layer, size_t start_pos,
  * ready, unit loop done, end, input arrived, norm factor known, operand
  * quantised; attention, items (KV head, split) in head-major order:
  * start, projections loaded, first tile staged, tiles done, partials
- * written, ticket taken, splits combined), the XCC id and HW_ID.  Slot -3:
- * the fused Q|K|V + attention launch (models that run it), 11 values per
- * workgroup: the attention's with its rows stored and the KV head's rows
- * all arrived after the start.  Returns the count written. */
+ * written, ticket taken, splits combined), the XCC id and HW_ID.  Returns
+ * the count written. */
 int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
                                int cap);
 /* Algorithmic weight bytes streamed per decode token (all linear weights). */
@@ -399,9 +414,9 @@ double llmrs_model_weight_bytes(const llmrs_model* m);
  * counterpart; tests and the benchmark report it): out[0] splits per KV head
  * of the standalone attention launch, out[1] its tile waves (f16 caches) or
  * tile streams (f32), out[2] 1 when a KV head's splits exchange partials
- * through one XCD's L2, out[3] 1 when the Q|K|V GEMV and the attention run
- * as one launch, out[4] that launch's splits per KV head. */
-int llmrs_model_decode_plan(const llmrs_model* m, int32_t out[5]);
+ * through one XCD's L2, out[3] 1 when the model runs the reference-order
+ * kernels (LLMRS_EXACT, see llmrs_model_create). */
+int llmrs_model_decode_plan(const llmrs_model* m, int32_t out[4]);
 
 /* ---- seeded synthetic inputs (benchmark and test data) ------------------ */
 /* Counter-based SplitMix64 generator keyed by (seed, tensor_id, index).

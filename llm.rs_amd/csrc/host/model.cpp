@@ -95,11 +95,9 @@ struct llmrs_model {
   // decode attention: the splits of a KV head on one XCD, exchanging
   // partials through its L2 (the attention kernels' _l variants)
   bool attn_local = false;
-  // decode: the Q|K|V GEMV and the attention as one launch (qkv_attn.hip)
-  // of fused_nsplit workgroups per KV head; attention partials are sized for
-  // max(nsplit, fused_nsplit) splits
-  bool fused_qkv = false;
-  int fused_nsplit = 0;
+  // single-sequence steps on the reference-order kernels (exact.hip)
+  bool exact = false;
+  float* ex_gu = nullptr;  // [2 ffn] gate|up rows of the exact step
   size_t host_pos = 0;
   bool begun = false;
   hipGraph_t graph = nullptr;
@@ -416,69 +414,13 @@ void enqueue_attention(llmrs_model* m, Launcher& L, int li, unsigned long long* 
   L(attn_kernel(m), kvb, dim3((unsigned)m->nsplit, (unsigned)nkv), dim3(attn_threads(m)), 0, a);
 }
 
-// The Q|K|V GEMV and decode attention of layer li in one launch
-// (qkv_attn.hip): grid (fused_nsplit, nkv), KV head = linear index % nkv.
-// `probe_xq` / `probe_xd` (may be null) receive the GEMV prologue's operand.
-void enqueue_qkv_attention(llmrs_model* m, Launcher& L, int li, int8_t* probe_xq = nullptr,
-                           float* probe_xd = nullptr, unsigned long long* stamps = nullptr,
-                           unsigned long long* stamps_mid = nullptr) {
-  const llmrs_model_config& c = m->c;
-  const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads;
-  const int rows = (nq / nkv + 2) * hd;  // one KV head's q, k and v rows
-  LayerBufs& Lb = m->layers[li];
-  QkvAttnArgs f{};
-  GemvArgs& g = f.gemv;
-  g.wq = Lb.qkv.codes;
-  g.ws = Lb.qkv.scales;
-  g.n = rows;
-  g.k = H;
-  g.eps = c.rms_eps;
-  g.y = m->qkv;
-  g.probe_xq = probe_xq;
-  g.probe_xd = probe_xd;
-  double bytes = linear_weight_bytes(m, Lb.qkv) + 4.0 * m->qkv_rows;
-  if (m->nq_x) {
-    g.xq = m->x_q;
-    g.xd = m->x_d;
-    g.xss = m->x_ss;
-    bytes += 1.125 * H;
-  } else {
-    g.x = m->x;
-    g.norm_w = Lb.norm[0];
-    bytes += 8.0 * H;
-  }
-  AttnArgs& a = f.attn;
-  a.qkv = m->qkv;
-  a.pos_ptr = m->pos;
-  a.kc = (uint8_t*)Lb.kc;
-  a.vc = (uint8_t*)Lb.vc;
-  a.rope_cos = m->rope_cos;
-  a.rope_sin = m->rope_sin;
-  a.rope_now = m->rope_now;
-  a.part_o = m->part_o;
-  a.part_ml = m->part_ml;
-  a.counters = m->counters + (size_t)li * nkv * llmrs::kTicketStride;
-  a.ctx = m->ctxv;
-  a.ctx_q = m->ctx_q;
-  a.ctx_d = m->ctx_d;
-  a.max_seq = kv_rows(m);
-  a.nq = nq;
-  a.nkv = nkv;
-  a.nsplit = m->fused_nsplit;
-  a.scale = 1.0f / std::sqrt((float)hd);  // layer.rs:258
-  a.ts = stamps;
-  f.ts_mid = stamps_mid;
-  f.err = m->err;
-  f.spin_limit = 1 << 16;  // polls, each an L2 round trip: tens of ms at most
-  bytes += 2.0 * nkv * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
-  const int U = (H / 32) % 128 == 0 ? 2 : 1;
-  const std::string name = std::string("qkv_attn_") + wt_tag(m->wt) + (m->nq_x ? "_nq" : "_norm") + "_hd" +
-                           std::to_string(hd) + "_u" + std::to_string(U);
-  const size_t lds = llmrs::gemv_lds_bytes(0, rows, H, 2, m->fused_nsplit, 4);
-  L(name, bytes, dim3((unsigned)m->fused_nsplit, (unsigned)nkv), dim3(256), lds, f);
-}
+void enqueue_exact_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev);
 
 void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
+  if (m->exact) {
+    enqueue_exact_step(m, L, write_logits, trace_dev);
+    return;
+  }
   const llmrs_model_config& c = m->c;
   const int H = c.hidden;
 
@@ -488,12 +430,8 @@ void enqueue_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_d
     if (trace_dev)
       LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)li * H, m->x, H * sizeof(float),
                                hipMemcpyDeviceToDevice, L.s));
-    if (m->fused_qkv) {
-      enqueue_qkv_attention(m, L, li);
-    } else {
-      enqueue_linear(m, L, li, LLMRS_W_Q);
-      enqueue_attention(m, L, li);
-    }
+    enqueue_linear(m, L, li, LLMRS_W_Q);
+    enqueue_attention(m, L, li);
     enqueue_linear(m, L, li, LLMRS_W_O);
     enqueue_linear(m, L, li, LLMRS_W_GATE);
     enqueue_linear(m, L, li, LLMRS_W_DOWN);
@@ -551,6 +489,153 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
   }
   ArgmaxFinalArgs f{m->part_val, m->part_idx, m->lm_grid, m->pos, m->n_prompt, m->tokens, m->gen, m->cap};
   L("argmax_final", 8.0 * m->lm_grid, dim3(1), dim3(256), 0, f);
+}
+
+// ---- the decode step in the reference's operation order (exact.hip) --------
+// Eight launches per layer: RMSNorm + Q8_0, Q|K|V GEMV, attention, O GEMV +
+// residual, RMSNorm + Q8_0, gate|up GEMV, SwiGLU + Q8_0, down GEMV +
+// residual; then the final RMSNorm, the lm_head GEMV with argmax partials and
+// argmax_final (or the sampler).  Every sum runs in the reference's order,
+// so each value equals the reference CPU path's (x86-64 build) bit for bit.
+
+// Cache positions the exact attention keeps in LDS (scores, then
+// probabilities): 64 KB.
+constexpr int kExactMaxRows = 16384;
+
+// Workgroups of an exact GEMV over n rows (four rows, one per wave, at a time).
+unsigned exact_gemv_grid(int n, int cap) { return (unsigned)std::max(1, std::min((n + 3) / 4, cap)); }
+
+void exact_norm(llmrs_model* m, Launcher& L, const float* x, const float* w, int8_t* xq, float* xd,
+                float* y = nullptr) {
+  const int H = m->c.hidden;
+  ExactNormArgs a{x, w, xq, xd, y, H, m->c.rms_eps};
+  L("exact_norm_q8", 9.125 * H, dim3(1), dim3(256), (size_t)H * 4, a);
+}
+
+void exact_linear(llmrs_model* m, Launcher& L, const DevLinear& W, const char* epi, const int8_t* xq,
+                  const float* xd, float* y, const float* res) {
+  ExactGemvArgs a{W.codes, W.scales, xq, xd, y, res, nullptr, nullptr, W.n, W.k};
+  const unsigned grid = exact_gemv_grid(W.n, 8 * ctx().num_cus);
+  L(std::string("exact_gemv_") + wt_tag(m->wt) + "_" + epi,
+    linear_weight_bytes(m, W) + 1.125 * W.k + (res ? 8.0 : 4.0) * W.n, dim3(grid), dim3(256), 0, a);
+}
+
+void exact_attention(llmrs_model* m, Launcher& L, int li) {
+  const llmrs_model_config& c = m->c;
+  const int hd = c.head_dim;
+  LayerBufs& Lb = m->layers[li];
+  ExactAttnArgs a{m->qkv, m->pos, Lb.kc, Lb.vc, m->rope_cos, m->rope_sin, m->ctxv, m->ctx_q, m->ctx_d,
+                  kv_rows(m), c.n_heads, c.n_kv_heads, 1.0f / std::sqrt((float)hd)};  // layer.rs:258
+  const std::string name = "exact_attn_hd" + std::to_string(hd) + (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32");
+  const double kvb = 2.0 * c.n_kv_heads * (double)(m->host_pos + 1) * hd * kv_elem_bytes(m);
+  L(name, kvb, dim3((unsigned)c.n_heads), dim3(256), (size_t)kv_rows(m) * 4, a);
+}
+
+// `after(stage)` (may be empty) runs after stage s of the layer has been
+// enqueued: 0 norm, 1 Q|K|V, 2 attention, 3 O, 4 norm, 5 gate|up, 6 SwiGLU,
+// 7 down.
+void enqueue_exact_layer(llmrs_model* m, Launcher& L, int li, const std::function<void(int)>& after = {}) {
+  LayerBufs& Lb = m->layers[li];
+  auto done = [&](int s) {
+    if (after) after(s);
+  };
+  exact_norm(m, L, m->x, Lb.norm[0], m->x_q, m->x_d);                      // layer.rs:378
+  done(0);
+  exact_linear(m, L, Lb.qkv, "store", m->x_q, m->x_d, m->qkv, nullptr);    // layer.rs:177-179
+  done(1);
+  exact_attention(m, L, li);                                               // layer.rs:216-326
+  done(2);
+  exact_linear(m, L, Lb.o, "resid", m->ctx_q, m->ctx_d, m->h, m->x);      // layer.rs:332,386
+  done(3);
+  exact_norm(m, L, m->h, Lb.norm[1], m->h_q, m->h_d);                      // layer.rs:393
+  done(4);
+  exact_linear(m, L, Lb.gu, "store", m->h_q, m->h_d, m->ex_gu, nullptr);   // layer.rs:40
+  done(5);
+  {  // layer.rs:75-79
+    const int F = m->c.ffn;
+    ExactSiluArgs a{m->ex_gu, m->m_q, m->m_d, m->mf, F};
+    L("exact_silu_q8", 13.125 * F, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, a);
+  }
+  done(6);
+  exact_linear(m, L, Lb.down, "resid", m->m_q, m->m_d, m->x, m->h);       // layer.rs:93-96,403
+  done(7);
+}
+
+// Final RMSNorm, lm_head with argmax partials, then argmax_final or the
+// sampler (model.rs:39-47, main.rs:185-190).
+void enqueue_exact_head(llmrs_model* m, Launcher& L, bool write_logits) {
+  const llmrs_model_config& c = m->c;
+  exact_norm(m, L, m->x, m->final_norm, m->x_q, m->x_d);
+  const unsigned grid = exact_gemv_grid(c.vocab, m->lm_grid);
+  ExactGemvArgs a{m->lm_head.codes, m->lm_head.scales, m->x_q, m->x_d,
+                  write_logits || m->sampling ? m->logits : nullptr, nullptr, m->part_val, m->part_idx,
+                  c.vocab, c.hidden};
+  L(std::string("exact_gemv_") + wt_tag(m->wt) + "_argmax", linear_weight_bytes(m, m->lm_head) + 1.125 * c.hidden,
+    dim3(grid), dim3(256), 0, a);
+  if (m->sampling) {
+    SampleArgs s = sample_args(m->samp, c.vocab);
+    s.logits = m->logits;
+    s.probs = m->probs;
+    s.st = m->samp_state;
+    s.pos = m->pos;
+    s.n_prompt = m->n_prompt;
+    s.tokens = m->tokens;
+    s.gen = m->gen;
+    s.cap = m->cap;
+    s.eos = m->eos;
+    s.stopped = m->stopped;
+    enqueue_sample(L, s);
+    return;
+  }
+  ArgmaxFinalArgs f{m->part_val, m->part_idx, (int)grid, m->pos, m->n_prompt, m->tokens, m->gen, m->cap};
+  L("argmax_final", 8.0 * grid, dim3(1), dim3(256), 0, f);
+}
+
+void enqueue_exact_step(llmrs_model* m, Launcher& L, bool write_logits, float* trace_dev) {
+  const llmrs_model_config& c = m->c;
+  const int H = c.hidden;
+  EmbedArgs e{};  // x = E[token at the device position] (main.rs:159-167)
+  e.table = m->embed;
+  e.tokens = m->tokens;
+  e.pos_ptr = m->pos;
+  e.x = m->x;
+  e.err = m->err;
+  e.hidden = H;
+  e.vocab = c.vocab;
+  L("embed_gather", 8.0 * H, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, e);
+  for (int li = 0; li < c.n_layers; ++li) {
+    if (trace_dev)
+      LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)li * H, m->x, H * sizeof(float), hipMemcpyDeviceToDevice, L.s));
+    enqueue_exact_layer(m, L, li);
+  }
+  if (trace_dev)
+    LLMRS_HIP(hipMemcpyAsync(trace_dev + (size_t)c.n_layers * H, m->x, H * sizeof(float),
+                             hipMemcpyDeviceToDevice, L.s));
+  enqueue_exact_head(m, L, write_logits);
+}
+
+// Switches a model between the fast and the reference-order step; the first
+// switch to the latter allocates its gate|up buffer and resolves its kernels.
+void set_exact(llmrs_model* m, bool on) {
+  if (on) {
+    const llmrs_model_config& c = m->c;
+    LLMRS_REQUIRE(kv_rows(m) <= kExactMaxRows, LLMRS_E_INVALID,
+                  "the reference-order step supports max_seq up to " + std::to_string(kExactMaxRows));
+    if (!m->ex_gu) m->ex_gu = m->dalloc<float>((size_t)2 * c.ffn);
+    for (const char* epi : {"store", "resid", "argmax"}) (void)kernel(std::string("exact_gemv_") + wt_tag(m->wt) + "_" + epi);
+    (void)kernel("exact_norm_q8");
+    (void)kernel("exact_silu_q8");
+    (void)kernel("exact_attn_hd" + std::to_string(c.head_dim) + (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32"));
+    LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+  }
+  if (m->exact != on) {  // the captured step changes
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+    m->graph_failed = false;
+  }
+  m->exact = on;
 }
 
 // Batched prompt processing (prefill).  The reference runs the whole prompt
@@ -800,8 +885,6 @@ void check_err(llmrs_model* m) {
     int zero = 0;
     LLMRS_HIP(hipMemcpyAsync(m->err, &zero, sizeof(int), hipMemcpyHostToDevice, ctx().stream));
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));
-    if (e == 2)  // qkv_attn.hip: a workgroup stopped waiting for its KV head's projection rows
-      fail(LLMRS_E_HIP, "fused Q|K|V + attention launch: the wait for a KV head's rows timed out");
     fail(LLMRS_E_RANGE, "token id out of range [0, vocab)");
   }
 }
@@ -927,33 +1010,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     // the XCD-local split exchange needs a head's workgroups on one XCD
     m->attn_local = nkv % 8 == 0 && env_int("LLMRS_ATTN_LOCAL", 1) == 1 &&
                     xcd_dealt_mod8((unsigned)m->nsplit, (unsigned)nkv);
-    // The fused Q|K|V + attention launch (qkv_attn.hip), with
-    // LLMRS_FUSED_QKV=1: f16 caches with the one-tile-wave attention and its
-    // XCD-local split exchange, 8 KV heads (one per XCD), one workgroup per
-    // CU that all fit at once, and the XCD dealing checked on its grid; a
-    // split count set with LLMRS_ATTN_SPLITS keeps the two launches.  Off by
-    // default: measured on one MI355X it runs as fast as the two launches
-    // (8B 725.4 vs 726.1, 1B Q8_0 1904.8 vs 1898.7 tok/s).
-    {
-      const int fs = cx.num_cus / std::max(1, nkv);
-      const char* es = std::getenv("LLMRS_ATTN_SPLITS");
-      bool ok = env_int("LLMRS_FUSED_QKV", 0) == 1 && !(es && *es) && m->attn_local &&
-                c.kv_dtype == LLMRS_F16 && m->attn_waves == 1 &&
-                nkv == 8 && nq % nkv == 0 && nq / nkv <= 16 && (hd == 64 || hd == 128) && fs >= 1 &&
-                fs <= llmrs::kMfmaAttnMaxSplits && H % 32 == 0;
-      if (ok) {
-        const int U = (H / 32) % 128 == 0 ? 2 : 1;
-        const std::string name = std::string("qkv_attn_") + wt_tag(m->wt) + "_norm_hd" + std::to_string(hd) +
-                                 "_u" + std::to_string(U);
-        const size_t lds = llmrs::gemv_lds_bytes(0, (nq / nkv + 2) * hd, H, 2, fs, 4);
-        int per_cu = 0;
-        LLMRS_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel(name, dim3(256)), 256, lds));
-        ok = per_cu >= 1 && (long)per_cu * cx.num_cus >= (long)fs * nkv && xcd_dealt_mod8((unsigned)fs, (unsigned)nkv);
-      }
-      m->fused_qkv = ok;
-      m->fused_nsplit = ok ? fs : 0;
-    }
-    const int psplit = std::max(m->nsplit, m->fused_nsplit);  // attention partials per query head
+    const int psplit = m->nsplit;  // attention partials per query head
     m->lm_grid = (int)gemv_plan(m->wt, "nq_argmax", c.vocab, H, cx.num_cus).grid;
     m->layers.resize(c.n_layers);
     for (auto& L : m->layers) {
@@ -1031,6 +1088,7 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
     for (const char* k : {"sample_prep", "sample_probs", "sample_refine", "sample_pick"})
       (void)kernel(k, dim3(llmrs::kSampleThreads));
     (void)kernel(attn_kernel(m.get()), dim3(attn_threads(m.get())));
+    if (env_int("LLMRS_EXACT", 0) == 1) set_exact(m.get(), true);
     *out = m.release();
   });
 }
@@ -1250,7 +1308,7 @@ int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n, size_t 
     const size_t H = m->c.hidden, L = m->c.n_layers;
     upload_tokens(m, start_pos, tokens, n);
     hipStream_t s = ctx().stream;
-    const bool batched = n > 1 && prefill_enabled();
+    const bool batched = n > 1 && prefill_enabled() && !m->exact;
     if (batched)
       run_prefill(m, start_pos, n, INT_MAX, logits != nullptr, trace);
     else
@@ -1284,7 +1342,7 @@ int llmrs_model_begin_at(llmrs_model* m, const int32_t* prompt, size_t n_prompt,
     upload_tokens(m, start_pos, prompt, n_prompt);
     set_state(m, start_pos, (int)end);
     m->host_n_prompt = (int)end;
-    if (n_prompt > 1 && prefill_enabled()) {
+    if (n_prompt > 1 && prefill_enabled() && !m->exact) {
       run_prefill(m, start_pos, n_prompt, (int)end, false, nullptr);
     } else {
       for (size_t p = start_pos; p < end; ++p) {
@@ -1378,6 +1436,13 @@ int llmrs_model_set_sampling(llmrs_model* m, const llmrs_sampling* s) {
     m->exec = nullptr;
     m->graph = nullptr;
     m->graph_failed = false;
+  });
+}
+
+int llmrs_model_set_exact(llmrs_model* m, int on) {
+  return guard([&] {
+    LLMRS_REQUIRE(m, LLMRS_E_INVALID, "null model");
+    set_exact(m, on != 0);
   });
 }
 
@@ -1547,12 +1612,8 @@ int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
     LLMRS_REQUIRE(m && m->begun && out, LLMRS_E_INVALID, "llmrs_model_begin has not been called");
     LLMRS_REQUIRE(layer >= 0 && layer < m->c.n_layers, LLMRS_E_RANGE, "layer out of range");
     LLMRS_REQUIRE(m->host_pos + 1 <= (size_t)m->c.max_seq, LLMRS_E_RANGE, "decode beyond max_seq");
-    const bool fused = slot == -3;
-    LLMRS_REQUIRE(!fused || m->fused_qkv, LLMRS_E_INVALID, "slot -3: this model runs Q|K|V and attention apart");
-    const unsigned nwg = slot == -2   ? (unsigned)(m->nsplit * m->c.n_kv_heads)
-                         : fused      ? (unsigned)(m->fused_nsplit * m->c.n_kv_heads)
-                                      : linear_grid(m, slot);
-    const int per = fused ? 10 : 8;  // stamps per workgroup (the fused launch: 8 + rows stored, rows arrived)
+    const unsigned nwg = slot == -2 ? (unsigned)(m->nsplit * m->c.n_kv_heads) : linear_grid(m, slot);
+    const int per = 8;  // stamps per workgroup
     unsigned long long* ts = nullptr;
     LLMRS_HIP(hipMalloc(&ts, (size_t)nwg * per * sizeof(unsigned long long)));
     hipStream_t s = ctx().stream;
@@ -1563,13 +1624,8 @@ int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
       Launcher L{s};
       enqueue_embed(m, L, nullptr, m->layers[0].norm[0]);
       for (int li = 0; li < c.n_layers; ++li) {
-        if (m->fused_qkv && (fused || slot == LLMRS_W_O || slot == LLMRS_W_GATE || slot == LLMRS_W_DOWN)) {
-          const bool on = li == layer && fused;
-          enqueue_qkv_attention(m, L, li, nullptr, nullptr, on ? ts : nullptr, on ? ts + (size_t)nwg * 8 : nullptr);
-        } else {
-          enqueue_linear(m, L, li, LLMRS_W_Q, nullptr, nullptr, li == layer && slot == LLMRS_W_Q ? ts : nullptr);
-          enqueue_attention(m, L, li, li == layer && slot == -2 ? ts : nullptr);
-        }
+        enqueue_linear(m, L, li, LLMRS_W_Q, nullptr, nullptr, li == layer && slot == LLMRS_W_Q ? ts : nullptr);
+        enqueue_attention(m, L, li, li == layer && slot == -2 ? ts : nullptr);
         enqueue_linear(m, L, li, LLMRS_W_O, nullptr, nullptr, li == layer && slot == LLMRS_W_O ? ts : nullptr);
         enqueue_linear(m, L, li, LLMRS_W_GATE, nullptr, nullptr,
                        li == layer && slot == LLMRS_W_GATE ? ts : nullptr);
@@ -1587,19 +1643,13 @@ int llmrs_model_profile_stamps(llmrs_model* m, int layer, int slot, double* out,
     (void)hipFree(ts);
     m->host_pos += 1;
     // per workgroup: stamps 0-6 in us from the launch's earliest start (-1 =
-    // not recorded), then the XCC id and the HW_ID word; the fused launch
-    // puts its rows-stored and rows-arrived stamps after stamp 0
+    // not recorded), then the XCC id and the HW_ID word
     unsigned long long t0 = ~0ull;
     for (unsigned w = 0; w < nwg; ++w)
       if (h[8 * w]) t0 = std::min(t0, h[8 * w]);
     auto us = [&](unsigned long long v) { return v ? (double)(v - t0) / 100.0 : -1.0; };
-    for (unsigned w = 0; w < nwg && count + (fused ? 11 : 9) <= cap; ++w) {
-      out[count++] = us(h[8 * w]);
-      if (fused) {
-        out[count++] = us(h[(size_t)nwg * 8 + 2 * w]);
-        out[count++] = us(h[(size_t)nwg * 8 + 2 * w + 1]);
-      }
-      for (int i = 1; i < 7; ++i) out[count++] = us(h[8 * w + i]);
+    for (unsigned w = 0; w < nwg && count + 9 <= cap; ++w) {
+      for (int i = 0; i < 7; ++i) out[count++] = us(h[8 * w + i]);
       out[count++] = (double)(h[8 * w + 7] >> 32);
       out[count++] = (double)(h[8 * w + 7] & 0xFFFFFFFFull);
     }
@@ -1614,14 +1664,13 @@ int llmrs_model_get_config(const llmrs_model* m, llmrs_model_config* out) {
   });
 }
 
-int llmrs_model_decode_plan(const llmrs_model* m, int32_t out[5]) {
+int llmrs_model_decode_plan(const llmrs_model* m, int32_t out[4]) {
   return guard([&] {
     LLMRS_REQUIRE(m && out, LLMRS_E_INVALID, "null argument");
     out[0] = m->nsplit;
     out[1] = m->c.kv_dtype == LLMRS_F16 ? m->attn_waves : m->attn_streams;
     out[2] = m->attn_local ? 1 : 0;
-    out[3] = m->fused_qkv ? 1 : 0;
-    out[4] = m->fused_nsplit;
+    out[3] = m->exact ? 1 : 0;
   });
 }
 
@@ -1691,20 +1740,45 @@ int llmrs_model_probe_decode_layer(llmrs_model* m, int layer, size_t pos, const 
     LLMRS_HIP(hipMemcpyAsync(xin, x, H * sizeof(float), hipMemcpyHostToDevice, s));
     Launcher L{s};
     auto sync = [&] { LLMRS_HIP(hipStreamSynchronize(s)); };
-    enqueue_embed(m, L, xin, m->layers[layer].norm[0]);
-    if (m->fused_qkv) {  // one launch: projection rows and attention
-      enqueue_qkv_attention(m, L, layer, xq, xd);
-      probe_copy(out->qkv, m->qkv, m->qkv_rows * sizeof(float));
-      probe_copy(out->xq, xq, H);
-      probe_copy(out->xd, xd, H / 32 * sizeof(float));
-    } else {
-      enqueue_linear(m, L, layer, LLMRS_W_Q, xq, xd);
-      probe_copy(out->qkv, m->qkv, m->qkv_rows * sizeof(float));
-      probe_copy(out->xq, xq, H);
-      probe_copy(out->xd, xd, H / 32 * sizeof(float));
-      sync();
-      enqueue_attention(m, L, layer);
+    if (m->exact) {  // the reference-order kernels, every stage copied out
+      LLMRS_HIP(hipMemcpyAsync(m->x, xin, H * sizeof(float), hipMemcpyDeviceToDevice, s));
+      enqueue_exact_layer(m, L, layer, [&](int stage) {
+        switch (stage) {
+          case 0:
+            probe_copy(out->xq, m->x_q, H);
+            probe_copy(out->xd, m->x_d, H / 32 * sizeof(float));
+            break;
+          case 1: probe_copy(out->qkv, m->qkv, m->qkv_rows * sizeof(float)); break;
+          case 2:
+            probe_copy(out->ctx, m->ctxv, qd * sizeof(float));
+            probe_copy(out->ctx_q, m->ctx_q, qd);
+            probe_copy(out->ctx_d, m->ctx_d, qd / 32 * sizeof(float));
+            break;
+          case 3: probe_copy(out->h, m->h, H * sizeof(float)); break;
+          case 4:
+            probe_copy(out->hq, m->h_q, H);
+            probe_copy(out->hd, m->h_d, H / 32 * sizeof(float));
+            break;
+          case 6:
+            probe_copy(out->m, m->mf, F * sizeof(float));
+            probe_copy(out->m_q, m->m_q, F);
+            probe_copy(out->m_d, m->m_d, F / 32 * sizeof(float));
+            break;
+          case 7: probe_copy(out->out, m->x, H * sizeof(float)); break;
+        }
+        sync();
+      });
+      check_err(m);
+      m->begun = false;
+      return;
     }
+    enqueue_embed(m, L, xin, m->layers[layer].norm[0]);
+    enqueue_linear(m, L, layer, LLMRS_W_Q, xq, xd);
+    probe_copy(out->qkv, m->qkv, m->qkv_rows * sizeof(float));
+    probe_copy(out->xq, xq, H);
+    probe_copy(out->xd, xd, H / 32 * sizeof(float));
+    sync();
+    enqueue_attention(m, L, layer);
     probe_copy(out->ctx, m->ctxv, qd * sizeof(float));
     probe_copy(out->ctx_q, m->ctx_q, qd);
     probe_copy(out->ctx_d, m->ctx_d, qd / 32 * sizeof(float));
@@ -1741,8 +1815,15 @@ int llmrs_model_probe_head(llmrs_model* m, const float* x, int8_t* xq, float* xd
     set_state(m, 0, INT_MAX);
     LLMRS_HIP(hipMemcpyAsync(xin, x, H * sizeof(float), hipMemcpyHostToDevice, s));
     Launcher L{s};
-    enqueue_embed(m, L, xin, m->final_norm);
-    enqueue_head(m, L, logits != nullptr, dq, dd);
+    if (m->exact) {
+      LLMRS_HIP(hipMemcpyAsync(m->x, xin, H * sizeof(float), hipMemcpyDeviceToDevice, s));
+      enqueue_exact_head(m, L, logits != nullptr);
+      dq = m->x_q;
+      dd = m->x_d;
+    } else {
+      enqueue_embed(m, L, xin, m->final_norm);
+      enqueue_head(m, L, logits != nullptr, dq, dd);
+    }
     probe_copy(xq, dq, H);
     probe_copy(xd, dd, H / 32 * sizeof(float));
     probe_copy(logits, m->logits, (size_t)m->c.vocab * sizeof(float));

@@ -322,7 +322,7 @@ int llmrs_init(int device_ordinal, const char* hsaco_dir) {
         c->noalloc_error = e.what();
       }
       std::string dir = hsaco_dir ? std::string(hsaco_dir) : library_dir();
-      for (const char* name : {"gemv", "gemv_w8", "attention", "qkv_attn", "ops", "prefill", "sample", "sgemm"}) {
+      for (const char* name : {"gemv", "gemv_w8", "attention", "exact", "ops", "prefill", "sample", "sgemm"}) {
         std::string path = dir + "/" + name + ".hsaco";
         LLMRS_REQUIRE(std::filesystem::exists(path), LLMRS_E_MODULE, "missing code object " + path);
         hipModule_t m = nullptr;

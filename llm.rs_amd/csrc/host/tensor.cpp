@@ -271,6 +271,28 @@ int llmrs_silu_mul(llmrs_tensor* gate, const llmrs_tensor* up) {
   });
 }
 
+// The device exponential of the SiLU and softmax kernels on n host values
+// (test probe): out[i] = expf(x[i]) as glibc computes it.
+int llmrs_probe_expf(const float* x, size_t n, float* out) {
+  return guard([&] {
+    LLMRS_REQUIRE((x && out) || n == 0, LLMRS_E_INVALID, "null argument");
+    if (!n) return;
+    void* d = ctx().alloc.alloc(2 * n * sizeof(float));
+    try {
+      upload(d, x, n * sizeof(float));
+      EwArgs e{(float*)d, nullptr, (float*)d + n, 0.0f, (long)n};
+      launch("expf_probe", dim3(grid_for(e.n)), dim3(kBlock), 0, ctx().stream, e);
+      LLMRS_HIP(hipMemcpyAsync(out, (float*)d + n, n * sizeof(float), hipMemcpyDeviceToHost, ctx().stream));
+      LLMRS_HIP(hipStreamSynchronize(ctx().stream));
+    } catch (...) {
+      (void)hipStreamSynchronize(ctx().stream);
+      ctx().alloc.release(d);
+      throw;
+    }
+    ctx().alloc.release(d);
+  });
+}
+
 // Backend::rope_inplace (backend.rs:33; cpu.rs:326-357).
 int llmrs_rope_inplace(llmrs_tensor* x, size_t start_pos) {
   return guard([&] {

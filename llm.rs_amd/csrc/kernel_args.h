@@ -37,11 +37,6 @@ struct GemvArgs {
   // [rows][k], scales [rows][k/32]; outputs at the row's stride) over
   // batch_nwg workgroups per row.
   int batch_rows, batch_nwg;
-  // Mapped rows (the fused Q|K|V + attention launch): logical row r < n
-  // stands for physical row map_b0 + r (r < map_n1), map_b1 + r - map_n1
-  // (r < map_n1 + map_n2) or map_b2 + r - map_n1 - map_n2, in the weights
-  // and in y: one KV head's query, key and value rows as one range.
-  int map_n1, map_n2, map_b0, map_b1, map_b2;
 };
 
 // Dynamic LDS of a decode GEMV (gemv_core.h): the quantised activation row
@@ -325,24 +320,49 @@ struct PrefillAttnArgs {
 // ints between the split tickets of two KV heads: each head's counter has a
 // 256-byte line of its own, so the heads' atomics do not queue on one line.
 constexpr int kTicketStride = 64;
-// Word of a KV head's counter line that counts the workgroups of the fused
-// Q|K|V + attention launch whose projection rows are stored (qkv_attn.hip);
-// reset with the ticket by the workgroup that combines the splits.
-constexpr int kArrivalWord = 32;
+// Reference-order decode kernels (exact.hip).
+struct ExactNormArgs {
+  const float* x;        // [n] input row
+  const float* w;        // [n] RMSNorm weight
+  int8_t* xq;            // [n] Q8_0 codes of the normed row
+  float* xd;             // [n/32] their scales
+  float* y;              // [n] the normed row (may be null)
+  int n;
+  float eps;
+};
 
-// Fused Q|K|V GEMV + decode attention (qkv_attn.hip): nkv * nsplit
-// workgroups of 256 threads, one per CU, KV head = linear index % nkv so a
-// head's workgroups share one XCD; each first computes its share of the
-// head's query, key and value rows (gemv, mapped rows), then its attention
-// split.  err: set to 2 when a wait for the head's rows exceeds its spin limit.
-struct QkvAttnArgs {
-  GemvArgs gemv;         // wq/ws/k/x/norm_w/eps or xq/xd/xss, y = attn.qkv
-  AttnArgs attn;
-  int* err;
-  int spin_limit;        // polls of the arrival count before giving up
-  // profiling (with attn.ts): per item, the rows stored and the head's rows
-  // all arrived (null = off)
-  unsigned long long* ts_mid;
+struct ExactGemvArgs {
+  const uint8_t* wq;     // weight codes [n][nb][B]
+  const void* ws;        // weight scales [n][nb]
+  const int8_t* xq;      // [k] activation codes
+  const float* xd;       // [k/32] activation scales
+  float* y;              // [n] (may be null for the argmax epilogue)
+  const float* res;      // [n] residual (resid epilogue; may alias y)
+  float* part_val;       // [gridDim.x] (argmax epilogue)
+  int* part_idx;
+  int n, k;
+};
+
+struct ExactAttnArgs {
+  const float* qkv;      // [nq*hd | nkv*hd | nkv*hd] projections of this token
+  const int* pos_ptr;    // device position
+  void* kc;              // layer K cache [nkv][max_seq][hd]
+  void* vc;              // layer V cache (v_offset)
+  const float* rope_cos; // [positions][hd/2]
+  const float* rope_sin;
+  float* ctx;            // [nq*hd]
+  int8_t* ctx_q;         // [nq*hd]
+  float* ctx_d;          // [nq*hd/32]
+  int max_seq, nq, nkv;  // max_seq: cache rows per KV head (kv_rows)
+  float scale;           // fl(1 / fl(sqrt(hd)))
+};
+
+struct ExactSiluArgs {
+  const float* gu;       // [2n] gate|up GEMV rows (runs of 32 gate, then 32 up)
+  int8_t* mq;            // [n] Q8_0 codes of m = silu(g) * u
+  float* md;             // [n/32]
+  float* mf;             // [n] m as f32 (may be null)
+  int n;
 };
 
 // Positions per decode-attention tile (attn_core.h, attn_mfma.h).

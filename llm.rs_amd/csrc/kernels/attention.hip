@@ -47,7 +47,7 @@ template <int HD, int TW, bool LOCAL>
 __device__ __forceinline__ void attn_decode_mfma_impl(const AttnArgs& a0) {
   __shared__ __align__(16) uint8_t lds[MfmaAttnLds<HD, TW>::BYTES];
   const AttnArgs a = sequence_args<HD>(a0);
-  attn_mfma_item<HD, TW, LOCAL>(a, *a.pos_ptr, lds, [] {});
+  attn_mfma_item<HD, TW, LOCAL>(a, *a.pos_ptr, lds);
 }
 
 // Variant names: attn_decode_hd<HD>_f32[_s<streams>][_l], where _l is the

@@ -74,11 +74,9 @@ struct MfmaAttnLds {
 
 // `pos` (the new token's position) is read by the caller at kernel entry, so
 // it arrives through the scalar cache while the vector loads below are in
-// flight.  `mid()` runs on every wave after the first tile's loads are
-// requested and before q, k and v are read: the fused Q|K|V launch computes
-// them there (qkv_attn.hip); the standalone kernels pass a no-op.
-template <int HD, int TW, bool LOCAL, class Mid>
-__device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8_t* lds, Mid&& mid) {
+// flight.
+template <int HD, int TW, bool LOCAL>
+__device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8_t* lds) {
   constexpr int NS = HD / 32, NB = HD / 16, MID = HD / 2, TILE = kAttnTile;
   constexpr float kLog2e = 1.4426950408889634f;
   constexpr float kP = 16384.0f;  // p is scaled by 2^14 before its hi/lo split
@@ -186,7 +184,7 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
         x[s + NS / 2][e] = re * sn[s][e] + im * cs[s][e];
       }
   };
-  // cs, sn: the RoPE row, requested by the caller (before mid()).
+  // cs, sn: the RoPE row, requested by the caller.
   auto q_prologue = [&](auto&& prefetch, const float (&cs)[NS / 2][8], const float (&sn)[NS / 2][8]) {
     float qv[NS][8];
     load_row(qv, a.qkv + (size_t)(g * n_rep + min(c, n_rep - 1)) * HD + 8 * r);
@@ -266,7 +264,6 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
     float cs[NS / 2][8], sn[NS / 2][8];  // the RoPE row (waves 1 and 2)
     if (wave == 0) prefetch_first();
     else if (wave <= 2) load_rope(cs, sn);
-    mid();
     if (wave == 1) {
       q_prologue([] {}, cs, sn);
 #pragma unroll
@@ -304,7 +301,6 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
       append();  // after the handoff: the barrier does not wait for these stores
     }
   } else {
-    mid();
     float cs[NS / 2][8], sn[NS / 2][8];
     load_rope(cs, sn);
     q_prologue(prefetch_first, cs, sn);
@@ -587,14 +583,9 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
     }
     if (lane % (32 / DPL) == 0) a.ctx_d[e / 32] = bmax == 0.0f ? 0.0f : d;
   }
-  if (tid == 0) {  // every split has taken its ticket: the ticket and the arrival count restart
-    if (loc) {
-      xcd_stu(a.counters, 4 * g * kTicketStride, 0u);
-      xcd_stu(a.counters, 4 * (g * kTicketStride + kArrivalWord), 0u);
-    } else {
-      dev_stu(a.counters, 4 * g * kTicketStride, 0u);
-      dev_stu(a.counters, 4 * (g * kTicketStride + kArrivalWord), 0u);
-    }
+  if (tid == 0) {  // every split has taken its ticket: the ticket restarts
+    if (loc) xcd_stu(a.counters, 4 * g * kTicketStride, 0u);
+    else dev_stu(a.counters, 4 * g * kTicketStride, 0u);
   }
   stamp(6);
   flush_stamps();

@@ -540,15 +540,7 @@ struct UnitRegs {
   unsigned sc[R][U];  // raw scale bits
 };
 
-// Physical row of logical row r (GemvArgs::map_*); MAP = false: r itself.
-template <bool MAP>
-__device__ __forceinline__ int phys_row(const GemvArgs& a, int r) {
-  if (!MAP) return r;
-  return r < a.map_n1 ? a.map_b0 + r
-                      : r < a.map_n1 + a.map_n2 ? a.map_b1 + (r - a.map_n1) : a.map_b2 + (r - a.map_n1 - a.map_n2);
-}
-
-template <int WT, int EPI, int R, int U, bool MAP = false>
+template <int WT, int EPI, int R, int U>
 struct Gemv {
   static constexpr bool Q4 = (WT != WT_Q8H);
   static constexpr int BS = Q4 ? 16 : 32;       // code bytes per block
@@ -601,7 +593,7 @@ struct Gemv {
     const int b0 = (unit < 0 ? 0 : unit % nchunk) * BPU + lane;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int row = phys_row<MAP>(a, min(max(rg * R + r, 0), a.n - 1));
+      const int row = min(max(rg * R + r, 0), a.n - 1);
 #pragma unroll
       for (int v = 0; v < U; ++v) {
         const int b = min(b0 + LLMRS_WAVE * v, nb - 1);
@@ -697,12 +689,11 @@ static_assert(kWaves == 4 || kWaves == 8, "gemv_lds_bytes takes the wave count")
 // join the compiler cannot count through, inside the loop would make the
 // next compute wait for every outstanding load and collapse the two-unit
 // pipeline.  Row results go to LDS and are written after the loop.
-template <int WT, int PRO, int EPI, int R, int U, bool DEV, int PRE = 2, bool MAP = false>
+template <int WT, int PRO, int EPI, int R, int U, bool DEV, int PRE = 2>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, int nwg,
                                           UnitRegs<WT, R, U>& ua, UnitRegs<WT, R, U>& ub,
                                           bool preloaded, uint8_t* act, GemvShared& sh) {
-  typedef Gemv<WT, EPI, R, U, MAP> G;
-  static_assert(!MAP || EPI == EPI_STORE, "mapped rows: plain stores only");
+  typedef Gemv<WT, EPI, R, U> G;
   const int k = a.k, nb = k >> 5;
   int8_t* s_q = (int8_t*)act;
   float* s_d = (float*)(act + k);
@@ -883,7 +874,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int mrow, int wg, i
           if (v0 > 0) rv = ld_act<DEV>(a.res, ybase + row);
           out = out + rv;  // layer.rs:386,403
         }
-        st_act<DEV>(a.y, ybase + phys_row<MAP>(a, row), out);
+        st_act<DEV>(a.y, ybase + row, out);
       }
     }
   }

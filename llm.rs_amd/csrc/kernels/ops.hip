@@ -1,10 +1,14 @@
 // ops.hip - the remaining trait Backend operators (src/backend.rs:21-39) and
 // the embedding gather, for gfx950.
 //
-// The f32 matmuls keep the reference's per-output sequential order (one lane
-// per output element), so their results are bit-identical to cpu.rs:157-269
-// on non-aarch64 hosts; they are off the quantised decode hot path.
+// Every operator keeps the reference's f32 operation order, so its results
+// are bit-identical to the reference CPU backend's (x86-64 build): the f32
+// matmuls sum each output sequentially (one lane per output element,
+// cpu.rs:157-269), RMSNorm and softmax fold their row sums in index order
+// (cpu.rs:381, 410-415), and SiLU and softmax use glibc's expf
+// (exact_math.h).  They are off the quantised decode hot path.
 #include "common.h"
+#include "exact_math.h"
 #include "../kernel_args.h"
 
 using namespace llmrs;
@@ -20,7 +24,7 @@ extern "C" __global__ __launch_bounds__(256) void add_assign_f32(EwArgs e) {
 extern "C" __global__ __launch_bounds__(256) void silu_mul_f32(EwArgs e) {
   for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < e.n; i += (long)gridDim.x * blockDim.x) {
     const float v = e.a[i];
-    e.a[i] = (v / (1.0f + expf(-v))) * e.b[i];
+    e.a[i] = (v / (1.0f + exact_expf(-v))) * e.b[i];
   }
 }
 
@@ -47,52 +51,68 @@ extern "C" __global__ __launch_bounds__(256) void rope_f32(RopeArgs r) {
 }
 
 
-// Backend::rms_norm (cpu.rs:359-393); one workgroup per row.
+// Row sums in index order: the row is staged through LDS in chunks of
+// kChunk floats and lane 0 of the workgroup folds acc = acc + f(v).
+constexpr int kChunk = 2048;
+
+// Backend::rms_norm (cpu.rs:359-393); one workgroup per row:
+// ss = fold(0, acc + v*v), rms = sqrt(ss/n + eps), y = (x * (1/rms)) * w.
 extern "C" __global__ __launch_bounds__(256) void rms_norm_f32(RowArgs r) {
-  __shared__ float s_red[8];
-  const int row = blockIdx.x;
+  __shared__ float s_x[kChunk];
+  __shared__ float s_scale;
+  const int row = blockIdx.x, tid = threadIdx.x;
   const float* x = r.x + (size_t)row * r.dim;
-  float ss = 0.0f;
-  for (int i = threadIdx.x; i < r.dim; i += blockDim.x) ss = ss + x[i] * x[i];
-  ss = group_sum(ss);
-  if (lane_id() == 0) s_red[wave_id()] = ss;
+  float ss = 0.0f;  // lane 0's running sum
+  for (int c0 = 0; c0 < r.dim; c0 += kChunk) {
+    const int n = min(kChunk, r.dim - c0);
+    for (int i = tid; i < n; i += blockDim.x) s_x[i] = x[c0 + i];
+    __syncthreads();
+    if (tid == 0)
+      for (int i = 0; i < n; ++i) ss = ss + s_x[i] * s_x[i];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const float rms = __builtin_sqrtf(ss / (float)r.dim + r.eps);
+    s_scale = 1.0f / rms;
+  }
   __syncthreads();
-  float tot = 0.0f;
-  for (int w = 0; w < (int)(blockDim.x / LLMRS_WAVE); ++w) tot = tot + s_red[w];
-  const float rms = sqrtf(tot / (float)r.dim + r.eps);
-  const float scale = 1.0f / rms;
-  for (int i = threadIdx.x; i < r.dim; i += blockDim.x)
-    r.out[(size_t)row * r.dim + i] = x[i] * scale * r.w[i];
+  const float scale = s_scale;
+  for (int i = tid; i < r.dim; i += blockDim.x) r.out[(size_t)row * r.dim + i] = x[i] * scale * r.w[i];
 }
 
 // Backend::softmax (cpu.rs:395-423): max from f32::MIN, e = exp(x - max),
-// p = e * (1/sum).  One workgroup per row.
+// sum of the e in index order, p = e * (1/sum).  One workgroup per row.
 extern "C" __global__ __launch_bounds__(256) void softmax_f32(RowArgs r) {
   __shared__ float s_red[8];
-  const int row = blockIdx.x;
+  __shared__ float s_x[kChunk];
+  __shared__ float s_inv;
+  const int row = blockIdx.x, tid = threadIdx.x;
   const float* x = r.x + (size_t)row * r.dim;
   float* o = r.out + (size_t)row * r.dim;
   float mx = -3.40282347e+38f;
-  for (int i = threadIdx.x; i < r.dim; i += blockDim.x) mx = fmaxf(mx, x[i]);
+  for (int i = tid; i < r.dim; i += blockDim.x) mx = fmaxf(mx, x[i]);
   mx = group_max(mx);
   if (lane_id() == 0) s_red[wave_id()] = mx;
   __syncthreads();
   mx = s_red[0];
   for (int w = 1; w < (int)(blockDim.x / LLMRS_WAVE); ++w) mx = fmaxf(mx, s_red[w]);
-  __syncthreads();
-  float sum = 0.0f;
-  for (int i = threadIdx.x; i < r.dim; i += blockDim.x) {
-    const float e = expf(x[i] - mx);
-    o[i] = e;
-    sum = sum + e;
+  float sum = 0.0f;  // lane 0's running sum
+  for (int c0 = 0; c0 < r.dim; c0 += kChunk) {
+    const int n = min(kChunk, r.dim - c0);
+    for (int i = tid; i < n; i += blockDim.x) {
+      const float e = exact_expf(x[c0 + i] - mx);
+      o[c0 + i] = e;
+      s_x[i] = e;
+    }
+    __syncthreads();
+    if (tid == 0)
+      for (int i = 0; i < n; ++i) sum = sum + s_x[i];
+    __syncthreads();
   }
-  sum = group_sum(sum);
-  if (lane_id() == 0) s_red[wave_id()] = sum;
+  if (tid == 0) s_inv = 1.0f / sum;
   __syncthreads();
-  float tot = 0.0f;
-  for (int w = 0; w < (int)(blockDim.x / LLMRS_WAVE); ++w) tot = tot + s_red[w];
-  const float inv = 1.0f / tot;
-  for (int i = threadIdx.x; i < r.dim; i += blockDim.x) o[i] = o[i] * inv;
+  const float inv = s_inv;
+  for (int i = tid; i < r.dim; i += blockDim.x) o[i] = o[i] * inv;
 }
 
 
@@ -181,4 +201,11 @@ extern "C" __global__ __launch_bounds__(256) void embed_gather(EmbedArgs e) {
 // lets the host check how workgroups are dealt to the XCDs.
 extern "C" __global__ __launch_bounds__(64) void xcc_ids(int* out) {
   if (threadIdx.x == 0) out[blockIdx.x + blockIdx.y * gridDim.x] = __builtin_amdgcn_s_getreg((15 << 11) | 20);
+}
+
+// The device exponential on n values: out[i] = exp(a[i]) as glibc's expf
+// computes it (exact_math.h; test probe).
+extern "C" __global__ __launch_bounds__(256) void expf_probe(EwArgs e) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < e.n; i += (long)gridDim.x * blockDim.x)
+    e.out[i] = exact_expf(e.a[i]);
 }

@@ -98,6 +98,8 @@ _SIGS = {
     "llmrs_model_decode_steps": (C.c_int, [C.c_void_p, C.c_size_t]),
     "llmrs_model_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "llmrs_model_set_sampling": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "llmrs_model_set_exact": (C.c_int, [C.c_void_p, C.c_int]),
+    "llmrs_probe_expf": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
     "llmrs_batch_create": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_void_p)]),
     "llmrs_batch_free": (C.c_int, [C.c_void_p]),
     "llmrs_batch_begin": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_size_t]),
@@ -168,6 +170,15 @@ def init(device: int = 0) -> None:
 
 def sync() -> None:
     _check(lib().llmrs_sync())
+
+
+def probe_expf(x) -> np.ndarray:
+    """The device exponential of the SiLU and softmax kernels on x
+    (llmrs_probe_expf): glibc's expf, bit for bit."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    _check(lib().llmrs_probe_expf(_ptr(x), x.size, _ptr(out)))
+    return out
 
 
 def num_cus() -> int:
@@ -494,6 +505,12 @@ class HipModel:
         restores greedy decoding."""
         _check(lib().llmrs_model_set_sampling(self._h, C.byref(sampling) if sampling is not None else None))
 
+    def set_exact(self, on: bool = True) -> None:
+        """Reference-order decode kernels (llmrs_model_set_exact): every f32
+        sum in the reference CPU path's order, so logits and greedy tokens
+        equal the reference's bit for bit."""
+        _check(lib().llmrs_model_set_exact(self._h, 1 if on else 0))
+
     def produced(self) -> tuple[int, bool]:
         """(tokens produced since begin, whether an end-of-sequence id stopped the run)."""
         n = C.c_size_t(0)
@@ -588,10 +605,10 @@ class HipModel:
 
     def decode_plan(self) -> dict:
         """How a decode step runs its attention (llmrs_model_decode_plan)."""
-        out = np.zeros(5, np.int32)
+        out = np.zeros(4, np.int32)
         _check(lib().llmrs_model_decode_plan(self._h, _ptr(out)))
         return {"nsplit": int(out[0]), "tile_waves": int(out[1]), "xcd_local": bool(out[2]),
-                "fused_qkv": bool(out[3]), "fused_nsplit": int(out[4])}
+                "exact": bool(out[3])}
 
 
 # -- seeded synthetic inputs (llmrs_synth_*) ------------------------------

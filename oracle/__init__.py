@@ -42,6 +42,7 @@ _SIGS = {
     "orc_matmul_slice": (None, [_P, _I64, _I64, _P, _I64, _P]),
     "orc_add_assign": (None, [_P, _P, _I64]),
     "orc_silu_mul": (None, [_P, _P, _I64]),
+    "orc_expf": (None, [_P, _I64, _P]),
     "orc_rope_inplace": (None, [_P, _I64, _I64, _I64]),
     "orc_rms_norm": (None, [_P, _I64, _I64, _P, C.c_float, _P]),
     "orc_softmax": (None, [_P, _I64, _I64, _P]),
@@ -237,6 +238,13 @@ def silu_mul(g, u):
     g = _f32(g).copy()
     lib().orc_silu_mul(_p(g), _p(_f32(u)), g.size)
     return g
+
+
+def expf(x):
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().orc_expf(_p(x), x.size, _p(out))
+    return out
 
 
 def rope_inplace(x, start_pos):

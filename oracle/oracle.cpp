@@ -492,6 +492,11 @@ void orc_silu_mul(float* gate, const float* up, int64_t n) {
   }
 }
 
+// f32::exp (layer.rs:75-79, cpu.rs:410): the host libm's expf.
+void orc_expf(const float* x, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = std::exp(x[i]);
+}
+
 // cpu.rs:326-357: rotate-half; chunk i (of head_dim) sits at start_pos + i;
 // theta = 1 / 500000^(2j/hd) in f32 via powf; sin/cos of pos*theta.
 void orc_rope_inplace(float* x, int64_t count, int64_t head_dim, int64_t start_pos) {

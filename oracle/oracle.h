@@ -83,6 +83,8 @@ void orc_matmul_slice(const float* a, int64_t m, int64_t k,
                       const float* other, int64_t rows, float* out);
 void orc_add_assign(float* a, const float* b, int64_t n);
 void orc_silu_mul(float* gate, const float* up, int64_t n);
+/* f32::exp as the reference calls it (host libm expf), element-wise. */
+void orc_expf(const float* x, int64_t n, float* out);
 void orc_rope_inplace(float* x, int64_t count, int64_t head_dim,
                       int64_t start_pos);
 void orc_rms_norm(const float* x, int64_t rows, int64_t dim, const float* w,

@@ -265,51 +265,6 @@ def test_decode_attention_xcd_local(hip, orc, kv, head_dim, waves, splits, monke
             assert np.array_equal(a[key], b[key]), f"{key} differs with the XCD-local exchange"
 
 
-# The fused Q|K|V GEMV + decode attention launch (8 KV heads, f16 caches,
-# one tile wave; a KV head's workgroups on one XCD) against the two
-# standalone launches with the same split count: bit-identical projection
-# rows, ctx, its codes and the appended K/V rows, and within the oracle's bar.
-# Positions 5, 700 and 1500 put 1, 22 and 47 tiles of 32 over the splits
-# (one per CU of an XCD: most idle, one tile each, two in some); four steps
-# in a row reuse the arrival and ticket counters.  Query heads per KV head: 4
-# and 8; head_dim 128 and 64.
-@pytest.mark.parametrize("weight", [DType.Q4_0, DType.Q8_0], ids=["q4_0", "q8_0"])
-@pytest.mark.parametrize("head_dim,n_heads", [(128, 32), (64, 32), (128, 64)], ids=lambda v: str(v))
-@pytest.mark.parametrize("pos", [5, 700, 1500])
-def test_fused_qkv_attention(hip, orc, weight, head_dim, n_heads, pos, monkeypatch):
-    fs = hip.num_cus() // 8
-    spec = syn.tiny(weight, DType.F16, head_dim=head_dim, n_layers=1, n_heads=n_heads, n_kv_heads=8, ffn=512,
-                    seed=51 + head_dim + n_heads)
-    got = {}
-    for mode in ("fused", "split"):
-        monkeypatch.setenv("LLMRS_FUSED_QKV", "1" if mode == "fused" else "0")
-        if mode == "split":
-            monkeypatch.setenv("LLMRS_ATTN_SPLITS", str(fs))
-        gm, om, w = layer_models(hip, orc, spec, pos + 6)
-        plan = gm.decode_plan()
-        assert plan["fused_qkv"] == (mode == "fused"), plan
-        if mode == "fused":
-            assert plan["fused_nsplit"] == fs and plan["tile_waves"] == 1, plan
-        fill_cache(gm, om, spec, pos)
-        got[mode] = []
-        for i in range(4):
-            x = synth_normal(spec.seed, 90 + i, spec.hidden, 0.0, 1.0)
-            pr = gm.probe_decode_layer(0, pos + i, x)
-            pr["kv"] = [gm.kv_read(0, g, pos + i, 1) for g in range(8)]
-            if mode == "fused":
-                qkv = np.concatenate([gemv(orc, spec, pr["xq"], pr["xd"], w.linears[0][s])[0]
-                                      for s in (W_Q, W_K, W_V)])
-                assert_close(pr["qkv"], qkv, "fused Q|K|V rows")
-                check_decode_attention(gm, om, orc, spec, pr, pos + i)
-            got[mode].append(pr)
-        gm.close()
-    for a, b in zip(got["fused"], got["split"]):
-        for key in ("xq", "xd", "qkv", "ctx", "ctx_q", "ctx_d", "h", "out"):
-            assert np.array_equal(a[key], b[key]), f"{key} differs between the fused and the two launches"
-        for (ka, va), (kb, vb) in zip(a["kv"], b["kv"]):
-            assert np.array_equal(ka, kb) and np.array_equal(va, vb), "appended K/V rows differ"
-
-
 def check_prefill_layer(hip, orc, spec, start, M):
     """Every prefill kernel of one layer on M rows at positions start..:
     GEMMs bit-exact on the GPU's own operands (the tile GEMM, or for up to
