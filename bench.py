@@ -17,6 +17,13 @@ prefill: the 2048-token prompt of the prefill workload through the same 8B
 model (batched prefill, int8 MFMA GEMMs), timed in the same run.
 cpu_baseline: the CPU oracle (C++ restatement of the reference CPU backend)
 decoding at the GPU's context length on a bounded sample.
+exact_decode: the same model on the reference-order kernels
+(llmrs_model_set_exact), whose logits and tokens are bit-identical to the
+reference CPU path's.
+long_context: the 70B-shaped Q4_0 model decoding from 8192 pre-filled f16
+positions (its own model, timed in the same run): tok/s, the decode
+attention's duration and HBM rate, the weights + K/V roofline, and the CPU
+oracle on a bounded sample of the same steps when the host has the memory.
 
 --workload 3: the 2048-token batched prefill alone (prefill tok/s; roofline
 against the int8 MFMA peak).
@@ -127,6 +134,116 @@ def cpu_prefill_baseline(spec, w, seconds: float) -> dict:
             "cpu": cpu_model(),
             "sample": f"one batched forward of the first {n2} prompt tokens of the same model, "
                       f"oracle threads={oracle.threads()}"}
+
+
+def host_mem_available() -> int:
+    """Bytes of host memory available (MemAvailable), 0 when unknown."""
+    try:
+        for line in Path("/proc/meminfo").read_text().splitlines():
+            if line.startswith("MemAvailable:"):
+                return int(line.split()[1]) * 1024
+    except (OSError, ValueError):
+        pass
+    return 0
+
+
+def exact_decode(model, lh, prompt, pre: int, steps: int) -> dict:
+    """The reference-order kernels on the same model: the prompt (one
+    position per step), then `steps` timed greedy steps."""
+    model.set_exact(True)
+    try:
+        t0 = time.perf_counter()
+        model.begin(prompt, start_pos=pre)
+        lh.sync()
+        prompt_s = time.perf_counter() - t0
+        model.decode_steps(2)
+        lh.sync()
+        t0 = time.perf_counter()
+        model.decode_steps(steps)
+        lh.sync()
+        dt = time.perf_counter() - t0
+    finally:
+        model.set_exact(False)
+    return {"tok_s": round(steps / dt, 1), "ms_per_token": round(dt / steps * 1e3, 3), "steps": steps,
+            "prompt_ms": round(prompt_s * 1e3, 1),
+            "note": "reference-order kernels (llmrs_model_set_exact): every f32 sum in the reference CPU "
+                    "path's order, logits and greedy tokens bit-identical to it; the prompt runs one "
+                    "position per step"}
+
+
+def long_context(lh, syn, warmup: int, steps: int, cpu_seconds: float, cpu: bool) -> dict:
+    """The 70B-shaped Q4_0 workload: decode from 8192 pre-filled N(0,1) f16
+    positions on its own model."""
+    import numpy as np
+    spec = syn.with_sizes(syn.WORKLOADS[4], decode=warmup + steps)
+    max_seq = spec.max_seq + 2
+    pre = spec.prefilled
+    t0 = time.perf_counter()
+    model = lh.HipModel(spec.config(max_seq))
+    # the oracle's sample needs its own host copy of the weights (Q4 codes
+    # + f32 scales, the f32 embedding) and of the f16 cache
+    need = spec.linear_bytes() * 20 / 18 + 4.0 * spec.vocab * spec.hidden + \
+        2.0 * 2 * spec.n_layers * spec.n_kv_heads * spec.head_dim * max_seq
+    avail = host_mem_available()
+    run_cpu = cpu and avail > 1.5 * need
+    if run_cpu:
+        w = syn.make_weights(spec)
+        syn.load_model(model, w)
+    else:
+        w = None
+        syn.stream_model(model, spec)
+    log(f"long context: {spec.name} uploaded in {time.perf_counter() - t0:.1f}s "
+        f"({model.weight_bytes() / 1e9:.2f} GB of linear weights)")
+    t0 = time.perf_counter()
+    for layer in range(spec.n_layers):
+        for g in range(spec.n_kv_heads):
+            model.kv_write(layer, g, 0, *syn.prefill_kv(spec, layer, g))
+    log(f"long context: K/V cache pre-filled ({pre} positions) in {time.perf_counter() - t0:.1f}s")
+    prompt = syn.prompt(spec)
+    model.begin(prompt, start_pos=pre)
+    model.decode_steps(warmup)
+    lh.sync()
+    t0 = time.perf_counter()
+    model.decode_steps(steps)
+    lh.sync()
+    dt = time.perf_counter() - t0
+    first = pre + spec.prompt + warmup
+    value = steps / dt
+    attn = defaultdict(lambda: [0.0, 0.0, 0])
+    for _ in range(2):
+        for k in model.profile_step():
+            if k.name.startswith("attn_decode"):
+                e = attn[k.name]
+                e[0] += k.ms
+                e[1] += k.bytes
+                e[2] += 1
+    name, (ams, aby, an) = max(attn.items(), key=lambda kv: kv[1][0])
+    a_us, a_bytes = ams / an * 1e3, aby / an
+    wbytes = model.weight_bytes()
+    kv_bytes = 2.0 * spec.n_layers * spec.n_kv_heads * spec.head_dim * (first + (steps - 1) / 2 + 1) * 2
+    roof = HBM_PEAK_GBS * 1e9 / (wbytes + kv_bytes)
+    model.close()
+    log(f"long context: {value:.1f} tok/s, {name} {a_us:.2f} us per layer "
+        f"({a_bytes / a_us / 1e3:.0f} GB/s)")
+    out = {"workload": f"{spec.name} decode", "tok_s": round(value, 2), "ms_per_token": round(dt / steps * 1e3, 3),
+           "steps": steps, "warmup": warmup, "timed_positions": [first, first + steps - 1],
+           "attention": {"kernel": name, "avg_us": round(a_us, 2), "kv_bytes_per_launch": round(a_bytes),
+                         "gb_s": round(a_bytes / a_us / 1e3, 1),
+                         "frac_of_hbm_peak": round(a_bytes / a_us / 1e3 / HBM_PEAK_GBS, 4)},
+           "weights_kv_roofline_tok_s": round(roof, 1), "frac_of_weights_kv_roofline": round(value / roof, 4),
+           "weights_roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / wbytes, 1),
+           "frac_of_weights_roofline": round(value * wbytes / (HBM_PEAK_GBS * 1e9), 4)}
+    if run_cpu:
+        log("long context: timing the CPU oracle on a bounded sample ...")
+        out["cpu_baseline"] = cpu_baseline(spec, w, first, cpu_seconds)
+        log(f"long context cpu baseline: {out['cpu_baseline']['value']} tok/s")
+    else:
+        out["cpu_baseline"] = {"value": None, "unit": "tok/s",
+                               "note": f"not run: the oracle's copy of the weights and cache needs about "
+                                       f"{need / 2**30:.0f} GiB of host memory; {avail / 2**30:.0f} GiB available"
+                                       if cpu else "not run (--no-cpu-baseline)"}
+    del w
+    return out
 
 
 def measure_prefill(model, lh, prompt, warmup: int, steps: int, profile_steps: int, workload: str) -> dict:
@@ -277,6 +394,10 @@ def main() -> int:
     ap.add_argument("--batch-sizes", type=lambda v: [int(x) for x in v.split(",") if x], default=[4, 16, 64],
                     help="batched-decode sizes measured after the single-sequence run (empty: none)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--exact-steps", type=int, default=32,
+                    help="timed steps of the reference-order kernels in the decode run (0 = none)")
+    ap.add_argument("--long-context-steps", type=int, default=32,
+                    help="timed steps of the 70B long-context workload in the 8B decode run (0 = none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: the workload's prompt prefill, eager decode steps, then one "
@@ -417,6 +538,11 @@ def main() -> int:
                "temperature": 0.8, "top_p": 0.9, "repeat_penalty": 1.2, "penalty_window": 64}
     log(f"sampled decode: {sampled['tok_s']} tok/s, sampler {sampled['sampler_us']} us per token")
 
+    exact = None
+    if args.exact_steps > 0:
+        exact = exact_decode(model, lh, prompt, pre, args.exact_steps)
+        log(f"reference-order decode: {exact['tok_s']} tok/s ({exact['ms_per_token']} ms/token)")
+
     # Batched decode: B sequences with their own prompts and caches stepping
     # together (greedy), on the same weights; aggregate tok/s per batch size.
     batched = None
@@ -462,6 +588,12 @@ def main() -> int:
         cpu = cpu_baseline(spec, w, first, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads")
 
+    lc = None
+    if args.workload == 2 and args.long_context_steps > 0:
+        model.close()
+        w = None
+        lc = long_context(lh, syn, 4, args.long_context_steps, args.cpu_seconds, not args.no_cpu_baseline)
+
     line = {
         "metric": metric_for(args.workload, spec.name), "value": round(value, 2), "unit": "tok/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4),
@@ -489,6 +621,8 @@ def main() -> int:
         "weight_gb_per_token": round(wbytes / 1e9, 4),
         "prompt_ms": round(prompt_s * 1e3, 1),
         "prefill": prefill,
+        "long_context": lc,
+        "exact_decode": exact,
         "sampled_decode": sampled,
         "batched_decode": batched,
         "kernels": kernels,

@@ -184,6 +184,9 @@ typedef struct {
 #define LLMRS_N_FINAL 2
 
 int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out);
+/* Frees the model; LLMRS_E_INVALID while batches created on it
+ * (llmrs_batch_create) are alive, which hold its weights and must be freed
+ * first. */
 int llmrs_model_free(llmrs_model* m);
 /* The configuration a model was created with (e.g. by a loader). */
 int llmrs_model_get_config(const llmrs_model* m, llmrs_model_config* out);
@@ -287,8 +290,8 @@ int llmrs_model_set_sampling(llmrs_model* m, const llmrs_sampling* s);
  * for SiLU and softmax (layer.rs:75-79).  For the same weights and tokens,
  * logits and greedy tokens then equal the reference's bit for bit.  Prompts
  * run one position per step (the reference's batched prompt gives the same
- * values row by row).  Costs about 2x the fast step per token; needs max_seq
- * <= 16384.  Batches (llmrs_batch_*) always use the fast kernels. */
+ * values row by row).  Slower than the fast step (8B shape on MI355X: 6.7 vs
+ * 1.4 ms per token); needs max_seq <= 16384.  Batches (llmrs_batch_*) always use the fast kernels. */
 int llmrs_model_set_exact(llmrs_model* m, int on);
 /* Tokens produced since llmrs_model_begin (the first comes from the prompt's
  * last position) and whether an end-of-sequence id stopped the run. */

@@ -140,9 +140,14 @@ class Parser {
       }
     }
   }
-  Value value() {
+  // Nesting deeper than this is refused (a crafted header cannot exhaust
+  // the host stack); configs and safetensors headers nest two levels.
+  static constexpr int kMaxDepth = 64;
+
+  Value value(int depth = 0) {
     ws();
     if (p_ >= end_) fail("unexpected end");
+    if (depth >= kMaxDepth) fail("nesting too deep");
     Value v;
     const char c = *p_;
     if (c == '{') {
@@ -153,14 +158,14 @@ class Parser {
         expect('"');
         std::string k = string_body();
         expect(':');
-        v.obj[k] = value();
+        v.obj[k] = value(depth + 1);
       } while (eat(','));
       expect('}');
     } else if (c == '[') {
       ++p_;
       v.kind = Value::Array;
       if (eat(']')) return v;
-      do v.arr.push_back(value());
+      do v.arr.push_back(value(depth + 1));
       while (eat(','));
       expect(']');
     } else if (c == '"') {

@@ -295,8 +295,8 @@ struct GgufFile {
   size_t cur = 0;
   std::string path;
 
-  void need(size_t n) {
-    LLMRS_REQUIRE(cur + n <= map->size, LLMRS_E_FORMAT, path + ": truncated GGUF header");
+  void need(uint64_t n) {  // written so that no sum can wrap: cur <= size always holds
+    LLMRS_REQUIRE(n <= map->size - cur, LLMRS_E_FORMAT, path + ": truncated GGUF header");
   }
   template <class T>
   T rd() {
@@ -373,19 +373,27 @@ struct GgufFile {
     const size_t align = meta.count("general.alignment") ? (size_t)meta["general.alignment"].i : 32;
     LLMRS_REQUIRE(align > 0, LLMRS_E_FORMAT, path + ": bad alignment");
     const size_t base = align_up(cur, align);
+    LLMRS_REQUIRE(base <= map->size, LLMRS_E_FORMAT, path + ": tensor data beyond the file");
+    const uint64_t avail = map->size - base;  // bytes of the data section
     for (auto& in : infos) {
+      // element count and byte size, each bounded by the file before the
+      // next multiplication, so no product can wrap
       uint64_t n = 1;
-      for (uint64_t d : in.t.ne) n *= d;
-      size_t bytes = 0;
+      for (uint64_t d : in.t.ne) {
+        LLMRS_REQUIRE(d == 0 || n <= avail / d, LLMRS_E_FORMAT,
+                      path + ": tensor " + in.name + " is larger than the file");
+        n *= d;
+      }
+      uint64_t bytes = 0;
       switch (in.t.type) {
-        case G_F32: bytes = 4 * n; break;
+        case G_F32: bytes = n <= avail / 4 ? 4 * n : UINT64_MAX; break;
         case G_F16:
-        case G_BF16: bytes = 2 * n; break;
-        case G_Q4_0: bytes = n / 32 * 18; break;
+        case G_BF16: bytes = n <= avail / 2 ? 2 * n : UINT64_MAX; break;
+        case G_Q4_0: bytes = n / 32 * 18; break;   // n <= avail, so n / 32 * 18 cannot wrap
         case G_Q8_0: bytes = n / 32 * 34; break;
         default: bytes = 0;  // unsupported types are rejected where they are used
       }
-      LLMRS_REQUIRE(base + in.off + bytes <= map->size, LLMRS_E_FORMAT,
+      LLMRS_REQUIRE(in.off <= avail && bytes <= avail - in.off, LLMRS_E_FORMAT,
                     path + ": data of " + in.name + " beyond the file");
       in.t.data = map->data + base + in.off;
       in.t.bytes = bytes;
@@ -681,6 +689,23 @@ int llmrs_model_load_gguf(const char* path, const llmrs_load_options* opt, llmrs
                     std::string(path) + ": its weights load as weight dtype " + std::to_string(wt));
     }
     cfg.weight_dtype = wt;
+    // Every other tensor's type and shape, before any device work: the
+    // embedding and lm_head (float, Q4_0 or Q8_0) and the norms (float).
+    {
+      auto check = [&](const std::string& name, uint64_t rows, uint64_t cols, bool quant_ok) {
+        const GgufTensor& t = g.get(name, rows, cols);
+        LLMRS_REQUIRE(ggml_float(t.type) || (quant_ok && (t.type == G_Q4_0 || t.type == G_Q8_0)), LLMRS_E_FORMAT,
+                      std::string(path) + ": " + name + " has ggml type " + std::to_string(t.type) + " (" +
+                          ggml_type_name(t.type) + "); supported: F32, F16, BF16" + (quant_ok ? ", Q4_0, Q8_0" : ""));
+      };
+      const uint64_t Hc = (uint64_t)cfg.hidden, Vc = (uint64_t)cfg.vocab;
+      check("token_embd.weight", Vc, Hc, true);
+      if (g.find("output.weight")) check("output.weight", Vc, Hc, true);
+      check("output_norm.weight", Hc, 0, false);
+      for (int l = 0; l < cfg.n_layers; ++l)
+        for (const char* nn : {"attn_norm", "ffn_norm"})
+          check("blk." + std::to_string(l) + "." + nn + ".weight", Hc, 0, false);
+    }
     apply_options(cfg, opt);
     int rc2 = llmrs_model_create(&cfg, &m);
     if (rc2 != LLMRS_OK) throw Error(rc2, llmrs_last_error());

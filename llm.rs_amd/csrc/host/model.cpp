@@ -95,6 +95,8 @@ struct llmrs_model {
   // decode attention: the splits of a KV head on one XCD, exchanging
   // partials through its L2 (the attention kernels' _l variants)
   bool attn_local = false;
+  // batches created on this model and not yet freed: the model outlives them
+  int live_batches = 0;
   // single-sequence steps on the reference-order kernels (exact.hip)
   bool exact = false;
   float* ex_gu = nullptr;  // [2 ffn] gate|up rows of the exact step
@@ -1096,6 +1098,8 @@ int llmrs_model_create(const llmrs_model_config* cfg, llmrs_model** out) {
 int llmrs_model_free(llmrs_model* m) {
   return guard([&] {
     if (!m) return;
+    LLMRS_REQUIRE(m->live_batches == 0, LLMRS_E_INVALID,
+                  std::to_string(m->live_batches) + " batch(es) of this model are still alive: free them first");
     (void)hipStreamSynchronize(ctx().stream);
     delete m;
   });
@@ -2152,6 +2156,7 @@ int llmrs_batch_create(llmrs_model* m, int32_t batch, llmrs_batch** out) {
       (void)kernel(batch_linear_kernel(b.get(), epi, W), dim3(256));
     }
     *out = b.release();
+    ++m->live_batches;
   });
 }
 
@@ -2159,6 +2164,7 @@ int llmrs_batch_free(llmrs_batch* b) {
   return guard([&] {
     if (!b) return;
     (void)hipStreamSynchronize(ctx().stream);
+    --b->m->live_batches;
     delete b;
   });
 }

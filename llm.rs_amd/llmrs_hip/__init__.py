@@ -598,7 +598,7 @@ class HipModel:
         quantised [us], XCC id, HW_ID)."""
         out = np.zeros(cap, np.float64)
         n = _check(lib().llmrs_model_profile_stamps(self._h, layer, slot, _ptr(out), cap))
-        return out[:n].reshape(-1, 11 if slot == -3 else 9)
+        return out[:n].reshape(-1, 9)
 
     def weight_bytes(self) -> float:
         return float(lib().llmrs_model_weight_bytes(self._h))

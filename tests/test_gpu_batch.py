@@ -3,15 +3,16 @@
 The reference decodes one sequence; a row's values in its layer code depend
 only on that row and its own cache (layer.rs:175-333).  Bars: each slot's
 logits within 1e-2 of the oracle's forward over that slot's sequence and its
-greedy stream identical to the oracle's (a divergence only at a near-tie,
-as for single-sequence decoding); a slot's logits bit-identical whichever
-other sequences share the batch; every slot at its own position."""
+greedy stream identical to the oracle's for the first 64 steps (a slot whose
+stream parts earlier at a near-tie makes the test an expected failure that
+names it; parting anywhere else fails); a slot's logits bit-identical
+whichever other sequences share the batch; every slot at its own position."""
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from conftest import check_stream
+from conftest import NEAR_TIE, check_stream
 from llmrs_hip import DType, HipBatch, synthetic as syn
 
 pytestmark = pytest.mark.gpu
@@ -47,17 +48,27 @@ def test_batch_streams_vs_oracle(hip, orc, spec, mode, monkeypatch):
         bt.begin(s, p)
     bt.decode_steps(steps - 1)
     lg = bt.logits()
+    early = []
     for s, p in enumerate(ps):
         toks = bt.tokens(s, p.size + steps)
         assert np.array_equal(toks[:p.size], p)
         gen = toks[p.size:]
         ref, margins = om.generate(p, steps)
-        check_stream(gen, ref, margins)
         # the last step's logits against the oracle's forward over the same sequence
         olg, _ = om.forward(toks[:-1], 0)
         assert np.max(np.abs(lg[s] - olg)) < 1e-2, f"slot {s}"
+        mism = np.nonzero(gen != ref)[0]
+        if mism.size and mism[0] < 64 and margins[mism[0]] < NEAR_TIE:
+            early.append(f"slot {s} at step {mism[0]} (oracle margin {margins[mism[0]]:.2g})")
+        else:
+            check_stream(gen, ref, margins)
     bt.close()
     gm.close()
+    if early:
+        # measured on MI355X: tiny-Q8_0-F32 (all three paths) parts at step 36
+        # (margin 0.002), tiny-Q4-F16 on the skinny GEMM at step 22 (0.0017)
+        pytest.xfail("fast kernels: greedy stream parts from the oracle before step 64 at a near-tie: "
+                     + "; ".join(early))
 
 
 def test_batch_rows_independent(hip, orc):
@@ -133,4 +144,53 @@ def test_batch_errors(hip):
     bt.close()
     with pytest.raises(hip.LlmrsError):
         HipBatch(gm, 0)
+    gm.close()
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("B", [16, 64])
+def test_batch_8b_widths(hip, orc, B):
+    """Two 8B-width layers with the full 128256-row lm_head, B sequences of
+    1-20 prompt tokens decoding 16 greedy steps on the skinny GEMM (its
+    8B-width launches, the ones the benchmark times): every slot's stream
+    identical to the oracle's for all 16 steps and its last logits within
+    1e-2."""
+    spec = syn.with_sizes(syn.WORKLOADS[2], n_layers=2)
+    steps = 16
+    w = syn.make_weights(spec)
+    gm = hip.HipModel(spec.config(64))
+    syn.load_model(gm, w)
+    om = orc.OracleModel.from_spec(spec, max_seq=64)
+    om.load(w)
+    ps = prompts(spec, B, seed=B)
+    bt = HipBatch(gm, B)
+    for s, p in enumerate(ps):
+        bt.begin(s, p)
+    bt.decode_steps(steps - 1)
+    lg = bt.logits()
+    worst = 0.0
+    for s, p in enumerate(ps):
+        toks = bt.tokens(s, p.size + steps)
+        ref, margins = om.generate(p, steps)
+        check_stream(toks[p.size:], ref, margins, min_steps=steps)
+        olg, _ = om.forward(toks[:-1], 0)
+        worst = max(worst, float(np.max(np.abs(lg[s] - olg))))
+    print(f"\nRAW batch of {B} at 8B widths: {steps}/{steps} identical steps in every slot; "
+          f"last logits max-abs error {worst:.3g}", flush=True)
+    assert worst < 1e-2
+    bt.close()
+    gm.close()
+
+
+def test_model_free_refused_while_a_batch_lives(hip):
+    """A batch holds its model's weights: freeing the model first is
+    refused (LLMRS_E_INVALID) and works once the batch is freed."""
+    spec = SPECS[0]
+    gm = hip.HipModel(spec.config(32))
+    syn.load_model(gm, syn.make_weights(spec))
+    bt = HipBatch(gm, 2)
+    with pytest.raises(hip.LlmrsError) as e:
+        gm.close()
+    assert e.value.code == hip.E_INVALID and "batch" in str(e.value)
+    bt.close()
     gm.close()

@@ -218,6 +218,25 @@ def test_exact_workload_north_star_bar(hip, orc, index, prompt_len, steps):
     assert n == steps and n >= 64
 
 
+@pytest.mark.timeout(900)
+def test_exact_prefill_8b_2048(hip, orc):
+    """The 2048-token prompt workload through two 8B-width layers and the
+    full lm_head, one position per step on the reference-order kernels:
+    the residual stream of every row and the last row's logits equal the
+    oracle's batched forward (the reference adds each row's sums in the same
+    orders in its batched path)."""
+    spec = syn.with_sizes(syn.WORKLOADS[3], n_layers=2, prompt=2048, decode=0)
+    print("\n8B-width 2-layer model, 2048-token prompt, reference-order kernels: building", flush=True)
+    gm, om, _ = exact_model(hip, orc, spec, max_seq=2048)
+    toks = syn.prompt(spec)
+    lg, nxt, tr = gm.forward(toks, 0, trace=True)
+    olg, otr = om.forward(toks, 0, all_rows=False, trace=True)
+    same(tr, otr, "residual trace")
+    same(lg, olg, "logits")
+    assert nxt == orc.argmax(olg)[0]
+    print("RAW exact 8B 2-layer 2048-token prefill: trace and logits bit-identical", flush=True)
+
+
 @pytest.mark.timeout(1200)
 def test_exact_70b_widths_4_layers_long_context(hip, orc):
     """Four 70B-width layers (hidden 8192, 64 query / 8 KV heads, FFN 28672)

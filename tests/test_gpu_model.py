@@ -1,9 +1,13 @@
-"""GPU decode model vs the CPU oracle on identical seeded weights and prompts.
+"""The fast decode kernels (the default) against the CPU oracle on identical
+seeded weights and prompts.  The reference-order kernels, which match the
+oracle bit for bit, are tested in test_gpu_exact.py.
 
 Bars: final logits within 1e-2 max-abs; an identical greedy token stream for
-at least 64 steps.  A stream may only diverge at a step whose oracle
-top1-top2 margin is below NEAR_TIE (a near-tie the f32 summation-order
-differences can flip), and never before step 64 unless so.
+the first 64 steps (or all of a shorter run), with no allowance; after that a
+stream may only part at a step whose oracle top1-top2 margin is below
+NEAR_TIE (a near-tie that f32 summation-order differences can flip).  Where
+the fast kernels miss a bar, the test is an expected failure whose reason
+gives the measured numbers, so the gap stays visible.
 
 Why residuals deeper than layer 0 get a norm-relative bound: every layer
 re-quantises activations to Q8_0 (cpu.rs:663-745) after RMSNorm, attention
@@ -22,13 +26,14 @@ dominate a small residual, so one such code step moves the logits by up to
 away with its product within MIDPOINT_TOL of the rounding midpoint, and the
 logits of the replay are held to 1e-2.
 
-The 1B Q8_0 workload is the exception the reference itself makes: its two
-builds (x86-64, and aarch64 with NEON summation orders, cpu.rs:461-619,
-747-886; restated by the oracle's orc_set_arch) disagree on it by about 0.15
-in the prompt logits and their greedy streams part after a few steps.  Its
-test asserts the GPU is no further from the x86 build than the aarch64 build
-is (measured in the test, factor 1), and keeps the strict bar as an
-expected failure.
+The 1B Q8_0 workload makes the reference's own two builds (x86-64, and
+aarch64 with NEON summation orders, cpu.rs:461-619, 747-886; restated by the
+oracle's orc_set_arch) disagree by about 0.15 in the prompt logits, and
+their greedy streams part after a few steps: zero-mean Q8 weights keep the
+residual O(1), so one Q8 code step survives to the logits.  The fast
+kernels, which add in a third order, are held to "no further from the x86
+build than the aarch64 build is" (factor 1), and the strict bar is an
+expected failure for them; the reference-order kernels meet it bit-exactly.
 """
 from __future__ import annotations
 
@@ -113,7 +118,21 @@ TINY = [
 ]
 
 
-@pytest.mark.parametrize("spec", TINY, ids=lambda s: s.name)
+def _tiny_stream_cases():
+    out = []
+    for s in TINY:
+        if s.weight == DType.Q8_0 and s.kv == DType.F32:
+            # measured on MI355X: logits 7.2e-7 from the oracle, greedy stream
+            # parts at step 43 where the oracle's top two logits are 0.0014 apart
+            out.append(pytest.param(s, marks=pytest.mark.xfail(
+                strict=True, reason="fast kernels: stream parts from the oracle at step 43 of 80 at a near-tie "
+                "(oracle margin 0.0014); the reference-order kernels match all 80 steps")))
+        else:
+            out.append(s)
+    return out
+
+
+@pytest.mark.parametrize("spec", _tiny_stream_cases(), ids=lambda s: s.name)
 def test_tiny_trace_logits_stream(hip, orc, spec):
     gm, om, _ = build(hip, orc, spec, max_seq=96)
     toks = syn.prompt(spec)
@@ -126,12 +145,16 @@ def test_tiny_trace_logits_stream(hip, orc, spec):
     for li in range(1, spec.n_layers + 1):
         e = rel_norm_err(tr[:, li], otr[:, li])
         assert e < 1e-2, f"layer {li} residual relative error {e:.3g}"
-    assert np.max(np.abs(lg - olg)) < 1e-2
-    assert nxt == orc.argmax(olg)[0] or orc.argmax(olg)[1] < NEAR_TIE
+    err = float(np.max(np.abs(lg - olg)))
     # greedy generation (both restart at position 0)
     steps = 80
     gtoks = gm.generate(toks, steps)
     otoks, margins = om.generate(toks, steps)
+    mism = np.nonzero(gtoks != otoks)[0]
+    print(f"\nRAW {spec.name}: logits max-abs error {err:.3g}; "
+          f"{int(mism[0]) if mism.size else steps}/{steps} identical greedy steps", flush=True)
+    assert err < 1e-2
+    assert nxt == orc.argmax(olg)[0] or orc.argmax(olg)[1] < NEAR_TIE
     check_stream(gtoks, otoks, margins)
 
 
@@ -203,10 +226,12 @@ def replay_gpu_codes(gm, om, orc, spec, w, tok, pos):
     return lg, st
 
 
-def prefilled_decode(hip, orc, spec, steps):
+def prefilled_decode(hip, orc, spec, steps, replay=True):
     """Decode `steps` tokens after N(0,1) K/V pre-filled below
     spec.prefilled, eagerly against the oracle, then as a resident HIP-graph
-    run from the same position, which must repeat the eager stream."""
+    run from the same position, which must repeat the eager stream.  Asserts
+    the replay bar (below) and the greedy-stream bar; returns the raw
+    max-abs logit error of the first step for the caller's 1e-2 check."""
     gm, om, w = build(hip, orc, spec)
     for l in range(spec.n_layers):
         for g in range(spec.n_kv_heads):
@@ -235,14 +260,14 @@ def prefilled_decode(hip, orc, spec, steps):
     # dominate a small residual): the first step is also held to the oracle
     # replaying the GPU's own codes, every differing code one step away at a
     # rounding midpoint.
-    ilg, st = replay_gpu_codes(gm, om, orc, spec, w, tok, spec.prefilled)
-    ierr = float(np.max(np.abs(lg0 - ilg)))
-    print(f"\nlogits vs the reference {err:.3g}; {st['differ']} of {st['taken']} activation codes "
-          f"rounded the other way (at most {st['max_dist']:.2g} code units from a midpoint); logits vs "
-          f"the reference replaying the GPU's codes {ierr:.3g}", flush=True)
-    assert st["bad"] == 0, f"activation codes differ away from a rounding midpoint: {st}"
-    assert ierr < 1e-2 and (st["differ"] > 0 or err < 1e-2), (err, ierr)
-    check_stream(ids, oids, np.array(margins), min_steps=steps)
+    if replay:
+        ilg, st = replay_gpu_codes(gm, om, orc, spec, w, tok, spec.prefilled)
+        ierr = float(np.max(np.abs(lg0 - ilg)))
+        print(f"\nlogits vs the reference {err:.3g}; {st['differ']} of {st['taken']} activation codes "
+              f"rounded the other way (at most {st['max_dist']:.2g} code units from a midpoint); logits vs "
+              f"the reference replaying the GPU's codes {ierr:.3g}", flush=True)
+        assert st["bad"] == 0, f"activation codes differ away from a rounding midpoint: {st}"
+        assert ierr < 1e-2, (err, ierr)
     # the resident greedy run from the same position (HIP-graph replay) gives
     # the eager stream: the cache below start_pos is taken as pre-filled
     for l in range(spec.n_layers):
@@ -252,10 +277,21 @@ def prefilled_decode(hip, orc, spec, steps):
     gm.decode_steps(len(ids) - 1)
     run = gm.tokens(spec.prefilled + len(ids) + 1)[spec.prefilled + 1:]
     assert np.array_equal(run, np.array(ids)), f"graph run {run[:8]} vs eager {ids[:8]}"
+    n_same = len(ids) if ids == oids else len(ids) - 1
+    print(f"RAW {spec.name} from {spec.prefilled} pre-filled positions: logits max-abs error {err:.3g}; "
+          f"{n_same}/{steps} identical greedy steps", flush=True)
+    check_stream(ids, oids, np.array(margins), min_steps=steps)
+    return err
 
 
-@pytest.mark.parametrize("kv,streams", [(DType.F16, "0"), (DType.F32, "0"), (DType.F32, "4")],
-                         ids=["f16", "f32", "f32-streams4"])
+@pytest.mark.parametrize("kv,streams", [
+    # measured on MI355X: logits 0.0103 from the oracle (two Q8 codes rounded
+    # the other way at a midpoint; 1.4e-6 when the oracle replays them), the
+    # stream parts at step 14 where the oracle's top two are 0.00099 apart
+    pytest.param(DType.F16, "0", marks=pytest.mark.xfail(
+        strict=True, reason="fast kernels: logits 0.0103 from the oracle, stream parts at step 14 of 40 at a "
+        "near-tie (oracle margin 0.00099); replaying the GPU's codes gives 1.4e-6")),
+    (DType.F32, "0"), (DType.F32, "4")], ids=["f16", "f32", "f32-streams4"])
 def test_prefilled_kv_decode(hip, orc, kv, streams, monkeypatch):
     """Pre-filled N(0,1) K/V caches (the long-context workload's setup): the
     matrix-core attention (f16 cache), and the vector kernel (f32 cache) with
@@ -264,7 +300,8 @@ def test_prefilled_kv_decode(hip, orc, kv, streams, monkeypatch):
     monkeypatch.setenv("LLMRS_ATTN_STREAMS", streams)
     spec = syn.with_sizes(syn.tiny(DType.Q4_0, kv, head_dim=128, n_heads=8, n_kv_heads=2),
                           prefilled=300, prompt=1, decode=40)
-    prefilled_decode(hip, orc, spec, 40)
+    err = prefilled_decode(hip, orc, spec, 40)
+    assert err < 1e-2
 
 
 @pytest.mark.timeout(900)
@@ -279,7 +316,26 @@ def test_70b_layer_shapes_long_context(hip, orc):
     spec = syn.with_sizes(syn.tiny(DType.Q4_0, DType.F16, head_dim=128, n_layers=1, n_heads=64,
                                    n_kv_heads=8, ffn=28672, vocab=1024, seed=20260004),
                           prefilled=8192, prompt=1, decode=8)
-    prefilled_decode(hip, orc, spec, 8)
+    err = prefilled_decode(hip, orc, spec, 8)
+    if err >= 1e-2:  # measured on MI355X: 0.059 (3 of 86016 codes rounded the other way at a midpoint)
+        pytest.xfail(f"fast kernels: raw logits error {err:.3g} above 1e-2 (one Q8 code step at a rounding "
+                     "midpoint moves these logits); the replay bar and the stream bar passed")
+
+
+@pytest.mark.timeout(1200)
+def test_70b_widths_4_layers_full_head(hip, orc):
+    """Four 70B-width layers with the full 128256-row lm_head, 16 greedy
+    steps from 8192 pre-filled f16 positions on the fast kernels: the raw
+    1e-2 logits bar and the stream bar (measured on MI355X: 0.0096 and 16/16).
+    The code replay of the one-layer test is not used here: past the first
+    layer the residuals themselves carry the fast kernels' summation
+    differences, which move pre-rounding products by up to ~0.03 code units.
+    The reference-order kernels meet both bars bit-exactly
+    (test_gpu_exact.py)."""
+    spec = syn.with_sizes(syn.WORKLOADS[4], n_layers=4, decode=16)
+    print(f"\n{spec.name} x4 layers: building", flush=True)
+    err = prefilled_decode(hip, orc, spec, 16, replay=False)
+    assert err < 1e-2
 
 
 @pytest.mark.timeout(900)
@@ -301,7 +357,7 @@ def test_workload_greedy_stream(hip, orc, index, prompt_len, steps):
     gtoks = gm.generate(toks, steps)
     otoks, margins = om.generate(toks, steps)
     n_equal = check_stream(gtoks, otoks, margins)
-    print(f"workload {index}: {n_equal}/{steps} identical greedy steps; min margin {margins.min():.4g}",
+    print(f"RAW workload {index}: {n_equal}/{steps} identical greedy steps; min margin {margins.min():.4g}",
           flush=True)
 
 
@@ -336,11 +392,12 @@ def test_q8_workload_within_reference_builds(hip, orc):
 
 
 @pytest.mark.timeout(900)
-@pytest.mark.xfail(strict=True, reason="the reference's own x86 and aarch64 builds differ by ~0.15 in "
-                   "these logits and part after a few greedy steps (test_q8_workload_within_reference_builds)")
+@pytest.mark.xfail(strict=True, reason="fast kernels, measured on MI355X: logits 0.144 from the x86 reference, "
+                   "15 identical greedy steps (its aarch64 build: 0.148, 6 steps); the reference-order kernels "
+                   "meet the bar bit-exactly (test_gpu_exact.py)")
 def test_q8_workload_strict_bar(hip, orc):
-    """The north star's bar on the 1B Q8_0 workload, which no summation order
-    other than the x86 reference's own meets (see the test above)."""
+    """The north star's bar on the 1B Q8_0 workload with the fast kernels,
+    which add in an order of their own (see the test above)."""
     spec, _, _, lerr, gtoks, otoks, margins = q8_workload(hip, orc)
     assert lerr < 1e-2
     check_stream(gtoks, otoks, margins)
@@ -374,9 +431,10 @@ def test_prefill_8b_2048_vs_oracle(hip, orc, monkeypatch):
     err = float(np.max(np.abs(lg - olg)))
     top, margin = orc.argmax(olg)
     bar, dl = logit_bar(orc, spec, w, toks, max_seq=2048)
-    print(f"logits max-abs error {err:.3g} (reference rounding spread {dl:.3g}); argmax {nxt} vs {top} "
-          f"(margin {margin:.3g})", flush=True)
+    print(f"RAW 8B 2-layer 2048-token prefill: logits max-abs error {err:.3g} (reference rounding spread "
+          f"{dl:.3g}); argmax {nxt} vs {top} (margin {margin:.3g})", flush=True)
     assert err < bar
+    assert err < 1e-2
     assert nxt == top or margin < NEAR_TIE
     gm.close()
     monkeypatch.setenv("LLMRS_PREFILL_CHUNK", "1500")
@@ -473,7 +531,10 @@ def test_prefill_attention_mfma_vs_vector(hip, orc, spec, monkeypatch):
             e = rel_norm_err(tr[:, li], otr[:, li])
             assert e < 1e-2, f"{mode}: layer {li} residual relative error {e:.3g}"
         err = float(np.max(np.abs(lg - olg)))
+        print(f"\nRAW {spec.name} prefill attention {mode}: logits max-abs error {err:.3g} "
+              f"(reference rounding spread {dl:.3g})", flush=True)
         assert err < bar, f"{mode}: logits error {err:.3g}, reference rounding spread {dl:.3g}"
+        assert err < 1e-2, f"{mode}: logits error {err:.3g}"
     e = rel_norm_err(outs["mfma"][2], outs["valu"][2])
     assert e < 1e-2, f"mfma vs vector attention: residual relative error {e:.3g}"
 

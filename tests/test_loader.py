@@ -153,6 +153,29 @@ def test_gguf_rejects_malformed_files(tmp_path, hlib):
     rc, msg = load_rc(hlib, "llmrs_model_load_gguf", bad)
     assert rc == E_FORMAT and "ffn_up" in msg, msg
     assert load_rc(hlib, "llmrs_model_load_gguf", tmp_path / "missing.gguf")[0] == E_FORMAT
+    # crafted sizes: every bound is checked without wrapping, and unsupported
+    # tensor types are refused before any device work (E_FORMAT, not the
+    # E_NOINIT that creating the model on this host would give)
+    raw = good.read_bytes()
+    bad.write_bytes(raw[:24] + struct.pack("<Q", (1 << 64) - 8) + raw[32:])  # first key's length
+    rc, msg = load_rc(hlib, "llmrs_model_load_gguf", bad)
+    assert rc == E_FORMAT and "truncated" in msg, msg
+    name = b"output.weight"
+    at = raw.index(struct.pack("<Q", len(name)) + name) + 8 + len(name)  # nd, ne[2], type, offset
+    ne_pos, type_pos, off_pos = at + 4, at + 4 + 16, at + 4 + 16 + 4
+
+    def patched(pos, fmt, value):
+        return raw[:pos] + struct.pack(fmt, value) + raw[pos + struct.calcsize(fmt):]
+    for off in ((1 << 64) - 16, 1 << 63, len(raw)):
+        bad.write_bytes(patched(off_pos, "<Q", off))
+        rc, msg = load_rc(hlib, "llmrs_model_load_gguf", bad)
+        assert rc == E_FORMAT and "beyond" in msg, (off, msg)
+    bad.write_bytes(raw[:ne_pos] + struct.pack("<QQ", 1 << 40, 1 << 40) + raw[ne_pos + 16:])
+    rc, msg = load_rc(hlib, "llmrs_model_load_gguf", bad)
+    assert rc == E_FORMAT and "larger than the file" in msg, msg
+    bad.write_bytes(patched(type_pos, "<I", 14))  # Q6_K, as common llama.cpp Q4_0 files store output.weight
+    rc, msg = load_rc(hlib, "llmrs_model_load_gguf", bad)
+    assert rc == E_FORMAT and "output.weight" in msg and "type 14" in msg, msg
 
 
 def test_safetensors_rejects_malformed_files(tmp_path, hlib):
@@ -172,6 +195,11 @@ def test_safetensors_rejects_malformed_files(tmp_path, hlib):
     (d / "config.json").write_text("{\"hidden_size\": 64}")
     rc, msg = load_rc(hlib, "llmrs_model_load_safetensors", d)
     assert rc == E_FORMAT and "num_hidden_layers" in msg, msg
+    # a header nested far deeper than any real one is refused, not recursed into
+    deep = b'{"a":' + b"[" * 100000 + b"]" * 100000 + b"}"
+    (d / "model.safetensors").write_bytes(struct.pack("<Q", len(deep)) + deep)
+    rc, msg = load_rc(hlib, "llmrs_model_load_safetensors", d)
+    assert rc == E_FORMAT and "deep" in msg, msg
     (d / "config.json").unlink()
     assert load_rc(hlib, "llmrs_model_load_safetensors", d)[0] == E_FORMAT
 
