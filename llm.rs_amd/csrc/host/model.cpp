@@ -100,6 +100,8 @@ struct llmrs_model {
   // single-sequence steps on the reference-order kernels (exact.hip)
   bool exact = false;
   float* ex_gu = nullptr;  // [2 ffn] gate|up rows of the exact step
+  float* ex_part_val = nullptr;  // [exact_gemv_cap()] argmax partials of the exact lm_head
+  int* ex_part_idx = nullptr;
   size_t host_pos = 0;
   bool begun = false;
   hipGraph_t graph = nullptr;
@@ -504,8 +506,10 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
 // probabilities): 64 KB.
 constexpr int kExactMaxRows = 16384;
 
-// Workgroups of an exact GEMV over n rows (four rows, one per wave, at a time).
-unsigned exact_gemv_grid(int n, int cap) { return (unsigned)std::max(1, std::min((n + 3) / 4, cap)); }
+// Workgroups of an exact GEMV: one per 8-row tile, at most eight per CU
+// (they loop over the tiles beyond).
+int exact_gemv_cap() { return 8 * ctx().num_cus; }
+unsigned exact_gemv_grid(int n) { return (unsigned)std::max(1, std::min((n + 7) / 8, exact_gemv_cap())); }
 
 void exact_norm(llmrs_model* m, Launcher& L, const float* x, const float* w, int8_t* xq, float* xd,
                 float* y = nullptr) {
@@ -517,7 +521,7 @@ void exact_norm(llmrs_model* m, Launcher& L, const float* x, const float* w, int
 void exact_linear(llmrs_model* m, Launcher& L, const DevLinear& W, const char* epi, const int8_t* xq,
                   const float* xd, float* y, const float* res) {
   ExactGemvArgs a{W.codes, W.scales, xq, xd, y, res, nullptr, nullptr, W.n, W.k};
-  const unsigned grid = exact_gemv_grid(W.n, 8 * ctx().num_cus);
+  const unsigned grid = exact_gemv_grid(W.n);
   L(std::string("exact_gemv_") + wt_tag(m->wt) + "_" + epi,
     linear_weight_bytes(m, W) + 1.125 * W.k + (res ? 8.0 : 4.0) * W.n, dim3(grid), dim3(256), 0, a);
 }
@@ -568,9 +572,9 @@ void enqueue_exact_layer(llmrs_model* m, Launcher& L, int li, const std::functio
 void enqueue_exact_head(llmrs_model* m, Launcher& L, bool write_logits) {
   const llmrs_model_config& c = m->c;
   exact_norm(m, L, m->x, m->final_norm, m->x_q, m->x_d);
-  const unsigned grid = exact_gemv_grid(c.vocab, m->lm_grid);
+  const unsigned grid = exact_gemv_grid(c.vocab);
   ExactGemvArgs a{m->lm_head.codes, m->lm_head.scales, m->x_q, m->x_d,
-                  write_logits || m->sampling ? m->logits : nullptr, nullptr, m->part_val, m->part_idx,
+                  write_logits || m->sampling ? m->logits : nullptr, nullptr, m->ex_part_val, m->ex_part_idx,
                   c.vocab, c.hidden};
   L(std::string("exact_gemv_") + wt_tag(m->wt) + "_argmax", linear_weight_bytes(m, m->lm_head) + 1.125 * c.hidden,
     dim3(grid), dim3(256), 0, a);
@@ -589,7 +593,7 @@ void enqueue_exact_head(llmrs_model* m, Launcher& L, bool write_logits) {
     enqueue_sample(L, s);
     return;
   }
-  ArgmaxFinalArgs f{m->part_val, m->part_idx, (int)grid, m->pos, m->n_prompt, m->tokens, m->gen, m->cap};
+  ArgmaxFinalArgs f{m->ex_part_val, m->ex_part_idx, (int)grid, m->pos, m->n_prompt, m->tokens, m->gen, m->cap};
   L("argmax_final", 8.0 * grid, dim3(1), dim3(256), 0, f);
 }
 
@@ -623,7 +627,11 @@ void set_exact(llmrs_model* m, bool on) {
     const llmrs_model_config& c = m->c;
     LLMRS_REQUIRE(kv_rows(m) <= kExactMaxRows, LLMRS_E_INVALID,
                   "the reference-order step supports max_seq up to " + std::to_string(kExactMaxRows));
-    if (!m->ex_gu) m->ex_gu = m->dalloc<float>((size_t)2 * c.ffn);
+    if (!m->ex_gu) {
+      m->ex_gu = m->dalloc<float>((size_t)2 * c.ffn);
+      m->ex_part_val = m->dalloc<float>((size_t)exact_gemv_cap());
+      m->ex_part_idx = m->dalloc<int>((size_t)exact_gemv_cap());
+    }
     for (const char* epi : {"store", "resid", "argmax"}) (void)kernel(std::string("exact_gemv_") + wt_tag(m->wt) + "_" + epi);
     (void)kernel("exact_norm_q8");
     (void)kernel("exact_silu_q8");

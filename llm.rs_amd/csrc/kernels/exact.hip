@@ -11,9 +11,9 @@
 //   exact_norm_q8   RMSNorm with one sequential f32 fold of x*x
 //                   (cpu.rs:381-389), then Q8_0 (cpu.rs:724-743)
 //   exact_gemv_*    per output row, total = total + isum_b * (d_w * d_a) for
-//                   b = 0, 1, ... (kernel_avx2, cpu.rs:903-938); a wave per
-//                   row computes the terms of 64 blocks at once, then adds
-//                   them in block order
+//                   b = 0, 1, ... (kernel_avx2, cpu.rs:903-938); the block
+//                   terms are computed lane-parallel and parked in LDS, and
+//                   one lane per row adds them in block order
 //   exact_attn_*    one workgroup per query head: RoPE (cpu.rs:345-354),
 //                   K/V append, sequential q.k dots (matmul_slice,
 //                   cpu.rs:230-269) times 1/sqrt(hd) (layer.rs:257-258),
@@ -37,22 +37,46 @@ namespace {
 constexpr int kT = 256;
 
 // ---- RMSNorm + Q8_0 ---------------------------------------------------------
-// One workgroup; x staged in LDS (n <= 32768 floats), one lane folds x*x in
-// index order.  n is a multiple of 32, so a 32-lane group holds one block.
+// One workgroup.  All threads square the row into LDS (each product is the
+// reference's own rounding of x*x); one lane then adds the squares in index
+// order, reading them 32 at a time with the next 32 requested before the
+// current ones are added.  n <= 32768 and a multiple of 32, so a 32-lane
+// group holds one block.
 __device__ __forceinline__ void norm_q8(const ExactNormArgs& a) {
-  extern __shared__ __align__(16) float sx[];
+  extern __shared__ __align__(16) float sq[];
   __shared__ float s_scale;
   const int tid = threadIdx.x;
-  for (int i = tid; i < a.n; i += kT) sx[i] = a.x[i];
+  for (int i = tid; i < a.n; i += kT) {
+    const float v = a.x[i];
+    sq[i] = v * v;
+  }
   __syncthreads();
   if (tid == 0) {
     float ss = 0.0f;
-    for (int i = 0; i < a.n; i += 4) {
-      const f32x4 v = *(const f32x4*)(sx + i);
-      ss = ss + v[0] * v[0];
-      ss = ss + v[1] * v[1];
-      ss = ss + v[2] * v[2];
-      ss = ss + v[3] * v[3];
+    f32x4 A[8], B[8];
+    auto load = [&](f32x4 (&r)[8], int i) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[j] = *(const f32x4*)(sq + i + 4 * j);
+    };
+    auto add = [&](const f32x4 (&r)[8]) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        ss = ss + r[j][0];
+        ss = ss + r[j][1];
+        ss = ss + r[j][2];
+        ss = ss + r[j][3];
+      }
+    };
+    load(A, 0);
+    for (int i = 0;; i += 64) {
+      const bool more = i + 32 < a.n;
+      if (more) load(B, i + 32);
+      add(A);
+      if (!more) break;
+      const bool more2 = i + 64 < a.n;
+      if (more2) load(A, i + 64);
+      add(B);
+      if (!more2) break;
     }
     const float rms = __builtin_sqrtf(ss / (float)a.n + a.eps);
     s_scale = 1.0f / rms;
@@ -60,7 +84,7 @@ __device__ __forceinline__ void norm_q8(const ExactNormArgs& a) {
   __syncthreads();
   const float s = s_scale;
   for (int i = tid; i < a.n; i += kT) {
-    const float y = sx[i] * s * a.w[i];
+    const float y = a.x[i] * s * a.w[i];
     float d;
     const int q = q8_group32(y, &d);
     a.xq[i] = (int8_t)q;
@@ -70,93 +94,146 @@ __device__ __forceinline__ void norm_q8(const ExactNormArgs& a) {
 }
 
 // ---- GEMV -----------------------------------------------------------------
-// Exact integer sum of one block of weight codes with activation codes
-// (device Q4 layout: byte i = e[i] | e[i+16] << 4, value q - 8).
+// Rows per workgroup tile: wave w computes the block terms of rows w and
+// w + 4 (lanes over 64 blocks, coalesced loads), parks them in LDS, and lane
+// r of wave 0 adds row r's terms to its total in block order.
+constexpr int kExR = 8;
+constexpr int kExRW = kExR / (kT / LLMRS_WAVE);  // rows per wave
+
+// The loads of one 64-block chunk for a wave's rows.
 template <int WT>
-__device__ __forceinline__ int block_isum(const uint8_t* wblk, const int8_t* ablk) {
-  const i32x4 a0 = *(const i32x4*)ablk, a1 = *(const i32x4*)(ablk + 16);
+struct ExChunk {
+  i32x4 a0, a1;                          // activation codes of block b
+  float da;                              // activation scale of block b
+  u32x4 w0[kExRW], w1[WT == WT_Q8H ? kExRW : 1];  // weight codes (Q8: two halves)
+  unsigned sc[kExRW];                    // raw weight scales
+};
+
+template <int WT>
+__device__ __forceinline__ void ex_load(const ExactGemvArgs& a, int row0, int c, int nb, ExChunk<WT>& r) {
+  constexpr int BS = WT == WT_Q8H ? 32 : 16;
+  const int b = min(c + lane_id(), nb - 1);  // clamped: terms past the row end are not folded
+  r.a0 = *(const i32x4*)(a.xq + 32 * b);
+  r.a1 = *(const i32x4*)(a.xq + 32 * b + 16);
+  r.da = a.xd[b];
+#pragma unroll
+  for (int j = 0; j < kExRW; ++j) {
+    const int row = min(row0 + wave_id() + 4 * j, a.n - 1);
+    const size_t blk = (size_t)row * nb + b;
+    r.w0[j] = __builtin_nontemporal_load((const u32x4*)(a.wq + blk * BS));
+    if (WT == WT_Q8H) r.w1[j] = __builtin_nontemporal_load((const u32x4*)(a.wq + blk * BS + 16));
+    r.sc[j] = load_wscale_raw<WT>(a.ws, blk);
+  }
+}
+
+// Exact integer sum of one block: device Q4 layout (byte i = e[i] | e[i+16]
+// << 4, value q - 8) or Q8 codes, against the activation codes.
+template <int WT>
+__device__ __forceinline__ int ex_isum(const ExChunk<WT>& r, int j) {
   int s = 0;
   if (WT == WT_Q8H) {
-    const i32x4 w0 = *(const i32x4*)wblk, w1 = *(const i32x4*)(wblk + 16);
-    s = dot4(w0.x, a0.x, s);
-    s = dot4(w0.y, a0.y, s);
-    s = dot4(w0.z, a0.z, s);
-    s = dot4(w0.w, a0.w, s);
-    s = dot4(w1.x, a1.x, s);
-    s = dot4(w1.y, a1.y, s);
-    s = dot4(w1.z, a1.z, s);
-    s = dot4(w1.w, a1.w, s);
+    const u32x4 w0 = r.w0[j], w1 = r.w1[j];
+    s = dot4((int)w0.x, r.a0.x, s);
+    s = dot4((int)w0.y, r.a0.y, s);
+    s = dot4((int)w0.z, r.a0.z, s);
+    s = dot4((int)w0.w, r.a0.w, s);
+    s = dot4((int)w1.x, r.a1.x, s);
+    s = dot4((int)w1.y, r.a1.y, s);
+    s = dot4((int)w1.z, r.a1.z, s);
+    s = dot4((int)w1.w, r.a1.w, s);
   } else {
-    const u32x4 w = *(const u32x4*)wblk;
+    const u32x4 w = r.w0[j];
     const unsigned M = 0x0F0F0F0Fu;
-    s = dot4((int)(w.x & M), a0.x, s);
-    s = dot4((int)(w.y & M), a0.y, s);
-    s = dot4((int)(w.z & M), a0.z, s);
-    s = dot4((int)(w.w & M), a0.w, s);
-    s = dot4((int)((w.x >> 4) & M), a1.x, s);
-    s = dot4((int)((w.y >> 4) & M), a1.y, s);
-    s = dot4((int)((w.z >> 4) & M), a1.z, s);
-    s = dot4((int)((w.w >> 4) & M), a1.w, s);
-    int sa = 0;
-    sa = dot4(a0.x, 0x01010101, sa);
-    sa = dot4(a0.y, 0x01010101, sa);
-    sa = dot4(a0.z, 0x01010101, sa);
-    sa = dot4(a0.w, 0x01010101, sa);
-    sa = dot4(a1.x, 0x01010101, sa);
-    sa = dot4(a1.y, 0x01010101, sa);
-    sa = dot4(a1.z, 0x01010101, sa);
-    sa = dot4(a1.w, 0x01010101, sa);
-    s -= 8 * sa;
+    s = dot4((int)(w.x & M), r.a0.x, s);
+    s = dot4((int)(w.y & M), r.a0.y, s);
+    s = dot4((int)(w.z & M), r.a0.z, s);
+    s = dot4((int)(w.w & M), r.a0.w, s);
+    s = dot4((int)((w.x >> 4) & M), r.a1.x, s);
+    s = dot4((int)((w.y >> 4) & M), r.a1.y, s);
+    s = dot4((int)((w.z >> 4) & M), r.a1.z, s);
+    s = dot4((int)((w.w >> 4) & M), r.a1.w, s);
   }
   return s;
 }
 
+// The Q4 offset -8 * sum(a) of block b (0 for Q8 weights).
+template <int WT>
+__device__ __forceinline__ int ex_offset(const ExChunk<WT>& r) {
+  if (WT == WT_Q8H) return 0;
+  int sa = 0;
+  sa = dot4(r.a0.x, 0x01010101, sa);
+  sa = dot4(r.a0.y, 0x01010101, sa);
+  sa = dot4(r.a0.z, 0x01010101, sa);
+  sa = dot4(r.a0.w, 0x01010101, sa);
+  sa = dot4(r.a1.x, 0x01010101, sa);
+  sa = dot4(r.a1.y, 0x01010101, sa);
+  sa = dot4(r.a1.z, 0x01010101, sa);
+  sa = dot4(r.a1.w, 0x01010101, sa);
+  return -8 * sa;
+}
+
 // EPI: EPI_STORE (y = total), EPI_RESID (y = total + res), EPI_ARGMAX
 // (logits into y when set, and this workgroup's (max, lowest index) into
-// part_val / part_idx[blockIdx.x]).  Waves take rows round-robin.
+// part_val / part_idx[blockIdx.x]).  Workgroups take 8-row tiles
+// round-robin; the next chunk's loads are issued before the current chunk is
+// folded.
 template <int WT, int EPI>
 __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
-  constexpr int BS = WT == WT_Q8H ? 32 : 16;
-  __shared__ float s_bv[kT / LLMRS_WAVE];
-  __shared__ int s_bi[kT / LLMRS_WAVE];
+  __shared__ float s_p[kExR][LLMRS_WAVE + 1];  // padded: lane r's reads of row r hit distinct banks
   const int lane = lane_id(), wave = wave_id();
-  const int nb = a.k >> 5;
+  const int nb = a.k >> 5, nch = (nb + LLMRS_WAVE - 1) / LLMRS_WAVE;
+  const int ntiles = (a.n + kExR - 1) / kExR;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int row = blockIdx.x * (kT / LLMRS_WAVE) + wave; row < a.n; row += gridDim.x * (kT / LLMRS_WAVE)) {
-    float total = 0.0f;
-    for (int c = 0; c < nb; c += LLMRS_WAVE) {
-      const int b = c + lane;
-      float p = 0.0f;
-      if (b < nb) {
-        const size_t blk = (size_t)row * nb + b;
-        const int isum = block_isum<WT>(a.wq + blk * BS, a.xq + 32 * b);
-        p = (float)isum * (wscale<WT>(load_wscale_raw<WT>(a.ws, blk)) * a.xd[b]);
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int row0 = tile * kExR;
+    float total = 0.0f;  // lane r < kExR of wave 0: row row0 + r
+    // one chunk: the wave's block terms into LDS, then wave 0 folds them
+    auto step = [&](int c, const ExChunk<WT>& r) {
+      const int off = ex_offset<WT>(r);
+#pragma unroll
+      for (int j = 0; j < kExRW; ++j) {
+        const int isum = ex_isum<WT>(r, j) + off;
+        s_p[wave + 4 * j][lane] = (float)isum * (wscale<WT>(r.sc[j]) * r.da);
       }
-      const int cnt = min(LLMRS_WAVE, nb - c);
-      for (int l = 0; l < cnt; ++l) total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), l));
+      __syncthreads();
+      if (wave == 0 && lane < kExR) {
+        const int cnt = min(LLMRS_WAVE, nb - c);
+        for (int l = 0; l < cnt; ++l) total = total + s_p[lane][l];
+      }
+      __syncthreads();
+    };
+    ExChunk<WT> ra, rb;
+    ex_load<WT>(a, row0, 0, nb, ra);
+    for (int ci = 0; ci < nch; ci += 2) {
+      if (ci + 1 < nch) ex_load<WT>(a, row0, (ci + 1) * LLMRS_WAVE, nb, rb);
+      step(ci * LLMRS_WAVE, ra);
+      if (ci + 1 < nch) {
+        if (ci + 2 < nch) ex_load<WT>(a, row0, (ci + 2) * LLMRS_WAVE, nb, ra);
+        step((ci + 1) * LLMRS_WAVE, rb);
+      }
     }
-    if (lane == 0) {
+    if (wave == 0 && lane < kExR && row0 + lane < a.n) {
+      const int row = row0 + lane;
       if (EPI == EPI_RESID) a.y[row] = total + a.res[row];
       else if (a.y) a.y[row] = total;
-    }
-    if (EPI == EPI_ARGMAX && better(total, row, bv, bi)) {
-      bv = total;
-      bi = row;
+      if (EPI == EPI_ARGMAX && better(total, row, bv, bi)) {
+        bv = total;
+        bi = row;
+      }
     }
   }
-  if (EPI == EPI_ARGMAX) {
-    if (lane == 0) {
-      s_bv[wave] = bv;
-      s_bi[wave] = bi;
+  if (EPI == EPI_ARGMAX && wave == 0) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      for (int w = 1; w < kT / LLMRS_WAVE; ++w)
-        if (better(s_bv[w], s_bi[w], bv, bi)) {
-          bv = s_bv[w];
-          bi = s_bi[w];
-        }
+    if (lane == 0) {
       a.part_val[blockIdx.x] = bv;
       a.part_idx[blockIdx.x] = bi;
     }
