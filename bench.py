@@ -539,8 +539,9 @@ def main() -> int:
     log(f"sampled decode: {sampled['tok_s']} tok/s, sampler {sampled['sampler_us']} us per token")
 
     exact = None
-    if args.exact_steps > 0:
-        exact = exact_decode(model, lh, prompt, pre, args.exact_steps)
+    exact_steps = min(args.exact_steps, max_seq - pre - n_prompt - 3)  # what the cache still holds
+    if exact_steps > 0:
+        exact = exact_decode(model, lh, prompt, pre, exact_steps)
         log(f"reference-order decode: {exact['tok_s']} tok/s ({exact['ms_per_token']} ms/token)")
 
     # Batched decode: B sequences with their own prompts and caches stepping
