@@ -42,55 +42,89 @@ constexpr int kT = 256;
 // order, reading them 32 at a time with the next 32 requested before the
 // current ones are added.  n <= 32768 and a multiple of 32, so a 32-lane
 // group holds one block.
+
+// Lane 0's fold of sq[0..n) in index order; returns 1/rms (cpu.rs:381-383).
+__device__ __forceinline__ float fold_scale(const float* sq, int n, float eps) {
+  float ss = 0.0f;
+  f32x4 A[8], B[8];
+  auto load = [&](f32x4 (&r)[8], int i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = *(const f32x4*)(sq + i + 4 * j);
+  };
+  auto add = [&](const f32x4 (&r)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ss = ss + r[j][0];
+      ss = ss + r[j][1];
+      ss = ss + r[j][2];
+      ss = ss + r[j][3];
+    }
+  };
+  load(A, 0);
+  for (int i = 0;; i += 64) {
+    const bool more = i + 32 < n;
+    if (more) load(B, i + 32);
+    add(A);
+    if (!more) break;
+    const bool more2 = i + 64 < n;
+    if (more2) load(A, i + 64);
+    add(B);
+    if (!more2) break;
+  }
+  const float rms = __builtin_sqrtf(ss / (float)n + eps);
+  return 1.0f / rms;
+}
+
+// y = (x*s)*w (cpu.rs:389) and its Q8_0 block; element i is held by lane
+// i % 32 of a 32-lane group.
+__device__ __forceinline__ void norm_out(const ExactNormArgs& a, int i, float x, float s, float w) {
+  const float y = x * s * w;
+  float d;
+  const int q = q8_group32(y, &d);
+  a.xq[i] = (int8_t)q;
+  if ((i & 31) == 0) a.xd[i >> 5] = d;
+  if (a.y) a.y[i] = y;
+}
+
+// n == kT * EPT: thread t holds elements t + kT*j of x and w in registers
+// from the start, so nothing is loaded after the fold.
+template <int EPT>
+__device__ __forceinline__ void norm_q8_regs(const ExactNormArgs& a, float* sq, float* s_scale) {
+  const int tid = threadIdx.x;
+  float xv[EPT], wv[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) xv[j] = a.x[tid + kT * j];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) wv[j] = a.w[tid + kT * j];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) sq[tid + kT * j] = xv[j] * xv[j];
+  __syncthreads();
+  if (tid == 0) *s_scale = fold_scale(sq, a.n, a.eps);
+  __syncthreads();
+  const float s = *s_scale;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) norm_out(a, tid + kT * j, xv[j], s, wv[j]);
+}
+
 __device__ __forceinline__ void norm_q8(const ExactNormArgs& a) {
   extern __shared__ __align__(16) float sq[];
   __shared__ float s_scale;
+  switch (a.n) {
+    case 8 * kT: norm_q8_regs<8>(a, sq, &s_scale); return;
+    case 16 * kT: norm_q8_regs<16>(a, sq, &s_scale); return;
+    case 32 * kT: norm_q8_regs<32>(a, sq, &s_scale); return;
+    default: break;
+  }
   const int tid = threadIdx.x;
   for (int i = tid; i < a.n; i += kT) {
     const float v = a.x[i];
     sq[i] = v * v;
   }
   __syncthreads();
-  if (tid == 0) {
-    float ss = 0.0f;
-    f32x4 A[8], B[8];
-    auto load = [&](f32x4 (&r)[8], int i) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) r[j] = *(const f32x4*)(sq + i + 4 * j);
-    };
-    auto add = [&](const f32x4 (&r)[8]) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        ss = ss + r[j][0];
-        ss = ss + r[j][1];
-        ss = ss + r[j][2];
-        ss = ss + r[j][3];
-      }
-    };
-    load(A, 0);
-    for (int i = 0;; i += 64) {
-      const bool more = i + 32 < a.n;
-      if (more) load(B, i + 32);
-      add(A);
-      if (!more) break;
-      const bool more2 = i + 64 < a.n;
-      if (more2) load(A, i + 64);
-      add(B);
-      if (!more2) break;
-    }
-    const float rms = __builtin_sqrtf(ss / (float)a.n + a.eps);
-    s_scale = 1.0f / rms;
-  }
+  if (tid == 0) s_scale = fold_scale(sq, a.n, a.eps);
   __syncthreads();
   const float s = s_scale;
-  for (int i = tid; i < a.n; i += kT) {
-    const float y = a.x[i] * s * a.w[i];
-    float d;
-    const int q = q8_group32(y, &d);
-    a.xq[i] = (int8_t)q;
-    if ((tid & 31) == 0) a.xd[i >> 5] = d;
-    if (a.y) a.y[i] = y;
-  }
+  for (int i = tid; i < a.n; i += kT) norm_out(a, i, a.x[i], s, a.w[i]);
 }
 
 // ---- GEMV -----------------------------------------------------------------
@@ -246,7 +280,10 @@ __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
 // positions in LDS.  The new K/V row is rotated and rounded to the cache
 // type by every workgroup of the group (the values are identical) and
 // stored by the group's first; each workgroup uses its own copy for
-// position pos, so no workgroup reads a row another is writing.
+// position pos, so no workgroup adds a value another is writing (a V tile
+// may hold the bytes of row pos mid-write; only rows below pos are added).
+constexpr int kVTile = 16384;  // bytes of V per LDS tile
+
 template <int HD, bool F16>
 __device__ __forceinline__ void attn(const ExactAttnArgs& a) {
   constexpr int MID = HD / 2;
@@ -256,10 +293,33 @@ __device__ __forceinline__ void attn(const ExactAttnArgs& a) {
   __shared__ float s_v[HD];
   __shared__ float s_red[kT / LLMRS_WAVE];
   __shared__ float s_inv;
+  __shared__ __align__(16) u32x4 s_vt[2][kVTile / 16];  // V tiles
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int h = blockIdx.x, n_rep = a.nq / a.nkv, g = h / n_rep;
   const int pos = *a.pos_ptr, T = pos + 1;
   const size_t head = (size_t)g * a.max_seq * HD;
+  // V rows 0..pos-1 pass through LDS in 16 KB tiles that every thread loads
+  // (coalesced); the first tile is requested now, each later one while the
+  // previous one is added.
+  constexpr int VB = F16 ? 2 : 4;
+  constexpr int TP = kVTile / (HD * VB);    // positions per tile, a multiple of 8
+  constexpr int LPT = kVTile / 16 / kT;     // 16-byte loads per thread per tile
+  const char* vbase = (const char*)a.vc + head * VB;
+  const size_t head_bytes = (size_t)a.max_seq * HD * VB;
+  const int ntile = (pos + TP - 1) / TP;
+  u32x4 st[LPT];
+  auto vload = [&](int tile) {  // rows past pos read stale (in-bounds) bytes, never added
+#pragma unroll
+    for (int l = 0; l < LPT; ++l) {
+      const size_t off = min((size_t)tile * kVTile + 16 * (size_t)(tid + kT * l), head_bytes - 16);
+      st[l] = *(const u32x4*)(vbase + off);
+    }
+  };
+  auto vstore = [&](int buf) {
+#pragma unroll
+    for (int l = 0; l < LPT; ++l) s_vt[buf][tid + kT * l] = st[l];
+  };
+  if (ntile > 0) vload(0);
   if (tid < MID) {  // rotate-half RoPE of q and the new k (cpu.rs:345-354)
     const float co = a.rope_cos[(size_t)pos * MID + tid], sn = a.rope_sin[(size_t)pos * MID + tid];
     const float* q = a.qkv + (size_t)h * HD;
@@ -343,31 +403,41 @@ __device__ __forceinline__ void attn(const ExactAttnArgs& a) {
   __syncthreads();
   const float inv = s_inv;
   for (int t = tid; t < T; t += kT) s_p[t] = s_p[t] * inv;
+  if (ntile > 0) vstore(0);
   __syncthreads();
-  if (tid < HD) {  // ctx[d] = sum over t of p_t * V[t][d], sequential in t
-    const int d = tid;
-    float s = 0.0f;
-    int t = 0;
-    if (F16) {  // blocked V: the 8 positions of a block are 16 contiguous bytes per dim
-      const uint16_t* vr = (const uint16_t*)a.vc + head;
-      for (; t + 8 <= pos; t += 8) {
-        const u32x4 w = *(const u32x4*)(vr + v_offset(t, d, HD, true));
+  // ctx[d] = sum over t of p_t * V[t][d], sequential in t; the new row last.
+  const int d = tid;
+  float acc = 0.0f;
+  for (int i = 0; i < ntile; ++i) {
+    if (i + 1 < ntile) vload(i + 1);
+    if (d < HD) {
+      const int t0 = i * TP, t1 = min(t0 + TP, pos);
+      if (F16) {  // blocked V: the 8 positions of a block are 16 contiguous bytes per dim
+        const uint16_t* vt = (const uint16_t*)s_vt[i & 1];
+        int t = t0;
+        for (; t + 8 <= t1; t += 8) {
+          const u32x4 w = *(const u32x4*)(vt + ((t - t0) / 8 * HD + d) * 8);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s = s + s_p[t + 2 * i] * h2f((uint16_t)(w[i] & 0xFFFF));
-          s = s + s_p[t + 2 * i + 1] * h2f((uint16_t)(w[i] >> 16));
+          for (int e = 0; e < 4; ++e) {
+            acc = acc + s_p[t + 2 * e] * h2f((uint16_t)(w[e] & 0xFFFF));
+            acc = acc + s_p[t + 2 * e + 1] * h2f((uint16_t)(w[e] >> 16));
+          }
         }
+        for (; t < t1; ++t) acc = acc + s_p[t] * h2f(vt[((t - t0) / 8 * HD + d) * 8 + (t & 7)]);
+      } else {
+        const float* vt = (const float*)s_vt[i & 1];
+        for (int t = t0; t < t1; ++t) acc = acc + s_p[t] * vt[(t - t0) * HD + d];
       }
-      for (; t < pos; ++t) s = s + s_p[t] * h2f(vr[v_offset(t, d, HD, true)]);
-    } else {
-      const float* vr = (const float*)a.vc + head;
-      for (; t < pos; ++t) s = s + s_p[t] * vr[(size_t)t * HD + d];
     }
-    s = s + s_p[pos] * s_v[d];
+    if (i + 1 < ntile) vstore((i + 1) & 1);
+    __syncthreads();
+  }
+  if (d < HD) {
+    acc = acc + s_p[pos] * s_v[d];
     const size_t e = (size_t)h * HD + d;
-    a.ctx[e] = s;
+    a.ctx[e] = acc;
     float dq;
-    const int q = q8_group32(s, &dq);
+    const int q = q8_group32(acc, &dq);
     a.ctx_q[e] = (int8_t)q;
     if ((d & 31) == 0) a.ctx_d[e >> 5] = dq;
   }
