@@ -7,9 +7,11 @@
 //
 // MI355X design: M <= 64 activation rows (the sequences of a batch) against
 // a weight streamed once.  One v_mfma_i32_16x16x32_i8 per block gives the 16
-// rows x 16 tokens of exact block sums; the epilogue scales them in f32 as
-// the reference does (per output: the scale product, then the multiply, then
-// the add).  Lane (r, g) of a wave (r = lane % 16, g = lane / 16) loads 16
+// rows x 16 tokens of exact block sums, and one v_mfma_f32_16x16x1_4b_f32 per
+// four blocks every scale product d_w * d_a of the 16 x 16 tile as a single
+// IEEE product (lane 16 b + i supplies row / token i of block b; block b's
+// products sit in registers 4 b .. 4 b + 3 in the layout of the block sums);
+// the epilogue then multiplies and adds in f32 as the reference does.  Lane (r, g) of a wave (r = lane % 16, g = lane / 16) loads 16
 // bytes: one Q4 block of weight row r (four blocks per lane group), so each
 // load instruction reads 64 contiguous bytes of each of 16 rows; a 4x4 dword
 // transpose across the lane groups (v_permlane32_swap, v_permlane16_swap)
@@ -23,12 +25,15 @@
 // Batched decode: a wave takes RT 16-row tiles, which share its activation
 // operands (the activation bytes a group loads are twice its weight bytes
 // per tile): two, or one for the residual projections, whose few rows would
-// leave too few workgroups.  Workgroups of four waves.  STORE / RESID: 16 RT
-// weight rows per workgroup, the blocks split over the waves in contiguous
-// quarters, partial sums added in wave order.  SILU: 64 rows per workgroup -
-// a run of 32 gate and 32 up rows - two waves per 32 rows, each half of the
-// blocks; m = silu(gate) * up and its Q8_0 codes (one 32-element block per
-// run) in the operand order of the down projection.
+// leave too few workgroups.  A workgroup holds RS row sets of RT tiles and
+// splits the blocks of each over KP waves in contiguous parts, partial sums
+// added in part order.  STORE / RESID: one row set, KP = 4.  SILU: 64 rows
+// per workgroup - a run of 32 gate and 32 up rows, one row set each, KP = 2;
+// m = silu(gate) * up and its Q8_0 codes (one 32-element block per run) in
+// the operand order of the down projection.  (Same box, 8B: eight waves per
+// workgroup with twice the parts were slower at B = 16 and 64, e.g. the
+// SwiGLU launch 42.8 vs 39.7 us; plain instead of streaming weight loads
+// changed nothing.)
 //
 // EXACT launches (prompt prefill) give each output row's blocks to one wave
 // in order, as the reference adds them, so the result is bit-identical to
@@ -45,7 +50,7 @@ using namespace llmrs;
 
 namespace {
 
-constexpr int kT = 256;
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 // q - 8 for four nibbles held one per byte (0..15): (v + 0x78) ^ 0x80 per
 // byte, no carry between bytes.
@@ -75,11 +80,9 @@ template <int WT, int TT, int RT>
 struct Group {
   u32x4 w[RT];          // Q4: this lane's block of each row tile (transposed after arrival)
   unsigned w8[RT][4][2];  // Q8: dwords g and g + 4 of each block
-  // scales of 4 blocks of output row (lane % 4) of this lane's four per row
-  // tile (fp16 pairs or f32 bits); the other rows' come from the quad (DPP)
-  unsigned dw[RT][WT == WT_Q4F ? 4 : 2];
+  unsigned dw[RT];       // raw scale of (row lane % 16, block lane / 16) per row tile
   u32x4 x[TT][2];       // activation operands of 4 blocks, per token tile
-  f32x4 da[TT];         // activation scales of 4 blocks, per token tile
+  float da[TT];         // scale of (token lane % 16, block lane / 16) per token tile
 };
 
 // Loads of group q for the wave's rows n0 .. n0 + 16 RT - 1.
@@ -99,16 +102,7 @@ __device__ __forceinline__ void load_group(Group<WT, TT, RT>& G, const SgemmArgs
     } else {
       G.w[rt] = __builtin_nontemporal_load((const u32x4*)(a.wq + ((size_t)wrow * nb + 4 * q + g) * 16));
     }
-    const size_t s = (size_t)min(n0 + 16 * rt + 4 * g + (tok & 3), a.N - 1) * nb + 4 * q;
-    if (WT == WT_Q4F) {
-      const u32x4 v = *(const u32x4*)((const float*)a.ws + s);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) G.dw[rt][j] = v[j];
-    } else {
-      const uint2 v = *(const uint2*)((const uint16_t*)a.ws + s);
-      G.dw[rt][0] = v.x;
-      G.dw[rt][1] = v.y;
-    }
+    G.dw[rt] = load_wscale_raw<WT>(a.ws, (size_t)wrow * nb + 4 * q + g);
   }
 #pragma unroll
   for (int tt = 0; tt < TT; ++tt) {
@@ -116,68 +110,46 @@ __device__ __forceinline__ void load_group(Group<WT, TT, RT>& G, const SgemmArgs
     const u32x4* xp = (const u32x4*)(a.xq + (size_t)t * a.K + (size_t)q * 128 + g * 32);
     G.x[tt][0] = xp[0];
     G.x[tt][1] = xp[1];
-    G.da[tt] = *(const f32x4*)(a.xd + (size_t)t * nb + 4 * q);
+    G.da[tt] = a.xd[(size_t)t * nb + 4 * q + g];
   }
-}
-
-// Lane i of the lane's quad (DPP quad_perm [i, i, i, i]).
-template <int I>
-__device__ __forceinline__ unsigned quad_bcast(unsigned v) {
-  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, I * 0x55, 0xF, 0xF, false);
 }
 
 // One group's MFMAs and epilogue into acc[rt][tt][i] (output row n0 + 16 rt
 // + 4 g + i, token 16 tt + tok).
 template <int WT, int TT, int RT>
 __device__ __forceinline__ void compute_group(Group<WT, TT, RT>& G, f32x4 (&acc)[RT][TT]) {
-  constexpr int ND = WT == WT_Q4F ? 4 : 2;
-  unsigned sc[RT][4][ND];
-  unsigned wd[RT][4];
+  long op_a[RT][4];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
+    if (WT == WT_Q8H) {
 #pragma unroll
-    for (int d = 0; d < ND; ++d) {
-      sc[rt][0][d] = quad_bcast<0>(G.dw[rt][d]);
-      sc[rt][1][d] = quad_bcast<1>(G.dw[rt][d]);
-      sc[rt][2][d] = quad_bcast<2>(G.dw[rt][d]);
-      sc[rt][3][d] = quad_bcast<3>(G.dw[rt][d]);
-    }
-    if (WT != WT_Q8H) {
+      for (int j = 0; j < 4; ++j)
+        op_a[rt][j] = (long)((unsigned long long)G.w8[rt][j][0] | ((unsigned long long)G.w8[rt][j][1] << 32));
+    } else {
+      unsigned wd[4] = {G.w[rt][0], G.w[rt][1], G.w[rt][2], G.w[rt][3]};
+      transpose4(wd);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wd[rt][j] = G.w[rt][j];
-      transpose4(wd[rt]);
+      for (int j = 0; j < 4; ++j) {
+        const unsigned lo = nib_s8(wd[j] & 0x0F0F0F0Fu), hi = nib_s8((wd[j] >> 4) & 0x0F0F0F0Fu);
+        op_a[rt][j] = (long)((unsigned long long)lo | ((unsigned long long)hi << 32));
+      }
     }
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    long op_a[RT];
-    float dw[RT][4];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      if (WT == WT_Q8H) {
-        op_a[rt] = (long)((unsigned long long)G.w8[rt][j][0] | ((unsigned long long)G.w8[rt][j][1] << 32));
-      } else {
-        const unsigned lo = nib_s8(wd[rt][j] & 0x0F0F0F0Fu), hi = nib_s8((wd[rt][j] >> 4) & 0x0F0F0F0Fu);
-        op_a[rt] = (long)((unsigned long long)lo | ((unsigned long long)hi << 32));
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dw[rt][i] = WT == WT_Q4F ? __uint_as_float(sc[rt][i][j])
-                                 : h2f((uint16_t)(sc[rt][i][j >> 1] >> (16 * (j & 1))));
-    }
+  for (int rt = 0; rt < RT; ++rt) {
+    const float dw = wscale<WT>(G.dw[rt]);
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
-      const unsigned b0 = G.x[tt][j >> 1][2 * (j & 1)], b1 = G.x[tt][j >> 1][2 * (j & 1) + 1];
-      const long op_b = (long)((unsigned long long)b0 | ((unsigned long long)b1 << 32));
-      const float da = G.da[tt][j];
+      // sc[4 j + i] = fl(d_w * d_a) of block j, row 4 g + i, token tok
+      const v16f sc = __builtin_amdgcn_mfma_f32_16x16x1f32(dw, G.da[tt], v16f{}, 0, 0, 0);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const i32x4 isum = __builtin_amdgcn_mfma_i32_16x16x32_i8(op_a[rt], op_b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+      for (int j = 0; j < 4; ++j) {
+        const unsigned b0 = G.x[tt][j >> 1][2 * (j & 1)], b1 = G.x[tt][j >> 1][2 * (j & 1) + 1];
+        const long op_b = (long)((unsigned long long)b0 | ((unsigned long long)b1 << 32));
+        const i32x4 isum = __builtin_amdgcn_mfma_i32_16x16x32_i8(op_a[rt][j], op_b, i32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float sc2 = dw[rt][i] * da;                         // fl(d_w * d_a)
-          acc[rt][tt][i] = acc[rt][tt][i] + (float)isum[i] * sc2;   // cpu.rs:930-935
-        }
+        for (int i = 0; i < 4; ++i)  // cpu.rs:930-935
+          acc[rt][tt][i] = acc[rt][tt][i] + (float)isum[i] * sc[4 * j + i];
       }
     }
   }
@@ -218,39 +190,35 @@ __device__ __forceinline__ void run_groups(const SgemmArgs& a, int q0, int q1, i
   }
 }
 
-// EXACT: every output's blocks in order in one wave, as the reference adds
-// them (bit-identical to it for the same activation codes; prompt prefill).
-// Otherwise the blocks are split over the waves of a workgroup and the
-// partial sums added in wave order (batched decode: more workgroups).
-template <int WT, int EPI, int TT, bool EXACT>
+// Workgroup shape: RS row sets of RT 16-row tiles, each row set's blocks
+// split over KP waves (EXACT: KP = 1, every output's blocks in order in one
+// wave, as the reference adds them - bit-identical to it for the same
+// activation codes; prompt prefill).
+template <int EPI, bool EXACT, int KP>
+struct SgemmShape {
+  static constexpr int RT = EXACT || EPI == EPI_RESID ? 1 : 2;
+  static constexpr int RS = EPI == EPI_SILU ? 64 / (16 * RT) : 1;
+  static constexpr int WAVES = RS * KP;
+  static constexpr int THREADS = 64 * WAVES;
+  static_assert(!EXACT || KP == 1, "exact launches keep every output's blocks in one wave");
+};
+
+template <int WT, int EPI, int TT, bool EXACT, int KP>
 __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
-  // row tiles per wave: one for the residual projections (O, down: few
-  // rows, so the workgroups stay many) and in EXACT mode, two otherwise
-  constexpr int RT = EXACT || EPI == EPI_RESID ? 1 : 2;
-  __shared__ f32x4 s_acc[4][RT][TT][64];
+  typedef SgemmShape<EPI, EXACT, KP> S;
+  constexpr int RT = S::RT, RS = S::RS;
+  __shared__ f32x4 s_acc[S::WAVES][RT][TT][64];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int nb = a.K >> 5, ngroups = nb >> 2;
+  const int rs = w / KP, kp = w % KP;
   f32x4 acc[RT][TT];
-  if (EPI == EPI_SILU) {
-    if (EXACT) {
-      // waves 0, 1: the run's gate rows 0-15, 16-31; 2, 3: its up rows
-      run_groups<WT, TT, RT>(a, 0, ngroups, blockIdx.x * 64 + 16 * w, r, nb, g, acc);
-    } else {
-      // waves 0, 1: the run's 32 gate rows, 2, 3: its 32 up rows; each pair
-      // splits the blocks in halves
-      const int n0 = blockIdx.x * 64 + 32 * (w >> 1), ks = w & 1;
-      run_groups<WT, TT, RT>(a, ks * ngroups / 2, (ks + 1) * ngroups / 2, n0, r, nb, g, acc);
-    }
-  } else if (EXACT) {
-    // one wave per workgroup (64 threads): 16 rows over all blocks
-    run_groups<WT, TT, RT>(a, 0, ngroups, blockIdx.x * 16, r, nb, g, acc);
-  } else {
-    run_groups<WT, TT, RT>(a, w * ngroups / 4, (w + 1) * ngroups / 4, blockIdx.x * 16 * RT, r, nb, g, acc);
-  }
+  // row set rs: rows n0 .. n0 + 16 RT - 1 (SILU: the run's gate rows, then its up rows)
+  const int n0 = blockIdx.x * (16 * RT * RS) + 16 * RT * rs;
+  run_groups<WT, TT, RT>(a, kp * ngroups / KP, (kp + 1) * ngroups / KP, n0, r, nb, g, acc);
 
   if (EPI != EPI_SILU && EXACT) {
-    const int row0 = blockIdx.x * 16 + 4 * g;
+    const int row0 = n0 + 4 * g;
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       const int t = 16 * tt + r;
@@ -279,17 +247,16 @@ __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
     // pass; Q8_0 of the 32 elements of a token (one block of m)
     const int run = blockIdx.x;
     const int j = tid & 31;
-    // gate row j of the run: row tile (or, EXACT, wave), lane group, register
-    const int rt = j >> 4, gg = (j & 15) >> 2, ii = j & 3;
-    for (int t0 = tid >> 5; t0 < 16 * TT; t0 += kT / 32) {
+    // gate row j of the run: row set, row tile, lane group, register; the
+    // matching up row sits RS / 2 row sets later
+    const int gs = j / (16 * RT), rt = (j >> 4) % RT, gg = (j & 15) >> 2, ii = j & 3;
+    for (int t0 = tid >> 5; t0 < 16 * TT; t0 += S::THREADS / 32) {
       const int tt = t0 >> 4, l = 16 * gg + (t0 & 15);
-      float gv, uv;
-      if (EXACT) {
-        gv = s_acc[rt][0][tt][l][ii];
-        uv = s_acc[2 + rt][0][tt][l][ii];
-      } else {
-        gv = s_acc[0][rt][tt][l][ii] + s_acc[1][rt][tt][l][ii];
-        uv = s_acc[2][rt][tt][l][ii] + s_acc[3][rt][tt][l][ii];
+      float gv = s_acc[gs * KP][rt][tt][l][ii], uv = s_acc[(RS / 2 + gs) * KP][rt][tt][l][ii];
+#pragma unroll
+      for (int k = 1; k < KP; ++k) {
+        gv = gv + s_acc[gs * KP + k][rt][tt][l][ii];
+        uv = uv + s_acc[(RS / 2 + gs) * KP + k][rt][tt][l][ii];
       }
       const float mv = (gv / (1.0f + expf(-gv))) * uv;
       float amax = fabsf(mv);
@@ -310,13 +277,13 @@ __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
   if (w != 0) return;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const int row0 = blockIdx.x * 16 * RT + 16 * rt + 4 * g;
+    const int row0 = n0 + 16 * rt + 4 * g;
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       const int t = 16 * tt + r;
       f32x4 v = s_acc[0][rt][tt][lane];
 #pragma unroll
-      for (int k = 1; k < 4; ++k) v = v + s_acc[k][rt][tt][lane];
+      for (int k = 1; k < KP; ++k) v = v + s_acc[k][rt][tt][lane];
       if (t < a.M) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -334,21 +301,24 @@ __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
 
 }  // namespace
 
-#define LLMRS_SGEMM(name, WT, EPI, TT, EXACT) \
-  extern "C" __global__ __launch_bounds__(kT) void name(SgemmArgs a) { sgemm_impl<WT, EPI, TT, EXACT>(a); }
-#define LLMRS_SGEMM_TILES(tag, WT, EPI)                \
-  LLMRS_SGEMM(sgemm_##tag##_t1, WT, EPI, 1, false)     \
-  LLMRS_SGEMM(sgemm_##tag##_t2, WT, EPI, 2, false)     \
-  LLMRS_SGEMM(sgemm_##tag##_t4, WT, EPI, 4, false)     \
-  LLMRS_SGEMM(sgemm_##tag##_t1_exact, WT, EPI, 1, true) \
-  LLMRS_SGEMM(sgemm_##tag##_t2_exact, WT, EPI, 2, true) \
-  LLMRS_SGEMM(sgemm_##tag##_t4_exact, WT, EPI, 4, true)
-LLMRS_SGEMM_TILES(q4h_store, WT_Q4H, EPI_STORE)
-LLMRS_SGEMM_TILES(q4h_resid, WT_Q4H, EPI_RESID)
-LLMRS_SGEMM_TILES(q4h_silu, WT_Q4H, EPI_SILU)
-LLMRS_SGEMM_TILES(q4f_store, WT_Q4F, EPI_STORE)
-LLMRS_SGEMM_TILES(q4f_resid, WT_Q4F, EPI_RESID)
-LLMRS_SGEMM_TILES(q4f_silu, WT_Q4F, EPI_SILU)
-LLMRS_SGEMM_TILES(q8h_store, WT_Q8H, EPI_STORE)
-LLMRS_SGEMM_TILES(q8h_resid, WT_Q8H, EPI_RESID)
-LLMRS_SGEMM_TILES(q8h_silu, WT_Q8H, EPI_SILU)
+// Kernels: sgemm_<weights>_<epilogue>_t<token tiles>[_exact].
+#define LLMRS_SGEMM(name, WT, EPI, TT, EXACT, KP)                                               \
+  extern "C" __global__ __launch_bounds__((SgemmShape<EPI, EXACT, KP>::THREADS)) void name(SgemmArgs a) { \
+    sgemm_impl<WT, EPI, TT, EXACT, KP>(a);                                                        \
+  }
+#define LLMRS_SGEMM_TILES(tag, WT, EPI, KP)                            \
+  LLMRS_SGEMM(sgemm_##tag##_t1, WT, EPI, 1, false, KP)                 \
+  LLMRS_SGEMM(sgemm_##tag##_t2, WT, EPI, 2, false, KP)                 \
+  LLMRS_SGEMM(sgemm_##tag##_t4, WT, EPI, 4, false, KP)                 \
+  LLMRS_SGEMM(sgemm_##tag##_t1_exact, WT, EPI, 1, true, 1)             \
+  LLMRS_SGEMM(sgemm_##tag##_t2_exact, WT, EPI, 2, true, 1)             \
+  LLMRS_SGEMM(sgemm_##tag##_t4_exact, WT, EPI, 4, true, 1)
+LLMRS_SGEMM_TILES(q4h_store, WT_Q4H, EPI_STORE, 4)
+LLMRS_SGEMM_TILES(q4h_resid, WT_Q4H, EPI_RESID, 4)
+LLMRS_SGEMM_TILES(q4h_silu, WT_Q4H, EPI_SILU, 2)
+LLMRS_SGEMM_TILES(q4f_store, WT_Q4F, EPI_STORE, 4)
+LLMRS_SGEMM_TILES(q4f_resid, WT_Q4F, EPI_RESID, 4)
+LLMRS_SGEMM_TILES(q4f_silu, WT_Q4F, EPI_SILU, 2)
+LLMRS_SGEMM_TILES(q8h_store, WT_Q8H, EPI_STORE, 4)
+LLMRS_SGEMM_TILES(q8h_resid, WT_Q8H, EPI_RESID, 4)
+LLMRS_SGEMM_TILES(q8h_silu, WT_Q8H, EPI_SILU, 2)
