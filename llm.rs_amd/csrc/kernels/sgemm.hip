@@ -135,23 +135,32 @@ __device__ __forceinline__ void compute_group(Group<WT, TT, RT>& G, f32x4 (&acc)
       }
     }
   }
+  // Per token tile every MFMA first, then the epilogue: an MFMA result read
+  // right after its issue would stall the wave for the MFMA's latency.
+  float dw[RT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const float dw = wscale<WT>(G.dw[rt]);
+  for (int rt = 0; rt < RT; ++rt) dw[rt] = wscale<WT>(G.dw[rt]);
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-      // sc[4 j + i] = fl(d_w * d_a) of block j, row 4 g + i, token tok
-      const v16f sc = __builtin_amdgcn_mfma_f32_16x16x1f32(dw, G.da[tt], v16f{}, 0, 0, 0);
+  for (int tt = 0; tt < TT; ++tt) {
+    v16f sc[RT];  // sc[rt][4 j + i] = fl(d_w * d_a) of block j, row 4 g + i, token tok
+    i32x4 isum[RT][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const unsigned b0 = G.x[tt][j >> 1][2 * (j & 1)], b1 = G.x[tt][j >> 1][2 * (j & 1) + 1];
-        const long op_b = (long)((unsigned long long)b0 | ((unsigned long long)b1 << 32));
-        const i32x4 isum = __builtin_amdgcn_mfma_i32_16x16x32_i8(op_a[rt][j], op_b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+    for (int rt = 0; rt < RT; ++rt) sc[rt] = __builtin_amdgcn_mfma_f32_16x16x1f32(dw[rt], G.da[tt], v16f{}, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const unsigned b0 = G.x[tt][j >> 1][2 * (j & 1)], b1 = G.x[tt][j >> 1][2 * (j & 1) + 1];
+      const long op_b = (long)((unsigned long long)b0 | ((unsigned long long)b1 << 32));
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        isum[rt][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(op_a[rt][j], op_b, i32x4{0, 0, 0, 0}, 0, 0, 0);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i)  // cpu.rs:930-935
-          acc[rt][tt][i] = acc[rt][tt][i] + (float)isum[i] * sc[4 * j + i];
-      }
-    }
+          acc[rt][tt][i] = acc[rt][tt][i] + (float)isum[rt][j][i] * sc[rt][4 * j + i];
   }
 }
 
@@ -181,13 +190,19 @@ __device__ __forceinline__ void run_groups(const SgemmArgs& a, int q0, int q1, i
   Group<WT, TT, RT> ring[PF];
 #pragma unroll
   for (int s = 0; s < PF; ++s) load_group<WT, TT, RT>(ring[s], a, min(q0 + s, q1 - 1), n0, tok, nb, g);
-  for (int q = q0; q < q1; q += PF) {
+  // Whole rounds of PF groups without a branch (one block the scheduler can
+  // interleave), then the last partial round from the ring.
+  int q = q0;
+  for (; q + PF <= q1; q += PF) {
 #pragma unroll
     for (int s = 0; s < PF; ++s) {
-      if (q + s < q1) compute_group<WT, TT, RT>(ring[s], acc);
+      compute_group<WT, TT, RT>(ring[s], acc);
       load_group<WT, TT, RT>(ring[s], a, min(q + s + PF, q1 - 1), n0, tok, nb, g);
     }
   }
+#pragma unroll
+  for (int s = 0; s < PF - 1; ++s)
+    if (q + s < q1) compute_group<WT, TT, RT>(ring[s], acc);
 }
 
 // Workgroup shape: RS row sets of RT 16-row tiles, each row set's blocks
