@@ -511,11 +511,13 @@ constexpr int kExactMaxRows = 16384;
 int exact_gemv_cap() { return 8 * ctx().num_cus; }
 unsigned exact_gemv_grid(int n) { return (unsigned)std::max(1, std::min((n + 7) / 8, exact_gemv_cap())); }
 
+// RMSNorm + Q8_0 of `rows` rows of hidden floats (one workgroup each; the
+// codes in the operand order `layout`).
 void exact_norm(llmrs_model* m, Launcher& L, const float* x, const float* w, int8_t* xq, float* xd,
-                float* y = nullptr) {
+                float* y = nullptr, int rows = 1, int layout = llmrs::kActNatural) {
   const int H = m->c.hidden;
-  ExactNormArgs a{x, w, xq, xd, y, H, m->c.rms_eps};
-  L("exact_norm_q8", 9.125 * H, dim3(1), dim3(256), (size_t)H * 4, a);
+  ExactNormArgs a{x, w, xq, xd, y, H, m->c.rms_eps, layout};
+  L("exact_norm_q8", 9.125 * H * rows, dim3((unsigned)rows), dim3(256), (size_t)H * 4, a);
 }
 
 void exact_linear(llmrs_model* m, Launcher& L, const DevLinear& W, const char* epi, const int8_t* xq,
@@ -636,6 +638,7 @@ void set_exact(llmrs_model* m, bool on) {
     (void)kernel("exact_norm_q8");
     (void)kernel("exact_silu_q8");
     (void)kernel("exact_attn_hd" + std::to_string(c.head_dim) + (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32"));
+    (void)kernel("exact_attn_prefill_hd" + std::to_string(c.head_dim) + (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32"));
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));
   }
   if (m->exact != on) {  // the captured step changes
@@ -724,8 +727,12 @@ struct PrefillProbe {
 // K/V append, 3 causal attention, 4 O GEMM + residual, 5 RMSNorm+Q8,
 // 6 gate|up GEMM + SwiGLU + Q8, 7 down GEMM + residual.  The recorded figure
 // per launch is its FLOPs for the GEMMs and attention, bytes for the rest.
+// exact: the RMSNorms and the attention on the reference-order kernels
+// (exact.hip; the GEMMs, the RoPE / append and the SwiGLU epilogue already
+// compute the reference's values), so every row equals the reference's.
 void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, int M,
-                           const PrefillProbe* probe = nullptr, void* kc = nullptr, void* vc = nullptr) {
+                           const PrefillProbe* probe = nullptr, void* kc = nullptr, void* vc = nullptr,
+                           bool exact = false) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden, hd = c.head_dim, nq = c.n_heads, nkv = c.n_kv_heads, F = c.ffn;
   const int QR = m->qkv_rows;
@@ -765,7 +772,9 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
       L(gemm_kernel(m, epi), work, gemm_grid(M, W.n), blk, glds, g);
     }
   };
-  {  // RMSNorm + Q8_0 of each row (layer.rs:378; cpu.rs:90-93)
+  if (exact) {  // RMSNorm + Q8_0 of each row (layer.rs:378; cpu.rs:90-93)
+    exact_norm(m, L, m->pf_x, Lb.norm[0], m->pf_aq, m->pf_ad, nullptr, M, layout);
+  } else {
     PrefillRowArgs r{m->pf_x, Lb.norm[0], m->pf_aq, m->pf_ad, M, H, c.rms_eps, layout};
     L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
   }
@@ -783,7 +792,10 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
   {  // causal attention
     PrefillAttnArgs a{m->pf_q, kc, vc, probe ? probe->ctx : nullptr, m->pf_ctx_q, m->pf_ctx_d, M, nq,
                       nkv, kv_rows(m), (int)start, scale, layout};
-    if (mfma_attn)
+    if (exact)  // one workgroup per (query head, row); the scores of up to start + M positions in LDS
+      L("exact_attn_prefill_hd" + std::to_string(hd) + (kv16 ? "_f16" : "_f32"), attn_flops,
+        dim3((unsigned)nq, (unsigned)M), blk, (start + M) * 4, a);
+    else if (mfma_attn)
       L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nkv), dim3(512), 0, a);
     else
       L(attn, attn_flops, dim3((unsigned)((M + 31) / 32), (unsigned)nq), blk, 0, a);
@@ -791,7 +803,9 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
   after(3);
   linear("resid", Lb.o, m->pf_ctx_q, m->pf_ctx_d, m->pf_h, m->pf_x, nullptr, nullptr, H);  // O + residual
   after(4);
-  {  // post-attention RMSNorm + Q8_0
+  if (exact) {  // post-attention RMSNorm + Q8_0
+    exact_norm(m, L, m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, nullptr, M, layout);
+  } else {
     PrefillRowArgs r{m->pf_h, Lb.norm[1], m->pf_aq, m->pf_ad, M, H, c.rms_eps, layout};
     L("prefill_rows_q8", 5.0 * H * M, dim3((unsigned)M), blk, gemv_act_lds_host(H), r);
   }
@@ -808,7 +822,7 @@ void enqueue_prefill_layer(llmrs_model* m, Launcher& L, int li, size_t start, in
 // at the device position.  trace_dev, when set, is
 // [M][n_layers+1][hidden].
 void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head, bool write_logits,
-                     float* trace_dev, void* const* kcs = nullptr, void* const* vcs = nullptr) {
+                     float* trace_dev, void* const* kcs = nullptr, void* const* vcs = nullptr, bool exact = false) {
   const llmrs_model_config& c = m->c;
   const int H = c.hidden;
   auto trace = [&](int li) {
@@ -822,10 +836,14 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
   L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), dim3(256), 0, e);
   for (int li = 0; li < c.n_layers; ++li) {
     trace(li);
-    enqueue_prefill_layer(m, L, li, start, M, nullptr, kcs ? kcs[li] : nullptr, vcs ? vcs[li] : nullptr);
+    enqueue_prefill_layer(m, L, li, start, M, nullptr, kcs ? kcs[li] : nullptr, vcs ? vcs[li] : nullptr, exact);
   }
   trace(c.n_layers);
-  if (head) {
+  if (head && exact) {  // the last row on the reference-order head
+    LLMRS_HIP(hipMemcpyAsync(m->x, m->pf_x + (size_t)(M - 1) * H, H * sizeof(float), hipMemcpyDeviceToDevice,
+                             L.s));
+    enqueue_exact_head(m, L, write_logits);
+  } else if (head) {
     if (m->nq_x) {
       enqueue_embed(m, L, m->pf_x + (size_t)(M - 1) * H, m->final_norm);
     } else {
@@ -848,6 +866,7 @@ void run_prefill(llmrs_model* m, size_t start, size_t n, int n_prompt, bool writ
   ensure_prefill(m);
   const llmrs_model_config& c = m->c;
   const size_t rowf = (size_t)(c.n_layers + 1) * c.hidden;
+  const bool exact = m->exact && !kcs;  // a batch slot's prompt stays on the fast kernels
   float* tdev = nullptr;
   if (trace) {
     LLMRS_HIP(hipMalloc(&tdev, std::min<size_t>(n, m->pf_cap) * rowf * sizeof(float)));
@@ -860,7 +879,7 @@ void run_prefill(llmrs_model* m, size_t start, size_t n, int n_prompt, bool writ
       LLMRS_HIP(hipMemcpyAsync(m->pf_start, &s0, sizeof(int), hipMemcpyHostToDevice, ctx().stream));
       set_state(m, start + done + M - 1, n_prompt);  // synchronises the stream
       Launcher L{ctx().stream};
-      enqueue_prefill(m, L, start + done, M, last, write_logits && last, tdev, kcs, vcs);
+      enqueue_prefill(m, L, start + done, M, last, write_logits && last, tdev, kcs, vcs, exact);
       if (trace) {
         LLMRS_HIP(hipMemcpyAsync(trace + done * rowf, tdev, (size_t)M * rowf * sizeof(float),
                                  hipMemcpyDeviceToHost, ctx().stream));
@@ -1320,7 +1339,7 @@ int llmrs_model_forward(llmrs_model* m, const int32_t* tokens, size_t n, size_t 
     const size_t H = m->c.hidden, L = m->c.n_layers;
     upload_tokens(m, start_pos, tokens, n);
     hipStream_t s = ctx().stream;
-    const bool batched = n > 1 && prefill_enabled() && !m->exact;
+    const bool batched = n > 1 && prefill_enabled();
     if (batched)
       run_prefill(m, start_pos, n, INT_MAX, logits != nullptr, trace);
     else
@@ -1354,7 +1373,7 @@ int llmrs_model_begin_at(llmrs_model* m, const int32_t* prompt, size_t n_prompt,
     upload_tokens(m, start_pos, prompt, n_prompt);
     set_state(m, start_pos, (int)end);
     m->host_n_prompt = (int)end;
-    if (n_prompt > 1 && prefill_enabled() && !m->exact) {
+    if (n_prompt > 1 && prefill_enabled()) {
       run_prefill(m, start_pos, n_prompt, (int)end, false, nullptr);
     } else {
       for (size_t p = start_pos; p < end; ++p) {
@@ -1609,7 +1628,8 @@ int llmrs_model_profile_prefill(llmrs_model* m, const int32_t* tokens, size_t n,
     LLMRS_HIP(hipMemcpyAsync(m->pf_start, &s0, sizeof(int), hipMemcpyHostToDevice, ctx().stream));
     set_state(m, start_pos + n - 1, INT_MAX);
     count = profile_launches(
-        [&](Launcher& L) { enqueue_prefill(m, L, start_pos, (int)n, true, false, nullptr); }, names, ms,
+        [&](Launcher& L) { enqueue_prefill(m, L, start_pos, (int)n, true, false, nullptr, nullptr, nullptr, m->exact); },
+        names, ms,
         work, cap);
     check_err(m);
     m->host_pos = start_pos + n;
@@ -1888,7 +1908,7 @@ int llmrs_model_probe_prefill_layer(llmrs_model* m, int layer, size_t start_pos,
       LLMRS_HIP(hipStreamSynchronize(s));
     };
     Launcher L{s};
-    enqueue_prefill_layer(m, L, layer, start_pos, (int)M, &p);
+    enqueue_prefill_layer(m, L, layer, start_pos, (int)M, &p, nullptr, nullptr, m->exact);
     if (prefill_skinny(m, (int)M)) {  // codes back into element order
       auto natural = [&](int8_t* rows, size_t K) {
         if (!rows) return;

@@ -321,14 +321,16 @@ struct PrefillAttnArgs {
 // 256-byte line of its own, so the heads' atomics do not queue on one line.
 constexpr int kTicketStride = 64;
 // Reference-order decode kernels (exact.hip).
+// One workgroup per row (grid.x rows, row r at offset r * n).
 struct ExactNormArgs {
-  const float* x;        // [n] input row
+  const float* x;        // [rows][n] input rows
   const float* w;        // [n] RMSNorm weight
-  int8_t* xq;            // [n] Q8_0 codes of the normed row
-  float* xd;             // [n/32] their scales
-  float* y;              // [n] the normed row (may be null)
+  int8_t* xq;            // [rows][n] Q8_0 codes of the normed rows (act_offset order `layout`)
+  float* xd;             // [rows][n/32] their scales
+  float* y;              // [rows][n] the normed rows (may be null)
   int n;
   float eps;
+  int layout;
 };
 
 struct ExactGemvArgs {

@@ -22,9 +22,11 @@
 //   exact_silu_q8   g / (1 + exp(-g)) * u (layer.rs:75-79) with glibc's
 //                   expf (exact_math.h), Q8_0 of the product
 // The lm_head runs exact_gemv with the argmax partials of argmax_final.
-// A batched prompt is the same computation row by row (the reference's
-// batched path adds in the same per-row orders), so prompts run as
-// consecutive single-row steps.
+// A prompt of M rows runs as the reference's batched forward does, row by
+// row in its per-row orders: exact_norm_q8 over the M rows (one workgroup
+// each), the prefill GEMMs (prefill.hip, sgemm.hip: the same block loop,
+// bit-identical, glibc's expf in their SwiGLU epilogue), the prefill RoPE /
+// append, and exact_attn_prefill_* (one workgroup per query head and row).
 #include "common.h"
 #include "exact_math.h"
 #include "gemv_core.h"
@@ -75,13 +77,24 @@ __device__ __forceinline__ float fold_scale(const float* sq, int n, float eps) {
   return 1.0f / rms;
 }
 
+// The row this workgroup normalises.
+struct NormRow {
+  const float* x;
+  const float* w;
+  int8_t* xq;
+  float* xd;
+  float* y;
+  int n, layout;
+  float eps;
+};
+
 // y = (x*s)*w (cpu.rs:389) and its Q8_0 block; element i is held by lane
 // i % 32 of a 32-lane group.
-__device__ __forceinline__ void norm_out(const ExactNormArgs& a, int i, float x, float s, float w) {
+__device__ __forceinline__ void norm_out(const NormRow& a, int i, float x, float s, float w) {
   const float y = x * s * w;
   float d;
   const int q = q8_group32(y, &d);
-  a.xq[i] = (int8_t)q;
+  a.xq[act_offset(i, a.layout)] = (int8_t)q;
   if ((i & 31) == 0) a.xd[i >> 5] = d;
   if (a.y) a.y[i] = y;
 }
@@ -89,7 +102,7 @@ __device__ __forceinline__ void norm_out(const ExactNormArgs& a, int i, float x,
 // n == kT * EPT: thread t holds elements t + kT*j of x and w in registers
 // from the start, so nothing is loaded after the fold.
 template <int EPT>
-__device__ __forceinline__ void norm_q8_regs(const ExactNormArgs& a, float* sq, float* s_scale) {
+__device__ __forceinline__ void norm_q8_regs(const NormRow& a, float* sq, float* s_scale) {
   const int tid = threadIdx.x;
   float xv[EPT], wv[EPT];
 #pragma unroll
@@ -106,9 +119,12 @@ __device__ __forceinline__ void norm_q8_regs(const ExactNormArgs& a, float* sq, 
   for (int j = 0; j < EPT; ++j) norm_out(a, tid + kT * j, xv[j], s, wv[j]);
 }
 
-__device__ __forceinline__ void norm_q8(const ExactNormArgs& a) {
+__device__ __forceinline__ void norm_q8(const ExactNormArgs& args) {
   extern __shared__ __align__(16) float sq[];
   __shared__ float s_scale;
+  const size_t ro = (size_t)blockIdx.x * args.n;  // this workgroup's row
+  const NormRow a{args.x + ro, args.w, args.xq + ro, args.xd + ro / 32, args.y ? args.y + ro : nullptr,
+                  args.n, args.layout, args.eps};
   switch (a.n) {
     case 8 * kT: norm_q8_regs<8>(a, sq, &s_scale); return;
     case 16 * kT: norm_q8_regs<16>(a, sq, &s_scale); return;
@@ -275,40 +291,40 @@ __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
 }
 
 // ---- attention -------------------------------------------------------------
-// One workgroup per query head h (KV head g = h / n_rep) at the device
-// position pos: scores, exponentials and probabilities of the pos + 1
-// positions in LDS.  The new K/V row is rotated and rounded to the cache
-// type by every workgroup of the group (the values are identical) and
-// stored by the group's first; each workgroup uses its own copy for
-// position pos, so no workgroup adds a value another is writing (a V tile
-// may hold the bytes of row pos mid-write; only rows below pos are added).
 constexpr int kVTile = 16384;  // bytes of V per LDS tile
 
-template <int HD, bool F16>
-__device__ __forceinline__ void attn(const ExactAttnArgs& a) {
-  constexpr int MID = HD / 2;
-  extern __shared__ __align__(16) float s_p[];  // [pos + 1]
-  __shared__ __align__(16) float s_q[HD];
-  __shared__ __align__(16) float s_k[HD];
-  __shared__ float s_v[HD];
-  __shared__ float s_red[kT / LLMRS_WAVE];
-  __shared__ float s_inv;
-  __shared__ __align__(16) u32x4 s_vt[2][kVTile / 16];  // V tiles
-  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
-  const int h = blockIdx.x, n_rep = a.nq / a.nkv, g = h / n_rep;
-  const int pos = *a.pos_ptr, T = pos + 1;
-  const size_t head = (size_t)g * a.max_seq * HD;
-  // V rows 0..pos-1 pass through LDS in 16 KB tiles that every thread loads
-  // (coalesced); the first tile is requested now, each later one while the
-  // previous one is added.
+// LDS of one query row's attention (the scores are the dynamic LDS).
+template <int HD>
+struct AttnShared {
+  float q[HD], k[HD], v[HD];
+  float red[kT / LLMRS_WAVE];
+  float inv;
+  u32x4 vt[2][kVTile / 16];  // V tiles
+};
+
+// One query row's attention over the KV head at kbase / vbase: cache rows
+// 0 .. ncache-1, then (OWN) the row at position ncache from sh.k / sh.v.
+// Scores: the sequential dot over the head dims of q (sh.q) and each row,
+// then times the scale (matmul_slice cpu.rs:230-269, layer.rs:257-258);
+// softmax with the maximum from f32::MIN, glibc's expf, a sequential sum by
+// one lane and e * (1/sum) (cpu.rs:395-423); ctx[d] = sum over the rows of
+// p * V[d], sequential (layer.rs:276-299).  V rows pass through LDS in 16 KB
+// tiles that every thread loads (coalesced), each tile requested while the
+// previous one is added; `first` holds the first tile's loads, issued by the
+// caller.  Returns ctx[d] for thread d < HD.
+template <int HD, bool F16, bool OWN>
+__device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, size_t head_bytes, int ncache,
+                                          float scale, float* s_p, AttnShared<HD>& sh, const u32x4 (&first)[kVTile / 16 / kT]) {
   constexpr int VB = F16 ? 2 : 4;
   constexpr int TP = kVTile / (HD * VB);    // positions per tile, a multiple of 8
   constexpr int LPT = kVTile / 16 / kT;     // 16-byte loads per thread per tile
-  const char* vbase = (const char*)a.vc + head * VB;
-  const size_t head_bytes = (size_t)a.max_seq * HD * VB;
-  const int ntile = (pos + TP - 1) / TP;
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int T = ncache + (OWN ? 1 : 0);
+  const int ntile = (ncache + TP - 1) / TP;
   u32x4 st[LPT];
-  auto vload = [&](int tile) {  // rows past pos read stale (in-bounds) bytes, never added
+#pragma unroll
+  for (int l = 0; l < LPT; ++l) st[l] = first[l];
+  auto vload = [&](int tile) {  // rows past ncache read stale (in-bounds) bytes, never added
 #pragma unroll
     for (int l = 0; l < LPT; ++l) {
       const size_t off = min((size_t)tile * kVTile + 16 * (size_t)(tid + kT * l), head_bytes - 16);
@@ -317,15 +333,127 @@ __device__ __forceinline__ void attn(const ExactAttnArgs& a) {
   };
   auto vstore = [&](int buf) {
 #pragma unroll
-    for (int l = 0; l < LPT; ++l) s_vt[buf][tid + kT * l] = st[l];
+    for (int l = 0; l < LPT; ++l) sh.vt[buf][tid + kT * l] = st[l];
   };
-  if (ntile > 0) vload(0);
+  // scores: sequential dot over the head dims, then the scale
+  float mx = -3.40282347e+38f;  // f32::MIN (cpu.rs:408)
+  for (int t = tid; t < T; t += kT) {
+    float s = 0.0f;
+    if (OWN && t == ncache) {
+      for (int e = 0; e < HD; ++e) s = s + sh.q[e] * sh.k[e];
+    } else if (F16) {
+      const uint16_t* kr = (const uint16_t*)kbase + (size_t)t * HD;
+      for (int e = 0; e < HD; e += 8) {
+        const u32x4 w = *(const u32x4*)(kr + e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s = s + sh.q[e + 2 * i] * h2f((uint16_t)(w[i] & 0xFFFF));
+          s = s + sh.q[e + 2 * i + 1] * h2f((uint16_t)(w[i] >> 16));
+        }
+      }
+    } else {
+      const float* kr = (const float*)kbase + (size_t)t * HD;
+      for (int e = 0; e < HD; e += 4) {
+        const f32x4 w = *(const f32x4*)(kr + e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s = s + sh.q[e + i] * w[i];
+      }
+    }
+    s = s * scale;
+    s_p[t] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) sh.red[wave] = mx;
+  __syncthreads();
+  mx = sh.red[0];
+#pragma unroll
+  for (int w = 1; w < kT / LLMRS_WAVE; ++w) mx = fmaxf(mx, sh.red[w]);
+  for (int t = tid; t < T; t += kT) s_p[t] = exact_expf(s_p[t] - mx);
+  __syncthreads();
+  if (tid == 0) {  // sequential sum of the exponentials
+    float sum = 0.0f;
+    int t = 0;
+    for (; t + 4 <= T; t += 4) {
+      const f32x4 e = *(const f32x4*)(s_p + t);
+      sum = sum + e[0];
+      sum = sum + e[1];
+      sum = sum + e[2];
+      sum = sum + e[3];
+    }
+    for (; t < T; ++t) sum = sum + s_p[t];
+    sh.inv = 1.0f / sum;
+  }
+  __syncthreads();
+  const float inv = sh.inv;
+  for (int t = tid; t < T; t += kT) s_p[t] = s_p[t] * inv;
+  if (ntile > 0) vstore(0);
+  __syncthreads();
+  // ctx[d] = sum over t of p_t * V[t][d], sequential in t; the own row last.
+  const int d = tid;
+  float acc = 0.0f;
+  for (int i = 0; i < ntile; ++i) {
+    if (i + 1 < ntile) vload(i + 1);
+    if (d < HD) {
+      const int t0 = i * TP, t1 = min(t0 + TP, ncache);
+      if (F16) {  // blocked V: the 8 positions of a block are 16 contiguous bytes per dim
+        const uint16_t* vt = (const uint16_t*)sh.vt[i & 1];
+        int t = t0;
+        for (; t + 8 <= t1; t += 8) {
+          const u32x4 w = *(const u32x4*)(vt + ((t - t0) / 8 * HD + d) * 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            acc = acc + s_p[t + 2 * e] * h2f((uint16_t)(w[e] & 0xFFFF));
+            acc = acc + s_p[t + 2 * e + 1] * h2f((uint16_t)(w[e] >> 16));
+          }
+        }
+        for (; t < t1; ++t) acc = acc + s_p[t] * h2f(vt[((t - t0) / 8 * HD + d) * 8 + (t & 7)]);
+      } else {
+        const float* vt = (const float*)sh.vt[i & 1];
+        for (int t = t0; t < t1; ++t) acc = acc + s_p[t] * vt[(t - t0) * HD + d];
+      }
+    }
+    if (i + 1 < ntile) vstore((i + 1) & 1);
+    __syncthreads();
+  }
+  if (OWN && d < HD) acc = acc + s_p[ncache] * sh.v[d];
+  return acc;
+}
+
+// The first V tile's loads (tile 0 of the KV head), issued at kernel start.
+template <int HD, bool F16>
+__device__ __forceinline__ void attn_first_tile(const char* vbase, size_t head_bytes, u32x4 (&st)[kVTile / 16 / kT]) {
+#pragma unroll
+  for (int l = 0; l < kVTile / 16 / kT; ++l)
+    st[l] = *(const u32x4*)(vbase + min(16 * (size_t)(threadIdx.x + kT * l), head_bytes - 16));
+}
+
+// Decode: one workgroup per query head h (KV head g = h / n_rep) at the
+// device position pos.  The new K/V row is rotated and rounded to the
+// cache type by every workgroup of the group (the values are identical) and
+// stored by the group's first; each workgroup uses its own copy for
+// position pos, so no workgroup adds a value another is writing (a V tile
+// may hold the bytes of row pos mid-write; only rows below pos are added).
+template <int HD, bool F16>
+__device__ __forceinline__ void attn(const ExactAttnArgs& a) {
+  constexpr int MID = HD / 2, VB = F16 ? 2 : 4;
+  extern __shared__ __align__(16) float s_p[];  // [pos + 1]
+  __shared__ __align__(16) AttnShared<HD> sh;
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x, n_rep = a.nq / a.nkv, g = h / n_rep;
+  const int pos = *a.pos_ptr;
+  const size_t head = (size_t)g * a.max_seq * HD;
+  const size_t head_bytes = (size_t)a.max_seq * HD * VB;
+  const char* kbase = (const char*)a.kc + head * VB;
+  const char* vbase = (const char*)a.vc + head * VB;
+  u32x4 first[kVTile / 16 / kT];
+  attn_first_tile<HD, F16>(vbase, head_bytes, first);
   if (tid < MID) {  // rotate-half RoPE of q and the new k (cpu.rs:345-354)
     const float co = a.rope_cos[(size_t)pos * MID + tid], sn = a.rope_sin[(size_t)pos * MID + tid];
     const float* q = a.qkv + (size_t)h * HD;
     float re = q[tid], im = q[tid + MID];
-    s_q[tid] = re * co - im * sn;
-    s_q[tid + MID] = re * sn + im * co;
+    sh.q[tid] = re * co - im * sn;
+    sh.q[tid + MID] = re * sn + im * co;
     const float* k = a.qkv + (size_t)(a.nq + g) * HD;
     const float* v = a.qkv + (size_t)(a.nq + a.nkv + g) * HD;
     re = k[tid];
@@ -347,99 +475,50 @@ __device__ __forceinline__ void attn(const ExactAttnArgs& a) {
         if (is_k) ((float*)a.kc)[head + (size_t)pos * HD + dd[j]] = kv[j];
         else ((float*)a.vc)[head + v_offset(pos, dd[j], HD, false)] = kv[j];
       }
-      (is_k ? s_k : s_v)[dd[j]] = kv[j];
+      (is_k ? sh.k : sh.v)[dd[j]] = kv[j];
     }
   }
   __syncthreads();
-  // scores: sequential dot over the head dims, then the scale
-  float mx = -3.40282347e+38f;  // f32::MIN (cpu.rs:408)
-  for (int t = tid; t < T; t += kT) {
-    float s = 0.0f;
-    if (t == pos) {
-      for (int e = 0; e < HD; ++e) s = s + s_q[e] * s_k[e];
-    } else if (F16) {
-      const uint16_t* kr = (const uint16_t*)a.kc + head + (size_t)t * HD;
-      for (int e = 0; e < HD; e += 8) {
-        const u32x4 w = *(const u32x4*)(kr + e);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s = s + s_q[e + 2 * i] * h2f((uint16_t)(w[i] & 0xFFFF));
-          s = s + s_q[e + 2 * i + 1] * h2f((uint16_t)(w[i] >> 16));
-        }
-      }
-    } else {
-      const float* kr = (const float*)a.kc + head + (size_t)t * HD;
-      for (int e = 0; e < HD; e += 4) {
-        const f32x4 w = *(const f32x4*)(kr + e);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = s + s_q[e + i] * w[i];
-      }
-    }
-    s = s * a.scale;
-    s_p[t] = s;
-    mx = fmaxf(mx, s);
-  }
-  mx = wave_max(mx);
-  if (lane == 0) s_red[wave] = mx;
-  __syncthreads();
-  mx = s_red[0];
-#pragma unroll
-  for (int w = 1; w < kT / LLMRS_WAVE; ++w) mx = fmaxf(mx, s_red[w]);
-  for (int t = tid; t < T; t += kT) s_p[t] = exact_expf(s_p[t] - mx);
-  __syncthreads();
-  if (tid == 0) {  // sequential sum of the exponentials
-    float sum = 0.0f;
-    int t = 0;
-    for (; t + 4 <= T; t += 4) {
-      const f32x4 e = *(const f32x4*)(s_p + t);
-      sum = sum + e[0];
-      sum = sum + e[1];
-      sum = sum + e[2];
-      sum = sum + e[3];
-    }
-    for (; t < T; ++t) sum = sum + s_p[t];
-    s_inv = 1.0f / sum;
-  }
-  __syncthreads();
-  const float inv = s_inv;
-  for (int t = tid; t < T; t += kT) s_p[t] = s_p[t] * inv;
-  if (ntile > 0) vstore(0);
-  __syncthreads();
-  // ctx[d] = sum over t of p_t * V[t][d], sequential in t; the new row last.
-  const int d = tid;
-  float acc = 0.0f;
-  for (int i = 0; i < ntile; ++i) {
-    if (i + 1 < ntile) vload(i + 1);
-    if (d < HD) {
-      const int t0 = i * TP, t1 = min(t0 + TP, pos);
-      if (F16) {  // blocked V: the 8 positions of a block are 16 contiguous bytes per dim
-        const uint16_t* vt = (const uint16_t*)s_vt[i & 1];
-        int t = t0;
-        for (; t + 8 <= t1; t += 8) {
-          const u32x4 w = *(const u32x4*)(vt + ((t - t0) / 8 * HD + d) * 8);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc = acc + s_p[t + 2 * e] * h2f((uint16_t)(w[e] & 0xFFFF));
-            acc = acc + s_p[t + 2 * e + 1] * h2f((uint16_t)(w[e] >> 16));
-          }
-        }
-        for (; t < t1; ++t) acc = acc + s_p[t] * h2f(vt[((t - t0) / 8 * HD + d) * 8 + (t & 7)]);
-      } else {
-        const float* vt = (const float*)s_vt[i & 1];
-        for (int t = t0; t < t1; ++t) acc = acc + s_p[t] * vt[(t - t0) * HD + d];
-      }
-    }
-    if (i + 1 < ntile) vstore((i + 1) & 1);
-    __syncthreads();
-  }
-  if (d < HD) {
-    acc = acc + s_p[pos] * s_v[d];
-    const size_t e = (size_t)h * HD + d;
+  const float acc = attn_row<HD, F16, true>(kbase, vbase, head_bytes, pos, a.scale, s_p, sh, first);
+  if (tid < HD) {
+    const size_t e = (size_t)h * HD + tid;
     a.ctx[e] = acc;
     float dq;
     const int q = q8_group32(acc, &dq);
     a.ctx_q[e] = (int8_t)q;
-    if ((d & 31) == 0) a.ctx_d[e >> 5] = dq;
+    if ((tid & 31) == 0) a.ctx_d[e >> 5] = dq;
+  }
+}
+
+// Prompt rows: one workgroup per (query head h, row t) at position
+// start_pos + t over the cache rows 0 .. start_pos + t, which the RoPE /
+// append launch has written (layer.rs:248-270: the causal mask keeps
+// j <= start_pos + t); q rotated, ctx as f32 (optional) and Q8_0 in the
+// operand order ctx_layout.
+template <int HD, bool F16>
+__device__ __forceinline__ void attn_prefill(const PrefillAttnArgs& a) {
+  constexpr int VB = F16 ? 2 : 4;
+  extern __shared__ __align__(16) float s_p[];  // [start_pos + t + 1]
+  __shared__ __align__(16) AttnShared<HD> sh;
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x, t = blockIdx.y, g = h / (a.nq / a.nkv);
+  const int pos = a.start_pos + t;
+  const size_t head_bytes = (size_t)a.max_seq * HD * VB;
+  const char* kbase = (const char*)a.kc + (size_t)g * head_bytes;
+  const char* vbase = (const char*)a.vc + (size_t)g * head_bytes;
+  u32x4 first[kVTile / 16 / kT];
+  attn_first_tile<HD, F16>(vbase, head_bytes, first);
+  const int qd = a.nq * HD;
+  if (tid < HD) sh.q[tid] = a.q[(size_t)t * qd + (size_t)h * HD + tid];
+  __syncthreads();
+  const float acc = attn_row<HD, F16, false>(kbase, vbase, head_bytes, pos + 1, a.scale, s_p, sh, first);
+  if (tid < HD) {
+    const int e = h * HD + tid;
+    if (a.ctx) a.ctx[(size_t)t * qd + e] = acc;
+    float dq;
+    const int q = q8_group32(acc, &dq);
+    a.ctx_q[(size_t)t * qd + act_offset(e, a.ctx_layout)] = (int8_t)q;
+    if ((tid & 31) == 0) a.ctx_d[(size_t)t * (qd / 32) + (e >> 5)] = dq;
   }
 }
 
@@ -479,9 +558,12 @@ LLMRS_EXACT_GEMV(q4h, WT_Q4H)
 LLMRS_EXACT_GEMV(q4f, WT_Q4F)
 LLMRS_EXACT_GEMV(q8h, WT_Q8H)
 
-#define LLMRS_EXACT_ATTN(name, HD, F16) \
-  extern "C" __global__ __launch_bounds__(kT) void name(ExactAttnArgs a) { attn<HD, F16>(a); }
-LLMRS_EXACT_ATTN(exact_attn_hd64_f16, 64, true)
-LLMRS_EXACT_ATTN(exact_attn_hd128_f16, 128, true)
-LLMRS_EXACT_ATTN(exact_attn_hd64_f32, 64, false)
-LLMRS_EXACT_ATTN(exact_attn_hd128_f32, 128, false)
+#define LLMRS_EXACT_ATTN(tag, HD, F16)                                                                    \
+  extern "C" __global__ __launch_bounds__(kT) void exact_attn_##tag(ExactAttnArgs a) { attn<HD, F16>(a); } \
+  extern "C" __global__ __launch_bounds__(kT) void exact_attn_prefill_##tag(PrefillAttnArgs a) {        \
+    attn_prefill<HD, F16>(a);                                                                        \
+  }
+LLMRS_EXACT_ATTN(hd64_f16, 64, true)
+LLMRS_EXACT_ATTN(hd128_f16, 128, true)
+LLMRS_EXACT_ATTN(hd64_f32, 64, false)
+LLMRS_EXACT_ATTN(hd128_f32, 128, false)

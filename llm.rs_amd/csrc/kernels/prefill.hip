@@ -29,6 +29,7 @@
 // read 32 distinct consecutive chunks.  Q4 codes become (q - 8) bytes with
 // ((q | 0x80) - 8) ^ 0x80.
 #include "attn_core.h"
+#include "exact_math.h"
 #include "gemv_core.h"
 
 using namespace llmrs;
@@ -285,7 +286,7 @@ __device__ __forceinline__ void gemm_impl(const PrefillGemmArgs& a, uint8_t* lds
         // rows n0+wn .. +31 are gate, +32 .. +63 the matching up rows
         // (layer.rs:72-79); m index j = (n0+wn)/2 + col.
         const float g = acc[t][0][i], u = acc[t][1][i];
-        const float mv = (g / (1.0f + expf(-g))) * u;
+        const float mv = (g / (1.0f + exact_expf(-g))) * u;  // glibc expf (exact_math.h)
         const int run = (n0 + wn) / 64;
         const int j = run * 32 + col;
         float amax = fabsf(mv);

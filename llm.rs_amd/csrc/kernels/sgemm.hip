@@ -43,6 +43,7 @@
 // Each wave keeps PF groups of loads in flight (a ring of register sets, the
 // loop unrolled by PF so every set has a fixed place).
 #include "common.h"
+#include "exact_math.h"
 #include "gemv_core.h"
 #include "../kernel_args.h"
 
@@ -273,7 +274,7 @@ __device__ __forceinline__ void sgemm_impl(const SgemmArgs& a) {
         gv = gv + s_acc[gs * KP + k][rt][tt][l][ii];
         uv = uv + s_acc[(RS / 2 + gs) * KP + k][rt][tt][l][ii];
       }
-      const float mv = (gv / (1.0f + expf(-gv))) * uv;
+      const float mv = (gv / (1.0f + exact_expf(-gv))) * uv;  // glibc expf (exact_math.h)
       float amax = fabsf(mv);
 #pragma unroll
       for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
