@@ -148,8 +148,8 @@ def host_mem_available() -> int:
 
 
 def exact_decode(model, lh, prompt, pre: int, steps: int) -> dict:
-    """The reference-order kernels on the same model: the prompt (one
-    position per step), then `steps` timed greedy steps."""
+    """The reference-order kernels on the same model: the prompt (batched),
+    then `steps` timed greedy steps."""
     model.set_exact(True)
     try:
         t0 = time.perf_counter()
@@ -167,8 +167,8 @@ def exact_decode(model, lh, prompt, pre: int, steps: int) -> dict:
     return {"tok_s": round(steps / dt, 1), "ms_per_token": round(dt / steps * 1e3, 3), "steps": steps,
             "prompt_ms": round(prompt_s * 1e3, 1),
             "note": "reference-order kernels (llmrs_model_set_exact): every f32 sum in the reference CPU "
-                    "path's order, logits and greedy tokens bit-identical to it; the prompt runs one "
-                    "position per step"}
+                    "path's order, logits and greedy tokens bit-identical to it; the prompt runs as one "
+                    "batched forward"}
 
 
 def long_context(lh, syn, warmup: int, steps: int, cpu_seconds: float, cpu: bool) -> dict:

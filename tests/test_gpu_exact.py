@@ -221,10 +221,9 @@ def test_exact_workload_north_star_bar(hip, orc, index, prompt_len, steps):
 @pytest.mark.timeout(900)
 def test_exact_prefill_8b_2048(hip, orc):
     """The 2048-token prompt workload through two 8B-width layers and the
-    full lm_head, one position per step on the reference-order kernels:
-    the residual stream of every row and the last row's logits equal the
-    oracle's batched forward (the reference adds each row's sums in the same
-    orders in its batched path)."""
+    full lm_head, one batched forward on the reference-order kernels: the
+    residual stream of every row and the last row's logits equal the
+    oracle's batched forward."""
     spec = syn.with_sizes(syn.WORKLOADS[3], n_layers=2, prompt=2048, decode=0)
     print("\n8B-width 2-layer model, 2048-token prompt, reference-order kernels: building", flush=True)
     gm, om, _ = exact_model(hip, orc, spec, max_seq=2048)

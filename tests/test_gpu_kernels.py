@@ -10,8 +10,8 @@ the layers before it.  Bars:
   |gpu - oracle| <= 1e-4 + 1e-3 |oracle| (only the f32 summation order
   differs; the integer block sums are exact).
 * prefill GEMMs: bit-exact (the int8 MFMA GEMM keeps the reference's block
-  loop order and roundings, cpu.rs:910-937); the SwiGLU product within
-  4 ulps (expf of the device library against glibc's).
+  loop order and roundings, cpu.rs:910-937), the SwiGLU product included
+  (its epilogue calls the device restatement of glibc's expf).
 * Q8_0 codes a kernel builds from its own f32 values (ctx, m): equal to the
   reference quantiser's (cpu.rs:724-743) on those values, bit for bit.
 * Q8_0 codes of RMSNorm rows built inside a GEMV prologue: equal, or one
@@ -36,14 +36,6 @@ from llmrs_hip import synth_normal
 
 pytestmark = pytest.mark.gpu
 F32 = np.float32
-
-
-def ulps_apart(a, b):
-    """Distance in float32 ulps (0 for equal values, +0 == -0)."""
-    def ordered(x):
-        i = np.ascontiguousarray(x, F32).view(np.int32).astype(np.int64)
-        return np.where(i < 0, -(i & 0x7FFFFFFF), i)
-    return np.abs(ordered(a) - ordered(b))
 
 
 def check_norm_codes(orc, gq, gd, x, w, eps, ulps=8):
@@ -301,7 +293,7 @@ def check_prefill_layer(hip, orc, spec, start, M):
     g = gemv(orc, spec, pr["hq"], pr["hd"], L[W_GATE])
     u = gemv(orc, spec, pr["hq"], pr["hd"], L[W_UP])
     m = orc.silu_mul(g, u)
-    assert ulps_apart(pr["m"], m).max() <= 4, "gate|up GEMM + SwiGLU"
+    same(pr["m"], m, "gate|up GEMM + SwiGLU")
     for i in range(M):
         check_own_codes(orc, pr["m_q"][i], pr["m_d"][i], pr["m"][i])
     out = (gemv(orc, spec, pr["m_q"], pr["m_d"], L[W_DOWN]) + pr["h"]).astype(F32)
