@@ -517,7 +517,7 @@ void exact_norm(llmrs_model* m, Launcher& L, const float* x, const float* w, int
                 float* y = nullptr, int rows = 1, int layout = llmrs::kActNatural) {
   const int H = m->c.hidden;
   ExactNormArgs a{x, w, xq, xd, y, H, m->c.rms_eps, layout};
-  L("exact_norm_q8", 9.125 * H * rows, dim3((unsigned)rows), dim3(256), (size_t)H * 4, a);
+  L("exact_norm_q8", 9.125 * H * rows, dim3((unsigned)rows), dim3(1024), (size_t)H * 4, a);
 }
 
 void exact_linear(llmrs_model* m, Launcher& L, const DevLinear& W, const char* epi, const int8_t* xq,

@@ -39,15 +39,41 @@ namespace {
 constexpr int kT = 256;
 
 // ---- RMSNorm + Q8_0 ---------------------------------------------------------
-// One workgroup.  All threads square the row into LDS (each product is the
-// reference's own rounding of x*x); one lane then adds the squares in index
-// order, reading them 32 at a time with the next 32 requested before the
-// current ones are added.  n <= 32768 and a multiple of 32, so a 32-lane
-// group holds one block.
+// One workgroup of kNT threads per row.  All threads square the row into LDS
+// (each product is the reference's own rounding of x*x).  The sum of squares
+// is the reference's sequential fold (cpu.rs:381),
+//   ss = (...((0 + sq[0]) + sq[1]) + ...) + sq[n-1],
+// evaluated by chunks in parallel: wave c owns chunk c (kNW chunks of equal
+// length in index order) and folds it from kWin consecutive f32 start values
+// at once, one per lane, centred on the exact sum of the squares before the
+// chunk (added in f64): lane l starts at the float whose bit pattern is the
+// centre's plus l - kWin/2.  A fold from a given start is a fixed sequence
+// of IEEE additions, so when the sequential total at the chunk's start is one
+// of those floats, the lane that started there ends with exactly the
+// sequential total at the chunk's end.  One thread then walks the chunks in
+// order and takes each chunk's lane by the bit distance of the running total
+// from the chunk's centre; when the total lies outside the window (the
+// rounding drift of a long run of equal squares, for instance) it folds that
+// chunk itself from the total.  Either way the result is the sequential
+// fold, bit for bit.  Real rows drift from the exact sum by well under
+// kWin/2 ulps at every chunk start, so the walk rarely folds.  n <= 32768
+// and a multiple of 32, so a 32-lane group holds one block.
+constexpr int kNT = 1024;              // threads of the norm workgroup
+constexpr int kNW = kNT / LLMRS_WAVE;  // fold chunks, one per wave
+constexpr int kWin = LLMRS_WAVE;       // start values per chunk, one per lane
 
-// Lane 0's fold of sq[0..n) in index order; returns 1/rms (cpu.rs:381-383).
-__device__ __forceinline__ float fold_scale(const float* sq, int n, float eps) {
-  float ss = 0.0f;
+struct FoldShared {
+  double part[kNW];      // sum of each chunk's squares (f64)
+  unsigned centre[kNW];  // bit pattern of each chunk's centre start value
+  float end[kNW][kWin];  // chunk c folded from the start value of lane l
+  float scale;
+};
+
+// One lane's fold of sq[i0..i1) from acc in index order (i0, i1 multiples of
+// 32), reading the squares 32 at a time with the next 32 requested before
+// the current ones are added.
+__device__ __forceinline__ float fold_range(const float* sq, int i0, int i1, float acc) {
+  if (i0 >= i1) return acc;
   f32x4 A[8], B[8];
   auto load = [&](f32x4 (&r)[8], int i) {
 #pragma unroll
@@ -56,25 +82,57 @@ __device__ __forceinline__ float fold_scale(const float* sq, int n, float eps) {
   auto add = [&](const f32x4 (&r)[8]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      ss = ss + r[j][0];
-      ss = ss + r[j][1];
-      ss = ss + r[j][2];
-      ss = ss + r[j][3];
+      acc = acc + r[j][0];
+      acc = acc + r[j][1];
+      acc = acc + r[j][2];
+      acc = acc + r[j][3];
     }
   };
-  load(A, 0);
-  for (int i = 0;; i += 64) {
-    const bool more = i + 32 < n;
+  load(A, i0);
+  for (int i = i0;; i += 64) {
+    const bool more = i + 32 < i1;
     if (more) load(B, i + 32);
     add(A);
     if (!more) break;
-    const bool more2 = i + 64 < n;
+    const bool more2 = i + 64 < i1;
     if (more2) load(A, i + 64);
     add(B);
     if (!more2) break;
   }
-  const float rms = __builtin_sqrtf(ss / (float)n + eps);
-  return 1.0f / rms;
+  return acc;
+}
+
+// The sequential fold of sq[0..n) by chunks (all threads); returns 1/rms
+// (cpu.rs:381-383).
+__device__ __forceinline__ float fold_scale(const float* sq, int n, float eps, FoldShared& sh) {
+  const int lane = lane_id(), wave = wave_id();
+  const int len = (n + kNW * 32 - 1) / (kNW * 32) * 32;
+  const int c0 = min(wave * len, n), c1 = min(c0 + len, n);
+  double p = 0.0;
+  for (int i = c0 + lane; i < c1; i += LLMRS_WAVE) p += (double)sq[i];
+#pragma unroll
+  for (int o = LLMRS_WAVE / 2; o > 0; o >>= 1) p += __shfl_xor(p, o);
+  if (lane == 0) sh.part[wave] = p;
+  __syncthreads();
+  double before = 0.0;
+  for (int c = 0; c < wave; ++c) before += sh.part[c];
+  const unsigned centre = __float_as_uint((float)before);
+  // chunk 0 starts from the fold's own 0
+  const float start = wave == 0 ? 0.0f : __uint_as_float(centre + (unsigned)lane - (unsigned)(kWin / 2));
+  sh.end[wave][lane] = fold_range(sq, c0, c1, start);
+  if (lane == 0) sh.centre[wave] = centre;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float ss = sh.end[0][0];
+    for (int c = 1; c < kNW && c * len < n; ++c) {
+      const unsigned j = __float_as_uint(ss) - sh.centre[c] + (unsigned)(kWin / 2);
+      ss = j < (unsigned)kWin ? sh.end[c][j] : fold_range(sq, c * len, min(c * len + len, n), ss);
+    }
+    const float rms = __builtin_sqrtf(ss / (float)n + eps);
+    sh.scale = 1.0f / rms;
+  }
+  __syncthreads();
+  return sh.scale;
 }
 
 // The row this workgroup normalises.
@@ -99,48 +157,44 @@ __device__ __forceinline__ void norm_out(const NormRow& a, int i, float x, float
   if (a.y) a.y[i] = y;
 }
 
-// n == kT * EPT: thread t holds elements t + kT*j of x and w in registers
+// n == kNT * EPT: thread t holds elements t + kNT*j of x and w in registers
 // from the start, so nothing is loaded after the fold.
 template <int EPT>
-__device__ __forceinline__ void norm_q8_regs(const NormRow& a, float* sq, float* s_scale) {
+__device__ __forceinline__ void norm_q8_regs(const NormRow& a, float* sq, FoldShared& sh) {
   const int tid = threadIdx.x;
   float xv[EPT], wv[EPT];
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) xv[j] = a.x[tid + kT * j];
+  for (int j = 0; j < EPT; ++j) xv[j] = a.x[tid + kNT * j];
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) wv[j] = a.w[tid + kT * j];
+  for (int j = 0; j < EPT; ++j) wv[j] = a.w[tid + kNT * j];
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) sq[tid + kT * j] = xv[j] * xv[j];
+  for (int j = 0; j < EPT; ++j) sq[tid + kNT * j] = xv[j] * xv[j];
   __syncthreads();
-  if (tid == 0) *s_scale = fold_scale(sq, a.n, a.eps);
-  __syncthreads();
-  const float s = *s_scale;
+  const float s = fold_scale(sq, a.n, a.eps, sh);
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) norm_out(a, tid + kT * j, xv[j], s, wv[j]);
+  for (int j = 0; j < EPT; ++j) norm_out(a, tid + kNT * j, xv[j], s, wv[j]);
 }
 
 __device__ __forceinline__ void norm_q8(const ExactNormArgs& args) {
   extern __shared__ __align__(16) float sq[];
-  __shared__ float s_scale;
+  __shared__ FoldShared sh;
   const size_t ro = (size_t)blockIdx.x * args.n;  // this workgroup's row
   const NormRow a{args.x + ro, args.w, args.xq + ro, args.xd + ro / 32, args.y ? args.y + ro : nullptr,
                   args.n, args.layout, args.eps};
   switch (a.n) {
-    case 8 * kT: norm_q8_regs<8>(a, sq, &s_scale); return;
-    case 16 * kT: norm_q8_regs<16>(a, sq, &s_scale); return;
-    case 32 * kT: norm_q8_regs<32>(a, sq, &s_scale); return;
+    case 2 * kNT: norm_q8_regs<2>(a, sq, sh); return;
+    case 4 * kNT: norm_q8_regs<4>(a, sq, sh); return;
+    case 8 * kNT: norm_q8_regs<8>(a, sq, sh); return;
     default: break;
   }
   const int tid = threadIdx.x;
-  for (int i = tid; i < a.n; i += kT) {
+  for (int i = tid; i < a.n; i += kNT) {
     const float v = a.x[i];
     sq[i] = v * v;
   }
   __syncthreads();
-  if (tid == 0) s_scale = fold_scale(sq, a.n, a.eps);
-  __syncthreads();
-  const float s = s_scale;
-  for (int i = tid; i < a.n; i += kT) norm_out(a, i, a.x[i], s, a.w[i]);
+  const float s = fold_scale(sq, a.n, a.eps, sh);
+  for (int i = tid; i < a.n; i += kNT) norm_out(a, i, a.x[i], s, a.w[i]);
 }
 
 // ---- GEMV -----------------------------------------------------------------
@@ -541,7 +595,7 @@ __device__ __forceinline__ void silu_q8(const ExactSiluArgs& a) {
 
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(kT) void exact_norm_q8(ExactNormArgs a) { norm_q8(a); }
+extern "C" __global__ __launch_bounds__(kNT) void exact_norm_q8(ExactNormArgs a) { norm_q8(a); }
 extern "C" __global__ __launch_bounds__(kT) void exact_silu_q8(ExactSiluArgs a) { silu_q8(a); }
 
 #define LLMRS_EXACT_GEMV(tag, WT)                                                                     \

@@ -128,6 +128,42 @@ def test_exact_layer_kernels(hip, orc, spec, pos):
     check_exact_layer(hip, orc, spec, pos)
 
 
+@pytest.mark.parametrize("spec", [LAYERS[0][0], LAYERS[5][0], LAYERS[6][0]], ids=lambda s: s.name)
+def test_exact_norm_fold_rows(hip, orc, spec):
+    """The exact RMSNorm folds its sum of squares by chunks, each from a
+    window of start values around the exact sum before it, and folds a
+    chunk in order when the sequential total falls outside the window.  Rows
+    whose sequential fold drifts far from the exact sum (equal squares, a
+    heavy tail, a sparse row, sums that overflow to infinity) take that
+    fallback; on every row the final RMSNorm's codes and scales and the
+    logits equal the oracle's sequential arithmetic."""
+    gm, om, w = layer_models(hip, orc, spec, 4)
+    gm.set_exact(True)
+    n, eps = spec.hidden, spec.rms_eps
+    rng = np.random.default_rng(20261202)
+    g = rng.standard_normal(n)
+    sparse = np.zeros(n)
+    sparse[::7] = 1.5
+    rows = {
+        "normal": g,
+        "constant 0.3": np.full(n, 0.3),
+        "constant 1": np.ones(n),
+        "heavy tail": g * rng.exponential(1.0, n) ** 3,
+        "sparse": sparse,
+        "one outlier": np.where(np.arange(n) == n // 3, 4.0e3, g),
+        "overflow": np.full(n, 3.0e18),
+        "zero": np.zeros(n),
+    }
+    for name, x in rows.items():
+        x = x.astype(F32)
+        xq, xd, lg, nxt = gm.probe_head(x)
+        oq, od = orc.quantize_row_q8_0(orc.rms_norm(x[None], w.final_norm, eps)[0])
+        same(xq, oq, f"final RMSNorm codes, {name} row")
+        same(xd, od, f"final RMSNorm scales, {name} row")
+        same(lg, gemv(orc, spec, oq, od, w.lm_head)[0], f"logits, {name} row")
+    gm.close()
+
+
 @pytest.mark.timeout(900)
 def test_exact_layer_kernels_70b_widths(hip, orc):
     """The 70B widths (Q|K|V 10240 x 8192, gate|up 57344 x 8192, down 8192 x
