@@ -506,9 +506,9 @@ void enqueue_head(llmrs_model* m, Launcher& L, bool write_logits, int8_t* probe_
 // probabilities): 64 KB.
 constexpr int kExactMaxRows = 16384;
 
-// Workgroups of an exact GEMV: one per 8-row tile, at most eight per CU
-// (they loop over the tiles beyond).
-int exact_gemv_cap() { return 8 * ctx().num_cus; }
+// Workgroups of an exact GEMV: one per 8-row tile, at most four per CU (as
+// many as are resident at once; they loop over the tiles beyond).
+int exact_gemv_cap() { return 4 * ctx().num_cus; }
 unsigned exact_gemv_grid(int n) { return (unsigned)std::max(1, std::min((n + 7) / 8, exact_gemv_cap())); }
 
 // RMSNorm + Q8_0 of `rows` rows of hidden floats (one workgroup each; the

@@ -276,54 +276,100 @@ __device__ __forceinline__ int ex_offset(const ExChunk<WT>& r) {
   return -8 * sa;
 }
 
+// Chunk loads in flight per wave: the loads of item i + PF are issued right
+// after item i is computed, so PF - 1 items' loads are outstanding while an
+// item is computed.  Q8 chunks carry twice the weight bytes; three of them
+// keep the kernel at four workgroups per CU.
+template <int WT>
+constexpr int ex_prefetch() { return WT == WT_Q8H ? 3 : 4; }
+
 // EPI: EPI_STORE (y = total), EPI_RESID (y = total + res), EPI_ARGMAX
 // (logits into y when set, and this workgroup's (max, lowest index) into
 // part_val / part_idx[blockIdx.x]).  Workgroups take 8-row tiles
-// round-robin; the next chunk's loads are issued before the current chunk is
-// folded.
+// round-robin and walk their (tile, 64-block chunk) items in order through
+// a ring of loads, across tile boundaries.
 template <int WT, int EPI>
 __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
-  __shared__ float s_p[kExR][LLMRS_WAVE + 1];  // padded: lane r's reads of row r hit distinct banks
+  // Block terms of two items (a row padded to 68 floats: the 16-byte reads
+  // of the 8 folding lanes cover distinct banks).  Item i writes buffer
+  // i % 2 while wave 0 may still fold item i - 1 from the other; it cannot
+  // be two items ahead, since the barrier of item i - 1 waits for wave 0's
+  // fold of item i - 2.
+  constexpr int kPad = LLMRS_WAVE + 4;
+  __shared__ __align__(16) float s_p[2][kExR][kPad];
   const int lane = lane_id(), wave = wave_id();
   const int nb = a.k >> 5, nch = (nb + LLMRS_WAVE - 1) / LLMRS_WAVE;
   const int ntiles = (a.n + kExR - 1) / kExR;
+  const int my_tiles = (int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  const int nitems = my_tiles * nch;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int row0 = tile * kExR;
-    float total = 0.0f;  // lane r < kExR of wave 0: row row0 + r
-    // one chunk: the wave's block terms into LDS, then wave 0 folds them
-    auto step = [&](int c, const ExChunk<WT>& r) {
-      const int off = ex_offset<WT>(r);
+  float total = 0.0f;  // lane r < kExR of wave 0: row row0 + r of the current tile
+  auto row0_of = [&](int item) { return ((int)blockIdx.x + (item / nch) * (int)gridDim.x) * kExR; };
+  auto load = [&](int item, ExChunk<WT>& r) {
+    ex_load<WT>(a, row0_of(item), (item % nch) * LLMRS_WAVE, nb, r);
+  };
+  // one item: the wave's block terms into LDS, then wave 0 folds them; the
+  // tile's last chunk writes its rows
+  auto step = [&](int item, const ExChunk<WT>& r) {
+    const int c = (item % nch) * LLMRS_WAVE;
+    const int off = ex_offset<WT>(r);
+    float(*buf)[kPad] = s_p[item & 1];
 #pragma unroll
-      for (int j = 0; j < kExRW; ++j) {
-        const int isum = ex_isum<WT>(r, j) + off;
-        s_p[wave + 4 * j][lane] = (float)isum * (wscale<WT>(r.sc[j]) * r.da);
+    for (int j = 0; j < kExRW; ++j) {
+      const int isum = ex_isum<WT>(r, j) + off;
+      buf[wave + 4 * j][lane] = (float)isum * (wscale<WT>(r.sc[j]) * r.da);
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kExR) {
+      const int cnt = min(LLMRS_WAVE, nb - c);
+      if (cnt == LLMRS_WAVE) {  // 16 terms at a time, the next 16 read before these are added
+        f32x4 t[2][4];
+        const f32x4* src = (const f32x4*)buf[lane];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t[0][q] = src[q];
+#pragma unroll
+        for (int g = 0; g < LLMRS_WAVE / 16; ++g) {
+          if (g + 1 < LLMRS_WAVE / 16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) t[(g + 1) & 1][q] = src[4 * (g + 1) + q];
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            total = total + t[g & 1][q][0];
+            total = total + t[g & 1][q][1];
+            total = total + t[g & 1][q][2];
+            total = total + t[g & 1][q][3];
+          }
+        }
+      } else {
+        for (int l = 0; l < cnt; ++l) total = total + buf[lane][l];
       }
-      __syncthreads();
-      if (wave == 0 && lane < kExR) {
-        const int cnt = min(LLMRS_WAVE, nb - c);
-        for (int l = 0; l < cnt; ++l) total = total + s_p[lane][l];
-      }
-      __syncthreads();
-    };
-    ExChunk<WT> ra, rb;
-    ex_load<WT>(a, row0, 0, nb, ra);
-    for (int ci = 0; ci < nch; ci += 2) {
-      if (ci + 1 < nch) ex_load<WT>(a, row0, (ci + 1) * LLMRS_WAVE, nb, rb);
-      step(ci * LLMRS_WAVE, ra);
-      if (ci + 1 < nch) {
-        if (ci + 2 < nch) ex_load<WT>(a, row0, (ci + 2) * LLMRS_WAVE, nb, ra);
-        step((ci + 1) * LLMRS_WAVE, rb);
+      const int row = row0_of(item) + lane;
+      if (item % nch == nch - 1) {
+        if (row < a.n) {
+          if (EPI == EPI_RESID) a.y[row] = total + a.res[row];
+          else if (a.y) a.y[row] = total;
+          if (EPI == EPI_ARGMAX && better(total, row, bv, bi)) {
+            bv = total;
+            bi = row;
+          }
+        }
+        total = 0.0f;
       }
     }
-    if (wave == 0 && lane < kExR && row0 + lane < a.n) {
-      const int row = row0 + lane;
-      if (EPI == EPI_RESID) a.y[row] = total + a.res[row];
-      else if (a.y) a.y[row] = total;
-      if (EPI == EPI_ARGMAX && better(total, row, bv, bi)) {
-        bv = total;
-        bi = row;
+  };
+  constexpr int PF = ex_prefetch<WT>();
+  ExChunk<WT> ring[PF];
+#pragma unroll
+  for (int s = 0; s < PF; ++s)
+    if (s < nitems) load(s, ring[s]);
+  for (int i = 0; i < nitems; i += PF) {
+#pragma unroll
+    for (int s = 0; s < PF; ++s) {
+      if (i + s < nitems) {
+        step(i + s, ring[s]);
+        if (i + s + PF < nitems) load(i + s + PF, ring[s]);
       }
     }
   }
