@@ -99,7 +99,6 @@ struct llmrs_model {
   int live_batches = 0;
   // single-sequence steps on the reference-order kernels (exact.hip)
   bool exact = false;
-  float* ex_gu = nullptr;  // [2 ffn] gate|up rows of the exact step
   float* ex_part_val = nullptr;  // [exact_gemv_cap()] argmax partials of the exact lm_head
   int* ex_part_idx = nullptr;
   size_t host_pos = 0;
@@ -522,10 +521,21 @@ void exact_norm(llmrs_model* m, Launcher& L, const float* x, const float* w, int
 
 void exact_linear(llmrs_model* m, Launcher& L, const DevLinear& W, const char* epi, const int8_t* xq,
                   const float* xd, float* y, const float* res) {
-  ExactGemvArgs a{W.codes, W.scales, xq, xd, y, res, nullptr, nullptr, W.n, W.k};
+  ExactGemvArgs a{W.codes, W.scales, xq, xd, y, res, nullptr, nullptr, W.n, W.k, nullptr, nullptr};
   const unsigned grid = exact_gemv_grid(W.n);
   L(std::string("exact_gemv_") + wt_tag(m->wt) + "_" + epi,
     linear_weight_bytes(m, W) + 1.125 * W.k + (res ? 8.0 : 4.0) * W.n, dim3(grid), dim3(256), 0, a);
+}
+
+// The gate|up GEMV with the SwiGLU product and its Q8_0 (layer.rs:40,
+// 75-79): one workgroup per 64-row group (32 gate + 32 up rows), at most two
+// per CU (as many as are resident at once; they loop over the groups beyond).
+void exact_gate_up(llmrs_model* m, Launcher& L, const DevLinear& W) {
+  const int F = m->c.ffn;
+  ExactGemvArgs a{W.codes, W.scales, m->h_q, m->h_d, m->mf, nullptr, nullptr, nullptr, W.n, W.k, m->m_q, m->m_d};
+  const unsigned grid = (unsigned)std::max(1, std::min(W.n / 64, 2 * ctx().num_cus));
+  L(std::string("exact_gemv_") + wt_tag(m->wt) + "_silu", linear_weight_bytes(m, W) + 1.125 * W.k + 5.125 * F,
+    dim3(grid), dim3(256), 0, a);
 }
 
 void exact_attention(llmrs_model* m, Launcher& L, int li) {
@@ -557,13 +567,8 @@ void enqueue_exact_layer(llmrs_model* m, Launcher& L, int li, const std::functio
   done(3);
   exact_norm(m, L, m->h, Lb.norm[1], m->h_q, m->h_d);                      // layer.rs:393
   done(4);
-  exact_linear(m, L, Lb.gu, "store", m->h_q, m->h_d, m->ex_gu, nullptr);   // layer.rs:40
+  exact_gate_up(m, L, Lb.gu);                                              // layer.rs:40,75-79
   done(5);
-  {  // layer.rs:75-79
-    const int F = m->c.ffn;
-    ExactSiluArgs a{m->ex_gu, m->m_q, m->m_d, m->mf, F};
-    L("exact_silu_q8", 13.125 * F, dim3((unsigned)((F + 255) / 256)), dim3(256), 0, a);
-  }
   done(6);
   exact_linear(m, L, Lb.down, "resid", m->m_q, m->m_d, m->x, m->h);       // layer.rs:93-96,403
   done(7);
@@ -577,7 +582,7 @@ void enqueue_exact_head(llmrs_model* m, Launcher& L, bool write_logits) {
   const unsigned grid = exact_gemv_grid(c.vocab);
   ExactGemvArgs a{m->lm_head.codes, m->lm_head.scales, m->x_q, m->x_d,
                   write_logits || m->sampling ? m->logits : nullptr, nullptr, m->ex_part_val, m->ex_part_idx,
-                  c.vocab, c.hidden};
+                  c.vocab, c.hidden, nullptr, nullptr};
   L(std::string("exact_gemv_") + wt_tag(m->wt) + "_argmax", linear_weight_bytes(m, m->lm_head) + 1.125 * c.hidden,
     dim3(grid), dim3(256), 0, a);
   if (m->sampling) {
@@ -623,20 +628,19 @@ void enqueue_exact_step(llmrs_model* m, Launcher& L, bool write_logits, float* t
 }
 
 // Switches a model between the fast and the reference-order step; the first
-// switch to the latter allocates its gate|up buffer and resolves its kernels.
+// switch to the latter allocates its lm_head partials and resolves its kernels.
 void set_exact(llmrs_model* m, bool on) {
   if (on) {
     const llmrs_model_config& c = m->c;
     LLMRS_REQUIRE(kv_rows(m) <= kExactMaxRows, LLMRS_E_INVALID,
                   "the reference-order step supports max_seq up to " + std::to_string(kExactMaxRows));
-    if (!m->ex_gu) {
-      m->ex_gu = m->dalloc<float>((size_t)2 * c.ffn);
+    if (!m->ex_part_val) {
       m->ex_part_val = m->dalloc<float>((size_t)exact_gemv_cap());
       m->ex_part_idx = m->dalloc<int>((size_t)exact_gemv_cap());
     }
-    for (const char* epi : {"store", "resid", "argmax"}) (void)kernel(std::string("exact_gemv_") + wt_tag(m->wt) + "_" + epi);
+    for (const char* epi : {"store", "resid", "argmax", "silu"})
+      (void)kernel(std::string("exact_gemv_") + wt_tag(m->wt) + "_" + epi);
     (void)kernel("exact_norm_q8");
-    (void)kernel("exact_silu_q8");
     (void)kernel("exact_attn_hd" + std::to_string(c.head_dim) + (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32"));
     (void)kernel("exact_attn_prefill_hd" + std::to_string(c.head_dim) + (c.kv_dtype == LLMRS_F16 ? "_f16" : "_f32"));
     LLMRS_HIP(hipStreamSynchronize(ctx().stream));

@@ -338,11 +338,13 @@ struct ExactGemvArgs {
   const void* ws;        // weight scales [n][nb]
   const int8_t* xq;      // [k] activation codes
   const float* xd;       // [k/32] activation scales
-  float* y;              // [n] (may be null for the argmax epilogue)
+  float* y;              // [n] (may be null for the argmax epilogue; silu: [n/2] m as f32, may be null)
   const float* res;      // [n] residual (resid epilogue; may alias y)
   float* part_val;       // [gridDim.x] (argmax epilogue)
   int* part_idx;
   int n, k;
+  int8_t* mq;            // silu epilogue: [n/2] Q8_0 codes of m = silu(g) * u
+  float* md;             // [n/64]
 };
 
 struct ExactAttnArgs {
@@ -357,14 +359,6 @@ struct ExactAttnArgs {
   float* ctx_d;          // [nq*hd/32]
   int max_seq, nq, nkv;  // max_seq: cache rows per KV head (kv_rows)
   float scale;           // fl(1 / fl(sqrt(hd)))
-};
-
-struct ExactSiluArgs {
-  const float* gu;       // [2n] gate|up GEMV rows (runs of 32 gate, then 32 up)
-  int8_t* mq;            // [n] Q8_0 codes of m = silu(g) * u
-  float* md;             // [n/32]
-  float* mf;             // [n] m as f32 (may be null)
-  int n;
 };
 
 // Positions per decode-attention tile (attn_core.h, attn_mfma.h).

@@ -19,8 +19,9 @@
 //                   cpu.rs:230-269) times 1/sqrt(hd) (layer.rs:257-258),
 //                   softmax with a sequential sum (cpu.rs:395-423), P.V
 //                   sequential over positions (layer.rs:276-299), ctx Q8_0
-//   exact_silu_q8   g / (1 + exp(-g)) * u (layer.rs:75-79) with glibc's
-//                   expf (exact_math.h), Q8_0 of the product
+//   exact_gemv_*_silu  the gate|up GEMV (same block order) finished with
+//                   g / (1 + exp(-g)) * u (layer.rs:75-79) with glibc's expf
+//                   (exact_math.h) and the Q8_0 of the product
 // The lm_head runs exact_gemv with the argmax partials of argmax_final.
 // A prompt of M rows runs as the reference's batched forward does, row by
 // row in its per-row orders: exact_norm_q8 over the M rows (one workgroup
@@ -198,30 +199,32 @@ __device__ __forceinline__ void norm_q8(const ExactNormArgs& args) {
 }
 
 // ---- GEMV -----------------------------------------------------------------
-// Rows per workgroup tile: wave w computes the block terms of rows w and
-// w + 4 (lanes over 64 blocks, coalesced loads), parks them in LDS, and lane
-// r of wave 0 adds row r's terms to its total in block order.
-constexpr int kExR = 8;
-constexpr int kExRW = kExR / (kT / LLMRS_WAVE);  // rows per wave
+// A workgroup tile is 4 * RW rows: wave w computes the block terms of rows
+// w, w + 4, ... (lanes over 64 blocks, coalesced loads), parks them in LDS,
+// and lane r of wave 0 adds row r's terms to its total in block order.  RW
+// is 2 (8-row tiles), or 16 for the SwiGLU launch, whose tile is one 64-row
+// group of 32 gate and the 32 matching up rows.
+template <int EPI>
+constexpr int ex_rows_per_wave() { return EPI == EPI_SILU ? kSiluTile / 4 : 2; }
 
 // The loads of one 64-block chunk for a wave's rows.
-template <int WT>
+template <int WT, int RW>
 struct ExChunk {
-  i32x4 a0, a1;                          // activation codes of block b
-  float da;                              // activation scale of block b
-  u32x4 w0[kExRW], w1[WT == WT_Q8H ? kExRW : 1];  // weight codes (Q8: two halves)
-  unsigned sc[kExRW];                    // raw weight scales
+  i32x4 a0, a1;                                // activation codes of block b
+  float da;                                    // activation scale of block b
+  u32x4 w0[RW], w1[WT == WT_Q8H ? RW : 1];     // weight codes (Q8: two halves)
+  unsigned sc[RW];                             // raw weight scales
 };
 
-template <int WT>
-__device__ __forceinline__ void ex_load(const ExactGemvArgs& a, int row0, int c, int nb, ExChunk<WT>& r) {
+template <int WT, int RW>
+__device__ __forceinline__ void ex_load(const ExactGemvArgs& a, int row0, int c, int nb, ExChunk<WT, RW>& r) {
   constexpr int BS = WT == WT_Q8H ? 32 : 16;
   const int b = min(c + lane_id(), nb - 1);  // clamped: terms past the row end are not folded
   r.a0 = *(const i32x4*)(a.xq + 32 * b);
   r.a1 = *(const i32x4*)(a.xq + 32 * b + 16);
   r.da = a.xd[b];
 #pragma unroll
-  for (int j = 0; j < kExRW; ++j) {
+  for (int j = 0; j < RW; ++j) {
     const int row = min(row0 + wave_id() + 4 * j, a.n - 1);
     const size_t blk = (size_t)row * nb + b;
     r.w0[j] = __builtin_nontemporal_load((const u32x4*)(a.wq + blk * BS));
@@ -232,8 +235,8 @@ __device__ __forceinline__ void ex_load(const ExactGemvArgs& a, int row0, int c,
 
 // Exact integer sum of one block: device Q4 layout (byte i = e[i] | e[i+16]
 // << 4, value q - 8) or Q8 codes, against the activation codes.
-template <int WT>
-__device__ __forceinline__ int ex_isum(const ExChunk<WT>& r, int j) {
+template <int WT, int RW>
+__device__ __forceinline__ int ex_isum(const ExChunk<WT, RW>& r, int j) {
   int s = 0;
   if (WT == WT_Q8H) {
     const u32x4 w0 = r.w0[j], w1 = r.w1[j];
@@ -261,8 +264,8 @@ __device__ __forceinline__ int ex_isum(const ExChunk<WT>& r, int j) {
 }
 
 // The Q4 offset -8 * sum(a) of block b (0 for Q8 weights).
-template <int WT>
-__device__ __forceinline__ int ex_offset(const ExChunk<WT>& r) {
+template <int WT, int RW>
+__device__ __forceinline__ int ex_offset(const ExChunk<WT, RW>& r) {
   if (WT == WT_Q8H) return 0;
   int sa = 0;
   sa = dot4(r.a0.x, 0x01010101, sa);
@@ -279,49 +282,59 @@ __device__ __forceinline__ int ex_offset(const ExChunk<WT>& r) {
 // Chunk loads in flight per wave: the loads of item i + PF are issued right
 // after item i is computed, so PF - 1 items' loads are outstanding while an
 // item is computed.  Q8 chunks carry twice the weight bytes; three of them
-// keep the kernel at four workgroups per CU.
-template <int WT>
-constexpr int ex_prefetch() { return WT == WT_Q8H ? 3 : 4; }
+// keep the 8-row kernels at four workgroups per CU.  A SwiGLU chunk holds 16
+// rows per wave: two Q4 chunks fit the registers of two workgroups per CU,
+// one Q8 chunk (at the 1B width K = 2048 is a single chunk anyway).
+template <int WT, int EPI>
+constexpr int ex_prefetch() {
+  if (EPI == EPI_SILU) return WT == WT_Q8H ? 1 : 2;
+  return WT == WT_Q8H ? 3 : 4;
+}
 
 // EPI: EPI_STORE (y = total), EPI_RESID (y = total + res), EPI_ARGMAX
 // (logits into y when set, and this workgroup's (max, lowest index) into
-// part_val / part_idx[blockIdx.x]).  Workgroups take 8-row tiles
-// round-robin and walk their (tile, 64-block chunk) items in order through
-// a ring of loads, across tile boundaries.
+// part_val / part_idx[blockIdx.x]), EPI_SILU (gate|up rows, one 64-row group
+// per tile: m = g / (1 + expf(-g)) * u (layer.rs:75-79, glibc's expf) into y
+// when set, and its Q8_0 codes and scale into mq / md).  Workgroups take
+// tiles round-robin and walk their (tile, 64-block chunk) items in order
+// through a ring of loads, across tile boundaries.
 template <int WT, int EPI>
 __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
+  constexpr bool SILU = EPI == EPI_SILU;
+  constexpr int RW = ex_rows_per_wave<EPI>();
+  constexpr int R = 4 * RW;  // rows per tile
   // Block terms of two items (a row padded to 68 floats: the 16-byte reads
-  // of the 8 folding lanes cover distinct banks).  Item i writes buffer
-  // i % 2 while wave 0 may still fold item i - 1 from the other; it cannot
-  // be two items ahead, since the barrier of item i - 1 waits for wave 0's
-  // fold of item i - 2.
+  // of the folding lanes cover distinct banks in groups of 8).  Item i writes
+  // buffer i % 2 while wave 0 may still fold item i - 1 from the other; it
+  // cannot be two items ahead, since the barrier of item i - 1 waits for
+  // wave 0's fold of item i - 2.
   constexpr int kPad = LLMRS_WAVE + 4;
-  __shared__ __align__(16) float s_p[2][kExR][kPad];
+  __shared__ __align__(16) float s_p[2][R][kPad];
   const int lane = lane_id(), wave = wave_id();
   const int nb = a.k >> 5, nch = (nb + LLMRS_WAVE - 1) / LLMRS_WAVE;
-  const int ntiles = (a.n + kExR - 1) / kExR;
+  const int ntiles = (a.n + R - 1) / R;
   const int my_tiles = (int)blockIdx.x < ntiles ? (ntiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
   const int nitems = my_tiles * nch;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  float total = 0.0f;  // lane r < kExR of wave 0: row row0 + r of the current tile
-  auto row0_of = [&](int item) { return ((int)blockIdx.x + (item / nch) * (int)gridDim.x) * kExR; };
-  auto load = [&](int item, ExChunk<WT>& r) {
-    ex_load<WT>(a, row0_of(item), (item % nch) * LLMRS_WAVE, nb, r);
+  float total = 0.0f;  // lane r < R of wave 0: row row0 + r of the current tile
+  auto row0_of = [&](int item) { return ((int)blockIdx.x + (item / nch) * (int)gridDim.x) * R; };
+  auto load = [&](int item, ExChunk<WT, RW>& r) {
+    ex_load<WT, RW>(a, row0_of(item), (item % nch) * LLMRS_WAVE, nb, r);
   };
   // one item: the wave's block terms into LDS, then wave 0 folds them; the
   // tile's last chunk writes its rows
-  auto step = [&](int item, const ExChunk<WT>& r) {
+  auto step = [&](int item, const ExChunk<WT, RW>& r) {
     const int c = (item % nch) * LLMRS_WAVE;
-    const int off = ex_offset<WT>(r);
+    const int off = ex_offset<WT, RW>(r);
     float(*buf)[kPad] = s_p[item & 1];
 #pragma unroll
-    for (int j = 0; j < kExRW; ++j) {
-      const int isum = ex_isum<WT>(r, j) + off;
+    for (int j = 0; j < RW; ++j) {
+      const int isum = ex_isum<WT, RW>(r, j) + off;
       buf[wave + 4 * j][lane] = (float)isum * (wscale<WT>(r.sc[j]) * r.da);
     }
     __syncthreads();
-    if (wave == 0 && lane < kExR) {
+    if (wave == 0 && lane < R) {
       const int cnt = min(LLMRS_WAVE, nb - c);
       if (cnt == LLMRS_WAVE) {  // 16 terms at a time, the next 16 read before these are added
         f32x4 t[2][4];
@@ -347,7 +360,19 @@ __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
       }
       const int row = row0_of(item) + lane;
       if (item % nch == nch - 1) {
-        if (row < a.n) {
+        if (SILU) {  // lanes 0-31 hold the gate rows, 32-63 the up rows
+          const float u = __shfl(total, lane + 32);
+          if (lane < 32) {
+            const float silu = total / (1.0f + exact_expf(-total));
+            const float m = silu * u;
+            float d;
+            const int q = q8_group32(m, &d);
+            const int j = row0_of(item) / 2 + lane;
+            a.mq[j] = (int8_t)q;
+            if (lane == 0) a.md[j >> 5] = d;
+            if (a.y) a.y[j] = m;
+          }
+        } else if (row < a.n) {
           if (EPI == EPI_RESID) a.y[row] = total + a.res[row];
           else if (a.y) a.y[row] = total;
           if (EPI == EPI_ARGMAX && better(total, row, bv, bi)) {
@@ -359,8 +384,8 @@ __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
       }
     }
   };
-  constexpr int PF = ex_prefetch<WT>();
-  ExChunk<WT> ring[PF];
+  constexpr int PF = ex_prefetch<WT, EPI>();
+  ExChunk<WT, RW> ring[PF];
 #pragma unroll
   for (int s = 0; s < PF; ++s)
     if (s < nitems) load(s, ring[s]);
@@ -622,27 +647,9 @@ __device__ __forceinline__ void attn_prefill(const PrefillAttnArgs& a) {
   }
 }
 
-// ---- SwiGLU ------------------------------------------------------------------
-// m[j] = silu(gate[j]) * up[j] from the gate|up GEMV's rows (runs of 32 gate
-// rows then the 32 matching up rows), then Q8_0 of m.
-__device__ __forceinline__ void silu_q8(const ExactSiluArgs& a) {
-  const int j = blockIdx.x * kT + threadIdx.x;
-  if (j >= a.n) return;  // n % 32 == 0: whole 32-lane groups leave together
-  const size_t r = (size_t)(j >> 5) * 64 + (j & 31);
-  const float g = a.gu[r], u = a.gu[r + 32];
-  const float silu = g / (1.0f + exact_expf(-g));
-  const float m = silu * u;
-  float d;
-  const int q = q8_group32(m, &d);
-  a.mq[j] = (int8_t)q;
-  if ((j & 31) == 0) a.md[j >> 5] = d;
-  if (a.mf) a.mf[j] = m;
-}
-
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(kNT) void exact_norm_q8(ExactNormArgs a) { norm_q8(a); }
-extern "C" __global__ __launch_bounds__(kT) void exact_silu_q8(ExactSiluArgs a) { silu_q8(a); }
 
 #define LLMRS_EXACT_GEMV(tag, WT)                                                                     \
   extern "C" __global__ __launch_bounds__(kT) void exact_gemv_##tag##_store(ExactGemvArgs a) {      \
@@ -653,6 +660,9 @@ extern "C" __global__ __launch_bounds__(kT) void exact_silu_q8(ExactSiluArgs a) 
   }                                                                                                 \
   extern "C" __global__ __launch_bounds__(kT) void exact_gemv_##tag##_argmax(ExactGemvArgs a) {     \
     gemv<WT, EPI_ARGMAX>(a);                                                                        \
+  }                                                                                                 \
+  extern "C" __global__ __launch_bounds__(kT) void exact_gemv_##tag##_silu(ExactGemvArgs a) {       \
+    gemv<WT, EPI_SILU>(a);                                                                          \
   }
 LLMRS_EXACT_GEMV(q4h, WT_Q4H)
 LLMRS_EXACT_GEMV(q4f, WT_Q4F)
