@@ -51,11 +51,12 @@ constexpr int kT = 256;
 // centre's plus l - kWin/2.  A fold from a given start is a fixed sequence
 // of IEEE additions, so when the sequential total at the chunk's start is one
 // of those floats, the lane that started there ends with exactly the
-// sequential total at the chunk's end.  One thread then walks the chunks in
-// order and takes each chunk's lane by the bit distance of the running total
-// from the chunk's centre; when the total lies outside the window (the
-// rounding drift of a long run of equal squares, for instance) it folds that
-// chunk itself from the total.  Either way the result is the sequential
+// sequential total at the chunk's end.  Wave 0 then walks the chunks in
+// order, with every chunk's ends in registers (lane l: the end from start l),
+// and takes each chunk's end by the bit distance of the running total from
+// the chunk's centre; when the total lies outside the window (the rounding
+// drift of a long run of equal squares, for instance) it folds that chunk
+// itself from the total.  Either way the result is the sequential
 // fold, bit for bit.  Real rows drift from the exact sum by well under
 // kWin/2 ulps at every chunk start, so the walk rarely folds.  n <= 32768
 // and a multiple of 32, so a 32-lane group holds one block.
@@ -103,6 +104,28 @@ __device__ __forceinline__ float fold_range(const float* sq, int i0, int i1, flo
   return acc;
 }
 
+// Wave64 sum of doubles with DPP row operations (as wave_sum); uniform.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+  v = v + dpp_d<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = v + dpp_d<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = v + dpp_d<0x141>(v);  // row_half_mirror
+  v = v + dpp_d<0x140>(v);  // row_mirror
+  return ((readlane_d(v, 0) + readlane_d(v, 16)) + readlane_d(v, 32)) + readlane_d(v, 48);
+}
+
 // The sequential fold of sq[0..n) by chunks (all threads); returns 1/rms
 // (cpu.rs:381-383).
 __device__ __forceinline__ float fold_scale(const float* sq, int n, float eps, FoldShared& sh) {
@@ -111,8 +134,7 @@ __device__ __forceinline__ float fold_scale(const float* sq, int n, float eps, F
   const int c0 = min(wave * len, n), c1 = min(c0 + len, n);
   double p = 0.0;
   for (int i = c0 + lane; i < c1; i += LLMRS_WAVE) p += (double)sq[i];
-#pragma unroll
-  for (int o = LLMRS_WAVE / 2; o > 0; o >>= 1) p += __shfl_xor(p, o);
+  p = wave_sum_d(p);
   if (lane == 0) sh.part[wave] = p;
   __syncthreads();
   double before = 0.0;
@@ -123,14 +145,25 @@ __device__ __forceinline__ float fold_scale(const float* sq, int n, float eps, F
   sh.end[wave][lane] = fold_range(sq, c0, c1, start);
   if (lane == 0) sh.centre[wave] = centre;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float ss = sh.end[0][0];
-    for (int c = 1; c < kNW && c * len < n; ++c) {
-      const unsigned j = __float_as_uint(ss) - sh.centre[c] + (unsigned)(kWin / 2);
-      ss = j < (unsigned)kWin ? sh.end[c][j] : fold_range(sq, c * len, min(c * len + len, n), ss);
+  if (wave == 0) {  // the walk, uniform over wave 0: lane l holds every chunk's end from start l
+    float e[kNW];
+#pragma unroll
+    for (int c = 0; c < kNW; ++c) e[c] = sh.end[c][lane];
+    float ss = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[0]), 0));
+#pragma unroll
+    for (int c = 1; c < kNW; ++c) {
+      if (c * len < n) {
+        const unsigned cen = (unsigned)__builtin_amdgcn_readfirstlane((int)sh.centre[c]);
+        const unsigned j = __float_as_uint(ss) - cen + (unsigned)(kWin / 2);
+        const float f = j < (unsigned)kWin ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[c]), (int)j))
+                                           : fold_range(sq, c * len, min(c * len + len, n), ss);
+        ss = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(f)));
+      }
     }
-    const float rms = __builtin_sqrtf(ss / (float)n + eps);
-    sh.scale = 1.0f / rms;
+    if (lane == 0) {
+      const float rms = __builtin_sqrtf(ss / (float)n + eps);
+      sh.scale = 1.0f / rms;
+    }
   }
   __syncthreads();
   return sh.scale;
