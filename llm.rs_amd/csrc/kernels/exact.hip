@@ -39,47 +39,46 @@ namespace {
 
 constexpr int kT = 256;
 
-// ---- RMSNorm + Q8_0 ---------------------------------------------------------
-// One workgroup of kNT threads per row.  All threads square the row into LDS
-// (each product is the reference's own rounding of x*x).  The sum of squares
-// is the reference's sequential fold (cpu.rs:381),
-//   ss = (...((0 + sq[0]) + sq[1]) + ...) + sq[n-1],
-// evaluated by chunks in parallel: wave c owns chunk c (kNW chunks of equal
-// length in index order) and folds it from kWin consecutive f32 start values
-// at once, one per lane, centred on the exact sum of the squares before the
-// chunk (added in f64): lane l starts at the float whose bit pattern is the
-// centre's plus l - kWin/2.  A fold from a given start is a fixed sequence
-// of IEEE additions, so when the sequential total at the chunk's start is one
-// of those floats, the lane that started there ends with exactly the
-// sequential total at the chunk's end.  Wave 0 then walks the chunks in
-// order, with every chunk's ends in registers (lane l: the end from start l),
-// and takes each chunk's end by the bit distance of the running total from
-// the chunk's centre; when the total lies outside the window (the rounding
-// drift of a long run of equal squares, for instance) it folds that chunk
-// itself from the total.  Either way the result is the sequential
-// fold, bit for bit.  Real rows drift from the exact sum by well under
-// kWin/2 ulps at every chunk start, so the walk rarely folds.  n <= 32768
-// and a multiple of 32, so a 32-lane group holds one block.
-constexpr int kNT = 1024;              // threads of the norm workgroup
-constexpr int kNW = kNT / LLMRS_WAVE;  // fold chunks, one per wave
-constexpr int kWin = LLMRS_WAVE;       // start values per chunk, one per lane
+// ---- sequential sums by chunks ---------------------------------------------
+// The reference folds sums in index order, one rounding per term:
+//   sum = (...((0 + v[0]) + v[1]) + ...) + v[n-1]
+// (the RMSNorm sum of squares, cpu.rs:381; the softmax denominator,
+// cpu.rs:413-415).  seq_sum evaluates that fold with the NW waves of a
+// workgroup: wave c owns chunk c (NW chunks of equal length in index order)
+// and folds it from kWin consecutive f32 start values at once, one per lane,
+// centred on the exact sum of the terms before the chunk (added in f64):
+// lane l starts at the float whose bit pattern is the centre's plus
+// l - kWin/2.  A fold from a given start is a fixed sequence of IEEE
+// additions, so when the sequential total at the chunk's start is one of
+// those floats, the lane that started there ends with exactly the sequential
+// total at the chunk's end.  Wave 0 then walks the chunks in order, with
+// every chunk's ends in registers (lane l: the end from start l), and takes
+// each chunk's end by the bit distance of the running total from the chunk's
+// centre; when the total lies outside the window (the rounding drift of a
+// long run of equal terms, for instance) it folds that chunk itself from the
+// total.  Either way the result is the sequential fold, bit for bit.  On
+// real rows of non-negative terms the fold drifts from the exact sum by well
+// under kWin/2 ulps at every chunk start, so the walk rarely folds.
+constexpr int kWin = LLMRS_WAVE;  // start values per chunk, one per lane
 
+template <int NW>
 struct FoldShared {
-  double part[kNW];      // sum of each chunk's squares (f64)
-  unsigned centre[kNW];  // bit pattern of each chunk's centre start value
-  float end[kNW][kWin];  // chunk c folded from the start value of lane l
-  float scale;
+  double part[NW];      // sum of each chunk's terms (f64)
+  unsigned centre[NW];  // bit pattern of each chunk's centre start value
+  float end[NW][kWin];  // chunk c folded from the start value of lane l
+  float total;
 };
 
-// One lane's fold of sq[i0..i1) from acc in index order (i0, i1 multiples of
-// 32), reading the squares 32 at a time with the next 32 requested before
-// the current ones are added.
-__device__ __forceinline__ float fold_range(const float* sq, int i0, int i1, float acc) {
+// One lane's fold of v[i0..i1) from acc in index order (i1 - i0 a multiple
+// of 32, i0 a multiple of 4, v 16-byte aligned), reading the terms 32 at a
+// time with the next 32 requested before the current ones are added.  With
+// constant bounds the compiler unrolls it completely.
+__device__ __forceinline__ float fold_range(const float* v, int i0, int i1, float acc) {
   if (i0 >= i1) return acc;
   f32x4 A[8], B[8];
   auto load = [&](f32x4 (&r)[8], int i) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = *(const f32x4*)(sq + i + 4 * j);
+    for (int j = 0; j < 8; ++j) r[j] = *(const f32x4*)(v + i + 4 * j);
   };
   auto add = [&](const f32x4 (&r)[8]) {
 #pragma unroll
@@ -101,6 +100,13 @@ __device__ __forceinline__ float fold_range(const float* sq, int i0, int i1, flo
     add(B);
     if (!more2) break;
   }
+  return acc;
+}
+// The same for any i1 >= i0: whole groups of 32, then the rest one by one.
+__device__ __forceinline__ float fold_any(const float* v, int i0, int i1, float acc) {
+  const int i32 = i0 + (i1 - i0) / 32 * 32;
+  acc = fold_range(v, i0, i32, acc);
+  for (int i = i32; i < i1; ++i) acc = acc + v[i];
   return acc;
 }
 
@@ -126,14 +132,17 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   return ((readlane_d(v, 0) + readlane_d(v, 16)) + readlane_d(v, 32)) + readlane_d(v, 48);
 }
 
-// The sequential fold of sq[0..n) by chunks (all threads); returns 1/rms
-// (cpu.rs:381-383).
-__device__ __forceinline__ float fold_scale(const float* sq, int n, float eps, FoldShared& sh) {
+// The sequential sum of v[0..n) (v in LDS, 16-byte aligned, written before
+// the call and visible to every thread), by all NW waves of the workgroup;
+// every thread returns it.  WHOLE32: n is a multiple of 32 (so is every
+// chunk).
+template <int NW, bool WHOLE32>
+__device__ __forceinline__ float seq_sum(const float* v, int n, FoldShared<NW>& sh) {
   const int lane = lane_id(), wave = wave_id();
-  const int len = (n + kNW * 32 - 1) / (kNW * 32) * 32;
+  const int len = (n + NW * 32 - 1) / (NW * 32) * 32;
   const int c0 = min(wave * len, n), c1 = min(c0 + len, n);
   double p = 0.0;
-  for (int i = c0 + lane; i < c1; i += LLMRS_WAVE) p += (double)sq[i];
+  for (int i = c0 + lane; i < c1; i += LLMRS_WAVE) p += (double)v[i];
   p = wave_sum_d(p);
   if (lane == 0) sh.part[wave] = p;
   __syncthreads();
@@ -142,31 +151,44 @@ __device__ __forceinline__ float fold_scale(const float* sq, int n, float eps, F
   const unsigned centre = __float_as_uint((float)before);
   // chunk 0 starts from the fold's own 0
   const float start = wave == 0 ? 0.0f : __uint_as_float(centre + (unsigned)lane - (unsigned)(kWin / 2));
-  sh.end[wave][lane] = fold_range(sq, c0, c1, start);
+  sh.end[wave][lane] = WHOLE32 ? fold_range(v, c0, c1, start) : fold_any(v, c0, c1, start);
   if (lane == 0) sh.centre[wave] = centre;
   __syncthreads();
-  if (wave == 0) {  // the walk, uniform over wave 0: lane l holds every chunk's end from start l
-    float e[kNW];
+  if (wave == 0) {  // the walk, uniform over wave 0
+    float e[NW];
 #pragma unroll
-    for (int c = 0; c < kNW; ++c) e[c] = sh.end[c][lane];
+    for (int c = 0; c < NW; ++c) e[c] = sh.end[c][lane];
     float ss = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[0]), 0));
 #pragma unroll
-    for (int c = 1; c < kNW; ++c) {
+    for (int c = 1; c < NW; ++c) {
       if (c * len < n) {
         const unsigned cen = (unsigned)__builtin_amdgcn_readfirstlane((int)sh.centre[c]);
         const unsigned j = __float_as_uint(ss) - cen + (unsigned)(kWin / 2);
         const float f = j < (unsigned)kWin ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e[c]), (int)j))
-                                           : fold_range(sq, c * len, min(c * len + len, n), ss);
+                                           : WHOLE32 ? fold_range(v, c * len, min(c * len + len, n), ss)
+                                                     : fold_any(v, c * len, min(c * len + len, n), ss);
         ss = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(f)));
       }
     }
-    if (lane == 0) {
-      const float rms = __builtin_sqrtf(ss / (float)n + eps);
-      sh.scale = 1.0f / rms;
-    }
+    if (lane == 0) sh.total = ss;
   }
   __syncthreads();
-  return sh.scale;
+  return sh.total;
+}
+
+// ---- RMSNorm + Q8_0 ---------------------------------------------------------
+// One workgroup of kNT threads per row.  All threads square the row into LDS
+// (each product is the reference's own rounding of x*x), seq_sum folds the
+// squares (cpu.rs:381), then y = (x*s)*w and its Q8_0 blocks.  n <= 32768 and
+// a multiple of 32, so a 32-lane group holds one block.
+constexpr int kNT = 1024;              // threads of the norm workgroup
+constexpr int kNW = kNT / LLMRS_WAVE;  // fold chunks, one per wave
+
+// 1/rms of the squares sq[0..n) (cpu.rs:381-383), all threads.
+__device__ __forceinline__ float fold_scale(const float* sq, int n, float eps, FoldShared<kNW>& sh) {
+  const float ss = seq_sum<kNW, true>(sq, n, sh);
+  const float rms = __builtin_sqrtf(ss / (float)n + eps);
+  return 1.0f / rms;
 }
 
 // The row this workgroup normalises.
@@ -194,7 +216,7 @@ __device__ __forceinline__ void norm_out(const NormRow& a, int i, float x, float
 // n == kNT * EPT: thread t holds elements t + kNT*j of x and w in registers
 // from the start, so nothing is loaded after the fold.
 template <int EPT>
-__device__ __forceinline__ void norm_q8_regs(const NormRow& a, float* sq, FoldShared& sh) {
+__device__ __forceinline__ void norm_q8_regs(const NormRow& a, float* sq, FoldShared<kNW>& sh) {
   const int tid = threadIdx.x;
   float xv[EPT], wv[EPT];
 #pragma unroll
@@ -211,7 +233,7 @@ __device__ __forceinline__ void norm_q8_regs(const NormRow& a, float* sq, FoldSh
 
 __device__ __forceinline__ void norm_q8(const ExactNormArgs& args) {
   extern __shared__ __align__(16) float sq[];
-  __shared__ FoldShared sh;
+  __shared__ FoldShared<kNW> sh;
   const size_t ro = (size_t)blockIdx.x * args.n;  // this workgroup's row
   const NormRow a{args.x + ro, args.w, args.xq + ro, args.xd + ro / 32, args.y ? args.y + ro : nullptr,
                   args.n, args.layout, args.eps};
@@ -343,6 +365,8 @@ __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
   // wave 0's fold of item i - 2.
   constexpr int kPad = LLMRS_WAVE + 4;
   __shared__ __align__(16) float s_p[2][R][kPad];
+  __shared__ uint64_t s_exptab[SILU ? 32 : 1];  // exact_expf's table (visible after the first barrier)
+  if (SILU && threadIdx.x < 32) s_exptab[threadIdx.x] = expf_detail::kT[threadIdx.x];
   const int lane = lane_id(), wave = wave_id();
   const int nb = a.k >> 5, nch = (nb + LLMRS_WAVE - 1) / LLMRS_WAVE;
   const int ntiles = (a.n + R - 1) / R;
@@ -396,7 +420,7 @@ __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
         if (SILU) {  // lanes 0-31 hold the gate rows, 32-63 the up rows
           const float u = __shfl(total, lane + 32);
           if (lane < 32) {
-            const float silu = total / (1.0f + exact_expf(-total));
+            const float silu = total / (1.0f + exact_expf(-total, s_exptab));
             const float m = silu * u;
             float d;
             const int q = q8_group32(m, &d);
@@ -450,76 +474,130 @@ __device__ __forceinline__ void gemv(const ExactGemvArgs& a) {
 
 // ---- attention -------------------------------------------------------------
 constexpr int kVTile = 16384;  // bytes of V per LDS tile
+constexpr int kChunkedSum = 384;  // softmax rows from this length sum by chunks
 
-// LDS of one query row's attention (the scores are the dynamic LDS).
-template <int HD>
+// LDS of one query row's attention (the scores are the dynamic LDS); V tiles
+// for f32 caches only.
+template <int HD, bool F16>
 struct AttnShared {
   float q[HD], k[HD], v[HD];
+  uint64_t exptab[32];  // exact_expf's table
   float red[kT / LLMRS_WAVE];
-  float inv;
-  u32x4 vt[2][kVTile / 16];  // V tiles
+  FoldShared<kT / LLMRS_WAVE> fold;
+  u32x4 vt[F16 ? 1 : 2][F16 ? 1 : kVTile / 16];  // V tiles
 };
 
 // One query row's attention over the KV head at kbase / vbase: cache rows
 // 0 .. ncache-1, then (OWN) the row at position ncache from sh.k / sh.v.
-// Scores: the sequential dot over the head dims of q (sh.q) and each row,
-// then times the scale (matmul_slice cpu.rs:230-269, layer.rs:257-258);
-// softmax with the maximum from f32::MIN, glibc's expf, a sequential sum by
-// one lane and e * (1/sum) (cpu.rs:395-423); ctx[d] = sum over the rows of
-// p * V[d], sequential (layer.rs:276-299).  V rows pass through LDS in 16 KB
-// tiles that every thread loads (coalesced), each tile requested while the
-// previous one is added; `first` holds the first tile's loads, issued by the
-// caller.  Returns ctx[d] for thread d < HD.
+// Scores: the sequential dot over the head dims of q and each row, then
+// times the scale (matmul_slice cpu.rs:230-269, layer.rs:257-258); softmax
+// with the maximum from f32::MIN, glibc's expf, the sequential sum (seq_sum
+// for long rows) and e * (1/sum) (cpu.rs:395-423); ctx[d] = sum over the
+// rows of p * V[d], sequential (layer.rs:276-299).  f16 caches: each thread
+// requests its next K row before it folds the current one; thread d < HD
+// reads dim d of the blocked V rows (8 positions per 16-byte load) straight
+// from memory, kVRing blocks ahead (the first ones before the softmax).  f32 caches:
+// V rows pass through LDS in 16 KB tiles that every thread loads
+// (coalesced), each tile requested while the previous one is added; `first`
+// holds the first tile's loads, issued by the caller.  Returns ctx[d] for
+// thread d < HD.
+constexpr int kVRing = 16;
+// Start of a query row's attention: exact_expf's table into LDS (visible
+// after the caller's barrier).
+template <int HD, bool F16>
+__device__ __forceinline__ void attn_start(AttnShared<HD, F16>& sh) {
+  if (threadIdx.x < 32) sh.exptab[threadIdx.x] = expf_detail::kT[threadIdx.x];
+}
+
+template <bool F16>
+using VRing = u32x4[F16 ? kVRing : 1];
+
 template <int HD, bool F16, bool OWN>
 __device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, size_t head_bytes, int ncache,
-                                          float scale, float* s_p, AttnShared<HD>& sh, const u32x4 (&first)[kVTile / 16 / kT]) {
+                                          float scale, float* s_p, AttnShared<HD, F16>& sh,
+                                          const u32x4 (&first)[kVTile / 16 / kT]) {
   constexpr int VB = F16 ? 2 : 4;
-  constexpr int TP = kVTile / (HD * VB);    // positions per tile, a multiple of 8
-  constexpr int LPT = kVTile / 16 / kT;     // 16-byte loads per thread per tile
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int T = ncache + (OWN ? 1 : 0);
-  const int ntile = (ncache + TP - 1) / TP;
-  u32x4 st[LPT];
-#pragma unroll
-  for (int l = 0; l < LPT; ++l) st[l] = first[l];
-  auto vload = [&](int tile) {  // rows past ncache read stale (in-bounds) bytes, never added
-#pragma unroll
-    for (int l = 0; l < LPT; ++l) {
-      const size_t off = min((size_t)tile * kVTile + 16 * (size_t)(tid + kT * l), head_bytes - 16);
-      st[l] = *(const u32x4*)(vbase + off);
-    }
-  };
-  auto vstore = [&](int buf) {
-#pragma unroll
-    for (int l = 0; l < LPT; ++l) sh.vt[buf][tid + kT * l] = st[l];
-  };
+  const int d = tid;
+  const u32x4* vb = (const u32x4*)vbase + d;  // block b of dim d at vb[b * HD] (f16)
+  const int nblk = (ncache + 7) / 8;
   // scores: sequential dot over the head dims, then the scale
   float mx = -3.40282347e+38f;  // f32::MIN (cpu.rs:408)
-  for (int t = tid; t < T; t += kT) {
+  auto own_dot = [&]() {
     float s = 0.0f;
-    if (OWN && t == ncache) {
-      for (int e = 0; e < HD; ++e) s = s + sh.q[e] * sh.k[e];
-    } else if (F16) {
-      const uint16_t* kr = (const uint16_t*)kbase + (size_t)t * HD;
-      for (int e = 0; e < HD; e += 8) {
-        const u32x4 w = *(const u32x4*)(kr + e);
+    for (int e = 0; e < HD; ++e) s = s + sh.q[e] * sh.k[e];
+    return s;
+  };
+  if constexpr (F16) {
+    constexpr int KW = HD * 2 / 16;  // 16-byte words per K row
+    auto kload = [&](int t, u32x4 (&w)[KW]) {
+      const u32x4* kr = (const u32x4*)(kbase + (size_t)t * HD * 2);
+#pragma unroll
+      for (int j = 0; j < KW; ++j) w[j] = kr[j];
+    };
+    auto score = [&](int t, const u32x4 (&w)[KW]) {
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KW; ++j) {
+        const f32x4 qa = *(const f32x4*)&sh.q[8 * j], qb = *(const f32x4*)&sh.q[8 * j + 4];
+        const float qv[8] = {qa[0], qa[1], qa[2], qa[3], qb[0], qb[1], qb[2], qb[3]};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          s = s + sh.q[e + 2 * i] * h2f((uint16_t)(w[i] & 0xFFFF));
-          s = s + sh.q[e + 2 * i + 1] * h2f((uint16_t)(w[i] >> 16));
+          s = s + qv[2 * i] * h2f((uint16_t)(w[j][i] & 0xFFFF));
+          s = s + qv[2 * i + 1] * h2f((uint16_t)(w[j][i] >> 16));
         }
       }
-    } else {
-      const float* kr = (const float*)kbase + (size_t)t * HD;
-      for (int e = 0; e < HD; e += 4) {
-        const f32x4 w = *(const f32x4*)(kr + e);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = s + sh.q[e + i] * w[i];
-      }
+      s = s * scale;
+      s_p[t] = s;
+      mx = fmaxf(mx, s);
+    };
+    // loads are unconditional (rows clamped into the cache; a clamped row is
+    // never scored), so the next row's load never waits on the current one
+    const int last = max(ncache - 1, 0);
+    u32x4 ka[KW], kb[KW];
+    int t = tid;
+    kload(min(t, last), ka);
+    while (t < ncache) {
+      const int t2 = t + kT;
+      kload(min(t2, last), kb);
+      score(t, ka);
+      if (t2 >= ncache) break;
+      const int t3 = t2 + kT;
+      kload(min(t3, last), ka);
+      score(t2, kb);
+      t = t3;
     }
-    s = s * scale;
-    s_p[t] = s;
-    mx = fmaxf(mx, s);
+    if (OWN && tid == ncache % kT) {  // the new row, from LDS
+      const float s = own_dot() * scale;
+      s_p[ncache] = s;
+      mx = fmaxf(mx, s);
+    }
+  } else {
+    for (int t = tid; t < T; t += kT) {
+      float s = 0.0f;
+      if (OWN && t == ncache) {
+        s = own_dot();
+      } else {
+        const float* kr = (const float*)kbase + (size_t)t * HD;
+        for (int e = 0; e < HD; e += 4) {
+          const f32x4 w = *(const f32x4*)(kr + e);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) s = s + sh.q[e + i] * w[i];
+        }
+      }
+      s = s * scale;
+      s_p[t] = s;
+      mx = fmaxf(mx, s);
+    }
+  }
+  // f16: the first V blocks of dim d, requested before the softmax (blocks
+  // clamped into the cache, unconditionally, as the K rows)
+  const int lastb = max(nblk - 1, 0);
+  VRing<F16> ring;
+  if (F16 && d < HD) {
+#pragma unroll
+    for (int j = 0; j < (F16 ? kVRing : 1); ++j) ring[j] = vb[(size_t)min(j, lastb) * HD];
   }
   mx = wave_max(mx);
   if (lane == 0) sh.red[wave] = mx;
@@ -527,60 +605,119 @@ __device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, 
   mx = sh.red[0];
 #pragma unroll
   for (int w = 1; w < kT / LLMRS_WAVE; ++w) mx = fmaxf(mx, sh.red[w]);
-  for (int t = tid; t < T; t += kT) s_p[t] = exact_expf(s_p[t] - mx);
+  for (int t = tid; t < T; t += kT) s_p[t] = exact_expf(s_p[t] - mx, sh.exptab);
   __syncthreads();
-  if (tid == 0) {  // sequential sum of the exponentials
-    float sum = 0.0f;
-    int t = 0;
-    for (; t + 4 <= T; t += 4) {
-      const f32x4 e = *(const f32x4*)(s_p + t);
-      sum = sum + e[0];
-      sum = sum + e[1];
-      sum = sum + e[2];
-      sum = sum + e[3];
+  // the sequential sum of the exponentials: by chunks for long rows, by one
+  // lane below kChunkedSum terms (where the chunks' fixed cost exceeds the
+  // fold); both give the same sum
+  float sum;
+  if (T >= kChunkedSum) {
+    sum = seq_sum<kT / LLMRS_WAVE, false>(s_p, T, sh.fold);
+  } else {
+    if (tid == 0) {
+      float acc = 0.0f;
+      int t = 0;
+      for (; t + 4 <= T; t += 4) {
+        const f32x4 e = *(const f32x4*)(s_p + t);
+        acc = acc + e[0];
+        acc = acc + e[1];
+        acc = acc + e[2];
+        acc = acc + e[3];
+      }
+      for (; t < T; ++t) acc = acc + s_p[t];
+      sh.fold.total = acc;
     }
-    for (; t < T; ++t) sum = sum + s_p[t];
-    sh.inv = 1.0f / sum;
+    __syncthreads();
+    sum = sh.fold.total;
   }
-  __syncthreads();
-  const float inv = sh.inv;
+  const float inv = 1.0f / sum;
   for (int t = tid; t < T; t += kT) s_p[t] = s_p[t] * inv;
-  if (ntile > 0) vstore(0);
-  __syncthreads();
   // ctx[d] = sum over t of p_t * V[t][d], sequential in t; the own row last.
-  const int d = tid;
   float acc = 0.0f;
-  for (int i = 0; i < ntile; ++i) {
-    if (i + 1 < ntile) vload(i + 1);
+  if constexpr (F16) {
+    __syncthreads();
     if (d < HD) {
-      const int t0 = i * TP, t1 = min(t0 + TP, ncache);
-      if (F16) {  // blocked V: the 8 positions of a block are 16 contiguous bytes per dim
-        const uint16_t* vt = (const uint16_t*)sh.vt[i & 1];
-        int t = t0;
-        for (; t + 8 <= t1; t += 8) {
-          const u32x4 w = *(const u32x4*)(vt + ((t - t0) / 8 * HD + d) * 8);
+      // 8 positions of one block: p from LDS, V from the block's 16 bytes
+      auto block8 = [&](const u32x4& w, int t0, int cnt) {
+        if (cnt == 8) {
+          const f32x4 p0 = *(const f32x4*)(s_p + t0), p1 = *(const f32x4*)(s_p + t0 + 4);
+          acc = acc + p0[0] * h2f((uint16_t)(w[0] & 0xFFFF));
+          acc = acc + p0[1] * h2f((uint16_t)(w[0] >> 16));
+          acc = acc + p0[2] * h2f((uint16_t)(w[1] & 0xFFFF));
+          acc = acc + p0[3] * h2f((uint16_t)(w[1] >> 16));
+          acc = acc + p1[0] * h2f((uint16_t)(w[2] & 0xFFFF));
+          acc = acc + p1[1] * h2f((uint16_t)(w[2] >> 16));
+          acc = acc + p1[2] * h2f((uint16_t)(w[3] & 0xFFFF));
+          acc = acc + p1[3] * h2f((uint16_t)(w[3] >> 16));
+        } else {  // the last, partial block: rows past ncache are not added
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc = acc + s_p[t + 2 * e] * h2f((uint16_t)(w[e] & 0xFFFF));
-            acc = acc + s_p[t + 2 * e + 1] * h2f((uint16_t)(w[e] >> 16));
-          }
+          for (int e = 0; e < 8; ++e)
+            if (e < cnt) acc = acc + s_p[t0 + e] * h2f((uint16_t)(w[e / 2] >> (16 * (e & 1))));
         }
-        for (; t < t1; ++t) acc = acc + s_p[t] * h2f(vt[((t - t0) / 8 * HD + d) * 8 + (t & 7)]);
-      } else {
+      };
+      const int nfull = ncache / 8;
+      // the last whole blocks from slot 0 of a round, then the partial one
+      auto tail = [&](const VRing<F16>& r, int b0) {
+#pragma unroll
+        for (int j = 0; j < kVRing; ++j) {
+          const int b = b0 + j;
+          if (b < nfull) block8(r[j], 8 * b, 8);
+          else if (b == nfull && 8 * b < ncache) block8(r[j], 8 * b, ncache - 8 * b);
+        }
+      };
+      // whole rounds of the ring without a branch, the next round's loads
+      // (clamped, unconditional) issued as each block is consumed
+      int b0 = 0;
+      for (; b0 + kVRing <= nfull; b0 += kVRing) {
+#pragma unroll
+        for (int j = 0; j < kVRing; ++j) {
+          const u32x4 w = ring[j];
+          ring[j] = vb[(size_t)min(b0 + j + kVRing, lastb) * HD];
+          block8(w, 8 * (b0 + j), 8);
+        }
+      }
+      tail(ring, b0);
+    }
+  } else {
+    constexpr int TP = kVTile / (HD * VB);  // positions per tile, a multiple of 8
+    constexpr int LPT = kVTile / 16 / kT;   // 16-byte loads per thread per tile
+    const int ntile = (ncache + TP - 1) / TP;
+    u32x4 st[LPT];
+#pragma unroll
+    for (int l = 0; l < LPT; ++l) st[l] = first[l];
+    auto vload = [&](int tile) {  // rows past ncache read stale (in-bounds) bytes, never added
+#pragma unroll
+      for (int l = 0; l < LPT; ++l) {
+        const size_t off = min((size_t)tile * kVTile + 16 * (size_t)(tid + kT * l), head_bytes - 16);
+        st[l] = *(const u32x4*)(vbase + off);
+      }
+    };
+    auto vstore = [&](int buf) {
+#pragma unroll
+      for (int l = 0; l < LPT; ++l) sh.vt[buf][tid + kT * l] = st[l];
+    };
+    if (ntile > 0) vstore(0);
+    __syncthreads();
+    for (int i = 0; i < ntile; ++i) {
+      if (i + 1 < ntile) vload(i + 1);
+      if (d < HD) {
+        const int t0 = i * TP, t1 = min(t0 + TP, ncache);
         const float* vt = (const float*)sh.vt[i & 1];
         for (int t = t0; t < t1; ++t) acc = acc + s_p[t] * vt[(t - t0) * HD + d];
       }
+      if (i + 1 < ntile) vstore((i + 1) & 1);
+      __syncthreads();
     }
-    if (i + 1 < ntile) vstore((i + 1) & 1);
-    __syncthreads();
   }
   if (OWN && d < HD) acc = acc + s_p[ncache] * sh.v[d];
   return acc;
 }
 
-// The first V tile's loads (tile 0 of the KV head), issued at kernel start.
+// The first V tile's loads (tile 0 of the KV head; f32 caches), issued at
+// kernel start.
 template <int HD, bool F16>
 __device__ __forceinline__ void attn_first_tile(const char* vbase, size_t head_bytes, u32x4 (&st)[kVTile / 16 / kT]) {
+  if (F16) return;
 #pragma unroll
   for (int l = 0; l < kVTile / 16 / kT; ++l)
     st[l] = *(const u32x4*)(vbase + min(16 * (size_t)(threadIdx.x + kT * l), head_bytes - 16));
@@ -596,7 +733,7 @@ template <int HD, bool F16>
 __device__ __forceinline__ void attn(const ExactAttnArgs& a) {
   constexpr int MID = HD / 2, VB = F16 ? 2 : 4;
   extern __shared__ __align__(16) float s_p[];  // [pos + 1]
-  __shared__ __align__(16) AttnShared<HD> sh;
+  __shared__ __align__(16) AttnShared<HD, F16> sh;
   const int tid = threadIdx.x;
   const int h = blockIdx.x, n_rep = a.nq / a.nkv, g = h / n_rep;
   const int pos = *a.pos_ptr;
@@ -606,6 +743,7 @@ __device__ __forceinline__ void attn(const ExactAttnArgs& a) {
   const char* vbase = (const char*)a.vc + head * VB;
   u32x4 first[kVTile / 16 / kT];
   attn_first_tile<HD, F16>(vbase, head_bytes, first);
+  attn_start<HD, F16>(sh);
   if (tid < MID) {  // rotate-half RoPE of q and the new k (cpu.rs:345-354)
     const float co = a.rope_cos[(size_t)pos * MID + tid], sn = a.rope_sin[(size_t)pos * MID + tid];
     const float* q = a.qkv + (size_t)h * HD;
@@ -657,7 +795,7 @@ template <int HD, bool F16>
 __device__ __forceinline__ void attn_prefill(const PrefillAttnArgs& a) {
   constexpr int VB = F16 ? 2 : 4;
   extern __shared__ __align__(16) float s_p[];  // [start_pos + t + 1]
-  __shared__ __align__(16) AttnShared<HD> sh;
+  __shared__ __align__(16) AttnShared<HD, F16> sh;
   const int tid = threadIdx.x;
   const int h = blockIdx.x, t = blockIdx.y, g = h / (a.nq / a.nkv);
   const int pos = a.start_pos + t;
@@ -666,6 +804,7 @@ __device__ __forceinline__ void attn_prefill(const PrefillAttnArgs& a) {
   const char* vbase = (const char*)a.vc + (size_t)g * head_bytes;
   u32x4 first[kVTile / 16 / kT];
   attn_first_tile<HD, F16>(vbase, head_bytes, first);
+  attn_start<HD, F16>(sh);
   const int qd = a.nq * HD;
   if (tid < HD) sh.q[tid] = a.q[(size_t)t * qd + (size_t)h * HD + tid];
   __syncthreads();

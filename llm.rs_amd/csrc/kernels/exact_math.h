@@ -48,7 +48,9 @@ constexpr double kC1 = 0x1.ebfce50fac4f3p-13;
 constexpr double kC2 = 0x1.62e42ff0c52d6p-6;
 }  // namespace expf_detail
 
-LLMRS_HD inline float exact_expf(float x) {
+// `tab` holds kT (a device kernel passes a copy in LDS, so the lookup does
+// not wait on a memory round trip).
+LLMRS_HD inline float exact_expf(float x, const uint64_t* tab = expf_detail::kT) {
   using namespace expf_detail;
   const uint32_t ux = __builtin_bit_cast(uint32_t, x);
   const uint32_t abstop = (ux >> 20) & 0x7ff;
@@ -63,7 +65,7 @@ LLMRS_HD inline float exact_expf(float x) {
   const uint64_t ki = __builtin_bit_cast(uint64_t, kd0);
   const double kd = kd0 - kShift;
   const double r = __builtin_fma(kInvLn2N, xd, -kd);           // z - k
-  const uint64_t t = kT[ki % 32] + (ki << 47);
+  const uint64_t t = tab[ki % 32] + (ki << 47);
   const double s = __builtin_bit_cast(double, t);
   const double p = __builtin_fma(kC0, r, kC1);
   const double r2 = r * r;

@@ -164,6 +164,36 @@ def test_exact_norm_fold_rows(hip, orc, spec):
     gm.close()
 
 
+@pytest.mark.parametrize("spec,pos", [LAYERS[1], LAYERS[6]], ids=lambda v: getattr(v, "name", str(v)))
+def test_exact_attention_fold_equal_keys(hip, orc, spec, pos):
+    """Cached keys k0, -k0, then 0.5 k0 on every other row of a KV head: one
+    of the first two scores exceeds the repeated one, so the softmax
+    denominator holds a long run of equal terms below 1, whose sequential sum
+    drifts from the exact sum and takes the in-order fallback of the chunked
+    fold.  ctx and its codes equal the oracle's."""
+    gm, om, w = layer_models(hip, orc, spec, pos + 1)
+    gm.set_exact(True)
+    for g in range(spec.n_kv_heads):
+        k, v = syn.prefill_kv(syn.with_sizes(spec, prefilled=pos), 0, g)
+        k0 = k[0].copy()
+        k = np.repeat((0.5 * k0)[None], pos, axis=0).astype(k.dtype)
+        k[0], k[1] = k0, -k0
+        gm.kv_write(0, g, 0, k, v)
+        om.kv_write(0, g, 0, k, v)
+    L, (n_in, _) = w.linears[0], w.norms[0]
+    x = synth_normal(spec.seed, 71, spec.hidden, 0.0, 1.0)
+    pr = gm.probe_decode_layer(0, pos, x)
+    oq, od = orc.quantize_row_q8_0(orc.rms_norm(x[None], n_in, spec.rms_eps)[0])
+    qkv = np.concatenate([gemv(orc, spec, oq, od, L[s])[0] for s in (W_Q, W_K, W_V)])
+    same(pr["qkv"], qkv, "Q|K|V rows")
+    ctx = om.attention(0, qkv, pos)[0]
+    same(pr["ctx"], ctx, "attention ctx")
+    cq, cd = orc.quantize_row_q8_0(ctx)
+    same(pr["ctx_q"], cq, "ctx codes")
+    same(pr["ctx_d"], cd, "ctx scales")
+    gm.close()
+
+
 @pytest.mark.timeout(900)
 def test_exact_layer_kernels_70b_widths(hip, orc):
     """The 70B widths (Q|K|V 10240 x 8192, gate|up 57344 x 8192, down 8192 x
