@@ -493,10 +493,11 @@ struct AttnShared {
 // times the scale (matmul_slice cpu.rs:230-269, layer.rs:257-258); softmax
 // with the maximum from f32::MIN, glibc's expf, the sequential sum (seq_sum
 // for long rows) and e * (1/sum) (cpu.rs:395-423); ctx[d] = sum over the
-// rows of p * V[d], sequential (layer.rs:276-299).  f16 caches: each thread
-// requests its next K row before it folds the current one; thread d < HD
+// rows of p * V[d], sequential (layer.rs:276-299).  f16 caches: in decode
+// each thread requests its next K row before it folds the current one; thread d < HD
 // reads dim d of the blocked V rows (8 positions per 16-byte load) straight
-// from memory, kVRing blocks ahead (the first ones before the softmax).  f32 caches:
+// from memory, kVRing blocks ahead in decode (the first ones before the
+// softmax).  f32 caches:
 // V rows pass through LDS in 16 KB tiles that every thread loads
 // (coalesced), each tile requested while the previous one is added; `first`
 // holds the first tile's loads, issued by the caller.  Returns ctx[d] for
@@ -509,8 +510,6 @@ __device__ __forceinline__ void attn_start(AttnShared<HD, F16>& sh) {
   if (threadIdx.x < 32) sh.exptab[threadIdx.x] = expf_detail::kT[threadIdx.x];
 }
 
-template <bool F16>
-using VRing = u32x4[F16 ? kVRing : 1];
 
 template <int HD, bool F16, bool OWN>
 __device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, size_t head_bytes, int ncache,
@@ -555,18 +554,26 @@ __device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, 
     // loads are unconditional (rows clamped into the cache; a clamped row is
     // never scored), so the next row's load never waits on the current one
     const int last = max(ncache - 1, 0);
-    u32x4 ka[KW], kb[KW];
+    u32x4 ka[KW];
     int t = tid;
-    kload(min(t, last), ka);
-    while (t < ncache) {
-      const int t2 = t + kT;
-      kload(min(t2, last), kb);
-      score(t, ka);
-      if (t2 >= ncache) break;
-      const int t3 = t2 + kT;
-      kload(min(t3, last), ka);
-      score(t2, kb);
-      t = t3;
+    if constexpr (OWN) {  // decode: 32 workgroups, registers to spare
+      u32x4 kb[KW];
+      kload(min(t, last), ka);
+      while (t < ncache) {
+        const int t2 = t + kT;
+        kload(min(t2, last), kb);
+        score(t, ka);
+        if (t2 >= ncache) break;
+        const int t3 = t2 + kT;
+        kload(min(t3, last), ka);
+        score(t2, kb);
+        t = t3;
+      }
+    } else {  // prompt rows: many workgroups per CU, one K row per thread at a time
+      for (; t < ncache; t += kT) {
+        kload(t, ka);
+        score(t, ka);
+      }
     }
     if (OWN && tid == ncache % kT) {  // the new row, from LDS
       const float s = own_dot() * scale;
@@ -592,12 +599,14 @@ __device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, 
     }
   }
   // f16: the first V blocks of dim d, requested before the softmax (blocks
-  // clamped into the cache, unconditionally, as the K rows)
+  // clamped into the cache, unconditionally, as the K rows); prompt rows keep
+  // half the ring (their workgroups share a CU)
+  constexpr int RS = F16 ? (OWN ? kVRing : kVRing / 2) : 1;
   const int lastb = max(nblk - 1, 0);
-  VRing<F16> ring;
+  u32x4 ring[RS];
   if (F16 && d < HD) {
 #pragma unroll
-    for (int j = 0; j < (F16 ? kVRing : 1); ++j) ring[j] = vb[(size_t)min(j, lastb) * HD];
+    for (int j = 0; j < RS; ++j) ring[j] = vb[(size_t)min(j, lastb) * HD];
   }
   mx = wave_max(mx);
   if (lane == 0) sh.red[wave] = mx;
@@ -657,9 +666,9 @@ __device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, 
       };
       const int nfull = ncache / 8;
       // the last whole blocks from slot 0 of a round, then the partial one
-      auto tail = [&](const VRing<F16>& r, int b0) {
+      auto tail = [&](const u32x4 (&r)[RS], int b0) {
 #pragma unroll
-        for (int j = 0; j < kVRing; ++j) {
+        for (int j = 0; j < RS; ++j) {
           const int b = b0 + j;
           if (b < nfull) block8(r[j], 8 * b, 8);
           else if (b == nfull && 8 * b < ncache) block8(r[j], 8 * b, ncache - 8 * b);
@@ -668,11 +677,11 @@ __device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, 
       // whole rounds of the ring without a branch, the next round's loads
       // (clamped, unconditional) issued as each block is consumed
       int b0 = 0;
-      for (; b0 + kVRing <= nfull; b0 += kVRing) {
+      for (; b0 + RS <= nfull; b0 += RS) {
 #pragma unroll
-        for (int j = 0; j < kVRing; ++j) {
+        for (int j = 0; j < RS; ++j) {
           const u32x4 w = ring[j];
-          ring[j] = vb[(size_t)min(b0 + j + kVRing, lastb) * HD];
+          ring[j] = vb[(size_t)min(b0 + j + RS, lastb) * HD];
           block8(w, 8 * (b0 + j), 8);
         }
       }
