@@ -502,7 +502,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   // Combine: wave w takes query heads w, w + nw, ... of the group.  Lane s
   // loads split s's (max, sum) (one 8-byte load), so the maximum M is one
   // wave reduction and lane s forms the split's weight 2^(m_s - M); the
-  // weights and sums reach every lane by readlane.  Lane l owns dims
+  // weights and sums reach every lane through the wave's own 512 bytes at
+  // the start of the LDS (free once every wave has passed the ticket's
+  // barrier), read back as broadcasts: a readlane per split and value would
+  // make each multiply wait on its scalar result.  Lane l owns dims
   // DPL*l .. DPL*l + DPL-1 and adds the live splits' partial O in split
   // order, loaded in batches of 8, 16 or 32 (the live split count rounded
   // up; loads past it read zero with no memory access).  Splits past the
@@ -511,6 +514,8 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   constexpr int DPL = HD / 64;  // dims per lane
   const int nw = (int)(blockDim.x / LLMRS_WAVE), ns = a.nsplit, ns2 = ml_stride(ns);
   const int nlive = min(ns, (T + TILE - 1) / TILE);
+  float2* wsl = (float2*)lds + LLMRS_WAVE * wave;  // this wave's weights and sums, split s at [s]
+  static_assert(LY::TICKET >= (size_t)8 * LLMRS_WAVE * (TW > 4 ? TW : 4), "the combine's weight slots overlap the ticket");
   for (int hr = wave; hr < n_rep; hr += nw) {
     const size_t obase = (size_t)(g * n_rep + hr) * ns, mbase = (size_t)(g * n_rep + hr) * ns2;
     float Lx = 0.0f, Ox[DPL];
@@ -541,11 +546,12 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
         ls = lane < nlive ? __uint_as_float(mlv.y) : 0.0f;
         const float M = wave_max(ms);
         wl = __builtin_amdgcn_exp2f(ms - M);  // 0 past the live splits
+        wsl[lane] = make_float2(wl, ls);
       }
 #pragma unroll
       for (int u = 0; u < NL; ++u) {  // cpu.rs:395-423 order: sum, then weighted values
-        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), s0 + u));
-        const float l = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ls), s0 + u));
+        const float2 wv = wsl[s0 + u];  // split s0 + u's weight and sum, from lane s0 + u
+        const float w = wv.x, l = wv.y;
         Lx = Lx + w * l;
 #pragma unroll
         for (int i = 0; i < DPL; ++i) Ox[i] = Ox[i] + po[u][i] * w;
