@@ -512,7 +512,10 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
   // context hold no tile (split s starts at tile s): their partials (max
   // -inf, sum 0) would add exact zeros, so they are not read.
   constexpr int DPL = HD / 64;  // dims per lane
-  const int nw = (int)(blockDim.x / LLMRS_WAVE), ns = a.nsplit, ns2 = ml_stride(ns);
+  // waves of the launch (its launch bounds; the block size read at run time
+  // would be a memory load)
+  constexpr int nw = TW > 4 ? TW : 4;
+  const int ns = a.nsplit, ns2 = ml_stride(ns);
   const int nlive = min(ns, (T + TILE - 1) / TILE);
   float2* wsl = (float2*)lds + LLMRS_WAVE * wave;  // this wave's weights and sums, split s at [s]
   static_assert(LY::TICKET >= (size_t)8 * LLMRS_WAVE * (TW > 4 ? TW : 4), "the combine's weight slots overlap the ticket");

@@ -78,13 +78,18 @@ LLMRS_GEMV_FAMILY(q8h, WT_Q8H, 2)
 // Final reduction of the lm_head partials and the greedy step bookkeeping:
 // next = argmax (lowest index on ties); gen[pos+1] = next; tokens[pos+1] =
 // next once the prompt is consumed; pos += 1.
-extern "C" __global__ __launch_bounds__(256) void argmax_final(ArgmaxFinalArgs a) {
+// Block sizes of the launches below (their launch bounds): the block size
+// read at run time would be a vector load from the dispatch arguments and a
+// wait on every outstanding memory operation.
+constexpr int kArgmaxFinalThreads = 256, kArgmaxBatchThreads = 1024;
+
+extern "C" __global__ __launch_bounds__(kArgmaxFinalThreads) void argmax_final(ArgmaxFinalArgs a) {
   __shared__ float s_bv[8];
   __shared__ int s_bi[8];
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < a.nparts; i += blockDim.x)
+  for (int i = tid; i < a.nparts; i += kArgmaxFinalThreads)
     if (better(a.part_val[i], a.part_idx[i], bv, bi)) {
       bv = a.part_val[i];
       bi = a.part_idx[i];
@@ -104,7 +109,7 @@ extern "C" __global__ __launch_bounds__(256) void argmax_final(ArgmaxFinalArgs a
   }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < (int)(blockDim.x / LLMRS_WAVE); ++w)
+    for (int w = 1; w < kArgmaxFinalThreads / LLMRS_WAVE; ++w)
       if (better(s_bv[w], s_bi[w], bv, bi)) {
         bv = s_bv[w];
         bi = s_bi[w];
@@ -124,7 +129,7 @@ extern "C" __global__ __launch_bounds__(256) void argmax_final(ArgmaxFinalArgs a
 // as argmax_final advances one sequence (its prompt is consumed: the id is
 // both produced and the next input).  16-byte loads, four per thread in
 // flight.
-extern "C" __global__ __launch_bounds__(1024) void argmax_batch(ArgmaxBatchArgs a) {
+extern "C" __global__ __launch_bounds__(kArgmaxBatchThreads) void argmax_batch(ArgmaxBatchArgs a) {
   __shared__ float s_bv[16];
   __shared__ int s_bi[16];
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id(), b = blockIdx.x;
@@ -140,22 +145,22 @@ extern "C" __global__ __launch_bounds__(1024) void argmax_batch(ArgmaxBatchArgs 
   // rows start 16-byte aligned when vocab % 4 == 0; else scalar loads
   const int nv = a.vocab % 4 == 0 ? a.vocab / 4 : 0;
   const f32x4* row4 = (const f32x4*)row;
-  for (int v0 = tid; v0 < nv; v0 += 4 * (int)blockDim.x) {
+  for (int v0 = tid; v0 < nv; v0 += 4 * kArgmaxBatchThreads) {
     f32x4 x[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int v = v0 + u * (int)blockDim.x;
+      const int v = v0 + u * kArgmaxBatchThreads;
       x[u] = v < nv ? row4[v] : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int v = v0 + u * (int)blockDim.x;
+      const int v = v0 + u * kArgmaxBatchThreads;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (v < nv) take(x[u][e], 4 * v + e);
     }
   }
-  for (int i = 4 * nv + tid; i < a.vocab; i += blockDim.x) take(row[i], i);
+  for (int i = 4 * nv + tid; i < a.vocab; i += kArgmaxBatchThreads) take(row[i], i);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o);
@@ -171,7 +176,7 @@ extern "C" __global__ __launch_bounds__(1024) void argmax_batch(ArgmaxBatchArgs 
   }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < (int)(blockDim.x / LLMRS_WAVE); ++w)
+    for (int w = 1; w < kArgmaxBatchThreads / LLMRS_WAVE; ++w)
       if (better(s_bv[w], s_bi[w], bv, bi)) {
         bv = s_bv[w];
         bi = s_bi[w];

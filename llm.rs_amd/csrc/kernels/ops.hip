@@ -152,11 +152,15 @@ extern "C" __global__ __launch_bounds__(256) void matmul_t_f32(MatArgs g) {
 // or a given row; with norm_w set, also the first RMSNorm's operand: per
 // 32-element block (one half-wave), Q8_0 codes of x*w with d' = amax/127
 // (cpu.rs:724-743) and the block's sum of x^2 (cpu.rs:381, summed per block).
-extern "C" __global__ __launch_bounds__(256) void embed_gather(EmbedArgs e) {
+// Threads of an embed_gather launch (its launch bounds; the block size read
+// at run time would be a memory load).
+constexpr int kEmbedThreads = 256;
+
+extern "C" __global__ __launch_bounds__(kEmbedThreads) void embed_gather(EmbedArgs e) {
   if (e.rope_now && blockIdx.x == 0 && (e.batch_stride || blockIdx.y == 0)) {
     const int p = min(e.batch_stride ? e.pos_ptr[blockIdx.y] : *e.pos_ptr, e.rope_rows - 1);
     float* dst = e.rope_now + (size_t)blockIdx.y * 2 * e.rope_mid;
-    for (int t = threadIdx.x; t < e.rope_mid; t += blockDim.x) {
+    for (int t = threadIdx.x; t < e.rope_mid; t += kEmbedThreads) {
       dst[t] = e.rope_cos[(size_t)p * e.rope_mid + t];
       dst[e.rope_mid + t] = e.rope_sin[(size_t)p * e.rope_mid + t];
     }
@@ -176,7 +180,7 @@ extern "C" __global__ __launch_bounds__(256) void embed_gather(EmbedArgs e) {
     row = e.table + (size_t)tok * e.hidden;
   }
   float* x = e.x + (size_t)blockIdx.y * e.hidden;
-  for (int i0 = blockIdx.x * blockDim.x; i0 < e.hidden; i0 += gridDim.x * blockDim.x) {
+  for (int i0 = blockIdx.x * kEmbedThreads; i0 < e.hidden; i0 += gridDim.x * kEmbedThreads) {
     const int i = i0 + threadIdx.x;
     const bool ok = i < e.hidden;  // hidden is a multiple of 32: whole half-waves
     const float v = ok ? row[i] : 0.0f;
