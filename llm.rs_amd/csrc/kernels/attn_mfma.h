@@ -501,64 +501,71 @@ __device__ __forceinline__ void attn_mfma_item(const AttnArgs& a, int pos, uint8
 
   // Combine: wave w takes query heads w, w + nw, ... of the group.  Lane s
   // loads split s's (max, sum) (one 8-byte load), so the maximum M is one
-  // wave reduction and lane s forms the split's weight 2^(m_s - M); the
-  // weights and sums reach every lane through the wave's own 512 bytes at
-  // the start of the LDS (free once every wave has passed the ticket's
-  // barrier), read back as broadcasts: a readlane per split and value would
-  // make each multiply wait on its scalar result.  Lane l owns dims
-  // DPL*l .. DPL*l + DPL-1 and adds the live splits' partial O in split
-  // order, loaded in batches of 8, 16 or 32 (the live split count rounded
-  // up; loads past it read zero with no memory access).  Splits past the
-  // context hold no tile (split s starts at tile s): their partials (max
-  // -inf, sum 0) would add exact zeros, so they are not read.
+  // wave reduction, lane s forms the split's weight 2^(m_s - M) and the
+  // total sum is one wave sum of weight * sum (a fixed DPP tree); the
+  // weights reach every lane through the wave's own 256 bytes at the start
+  // of the LDS (free once every wave has passed the ticket's barrier), read
+  // back four at a time.  Lane l owns dims DPL*l .. DPL*l + DPL-1 and adds
+  // the live splits' partial O in split order, loaded in batches of 8, 16
+  // or 32 (the live split count rounded up) through a descriptor that ends
+  // at the head's last live split, so loads past it read zero with no
+  // memory access and need no per-load select.  Splits past the context
+  // hold no tile (split s starts at tile s): their partials (max -inf, sum
+  // 0) would add exact zeros, so they are not read.
   constexpr int DPL = HD / 64;  // dims per lane
   // waves of the launch (its launch bounds; the block size read at run time
   // would be a memory load)
   constexpr int nw = TW > 4 ? TW : 4;
   const int ns = a.nsplit, ns2 = ml_stride(ns);
   const int nlive = min(ns, (T + TILE - 1) / TILE);
-  float2* wsl = (float2*)lds + LLMRS_WAVE * wave;  // this wave's weights and sums, split s at [s]
-  static_assert(LY::TICKET >= (size_t)8 * LLMRS_WAVE * (TW > 4 ? TW : 4), "the combine's weight slots overlap the ticket");
-  for (int hr = wave; hr < n_rep; hr += nw) {
+  float* wsl = (float*)lds + LLMRS_WAVE * wave;  // this wave's split weights, split s at [s]
+  static_assert(LY::TICKET >= (size_t)4 * LLMRS_WAVE * nw, "the combine's weight slots overlap the ticket");
+  constexpr int pol = loc ? kSc0 : kSc1;
+  // hr is wave-uniform: made a scalar so the descriptors below stay in SGPRs
+  for (int hr = __builtin_amdgcn_readfirstlane(wave); hr < n_rep; hr += nw) {
     const size_t obase = (size_t)(g * n_rep + hr) * ns, mbase = (size_t)(g * n_rep + hr) * ns2;
+    // The head's live splits only: loads past them read zero, no memory access.
+    const __amdgpu_buffer_rsrc_t ro = span_rsrc(a.part_o + obase * HD, nlive * HD * 4);
     float Lx = 0.0f, Ox[DPL];
 #pragma unroll
     for (int i = 0; i < DPL; ++i) Ox[i] = 0.0f;
-    float ls = 0.0f, wl = 0.0f;
-    // NL partial-O loads from split s0 (zeros past the live splits), issued
-    // together; `ml` also requests the (max, sum) loads with the first batch
-    // and forms the weights, so nothing waits between the two requests.
+    // NL partial-O loads from split s0, issued together; `ml` also requests
+    // the (max, sum) loads with the first batch and forms the weights, so
+    // nothing waits between the two requests.
     auto batch = [&](auto nl_tag, int s0, bool ml) {
       constexpr int NL = decltype(nl_tag)::value;
       dev_u32x2 mlv = {0u, 0u};
-      if (ml) mlv = part_ld8(a.part_ml, lane < nlive ? (int)(8 * (mbase + lane)) : kOobOff, loc);
+      if (ml) mlv = __builtin_amdgcn_raw_buffer_load_b64(span_rsrc(a.part_ml + 2 * mbase, nlive * 8), 8 * lane, 0, pol);
       float po[NL][DPL];
 #pragma unroll
       for (int u = 0; u < NL; ++u) {
-        const int off = s0 + u < nlive ? (int)(((obase + s0 + u) * HD + DPL * lane) * 4) : kOobOff;
+        const int off = ((s0 + u) * HD + DPL * lane) * 4;
         if constexpr (DPL == 2) {
-          const dev_u32x2 v = part_ld8(a.part_o, off, loc);
+          const dev_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(ro, off, 0, pol);
           po[u][0] = __uint_as_float(v.x);
           po[u][1] = __uint_as_float(v.y);
         } else {
-          po[u][0] = __uint_as_float(part_ld4(a.part_o, off, loc));
+          po[u][0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ro, off, 0, pol));
         }
       }
       if (ml) {
         const float ms = lane < nlive ? __uint_as_float(mlv.x) : -INFINITY;  // split 0 holds position 0
-        ls = lane < nlive ? __uint_as_float(mlv.y) : 0.0f;
+        const float ls = lane < nlive ? __uint_as_float(mlv.y) : 0.0f;
         const float M = wave_max(ms);
-        wl = __builtin_amdgcn_exp2f(ms - M);  // 0 past the live splits
-        wsl[lane] = make_float2(wl, ls);
+        const float wl = __builtin_amdgcn_exp2f(ms - M);  // 0 past the live splits
+        Lx = wave_sum(wl * ls);
+        wsl[lane] = wl;
+      }
+      float w[NL];
+#pragma unroll
+      for (int u = 0; u < NL; u += 4) {
+        const f32x4 t = *(const f32x4*)(wsl + s0 + u);
+        w[u] = t.x; w[u + 1] = t.y; w[u + 2] = t.z; w[u + 3] = t.w;
       }
 #pragma unroll
-      for (int u = 0; u < NL; ++u) {  // cpu.rs:395-423 order: sum, then weighted values
-        const float2 wv = wsl[s0 + u];  // split s0 + u's weight and sum, from lane s0 + u
-        const float w = wv.x, l = wv.y;
-        Lx = Lx + w * l;
+      for (int u = 0; u < NL; ++u)
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) Ox[i] = Ox[i] + po[u][i] * w;
-      }
+        for (int i = 0; i < DPL; ++i) Ox[i] = Ox[i] + po[u][i] * w[u];
     };
     if (nlive <= 8) batch(std::integral_constant<int, 8>{}, 0, true);
     else if (nlive <= 16) batch(std::integral_constant<int, 16>{}, 0, true);

@@ -171,24 +171,12 @@ __device__ __forceinline__ void xcd_stu(void* base, int byte_off, unsigned v) {
 __device__ __forceinline__ dev_u32x4 xcd_ld16(const void* base, int byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(dev_rsrc(base), byte_off, 0, kSc0);
 }
-// Split-combine loads that may fall past the last split: an offset of
-// kOobOff reads as zero with no memory access (buffer range checking: the
-// descriptor's record count ends there).
-constexpr int kOobOff = 0x7FFFFFF0;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t oob_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, kOobOff, 0x00020000);
-}
-__device__ __forceinline__ dev_u32x4 part_ld16(const void* base, int byte_off, bool local) {
-  return local ? __builtin_amdgcn_raw_buffer_load_b128(oob_rsrc(base), byte_off, 0, kSc0)
-               : __builtin_amdgcn_raw_buffer_load_b128(oob_rsrc(base), byte_off, 0, kSc1);
-}
-__device__ __forceinline__ dev_u32x2 part_ld8(const void* base, int byte_off, bool local) {
-  return local ? __builtin_amdgcn_raw_buffer_load_b64(oob_rsrc(base), byte_off, 0, kSc0)
-               : __builtin_amdgcn_raw_buffer_load_b64(oob_rsrc(base), byte_off, 0, kSc1);
-}
-__device__ __forceinline__ unsigned part_ld4(const void* base, int byte_off, bool local) {
-  return local ? __builtin_amdgcn_raw_buffer_load_b32(oob_rsrc(base), byte_off, 0, kSc0)
-               : __builtin_amdgcn_raw_buffer_load_b32(oob_rsrc(base), byte_off, 0, kSc1);
+// A descriptor whose record count ends `bytes` past `base` (wave-uniform):
+// loads at or beyond it read zero with no memory access (buffer range
+// checking), so a loop over a variable number of items needs no per-load
+// select.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 __device__ __forceinline__ dev_u32x2 xcd_ld8(const void* base, int byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b64(dev_rsrc(base), byte_off, 0, kSc0);
