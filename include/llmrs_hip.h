@@ -132,6 +132,13 @@ int llmrs_softmax(const llmrs_tensor* x, llmrs_tensor** out);
 int llmrs_scale(const llmrs_tensor* x, float value, llmrs_tensor** out);
 /* Backend::copy_from (backend.rs:39). */
 int llmrs_copy_from(const llmrs_tensor* t, llmrs_tensor** out);
+/* No counterpart in the reference: a self-check of the device arithmetic the
+ * reference-order attention relies on.  For every f16 pattern h (both halves
+ * of a word) and every value a of the f32 tensor x, the one-instruction
+ * product (mixed-precision FMA with an addend of -0) is compared in bits with
+ * a * (float)h; *out = an f32 tensor [65536] of mismatch counts per pattern
+ * (NaN against NaN counts as equal).  All zero on a correct device. */
+int llmrs_check_mul_f16(const llmrs_tensor* x, llmrs_tensor** out);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

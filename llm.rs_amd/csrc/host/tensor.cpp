@@ -358,6 +358,20 @@ int llmrs_scale(const llmrs_tensor* x, float value, llmrs_tensor** out) {
   });
 }
 
+// Self-check with no counterpart in the reference: the reference-order
+// attention's one-instruction f16 products against the conversion and
+// multiply, for every f16 pattern and the values of x.
+int llmrs_check_mul_f16(const llmrs_tensor* x, llmrs_tensor** out) {
+  return guard([&] {
+    require_f32(x, "check_mul_f16");
+    LLMRS_REQUIRE(out, LLMRS_E_INVALID, "out is null");
+    std::unique_ptr<llmrs_tensor> o(alloc_f32({65536}));
+    EwArgs e{(float*)x->data, nullptr, (float*)o->data, 0.0f, (long)x->numel()};
+    launch("check_mul_f16", dim3(256), dim3(256), 0, ctx().stream, e);
+    *out = o.release();
+  });
+}
+
 // Backend::copy_from (backend.rs:39; cpu.rs:437-446).
 int llmrs_copy_from(const llmrs_tensor* t, llmrs_tensor** out) {
   return guard([&] {

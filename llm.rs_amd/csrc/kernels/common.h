@@ -90,6 +90,23 @@ __device__ __forceinline__ float xor16(float v) {
 __device__ __forceinline__ float h2f(uint16_t h) {
   return __half2float(__ushort_as_half(h));
 }
+// a * (float)h, rounded once as the f32 product, for the f16 h in the low
+// (high) half of w: the mixed-precision FMA with an addend of -0, whose sum
+// with the exact product is the product itself (sign of zero included).
+// One instruction instead of a conversion and a multiply; equal to them bit
+// for bit on gfx950 for every f16 pattern in either half against 8192 f32
+// values (signed zeros, denormals, infinities, NaNs, random bit patterns).
+// An addend of +0 would turn a -0 product into +0.
+__device__ __forceinline__ float mul_f16lo(float a, unsigned w) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel_hi:[0,1,0]" : "=v"(d) : "v"(a), "v"(w));
+  return d;
+}
+__device__ __forceinline__ float mul_f16hi(float a, unsigned w) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(d) : "v"(a), "v"(w));
+  return d;
+}
 // IEEE binary16 round-to-nearest-even.
 __device__ __forceinline__ uint16_t f2h(float f) {
   return __half_as_ushort(__float2half_rn(f));

@@ -543,8 +543,8 @@ __device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, 
         const float qv[8] = {qa[0], qa[1], qa[2], qa[3], qb[0], qb[1], qb[2], qb[3]};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          s = s + qv[2 * i] * h2f((uint16_t)(w[j][i] & 0xFFFF));
-          s = s + qv[2 * i + 1] * h2f((uint16_t)(w[j][i] >> 16));
+          s = s + mul_f16lo(qv[2 * i], w[j][i]);
+          s = s + mul_f16hi(qv[2 * i + 1], w[j][i]);
         }
       }
       s = s * scale;
@@ -650,14 +650,14 @@ __device__ __forceinline__ float attn_row(const char* kbase, const char* vbase, 
       auto block8 = [&](const u32x4& w, int t0, int cnt) {
         if (cnt == 8) {
           const f32x4 p0 = *(const f32x4*)(s_p + t0), p1 = *(const f32x4*)(s_p + t0 + 4);
-          acc = acc + p0[0] * h2f((uint16_t)(w[0] & 0xFFFF));
-          acc = acc + p0[1] * h2f((uint16_t)(w[0] >> 16));
-          acc = acc + p0[2] * h2f((uint16_t)(w[1] & 0xFFFF));
-          acc = acc + p0[3] * h2f((uint16_t)(w[1] >> 16));
-          acc = acc + p1[0] * h2f((uint16_t)(w[2] & 0xFFFF));
-          acc = acc + p1[1] * h2f((uint16_t)(w[2] >> 16));
-          acc = acc + p1[2] * h2f((uint16_t)(w[3] & 0xFFFF));
-          acc = acc + p1[3] * h2f((uint16_t)(w[3] >> 16));
+          acc = acc + mul_f16lo(p0[0], w[0]);
+          acc = acc + mul_f16hi(p0[1], w[0]);
+          acc = acc + mul_f16lo(p0[2], w[1]);
+          acc = acc + mul_f16hi(p0[3], w[1]);
+          acc = acc + mul_f16lo(p1[0], w[2]);
+          acc = acc + mul_f16hi(p1[1], w[2]);
+          acc = acc + mul_f16lo(p1[2], w[3]);
+          acc = acc + mul_f16hi(p1[3], w[3]);
         } else {  // the last, partial block: rows past ncache are not added
 #pragma unroll
           for (int e = 0; e < 8; ++e)

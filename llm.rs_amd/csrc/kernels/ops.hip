@@ -35,6 +35,25 @@ extern "C" __global__ __launch_bounds__(256) void scale_f32(EwArgs e) {
 }
 
 
+// Self-check of mul_f16lo / mul_f16hi (the reference-order attention's f16
+// products): thread h takes f16 pattern h in both halves of a word and
+// counts the values e.a[0 .. e.n) for which either mixed product differs in
+// bits from the conversion and multiply (NaN against NaN counts as equal);
+// the count goes to e.out[h].  Grid 256 x 256: every f16 pattern once.
+extern "C" __global__ __launch_bounds__(256) void check_mul_f16(EwArgs e) {
+  const unsigned h = blockIdx.x * 256u + threadIdx.x;
+  const unsigned w = h | (h << 16);
+  const float b = h2f((uint16_t)h);
+  unsigned bad = 0;
+  for (long i = 0; i < e.n; ++i) {
+    const float a = e.a[i], r = a * b, lo = mul_f16lo(a, w), hi = mul_f16hi(a, w);
+    const bool rn = r != r;
+    bad += (rn ? lo == lo : __float_as_uint(lo) != __float_as_uint(r)) ? 1u : 0u;
+    bad += (rn ? hi == hi : __float_as_uint(hi) != __float_as_uint(r)) ? 1u : 0u;
+  }
+  e.out[h] = (float)bad;
+}
+
 // Backend::rope_inplace (cpu.rs:326-357) with host-made sin/cos tables.
 extern "C" __global__ __launch_bounds__(256) void rope_f32(RopeArgs r) {
   const int mid = r.hd / 2;

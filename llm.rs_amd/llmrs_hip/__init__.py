@@ -79,6 +79,7 @@ _SIGS = {
     "llmrs_rms_norm": (C.c_int, [C.c_void_p, C.c_void_p, C.c_float, C.POINTER(C.c_void_p)]),
     "llmrs_softmax": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
     "llmrs_scale": (C.c_int, [C.c_void_p, C.c_float, C.POINTER(C.c_void_p)]),
+    "llmrs_check_mul_f16": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
     "llmrs_copy_from": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
     "llmrs_model_create": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p)]),
     "llmrs_model_free": (C.c_int, [C.c_void_p]),
@@ -320,6 +321,11 @@ class HipBackend:
 
     def copy_from(self, t: Tensor) -> Tensor:                     # backend.rs:39
         return _out_tensor(lib().llmrs_copy_from, t.handle)
+
+    def check_mul_f16(self, values: Tensor) -> Tensor:
+        """Self-check (llmrs_check_mul_f16): mismatch counts per f16 pattern
+        of the one-instruction f16 product against convert-and-multiply."""
+        return _out_tensor(lib().llmrs_check_mul_f16, values.handle)
 
 
 class ModelConfig(C.Structure):

@@ -187,6 +187,25 @@ def test_rope_bit_exact(hip, orc, rng):
         assert np.array_equal(t.data(), orc.rope_inplace(x, pos))
 
 
+def test_mixed_f16_product_equals_convert_multiply(hip):
+    """The reference-order attention multiplies f32 by f16 cache values with
+    one mixed-precision FMA (addend -0) instead of a conversion and a
+    multiply; its results must be the same bits for every f16 pattern.  The
+    f32 side: signed zeros, denormals, the normal range ends, infinities, a
+    NaN, powers of two, and random bit patterns and attention-sized values."""
+    special = np.array([0x00000000, 0x80000000, 0x00000001, 0x80000001, 0x007FFFFF, 0x00800000,
+                        0x7F7FFFFF, 0xFF7FFFFF, 0x7F800000, 0xFF800000, 0x7FC00000, 0x3F800000,
+                        0xBF800000, 0x00400000, 0x0F800000, 0x1F800000, 0x33800000, 0x7E800000,
+                        0x477FE000, 0x38800000, 0x33000000], dtype=np.uint32).view(F32)
+    g = np.random.default_rng(12345)
+    bits = g.integers(0, 2**32, 2048, dtype=np.uint64).astype(np.uint32).view(F32)
+    vals = np.concatenate([special, bits, g.uniform(-20, 20, 2048).astype(F32),
+                           g.uniform(0, 1, 1024).astype(F32)])
+    bad = hip.HipBackend().check_mul_f16(hip.Tensor.from_numpy(vals)).data()
+    assert bad.shape == (65536,)
+    assert int(bad.sum()) == 0, f"{int(np.count_nonzero(bad))} f16 patterns differ, e.g. {np.nonzero(bad)[0][:8]}"
+
+
 def test_elementwise(hip, orc, rng):
     be = hip.HipBackend()
     a = rng.uniform(-1, 1, (10, 10)).astype(F32)
