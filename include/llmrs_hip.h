@@ -297,8 +297,8 @@ int llmrs_model_set_sampling(llmrs_model* m, const llmrs_sampling* s);
  * for SiLU and softmax (layer.rs:75-79).  For the same weights and tokens,
  * logits and greedy tokens then equal the reference's bit for bit.  Prompts
  * run batched (the reference's batched prompt adds each row's sums in the
- * same orders).  Slower than the fast step (8B shape on MI355X: 2.2 vs
- * 1.4 ms per token at 512-600 positions); needs max_seq <= 16384.  Batches
+ * same orders).  Slower than the fast step (8B shape on MI355X: 2.17 vs
+ * 1.35 ms per token at 512-600 positions); needs max_seq <= 16384.  Batches
  * (llmrs_batch_*) always use the fast kernels. */
 int llmrs_model_set_exact(llmrs_model* m, int on);
 /* Tokens produced since llmrs_model_begin (the first comes from the prompt's
