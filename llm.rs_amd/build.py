@@ -1,6 +1,6 @@
 """Build the llmrs_hip backend: gfx950 code objects and the host library.
 
-Plays the role the north-star build.rs would: every ``csrc/kernels/*.hip``
+Plays the role a build.rs of the Rust crate would: every ``csrc/kernels/*.hip``
 becomes ``lib/<name>.hsaco`` (``hipcc --genco --offload-arch=gfx950``), which
 the host library loads with ``hipModuleLoad``; ``csrc/host/*.cpp`` becomes
 ``lib/libllmrs_hip.so`` with the C ABI of ``include/llmrs_hip.h``.

@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/oracle.cpp).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py - as the checker and the timed CPU baseline,
+cpu_baseline leg of bench.py - as the tests' parity reference and the timed CPU baseline,
 never as a product path.  Build with ``make -C oracle``.
 """
 from __future__ import annotations

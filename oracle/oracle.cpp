@@ -1,6 +1,6 @@
 // oracle.cpp - CPU restatement of the llm.rs reference CPU path.
 //
-// TEST INFRASTRUCTURE ONLY (the checker and the timed CPU baseline); the
+// TEST INFRASTRUCTURE ONLY (the tests' parity reference and the timed CPU baseline); the
 // product library never links it.  Compiled with -ffp-contract=off so that
 // every a*b+c rounds twice, as Rust code does.  Reference citations are
 // relative to the reference repository root.

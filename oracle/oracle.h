@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY.  Nothing on the product path (the llmrs_hip
  * library, its kernels, bench.py's GPU leg) may include, link or call this.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
- * as the checker and as the timed CPU baseline.
+ * as the parity reference of the tests and as the timed CPU baseline.
  *
  * Every function follows a reference file:line (paths relative to the
  * reference root), stated at its definition in oracle.cpp.  Floating-point

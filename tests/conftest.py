@@ -52,7 +52,7 @@ def rel_close(got, want, rtol=1e-3, atol=1e-4):
 
 
 # The greedy-stream bar: the GPU's stream equals the oracle's for the first
-# min(min_steps, length) steps (the north star's 64 identical steps), with no
+# min(min_steps, length) steps (the parity bar's 64 identical steps), with no
 # allowance; after that it may only part at a step whose oracle top1-top2
 # logit margin is below NEAR_TIE (a near-tie that f32 summation-order
 # differences can flip).

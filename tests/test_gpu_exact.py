@@ -11,7 +11,7 @@ kernels follow (exact.hip).  Bars, none with a tolerance:
   inputs;
 * model runs: the residual stream entering every layer, the final logits
   and the greedy stream equal the oracle's, every step (no near-tie
-  allowance).  The north star's bar (logits within 1e-2, 64 identical
+  allowance).  The parity bar (logits within 1e-2, 64 identical
   greedy steps) is asserted on its own besides, on the 1B Q4_0, 1B Q8_0,
   8B and 70B-width workloads.
 """
@@ -273,8 +273,8 @@ def run_workload(hip, orc, spec, steps):
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("index,prompt_len,steps", [(0, 32, 128), (1, 32, 128), (2, 512, 64)],
                          ids=["1b-q4_0-f32kv", "1b-q8_0-f16kv", "8b-q4_0-f16kv"])
-def test_exact_workload_north_star_bar(hip, orc, index, prompt_len, steps):
-    """The north star's parity bar on the full-size workloads (1B Q4_0 and
+def test_exact_workload_parity_bar(hip, orc, index, prompt_len, steps):
+    """The parity bar on the full-size workloads (1B Q4_0 and
     Q8_0 at 32+128, 8B at its 512-token prompt + 64 steps) with the
     reference-order kernels: logits within 1e-2 (here: equal) and every
     greedy step identical, with no near-tie allowance."""

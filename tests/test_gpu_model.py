@@ -69,7 +69,7 @@ def reference_builds(orc, spec, w, toks, steps=0, max_seq=None, prefill=None, st
 
 
 def logit_bar(orc, spec, w, toks, max_seq=None, prefill=None, start_pos=0):
-    """The north star's 1e-2 logit bar, or - where larger - how far the
+    """The 1e-2 logit bar, or - where larger - how far the
     reference's own rounding moves these logits (factor 1): its aarch64
     build against its x86 build, and its x86 build with the attention sums
     in float64 (the reference adds the softmax and P.V of a long context in
@@ -441,7 +441,7 @@ def test_q8_workload_within_reference_builds(hip, orc):
                    "15 identical greedy steps (its aarch64 build: 0.148, 6 steps); the reference-order kernels "
                    "meet the bar bit-exactly (test_gpu_exact.py)")
 def test_q8_workload_strict_bar(hip, orc):
-    """The north star's bar on the 1B Q8_0 workload with the fast kernels,
+    """The parity bar on the 1B Q8_0 workload with the fast kernels,
     which add in an order of their own (see the test above)."""
     spec, _, _, lerr, gtoks, otoks, margins = q8_workload(hip, orc)
     assert lerr < 1e-2

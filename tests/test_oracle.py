@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.cpp) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/oracle.cpp) before the tests trust it as their reference.
 
 Each reference known-answer test (src/test/cpu.rs, src/test/opencl.rs,
 src/core/layer.rs tests) is restated, and every function is also checked
