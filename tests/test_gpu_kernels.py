@@ -225,6 +225,28 @@ def test_decode_attention_layouts(hip, orc, kv, head_dim, nkv, streams, splits, 
     assert np.array_equal(again["ctx"], pr2["ctx"]), "attention is not deterministic"
 
 
+# The split combine's batches: the live splits (those holding a tile) are
+# read 8, 16 or 32 at a time, and past 32 in further batches of 32 whose
+# weights come from lanes 32-63 of the first (max, sum) load.  (splits, pos):
+# 12 live of 12 at 700 positions (22 tiles), 40 of 40 and 47 of 64 at 1500
+# (47 tiles).
+COMBINE_CASES = [(12, 700), (40, 1500), (64, 1500)]
+
+
+@pytest.mark.parametrize("kv", [DType.F16, DType.F32], ids=["f16", "f32"])
+@pytest.mark.parametrize("splits,pos", COMBINE_CASES, ids=lambda v: str(v))
+def test_decode_attention_combine_batches(hip, orc, kv, splits, pos, monkeypatch):
+    monkeypatch.setenv("LLMRS_ATTN_STREAMS" if kv == DType.F32 else "LLMRS_ATTN_WAVES", "1")
+    monkeypatch.setenv("LLMRS_ATTN_SPLITS", str(splits))
+    spec = syn.tiny(DType.Q4_0, kv, head_dim=128, n_layers=1, n_heads=32, n_kv_heads=8, ffn=512, seed=43)
+    gm, om, _ = layer_models(hip, orc, spec, pos + 3)
+    assert gm.decode_plan()["nsplit"] == splits
+    fill_cache(gm, om, spec, pos)
+    x = synth_normal(spec.seed, 96, spec.hidden, 0.0, 1.0)
+    pr = gm.probe_decode_layer(0, pos, x)
+    check_decode_attention(gm, om, orc, spec, pr, pos)
+
+
 @pytest.mark.parametrize("kv", [DType.F16, DType.F32], ids=["f16", "f32"])
 @pytest.mark.parametrize("head_dim", [128, 64])
 @pytest.mark.parametrize("waves,splits", [(1, 1), (4, 2), (8, 7), (1, 64), (8, 32), (4, 7)], ids=lambda v: str(v))
