@@ -835,8 +835,14 @@ void enqueue_prefill(llmrs_model* m, Launcher& L, size_t start, int M, bool head
                                  m->pf_x, H * sizeof(float), H * sizeof(float), M,
                                  hipMemcpyDeviceToDevice, L.s));
   };
-  EmbedArgs e{m->embed, m->tokens, m->pf_start, m->pf_x, m->err, H, c.vocab, nullptr, nullptr, nullptr,
-              nullptr, nullptr, 0};
+  EmbedArgs e{};  // no norm operand, no RoPE row: a chunk of rows from *pf_start
+  e.table = m->embed;
+  e.tokens = m->tokens;
+  e.pos_ptr = m->pf_start;
+  e.x = m->pf_x;
+  e.err = m->err;
+  e.hidden = H;
+  e.vocab = c.vocab;
   L("embed_gather", 8.0 * H * M, dim3((unsigned)((H + 255) / 256), (unsigned)M), dim3(256), 0, e);
   for (int li = 0; li < c.n_layers; ++li) {
     trace(li);
