@@ -584,6 +584,36 @@ def test_prefill_attention_mfma_vs_vector(hip, orc, spec, monkeypatch):
     assert e < 1e-2, f"mfma vs vector attention: residual relative error {e:.3g}"
 
 
+@pytest.mark.parametrize("spec", [TINY[0], TINY[1]], ids=lambda s: s.name)
+def test_decode_to_last_position(hip, orc, spec):
+    """Greedy decoding up to the cache's last position, with max_seq 40 (not
+    a whole number of 32-position tiles): the reference-order kernels give
+    the oracle's stream bit for bit, the fast kernels' logits at the last
+    position (over that cache) are within 1e-2 of the oracle's, and one more
+    step is refused."""
+    max_seq = 40
+    gm, om, _ = build(hip, orc, spec, max_seq=max_seq)
+    toks = syn.prompt(spec)
+    n = max_seq - len(toks) + 1  # the last decode step runs at position max_seq - 1
+    gm.set_exact(True)
+    gtoks = gm.generate(toks, n)
+    otoks, _ = om.generate(toks, n)
+    assert gtoks.size == n and np.array_equal(gtoks, otoks), \
+        f"streams part at step {int(np.nonzero(gtoks != otoks)[0][0])}"
+    with pytest.raises(hip.LlmrsError) as e:
+        gm.decode_steps(1)
+    assert e.value.code == hip.E_RANGE
+    # both caches now hold the same rows 0 .. max_seq - 2; the last position once more
+    last = int(otoks[-2])
+    gm.set_exact(False)
+    lg, _, _ = gm.forward([last], max_seq - 1)
+    olg, _ = om.forward([last], max_seq - 1)
+    err = float(np.max(np.abs(lg - olg)))
+    print(f"\nRAW {spec.name}: {n} identical reference-order steps to position {max_seq - 1}; "
+          f"fast logits there max-abs error {err:.3g}", flush=True)
+    assert err < 1e-2
+
+
 def test_error_paths(hip, orc):
     spec = syn.tiny(DType.Q4_0, DType.F32)
     gm, _, _ = build(hip, orc, spec, max_seq=16)
