@@ -234,11 +234,14 @@ COMBINE_CASES = [(12, 700), (40, 1500), (64, 1500)]
 
 
 @pytest.mark.parametrize("kv", [DType.F16, DType.F32], ids=["f16", "f32"])
+@pytest.mark.parametrize("head_dim", [128, 64])
 @pytest.mark.parametrize("splits,pos", COMBINE_CASES, ids=lambda v: str(v))
-def test_decode_attention_combine_batches(hip, orc, kv, splits, pos, monkeypatch):
+def test_decode_attention_combine_batches(hip, orc, kv, head_dim, splits, pos, monkeypatch):
+    """head_dim 128: two dims per lane in the combine (8-byte partial
+    loads); 64: one (4-byte loads)."""
     monkeypatch.setenv("LLMRS_ATTN_STREAMS" if kv == DType.F32 else "LLMRS_ATTN_WAVES", "1")
     monkeypatch.setenv("LLMRS_ATTN_SPLITS", str(splits))
-    spec = syn.tiny(DType.Q4_0, kv, head_dim=128, n_layers=1, n_heads=32, n_kv_heads=8, ffn=512, seed=43)
+    spec = syn.tiny(DType.Q4_0, kv, head_dim=head_dim, n_layers=1, n_heads=32, n_kv_heads=8, ffn=512, seed=43)
     gm, om, _ = layer_models(hip, orc, spec, pos + 3)
     assert gm.decode_plan()["nsplit"] == splits
     fill_cache(gm, om, spec, pos)
