@@ -188,6 +188,26 @@ def test_kv_contents_and_graph_vs_eager(hip, orc):
     assert list(ga) == eager
 
 
+@pytest.mark.parametrize("spec", [TINY[0], TINY[1]], ids=lambda s: s.name)
+def test_fast_kernels_repeat_bit_for_bit(hip, orc, spec):
+    """The fast kernels fix every reduction order (no float atomics; split
+    partials combined in split order), so two models on the same weights
+    replay the same HIP-graph stream, and their logits at the next position
+    are equal bit for bit, eager or replayed."""
+    w = syn.make_weights(spec)
+    toks = syn.prompt(spec)
+    runs = []
+    for _ in range(2):
+        gm, _, _ = build(hip, orc, spec, max_seq=256, weights=w)
+        ids = gm.generate(toks, 48)
+        lg, nxt, _ = gm.forward([int(ids[-1])], len(toks) + 47)
+        runs.append((ids, lg, nxt))
+        gm.close()
+    (ia, la, na), (ib, lb, nb) = runs
+    assert np.array_equal(ia, ib), "greedy streams differ between two runs"
+    assert np.array_equal(la.view(np.int32), lb.view(np.int32)) and na == nb, "logits differ between two runs"
+
+
 # Largest distance, in Q8_0 code units, of a pre-rounding product from the
 # midpoint between two codes for the GPU and the oracle to round it apart.
 # The products themselves differ by ~1e-5 code units (an ulp-level
